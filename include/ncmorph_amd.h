@@ -1,0 +1,152 @@
+/*
+ * ncmorph_amd: MI355X (gfx950) implementation of ncmorph's data-parallel hot
+ * path behind a plain C ABI. No HIP or torch types cross this boundary:
+ * pointers, sizes, int status codes and an opaque context.
+ *
+ * Two groups of entry points:
+ *   1. Drop-in replacements for the reference's Zig `kernels` functions
+ *      (host slices in, host slices out, synchronous). A Zig wrapper that
+ *      @cImport()s this header keeps the reference signatures and panics on
+ *      a nonzero status, as the reference panics on its asserts.
+ *   2. Device-resident, stream-ordered entry points (the benchmarked path):
+ *      device pointers, bf16 operands as uint16_t bit patterns, fp32 outputs.
+ *
+ * Status: 0 on success, a negative NCM_E_* value on failure; no entry point
+ * aborts. Device entry points are asynchronous on the context's stream.
+ *
+ * Layouts are row-major. A linear's weights are [out, in] (the reference's
+ * layout, packages/kernels/root.zig:57-58). RVQ codebooks are
+ * [levels][v][d] bf16; codes are int32 [b][sum_l t/s_l], level 0 first.
+ */
+#ifndef NCMORPH_AMD_H
+#define NCMORPH_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    NCM_OK = 0,
+    NCM_E_NULL = -1,      /* a required pointer is NULL */
+    NCM_E_SHAPE = -2,     /* dimensions inconsistent or unsupported */
+    NCM_E_LENGTH = -3,    /* a slice length does not match the dimensions */
+    NCM_E_HIP = -4,       /* a HIP runtime call failed */
+    NCM_E_NOMEM = -5,     /* device or host allocation failed */
+    NCM_E_DEVICE = -6,    /* no usable gfx950 device */
+    NCM_E_ARG = -7        /* an argument value is out of range */
+};
+
+/* Linear output modes. */
+enum {
+    NCM_OUT_F32 = 0,      /* fp32 accumulator, written as float */
+    NCM_OUT_BF16_F32 = 1, /* round_bf16(flush(sum)) written as float (the
+                             reference's output contract, root.zig:139) */
+    NCM_OUT_BF16 = 2      /* round_bf16(flush(sum)) written as uint16 bits */
+};
+
+typedef struct ncm_ctx ncm_ctx_t;
+
+/* Human-readable text for a status code. Never NULL. */
+const char* ncm_status_string(int status);
+/* Text of the last HIP error seen by this thread ("" if none). */
+const char* ncm_last_error(void);
+
+/* Context: one device, one stream, cached workspace. Not thread-safe: use
+ * one context per host thread. */
+int ncm_init(int device, ncm_ctx_t** out);
+int ncm_destroy(ncm_ctx_t* ctx);
+/* Route the context's work to a stream (a hipStream_t passed as void*;
+ * NULL is HIP's default stream). A new context uses a non-blocking stream
+ * of its own. */
+int ncm_set_stream(ncm_ctx_t* ctx, void* stream);
+void* ncm_get_stream(ncm_ctx_t* ctx);
+int ncm_synchronize(ncm_ctx_t* ctx);
+
+/* ===================================================================== */
+/* 1. Drop-in replacements (host memory, synchronous)                     */
+/* ===================================================================== */
+
+/* Replaces `kernels.matmul_bf16` (packages/kernels/root.zig:96-98):
+ * output[t, o] = round_bf16(sum_k bf16(input[t, k]) * bf16(weights[o, k])),
+ * fp32 accumulation. Operands are rounded to bf16 (RNE, subnormals flushed,
+ * as root.zig:124-135 do) on the device. Lengths are the Zig slice lengths
+ * and must equal the products of the dimensions (root.zig:107-109).
+ * Uses the calling thread's default context on device 0. */
+int ncm_matmul_bf16(const float* input, size_t input_len, const float* weights,
+                    size_t weights_len, float* output, size_t output_len,
+                    size_t token_count, size_t input_width, size_t output_width);
+
+/* Replaces `kernels.matmul_bf16_bias` (packages/kernels/root.zig:102-104):
+ * the bias (rounded to bf16) is added to the fp32 sum before the output
+ * rounding (root.zig:138). bias_len must equal output_width (:110). */
+int ncm_matmul_bf16_bias(const float* input, size_t input_len, const float* weights,
+                         size_t weights_len, const float* bias, size_t bias_len,
+                         float* output, size_t output_len, size_t token_count,
+                         size_t input_width, size_t output_width);
+
+/* Replaces `kernels.round_bf16` (packages/kernels/root.zig:10-12) and
+ * `bf16_t.from_f32` (packages/bf16/root.zig:17-22) for whole buffers:
+ * RNE, every NaN -> 0x7FC0, no flush. Host pointers. */
+int ncm_round_bf16(const float* values, float* out, size_t n);
+
+/* ===================================================================== */
+/* 2. Device-resident entry points (stream-ordered)                        */
+/* ===================================================================== */
+
+/* y[m, n] = sum_k x[m, k] * w[n, k] (+ bias[n]), fp32 accumulation on bf16
+ * MFMA. x: bf16 [m, k]; w: bf16 [n, k]; bias: bf16 [n] or NULL;
+ * y: float [m, n] (out_mode F32 or BF16_F32) or uint16 [m, n] (BF16).
+ * Requires k % 8 == 0 and 16-byte aligned x and w.
+ * Device counterpart of matmul_bf16_impl (packages/kernels/root.zig:106-142)
+ * with the accumulation order of the MFMA instead of oneDNN's pair order;
+ * results agree with the reference's fp32 sum within rel 1e-2 / abs 1e-3. */
+int ncm_linear_bf16(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                    const uint16_t* bias, void* y, int64_t m, int64_t k, int64_t n,
+                    int out_mode);
+
+/* f32 -> bf16 bits, RNE, NaN -> 0x7FC0 (packages/bf16/root.zig:17-22).
+ * flush != 0 additionally flushes subnormal results to signed zero (the
+ * operand treatment of root.zig:124-135). Device pointers. */
+int ncm_bf16_from_f32_dev(ncm_ctx_t* ctx, const float* src, uint16_t* dst, int64_t n,
+                          int flush);
+/* bf16 bits -> f32, exact (packages/bf16/root.zig:25-37). Device pointers. */
+int ncm_bf16_widen_dev(ncm_ctx_t* ctx, const uint16_t* src, float* dst, int64_t n);
+
+/* ---- multiscale residual vector quantization ---- */
+
+/* csq[l * v + k] = squared norm of codebook row (l, k), in the fixed fp32
+ * order of the oracle (64 strided lanes, halving tree). Device pointers. */
+int ncm_rvq_prepare(ncm_ctx_t* ctx, const uint16_t* codebooks, int64_t levels, int64_t v,
+                    int64_t d, float* csq);
+
+/* Multiscale RVQ encode. x: float [b, t, d]; strides: host int32 [levels],
+ * powers of two, non-increasing, t % strides[0] == 0 (level l pools by
+ * strides[l] and repeats back); codebooks: bf16 [levels, v, d]; csq from
+ * ncm_rvq_prepare. Outputs (device): codes int32 [b, sum_l t/s_l] (level 0
+ * first); recon float [b, t, d] or NULL (sum of the selected code vectors);
+ * gap float (codes layout) or NULL: relative gap between the two smallest
+ * full distances among the exactly rescored candidates (+inf when only one
+ * candidate needed rescoring). force_codes (device, codes layout) or NULL:
+ * teacher forcing; when given, later levels' residuals are built from these
+ * codes while `codes` still receives this library's own argmin.
+ * Requires d % 64 == 0, v <= 65536. n_flagged (host, nullable) receives the
+ * number of rows whose candidate list could not be proven complete and that
+ * were searched exhaustively (a synchronizing read). */
+int ncm_rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d,
+                   int64_t levels, const int32_t* strides, const uint16_t* codebooks,
+                   const float* csq, int64_t v, int32_t* codes, float* recon, float* gap,
+                   const int32_t* force_codes, int64_t* n_flagged);
+
+/* recon[b, t, :] = sum over levels (in order) of codebooks[l][codes_l]. */
+int ncm_rvq_decode(ncm_ctx_t* ctx, const int32_t* codes, int64_t b, int64_t t, int64_t d,
+                   int64_t levels, const int32_t* strides, const uint16_t* codebooks,
+                   int64_t v, float* recon);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NCMORPH_AMD_H */

@@ -1,0 +1,94 @@
+"""ctypes binding of the C ABI in include/ncmorph_amd.h.
+
+The shared library is built in-tree by ncmorph_amd/build.py. There is no
+fallback: if the library is missing or cannot be loaded, every entry point
+raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libncmorph_amd.so")
+
+NCM_OK = 0
+NCM_E_NULL = -1
+NCM_E_SHAPE = -2
+NCM_E_LENGTH = -3
+NCM_E_HIP = -4
+NCM_E_NOMEM = -5
+NCM_E_DEVICE = -6
+NCM_E_ARG = -7
+
+NCM_OUT_F32 = 0
+NCM_OUT_BF16_F32 = 1
+NCM_OUT_BF16 = 2
+
+# (name, restype, argtypes) of every exported entry point, in header order.
+vp, i32, i64, sz = C.c_void_p, C.c_int, C.c_int64, C.c_size_t
+SIGNATURES = [
+    ("ncm_status_string", C.c_char_p, [i32]),
+    ("ncm_last_error", C.c_char_p, []),
+    ("ncm_init", i32, [i32, C.POINTER(vp)]),
+    ("ncm_destroy", i32, [vp]),
+    ("ncm_set_stream", i32, [vp, vp]),
+    ("ncm_get_stream", vp, [vp]),
+    ("ncm_synchronize", i32, [vp]),
+    ("ncm_matmul_bf16", i32, [vp, sz, vp, sz, vp, sz, sz, sz, sz]),
+    ("ncm_matmul_bf16_bias", i32, [vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz]),
+    ("ncm_round_bf16", i32, [vp, vp, sz]),
+    ("ncm_linear_bf16", i32, [vp, vp, vp, vp, vp, i64, i64, i64, i32]),
+    ("ncm_bf16_from_f32_dev", i32, [vp, vp, vp, i64, i32]),
+    ("ncm_bf16_widen_dev", i32, [vp, vp, vp, i64]),
+    ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
+    ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
+    ("ncm_rvq_decode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, i64, vp]),
+]
+
+_lib = None
+
+
+class NcmError(RuntimeError):
+    """A nonzero status from the C ABI."""
+
+    def __init__(self, status: int, where: str):
+        self.status = status
+        text = "library not loaded"
+        detail = ""
+        if _lib is not None:
+            text = _lib.ncm_status_string(status).decode()
+            detail = _lib.ncm_last_error().decode()
+        msg = f"{where}: {text} ({status})"
+        if detail and status in (NCM_E_HIP, NCM_E_NOMEM, NCM_E_DEVICE):
+            msg += f" [{detail}]"
+        super().__init__(msg)
+
+
+def lib():
+    """Load the HIP library (raises if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"ncmorph_amd HIP library missing at {LIB_PATH}; "
+                "build it with `python -m ncmorph_amd.build`")
+        # One HIP runtime per process: when torch is present its bundled
+        # libamdhip64 must be loaded first so that this library binds to the
+        # same runtime (same SONAME) instead of loading a second copy.
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
+        L = C.CDLL(LIB_PATH)
+        for name, res, args in SIGNATURES:
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int, where: str) -> None:
+    if status != NCM_OK:
+        raise NcmError(status, where)

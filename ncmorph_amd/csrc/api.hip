@@ -1,0 +1,350 @@
+// C ABI of ncmorph_amd (include/ncmorph_amd.h): contexts, argument checks,
+// the host-slice drop-ins for the reference's Zig kernels, and the
+// device-resident entry points.
+#include <hip/hip_runtime.h>
+
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/ncmorph_amd.h"
+#include "linear.h"
+#include "rvq.h"
+
+struct ncm_ctx {
+    int device = 0;
+    hipStream_t own_stream = nullptr;
+    hipStream_t stream = nullptr;
+    void* ws = nullptr;  // grow-only device workspace
+    size_t ws_bytes = 0;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail_hip(hipError_t e, const char* what) {
+    g_last_error = std::string(what) + ": " + hipGetErrorString(e);
+    return NCM_E_HIP;
+}
+
+#define NCM_HIP(call)                                        \
+    do {                                                     \
+        hipError_t e_ = (call);                              \
+        if (e_ != hipSuccess) return fail_hip(e_, #call);    \
+    } while (0)
+
+bool is_gfx950(int device) {
+    hipDeviceProp_t p;
+    if (hipGetDeviceProperties(&p, device) != hipSuccess) return false;
+    return std::strncmp(p.gcnArchName, "gfx950", 6) == 0;
+}
+
+int ctx_bind(ncm_ctx_t* ctx) {
+    NCM_HIP(hipSetDevice(ctx->device));
+    return NCM_OK;
+}
+
+}  // namespace
+
+// Grow-only workspace. Growing waits for the stream so the old buffer is no
+// longer in use before it is released.
+int ncm_ctx_workspace(ncm_ctx_t* ctx, size_t bytes, void** out) {
+    if (bytes > ctx->ws_bytes) {
+        if (ctx->ws) {
+            NCM_HIP(hipStreamSynchronize(ctx->stream));
+            NCM_HIP(hipFree(ctx->ws));
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        size_t want = bytes + (bytes >> 3);
+        hipError_t e = hipMalloc(&ctx->ws, want);
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            ctx->ws = nullptr;
+            g_last_error = std::string("hipMalloc workspace: ") + hipGetErrorString(e);
+            return NCM_E_NOMEM;
+        }
+        ctx->ws_bytes = want;
+    }
+    *out = ctx->ws;
+    return NCM_OK;
+}
+
+hipStream_t ncm_ctx_stream(ncm_ctx_t* ctx) { return ctx->stream; }
+
+extern "C" {
+
+const char* ncm_status_string(int status) {
+    switch (status) {
+        case NCM_OK: return "ok";
+        case NCM_E_NULL: return "null pointer argument";
+        case NCM_E_SHAPE: return "invalid or unsupported shape";
+        case NCM_E_LENGTH: return "slice length does not match dimensions";
+        case NCM_E_HIP: return "HIP runtime error";
+        case NCM_E_NOMEM: return "allocation failed";
+        case NCM_E_DEVICE: return "no usable gfx950 device";
+        case NCM_E_ARG: return "argument out of range";
+        default: return "unknown status";
+    }
+}
+
+const char* ncm_last_error(void) { return g_last_error.c_str(); }
+
+int ncm_init(int device, ncm_ctx_t** out) {
+    if (!out) return NCM_E_NULL;
+    *out = nullptr;
+    int count = 0;
+    if (hipGetDeviceCount(&count) != hipSuccess || device < 0 || device >= count) {
+        (void)hipGetLastError();
+        g_last_error = "no HIP device with this index";
+        return NCM_E_DEVICE;
+    }
+    if (!is_gfx950(device)) {
+        g_last_error = "device is not gfx950";
+        return NCM_E_DEVICE;
+    }
+    ncm_ctx_t* ctx = new ncm_ctx();
+    ctx->device = device;
+    hipError_t e = hipSetDevice(device);
+    if (e == hipSuccess) e = hipStreamCreateWithFlags(&ctx->own_stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        delete ctx;
+        return fail_hip(e, "ncm_init");
+    }
+    ctx->stream = ctx->own_stream;
+    *out = ctx;
+    return NCM_OK;
+}
+
+int ncm_destroy(ncm_ctx_t* ctx) {
+    if (!ctx) return NCM_E_NULL;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
+    delete ctx;
+    return NCM_OK;
+}
+
+int ncm_set_stream(ncm_ctx_t* ctx, void* stream) {
+    if (!ctx) return NCM_E_NULL;
+    // NULL selects HIP's default (null) stream, as everywhere in HIP.
+    ctx->stream = (hipStream_t)stream;
+    return NCM_OK;
+}
+
+void* ncm_get_stream(ncm_ctx_t* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int ncm_synchronize(ncm_ctx_t* ctx) {
+    if (!ctx) return NCM_E_NULL;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    NCM_HIP(hipStreamSynchronize(ctx->stream));
+    return NCM_OK;
+}
+
+// ------------------------------------------------------------------ linear
+
+int ncm_linear_bf16(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                    void* y, int64_t m, int64_t k, int64_t n, int out_mode) {
+    if (!ctx) return NCM_E_NULL;
+    if (m < 0 || n < 0 || k < 0) return NCM_E_SHAPE;
+    if (out_mode < NCM_OUT_F32 || out_mode > NCM_OUT_BF16) return NCM_E_ARG;
+    if (m == 0 || n == 0) return NCM_OK;
+    if (!y || (k > 0 && (!x || !w))) return NCM_E_NULL;
+    // Rows must be 16-byte aligned for the vector loads; the loader's byte
+    // offsets must fit 31 bits inside one tile.
+    if (k % 8 != 0 || k > (int64_t(1) << 21)) return NCM_E_SHAPE;
+    if ((uintptr_t)x % 16 || (uintptr_t)w % 16) return NCM_E_ARG;
+    if (m > (int64_t(1) << 31) || n > (int64_t(1) << 31)) return NCM_E_SHAPE;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_linear(x, w, bias, y, m, k, n, out_mode, -1, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "linear kernel launch");
+    return NCM_OK;
+}
+
+int ncm_bf16_from_f32_dev(ncm_ctx_t* ctx, const float* src, uint16_t* dst, int64_t n,
+                          int flush) {
+    if (!ctx) return NCM_E_NULL;
+    if (n < 0) return NCM_E_SHAPE;
+    if (n == 0) return NCM_OK;
+    if (!src || !dst) return NCM_E_NULL;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_bf16_from_f32(src, dst, n, flush ? 1 : 0, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "bf16 conversion launch");
+    return NCM_OK;
+}
+
+int ncm_bf16_widen_dev(ncm_ctx_t* ctx, const uint16_t* src, float* dst, int64_t n) {
+    if (!ctx) return NCM_E_NULL;
+    if (n < 0) return NCM_E_SHAPE;
+    if (n == 0) return NCM_OK;
+    if (!src || !dst) return NCM_E_NULL;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_bf16_widen(src, dst, n, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "bf16 widen launch");
+    return NCM_OK;
+}
+
+// ------------------------------------------------------------------ drop-ins
+
+namespace {
+
+// One default context per host thread, created on first use (device 0).
+ncm_ctx_t* default_ctx(int* rc) {
+    thread_local ncm_ctx_t* ctx = nullptr;
+    thread_local int init_rc = 1;
+    if (init_rc == 1) init_rc = ncm_init(0, &ctx);
+    *rc = init_rc;
+    return ctx;
+}
+
+size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int host_linear(const float* input, size_t input_len, const float* weights, size_t weights_len,
+                const float* bias, size_t bias_len, float* output, size_t output_len, size_t T,
+                size_t K, size_t N) {
+    // root.zig:107-110: the slice lengths must match the dimensions.
+    if (input_len != T * K || weights_len != N * K || output_len != T * N) return NCM_E_LENGTH;
+    if (bias && bias_len != N) return NCM_E_LENGTH;
+    if (T == 0 || N == 0) return NCM_OK;
+    if (!input || !weights || !output) return NCM_E_NULL;
+    if (K > (size_t(1) << 21) || T > (size_t(1) << 31) || N > (size_t(1) << 31))
+        return NCM_E_SHAPE;
+    int rc = 0;
+    ncm_ctx_t* ctx = default_ctx(&rc);
+    if (rc) return rc;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    const size_t K8 = align_up(K, 8);
+    size_t off = 0;
+    auto carve = [&](size_t bytes) {
+        size_t o = off;
+        off = align_up(off + bytes, 256);
+        return o;
+    };
+    const size_t o_xf = carve(T * K * 4), o_wf = carve(N * K * 4), o_bf = carve(N * 4);
+    const size_t o_xb = carve(T * K8 * 2), o_wb = carve(N * K8 * 2), o_bb = carve(N * 2);
+    const size_t o_y = carve(T * N * 4);
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, off, &ws);
+    if (rc) return rc;
+    char* base = (char*)ws;
+    hipStream_t st = ctx->stream;
+    float* xf = (float*)(base + o_xf);
+    float* wf = (float*)(base + o_wf);
+    float* bf = (float*)(base + o_bf);
+    uint16_t* xb = (uint16_t*)(base + o_xb);
+    uint16_t* wb = (uint16_t*)(base + o_wb);
+    uint16_t* bb = (uint16_t*)(base + o_bb);
+    float* y = (float*)(base + o_y);
+    if (K > 0) {
+        NCM_HIP(hipMemcpyAsync(xf, input, T * K * 4, hipMemcpyHostToDevice, st));
+        NCM_HIP(hipMemcpyAsync(wf, weights, N * K * 4, hipMemcpyHostToDevice, st));
+    }
+    // Operands: round to bf16 and flush subnormals (root.zig:124-135),
+    // zero-padding K up to a multiple of 8.
+    NCM_HIP(ncm::launch_bf16_from_f32_2d(xf, xb, T, K, K8, 1, st));
+    NCM_HIP(ncm::launch_bf16_from_f32_2d(wf, wb, N, K, K8, 1, st));
+    if (bias) {
+        NCM_HIP(hipMemcpyAsync(bf, bias, N * 4, hipMemcpyHostToDevice, st));
+        NCM_HIP(ncm::launch_bf16_from_f32(bf, bb, N, 0, st));  // root.zig:138: no flush
+    }
+    NCM_HIP(ncm::launch_linear(xb, wb, bias ? bb : nullptr, y, T, K8, N, NCM_OUT_BF16_F32, -1,
+                               st));
+    NCM_HIP(hipMemcpyAsync(output, y, T * N * 4, hipMemcpyDeviceToHost, st));
+    NCM_HIP(hipStreamSynchronize(st));
+    return NCM_OK;
+}
+
+}  // namespace
+
+int ncm_matmul_bf16(const float* input, size_t input_len, const float* weights,
+                    size_t weights_len, float* output, size_t output_len, size_t token_count,
+                    size_t input_width, size_t output_width) {
+    return host_linear(input, input_len, weights, weights_len, nullptr, 0, output, output_len,
+                       token_count, input_width, output_width);
+}
+
+int ncm_matmul_bf16_bias(const float* input, size_t input_len, const float* weights,
+                         size_t weights_len, const float* bias, size_t bias_len, float* output,
+                         size_t output_len, size_t token_count, size_t input_width,
+                         size_t output_width) {
+    if (!bias) return NCM_E_NULL;
+    return host_linear(input, input_len, weights, weights_len, bias, bias_len, output,
+                       output_len, token_count, input_width, output_width);
+}
+
+int ncm_round_bf16(const float* values, float* out, size_t n) {
+    if (n == 0) return NCM_OK;
+    if (!values || !out) return NCM_E_NULL;
+    int rc = 0;
+    ncm_ctx_t* ctx = default_ctx(&rc);
+    if (rc) return rc;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    const size_t o_b = align_up(n * 4, 256);
+    rc = ncm_ctx_workspace(ctx, o_b + n * 4 + n * 2 + 256, &ws);
+    if (rc) return rc;
+    float* f = (float*)ws;
+    uint16_t* b = (uint16_t*)((char*)ws + o_b);
+    float* w = (float*)((char*)ws + o_b + align_up(n * 2, 256));
+    hipStream_t st = ctx->stream;
+    NCM_HIP(hipMemcpyAsync(f, values, n * 4, hipMemcpyHostToDevice, st));
+    NCM_HIP(ncm::launch_bf16_from_f32(f, b, (int64_t)n, 0, st));
+    NCM_HIP(ncm::launch_bf16_widen(b, w, (int64_t)n, st));
+    NCM_HIP(hipMemcpyAsync(out, w, n * 4, hipMemcpyDeviceToHost, st));
+    NCM_HIP(hipStreamSynchronize(st));
+    return NCM_OK;
+}
+
+// ------------------------------------------------------------------ RVQ
+
+int ncm_rvq_prepare(ncm_ctx_t* ctx, const uint16_t* codebooks, int64_t levels, int64_t v,
+                    int64_t d, float* csq) {
+    if (!ctx) return NCM_E_NULL;
+    if (levels < 1 || v < 1 || d < 1) return NCM_E_SHAPE;
+    if (!codebooks || !csq) return NCM_E_NULL;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_rvq_csq(codebooks, levels * v, d, csq, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "rvq csq launch");
+    return NCM_OK;
+}
+
+int ncm_rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d,
+                   int64_t levels, const int32_t* strides, const uint16_t* codebooks,
+                   const float* csq, int64_t v, int32_t* codes, float* recon, float* gap,
+                   const int32_t* force_codes, int64_t* n_flagged) {
+    if (!ctx) return NCM_E_NULL;
+    if (!x || !strides || !codebooks || !csq || !codes) return NCM_E_NULL;
+    int rc = ncm::rvq_check_shape(b, t, d, levels, strides, v);
+    if (rc) return rc;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    return ncm::rvq_encode(ctx, x, b, t, d, levels, strides, codebooks, csq, v, codes, recon,
+                           gap, force_codes, n_flagged);
+}
+
+int ncm_rvq_decode(ncm_ctx_t* ctx, const int32_t* codes, int64_t b, int64_t t, int64_t d,
+                   int64_t levels, const int32_t* strides, const uint16_t* codebooks, int64_t v,
+                   float* recon) {
+    if (!ctx) return NCM_E_NULL;
+    if (!codes || !strides || !codebooks || !recon) return NCM_E_NULL;
+    int rc = ncm::rvq_check_shape(b, t, d, levels, strides, v);
+    if (rc) return rc;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_rvq_decode(codes, b, t, d, levels, strides, codebooks, v, recon,
+                                          ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "rvq decode launch");
+    return NCM_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,63 @@
+// Shared device helpers for the gfx950 kernels: bf16 bit conversions,
+// buffer resources and the wave-level vector types.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ncmorph_amd.h"
+
+namespace ncm {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kWave = 64;
+
+// RNE f32 -> bf16 bits, every NaN -> 0x7FC0, no flush
+// (packages/bf16/root.zig:17-22).
+__device__ __forceinline__ uint32_t bf16_bits_rne(float v) {
+    uint32_t x = __float_as_uint(v);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    return (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
+}
+
+// Exponent bits zero -> signed zero (packages/kernels/root.zig:144-148).
+__device__ __forceinline__ float flush_subnormal(float v) {
+    uint32_t b = __float_as_uint(v);
+    return (b & 0x7F800000u) == 0 ? __uint_as_float(b & 0x80000000u) : v;
+}
+
+__device__ __forceinline__ float bf16_lo_to_f32(uint32_t packed) {
+    return __uint_as_float(packed << 16);
+}
+__device__ __forceinline__ float bf16_hi_to_f32(uint32_t packed) {
+    return __uint_as_float(packed & 0xFFFF0000u);
+}
+
+// Raw buffer resource over [base, base + bytes). Loads past `bytes` return
+// zero, which is how partial tiles are zero-filled without branches.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                             0x00020000);
+}
+
+// An offset that is always outside any resource built above.
+constexpr uint32_t kOobOffset = 0x80000000u;
+
+__device__ __forceinline__ u32x4_t buffer_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// Remap a linear workgroup id so that consecutive logical tiles land on the
+// same XCD (workgroups are dispatched round-robin over the 8 XCDs).
+__device__ __forceinline__ int xcd_remap(int bid, int nblk) {
+    constexpr int kXcd = 8;
+    if (nblk % kXcd != 0) return bid;
+    return (bid % kXcd) * (nblk / kXcd) + bid / kXcd;
+}
+
+}  // namespace ncm

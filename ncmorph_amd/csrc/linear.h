@@ -1,0 +1,25 @@
+// Host-side launchers of the HIP kernels (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ncm {
+
+// Tile configuration chosen for an M x N output: 0 = 256x256, 1 = 256x128,
+// 2 = 128x128. `forced` in [0, 2] overrides the choice.
+int linear_tile_config(int64_t M, int64_t N, int forced);
+
+hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, void* y,
+                         int64_t M, int64_t K, int64_t N, int out_mode, int config,
+                         hipStream_t stream);
+
+hipError_t launch_bf16_from_f32(const float* src, uint16_t* dst, int64_t n, int flush,
+                                hipStream_t stream);
+// Row-padded variant: src [rows, cols] -> dst [rows, ld] (ld >= cols),
+// columns [cols, ld) zero-filled.
+hipError_t launch_bf16_from_f32_2d(const float* src, uint16_t* dst, int64_t rows, int64_t cols,
+                                   int64_t ld, int flush, hipStream_t stream);
+hipError_t launch_bf16_widen(const uint16_t* src, float* dst, int64_t n, hipStream_t stream);
+
+}  // namespace ncm

@@ -1,0 +1,37 @@
+// Host-side RVQ launchers (internal to the library).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/ncmorph_amd.h"
+
+int ncm_ctx_workspace(ncm_ctx_t* ctx, size_t bytes, void** out);
+hipStream_t ncm_ctx_stream(ncm_ctx_t* ctx);
+
+namespace ncm {
+
+constexpr int kMaxLevels = 32;
+
+struct LevelTable {
+    int32_t stride[kMaxLevels];
+    int64_t offset[kMaxLevels];  // code offset of each level inside a batch row
+    int32_t levels;
+    int64_t total;               // codes per batch row
+};
+
+int rvq_check_shape(int64_t b, int64_t t, int64_t d, int64_t levels, const int32_t* strides,
+                    int64_t v);
+LevelTable make_level_table(int64_t t, int64_t levels, const int32_t* strides);
+
+hipError_t launch_rvq_csq(const uint16_t* codebooks, int64_t rows, int64_t d, float* csq,
+                          hipStream_t stream);
+hipError_t launch_rvq_decode(const int32_t* codes, int64_t b, int64_t t, int64_t d,
+                             int64_t levels, const int32_t* strides, const uint16_t* codebooks,
+                             int64_t v, float* recon, hipStream_t stream);
+int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
+               const int32_t* strides, const uint16_t* codebooks, const float* csq, int64_t v,
+               int32_t* codes, float* recon, float* gap, const int32_t* force_codes,
+               int64_t* n_flagged);
+
+}  // namespace ncm

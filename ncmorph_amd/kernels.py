@@ -1,0 +1,118 @@
+"""Mirror of the reference's Zig `kernels` operator surface for the linear.
+
+Host-slice functions keep the reference signatures and argument meaning
+(packages/kernels/root.zig:10-12, :96-104): flat float32 buffers, explicit
+dimensions, caller-owned output. Where the reference asserts
+(root.zig:107-110) these raise NcmError. They run on the GPU through the C
+ABI; nothing here computes on the CPU.
+
+`linear_bf16` is the device-resident path: torch tensors already in HBM,
+bf16 operands, fp32 (or bf16) output, stream-ordered on torch's current
+stream.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+
+from ._lib import NCM_OUT_BF16, NCM_OUT_BF16_F32, NCM_OUT_F32, NcmError, check, lib
+from .context import default_context
+
+_OUT_MODES = {"f32": NCM_OUT_F32, "bf16_f32": NCM_OUT_BF16_F32, "bf16": NCM_OUT_BF16}
+
+
+def _host_f32(a, name):
+    if not isinstance(a, np.ndarray) or a.dtype != np.float32 or not a.flags.c_contiguous:
+        raise TypeError(f"{name} must be a C-contiguous float32 numpy array")
+    return a
+
+
+def _p(a):
+    return C.c_void_p(a.ctypes.data) if a is not None and a.size else None
+
+
+def matmul_bf16(input, weights, output, token_count, input_width, output_width):
+    """kernels.matmul_bf16 (root.zig:96-98): output = round_bf16(input * weightsT)
+    with bf16 operands and fp32 accumulation, computed on the GPU."""
+    for a, n in ((input, "input"), (weights, "weights"), (output, "output")):
+        _host_f32(a, n)
+    check(lib().ncm_matmul_bf16(_p(input), input.size, _p(weights), weights.size, _p(output),
+                                output.size, token_count, input_width, output_width),
+          "matmul_bf16")
+
+
+def matmul_bf16_bias(input, weights, bias, output, token_count, input_width, output_width):
+    """kernels.matmul_bf16_bias (root.zig:102-104): the bf16 bias is added to
+    the fp32 sum before the single bf16 output rounding."""
+    for a, n in ((input, "input"), (weights, "weights"), (bias, "bias"), (output, "output")):
+        _host_f32(a, n)
+    check(lib().ncm_matmul_bf16_bias(_p(input), input.size, _p(weights), weights.size,
+                                     C.c_void_p(bias.ctypes.data), bias.size,
+                                     _p(output), output.size, token_count, input_width,
+                                     output_width),
+          "matmul_bf16_bias")
+
+
+def round_bf16(value):
+    """kernels.round_bf16 (root.zig:10-12) on a scalar or a float32 array,
+    RNE with every NaN -> 0x7FC0, computed on the GPU."""
+    scalar = np.isscalar(value) or np.ndim(value) == 0
+    a = np.ascontiguousarray(np.atleast_1d(np.asarray(value, dtype=np.float32)))
+    out = np.empty_like(a)
+    check(lib().ncm_round_bf16(_p(a), _p(out), a.size), "round_bf16")
+    return np.float32(out[0]) if scalar else out.reshape(np.shape(value))
+
+
+# ------------------------------------------------------------ device path
+def _dev_ptr(t, name):
+    if t is None:
+        return None
+    if not t.is_cuda or not t.is_contiguous():
+        raise ValueError(f"{name} must be a contiguous GPU tensor")
+    return C.c_void_p(t.data_ptr())
+
+
+def linear_bf16(x, w, bias=None, out=None, out_mode: str = "f32", ctx=None):
+    """y = x @ w.T with bf16 operands (torch.bfloat16 tensors [m, k] and
+    [n, k]), fp32 accumulation, on torch's current stream."""
+    import torch
+
+    m, k = x.shape
+    n, k2 = w.shape
+    if k != k2:
+        raise NcmError(-2, "linear_bf16")
+    mode = _OUT_MODES[out_mode]
+    if out is None:
+        dt = torch.int16 if mode == NCM_OUT_BF16 else torch.float32
+        out = torch.empty((m, n), dtype=dt, device=x.device)
+    ctx = ctx or default_context(x.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_linear_bf16(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
+                                _dev_ptr(bias, "bias"), _dev_ptr(out, "out"), m, k, n, mode),
+          "linear_bf16")
+    return out
+
+
+def bf16_from_f32(src, flush: bool = False, ctx=None):
+    """Device f32 -> bf16 (RNE, NaN -> 0x7FC0), returned as torch.bfloat16."""
+    import torch
+
+    out = torch.empty(src.shape, dtype=torch.bfloat16, device=src.device)
+    ctx = ctx or default_context(src.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_bf16_from_f32_dev(ctx.handle, _dev_ptr(src, "src"), _dev_ptr(out, "out"),
+                                      src.numel(), 1 if flush else 0), "bf16_from_f32")
+    return out
+
+
+def bf16_widen(src, ctx=None):
+    """Device bf16 -> f32 (exact)."""
+    import torch
+
+    out = torch.empty(src.shape, dtype=torch.float32, device=src.device)
+    ctx = ctx or default_context(src.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_bf16_widen_dev(ctx.handle, _dev_ptr(src, "src"), _dev_ptr(out, "out"),
+                                   src.numel()), "bf16_widen")
+    return out

@@ -1,0 +1,564 @@
+/*
+ * CPU oracle for the ncmorph hot path. TEST INFRASTRUCTURE ONLY: loaded by
+ * the test suite, the smoke check and the CPU-baseline leg of the benchmark,
+ * never by the product path. Build: oracle/Makefile (-O3 -mfma
+ * -ffp-contract=off; every fused multiply-add is an explicit fmaf).
+ *
+ * Parity status of each function:
+ *   bf16 from/to/widen/flush .... pinned (reference KAT vectors + exhaustive)
+ *   ncmo_matmul_bf16* ........... pinned (reference KATs root.zig:707-770)
+ *   ncmo_matmul_reference ....... pinned (hand-computed KAT root.zig:684-695,
+ *                                 D53 bound vs f64)
+ *   RVQ (dot, csq, encode, level_rows, decode) ... pinned by mathematics only
+ *     (f64 brute force, planted codes, tie-break, pooling invariants), since
+ *     the reference has no RVQ implementation or test.
+ */
+#include "ncm_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ */
+/* bf16 numerics                                                       */
+/* ------------------------------------------------------------------ */
+
+static inline uint32_t f2u(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    return u;
+}
+static inline float u2f(uint32_t u) {
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* packages/bf16/root.zig:17-22: RNE, every NaN -> 0x7FC0, no FTZ. */
+uint16_t ncmo_bf16_from_f32(float value) {
+    uint32_t x = f2u(value);
+    if ((x & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    uint32_t bias = 0x7FFFu + ((x >> 16) & 1u);
+    return (uint16_t)((x + bias) >> 16);
+}
+
+/* packages/bf16/root.zig:25-27: exact widen. */
+float ncmo_bf16_to_f32(uint16_t bits) { return u2f((uint32_t)bits << 16); }
+
+/* packages/kernels/root.zig:10-12 */
+float ncmo_round_bf16(float value) { return ncmo_bf16_to_f32(ncmo_bf16_from_f32(value)); }
+
+void ncmo_bf16_from_f32_array(const float* src, uint16_t* dst, size_t n) {
+    for (size_t i = 0; i < n; ++i) dst[i] = ncmo_bf16_from_f32(src[i]);
+}
+
+/* packages/bf16/root.zig:31-37: little-endian bf16 bytes -> f32. */
+void ncmo_widen_little_endian(float* dst, const uint8_t* src, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        uint16_t bits = (uint16_t)(src[2 * i] | ((uint16_t)src[2 * i + 1] << 8));
+        dst[i] = ncmo_bf16_to_f32(bits);
+    }
+}
+
+/* packages/kernels/root.zig:144-148: exponent bits zero -> signed zero. */
+float ncmo_flush_f32_subnormal(float value) {
+    uint32_t bits = f2u(value);
+    if ((bits & 0x7F800000u) == 0) return u2f(bits & 0x80000000u);
+    return value;
+}
+
+/* ------------------------------------------------------------------ */
+/* linear                                                              */
+/* ------------------------------------------------------------------ */
+
+/* K-block rule of root.zig:112: 512 when K <= 1024, 1024 when K > 1024,
+ * never more than K. */
+static size_t reduction_block(size_t input_width) {
+    size_t b = input_width > 1024 ? 1024 : 512;
+    return input_width < b ? input_width : b;
+}
+
+#define FTZ ncmo_flush_f32_subnormal
+
+/* root.zig:106-142, for one (token, output) pair. xin/win: f32 values that
+ * are rounded to bf16 on use (bf16 values pass through unchanged). */
+static float bf16_dot_f32(const float* xin, const float* win, size_t k, size_t kb) {
+    float sum = 0.0f;
+    for (size_t b0 = 0; b0 < k; b0 += kb) {
+        size_t b1 = b0 + kb < k ? b0 + kb : k;
+        float partial = 0.0f;
+        size_t i = b0;
+        for (; i + 1 < b1; i += 2) {
+            /* root.zig:124-129: the high element of each pair first. */
+            float ih = FTZ(ncmo_round_bf16(xin[i + 1]));
+            float wh = FTZ(ncmo_round_bf16(win[i + 1]));
+            float il = FTZ(ncmo_round_bf16(xin[i]));
+            float wl = FTZ(ncmo_round_bf16(win[i]));
+            partial = FTZ(fmaf(ih, wh, partial));
+            partial = FTZ(fmaf(il, wl, partial));
+        }
+        if (i < b1) { /* odd tail, root.zig:131-135 */
+            float iv = FTZ(ncmo_round_bf16(xin[i]));
+            float wv = FTZ(ncmo_round_bf16(win[i]));
+            partial = FTZ(fmaf(iv, wv, partial));
+        }
+        sum += partial; /* no flush on block sums, root.zig:136 */
+    }
+    return sum;
+}
+
+static float bf16_dot_u16(const uint16_t* xin, const uint16_t* win, size_t k, size_t kb) {
+    float sum = 0.0f;
+    for (size_t b0 = 0; b0 < k; b0 += kb) {
+        size_t b1 = b0 + kb < k ? b0 + kb : k;
+        float partial = 0.0f;
+        size_t i = b0;
+        for (; i + 1 < b1; i += 2) {
+            float ih = FTZ(ncmo_bf16_to_f32(xin[i + 1]));
+            float wh = FTZ(ncmo_bf16_to_f32(win[i + 1]));
+            float il = FTZ(ncmo_bf16_to_f32(xin[i]));
+            float wl = FTZ(ncmo_bf16_to_f32(win[i]));
+            partial = FTZ(fmaf(ih, wh, partial));
+            partial = FTZ(fmaf(il, wl, partial));
+        }
+        if (i < b1) {
+            float iv = FTZ(ncmo_bf16_to_f32(xin[i]));
+            float wv = FTZ(ncmo_bf16_to_f32(win[i]));
+            partial = FTZ(fmaf(iv, wv, partial));
+        }
+        sum += partial;
+    }
+    return sum;
+}
+
+void ncmo_matmul_bf16_rows(const float* input, const float* weights, const float* bias,
+                           float* output, float* sum_out, size_t token_count,
+                           size_t input_width, size_t output_width, size_t row_begin,
+                           size_t row_end) {
+    (void)token_count;
+    size_t kb = reduction_block(input_width);
+    for (size_t t = row_begin; t < row_end; ++t) {
+        for (size_t o = 0; o < output_width; ++o) {
+            float sum = kb ? bf16_dot_f32(input + t * input_width,
+                                          weights + o * input_width, input_width, kb)
+                           : 0.0f;
+            if (bias) sum += ncmo_round_bf16(bias[o]); /* root.zig:138 */
+            if (sum_out) sum_out[t * output_width + o] = sum;
+            output[t * output_width + o] = ncmo_round_bf16(sum); /* root.zig:139 */
+        }
+    }
+}
+
+void ncmo_matmul_bf16(const float* input, const float* weights, const float* bias,
+                      float* output, float* sum_out, size_t token_count, size_t input_width,
+                      size_t output_width) {
+    ncmo_matmul_bf16_rows(input, weights, bias, output, sum_out, token_count, input_width,
+                          output_width, 0, token_count);
+}
+
+void ncmo_matmul_bf16_u16_rows(const uint16_t* input, const uint16_t* weights,
+                               const uint16_t* bias, float* output, float* sum_out,
+                               size_t token_count, size_t input_width, size_t output_width,
+                               size_t row_begin, size_t row_end) {
+    (void)token_count;
+    size_t kb = reduction_block(input_width);
+    for (size_t t = row_begin; t < row_end; ++t) {
+        for (size_t o = 0; o < output_width; ++o) {
+            float sum = kb ? bf16_dot_u16(input + t * input_width,
+                                          weights + o * input_width, input_width, kb)
+                           : 0.0f;
+            if (bias) sum += ncmo_bf16_to_f32(bias[o]);
+            if (sum_out) sum_out[t * output_width + o] = sum;
+            output[t * output_width + o] = ncmo_round_bf16(sum);
+        }
+    }
+}
+
+/* root.zig:71-93: increasing k, f32 product then f32 add (no fusion). */
+void ncmo_matmul_reference(const float* input, const float* weights, float* output,
+                           size_t token_count, size_t input_width, size_t output_width) {
+    for (size_t t = 0; t < token_count; ++t)
+        for (size_t o = 0; o < output_width; ++o) {
+            float sum = 0.0f;
+            for (size_t k = 0; k < input_width; ++k) {
+                float p = input[t * input_width + k] * weights[o * input_width + k];
+                sum += p;
+            }
+            output[t * output_width + o] = sum;
+        }
+}
+
+void ncmo_matmul_f64(const float* input, const float* weights, double* output,
+                     double* abs_sum, size_t token_count, size_t input_width,
+                     size_t output_width) {
+    for (size_t t = 0; t < token_count; ++t)
+        for (size_t o = 0; o < output_width; ++o) {
+            double s = 0.0, a = 0.0;
+            for (size_t k = 0; k < input_width; ++k) {
+                double p = (double)input[t * input_width + k] *
+                           (double)weights[o * input_width + k];
+                s += p;
+                a += fabs(p);
+            }
+            output[t * output_width + o] = s;
+            if (abs_sum) abs_sum[t * output_width + o] = a;
+        }
+}
+
+/* FNV-1a-64 over the bf16 bits of each value, root.zig:734-739. */
+uint64_t ncmo_fnv1a_bf16_digest(const float* values, size_t n) {
+    uint64_t h = 14695981039346656037ull;
+    for (size_t i = 0; i < n; ++i) {
+        uint16_t bits = (uint16_t)(f2u(values[i]) >> 16);
+        h = (h ^ bits) * 1099511628211ull;
+    }
+    return h;
+}
+
+/* ------------------------------------------------------------------ */
+/* RVQ                                                                 */
+/* ------------------------------------------------------------------ */
+
+/* Fixed fp32 order for a length-d dot product: 64 lanes; lane j owns
+ * elements i = 256 m + 4 j + e (m ascending, then e = 0..3) and accumulates
+ * them with fmaf from +0; then a halving tree acc[j] += acc[j + off] for
+ * off = 32, 16, ..., 1. The GPU computes one such dot per wavefront
+ * (lane j loads float4 u[256m + 4j ..]) and reduces with an xor butterfly,
+ * which yields the same bits because fp32 addition is commutative. */
+float ncmo_dot_fixed(const float* u, const uint16_t* c, int64_t d) {
+    float acc[64];
+    for (int j = 0; j < 64; ++j) acc[j] = 0.0f;
+    for (int64_t m = 0; m * 256 < d; ++m) {
+        const float* um = u + m * 256;
+        const uint16_t* cm = c + m * 256;
+        int64_t rem = d - m * 256;
+        if (rem >= 256) {
+            for (int e = 0; e < 4; ++e)
+                for (int j = 0; j < 64; ++j)
+                    acc[j] = fmaf(um[4 * j + e], ncmo_bf16_to_f32(cm[4 * j + e]), acc[j]);
+        } else {
+            for (int e = 0; e < 4; ++e)
+                for (int j = 0; j < 64; ++j)
+                    if (4 * j + e < rem)
+                        acc[j] = fmaf(um[4 * j + e], ncmo_bf16_to_f32(cm[4 * j + e]), acc[j]);
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1)
+        for (int j = 0; j < off; ++j) acc[j] = acc[j] + acc[j + off];
+    return acc[0];
+}
+
+float ncmo_sumsq_bf16_fixed(const uint16_t* c, int64_t d) {
+    float acc[64];
+    for (int j = 0; j < 64; ++j) acc[j] = 0.0f;
+    for (int64_t m = 0; m * 256 < d; ++m)
+        for (int e = 0; e < 4; ++e)
+            for (int j = 0; j < 64; ++j) {
+                int64_t i = m * 256 + 4 * j + e;
+                if (i < d) {
+                    float v = ncmo_bf16_to_f32(c[i]);
+                    acc[j] = fmaf(v, v, acc[j]);
+                }
+            }
+    for (int off = 32; off >= 1; off >>= 1)
+        for (int j = 0; j < off; ++j) acc[j] = acc[j] + acc[j + off];
+    return acc[0];
+}
+
+float ncmo_sumsq_f32_fixed(const float* u, int64_t d) {
+    float acc[64];
+    for (int j = 0; j < 64; ++j) acc[j] = 0.0f;
+    for (int64_t m = 0; m * 256 < d; ++m)
+        for (int e = 0; e < 4; ++e)
+            for (int j = 0; j < 64; ++j) {
+                int64_t i = m * 256 + 4 * j + e;
+                if (i < d) acc[j] = fmaf(u[i], u[i], acc[j]);
+            }
+    for (int off = 32; off >= 1; off >>= 1)
+        for (int j = 0; j < off; ++j) acc[j] = acc[j] + acc[j + off];
+    return acc[0];
+}
+
+void ncmo_rvq_csq(const uint16_t* codebooks, int64_t levels, int64_t v, int64_t d,
+                  float* csq) {
+    for (int64_t r = 0; r < levels * v; ++r) csq[r] = ncmo_sumsq_bf16_fixed(codebooks + r * d, d);
+}
+
+static int is_pow2(int64_t s) { return s >= 1 && (s & (s - 1)) == 0; }
+
+int ncmo_rvq_check_strides(int64_t t, int64_t levels, const int32_t* strides) {
+    if (levels < 1 || t < 1) return -1;
+    for (int64_t l = 0; l < levels; ++l) {
+        if (!is_pow2(strides[l])) return -2;
+        if (l > 0 && strides[l] > strides[l - 1]) return -3;
+    }
+    if (t % strides[0] != 0) return -4;
+    return 0;
+}
+
+int64_t ncmo_rvq_codes_per_batch(int64_t t, int64_t levels, const int32_t* strides) {
+    int64_t n = 0;
+    for (int64_t l = 0; l < levels; ++l) n += t / strides[l];
+    return n;
+}
+
+static int64_t level_offset(int64_t t, const int32_t* strides, int64_t l) {
+    int64_t off = 0;
+    for (int64_t j = 0; j < l; ++j) off += t / strides[j];
+    return off;
+}
+
+/* P_s for one row: the pairwise tree over x rows [t0, t0 + s). */
+static void pooled_row(const float* x, int64_t d, int64_t t0, int64_t s, float* out,
+                       float* scratch) {
+    if (s == 1) {
+        memcpy(out, x + t0 * d, (size_t)d * sizeof(float));
+        return;
+    }
+    /* scratch holds s rows; halve in place, pairing (2t, 2t+1). */
+    memcpy(scratch, x + t0 * d, (size_t)(s * d) * sizeof(float));
+    for (int64_t n = s; n > 1; n >>= 1)
+        for (int64_t r = 0; r < n / 2; ++r)
+            for (int64_t i = 0; i < d; ++i)
+                scratch[r * d + i] = (scratch[2 * r * d + i] + scratch[(2 * r + 1) * d + i]) * 0.5f;
+    memcpy(out, scratch, (size_t)d * sizeof(float));
+}
+
+/* u = P_{s_l}[row] - (sum over j < l, in order, of C_j[code_j]) */
+static void residual_row(const float* x, int64_t t, int64_t d, const int32_t* strides,
+                         const uint16_t* codebooks, int64_t v, const int32_t* codes_b,
+                         int64_t l, int64_t tp, float* u, float* dacc, float* scratch) {
+    int64_t s = strides[l];
+    pooled_row(x, d, tp * s, s, u, scratch);
+    for (int64_t i = 0; i < d; ++i) dacc[i] = 0.0f;
+    int64_t off = 0;
+    for (int64_t j = 0; j < l; ++j) {
+        int64_t rj = (tp * s) / strides[j];
+        int32_t k = codes_b[off + rj];
+        const uint16_t* c = codebooks + ((int64_t)j * v + k) * d;
+        for (int64_t i = 0; i < d; ++i) dacc[i] = dacc[i] + ncmo_bf16_to_f32(c[i]);
+        off += t / strides[j];
+    }
+    for (int64_t i = 0; i < d; ++i) u[i] = u[i] - dacc[i];
+}
+
+/* argmin over all codes of fmaf(-2, dot, csq); lowest index on ties;
+ * relative gap of the two smallest full distances in f64. */
+static void nearest_code(const float* u, int64_t d, const uint16_t* cb_level,
+                         const float* csq_level, int64_t v, int32_t* code, float* gap) {
+    float best = INFINITY, second = INFINITY;
+    int32_t best_k = 0;
+    for (int64_t k = 0; k < v; ++k) {
+        float dot = ncmo_dot_fixed(u, cb_level + k * d, d);
+        float dist = fmaf(-2.0f, dot, csq_level[k]);
+        if (dist < best) {
+            second = best;
+            best = dist;
+            best_k = (int32_t)k;
+        } else if (dist < second) {
+            second = dist;
+        }
+    }
+    *code = best_k;
+    if (gap) {
+        double un = 0.0;
+        for (int64_t i = 0; i < d; ++i) un += (double)u[i] * (double)u[i];
+        double e1 = un + (double)best, e2 = un + (double)second;
+        double g = (v < 2 || isinf(second)) ? INFINITY : (e2 - e1) / fmax(fabs(e1), 1e-300);
+        *gap = (float)g;
+    }
+}
+
+typedef struct {
+    const float* x;
+    int64_t b, t, d, v, l;
+    const int32_t* strides;
+    const uint16_t* codebooks;
+    const float* csq;
+    const int32_t* resid_codes; /* codes used for the residual of level l */
+    int32_t* codes;             /* output codes (own argmin) */
+    float* gap;
+    int64_t row_begin, row_end, total;
+} level_job_t;
+
+static void* level_worker(void* arg) {
+    level_job_t* j = (level_job_t*)arg;
+    int64_t s = j->strides[j->l];
+    int64_t per_b = j->t / s;
+    int64_t off = level_offset(j->t, j->strides, j->l);
+    float* u = (float*)malloc((size_t)j->d * sizeof(float));
+    float* dacc = (float*)malloc((size_t)j->d * sizeof(float));
+    float* scratch = (float*)malloc((size_t)(s * j->d) * sizeof(float));
+    const uint16_t* cbl = j->codebooks + j->l * j->v * j->d;
+    const float* csql = j->csq + j->l * j->v;
+    for (int64_t r = j->row_begin; r < j->row_end; ++r) {
+        int64_t bb = r / per_b, tp = r % per_b;
+        residual_row(j->x + bb * j->t * j->d, j->t, j->d, j->strides, j->codebooks, j->v,
+                     j->resid_codes + bb * j->total, j->l, tp, u, dacc, scratch);
+        nearest_code(u, j->d, cbl, csql, j->v, &j->codes[bb * j->total + off + tp],
+                     j->gap ? &j->gap[bb * j->total + off + tp] : NULL);
+    }
+    free(u);
+    free(dacc);
+    free(scratch);
+    return NULL;
+}
+
+int ncmo_rvq_encode(const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
+                    const int32_t* strides, const uint16_t* codebooks, const float* csq,
+                    int64_t v, int32_t* codes, float* recon, float* gap,
+                    const int32_t* forced, int threads) {
+    int rc = ncmo_rvq_check_strides(t, levels, strides);
+    if (rc) return rc;
+    if (b < 1 || d < 1 || v < 1) return -5;
+    int64_t total = ncmo_rvq_codes_per_batch(t, levels, strides);
+    if (threads < 1) threads = 1;
+    /* Residual codes: the oracle's own codes, or the forced ones. */
+    const int32_t* resid = forced ? forced : codes;
+    for (int64_t l = 0; l < levels; ++l) {
+        int64_t rows = b * (t / strides[l]);
+        int nt = threads;
+        if (nt > rows) nt = (int)rows;
+        level_job_t* jobs = (level_job_t*)calloc((size_t)nt, sizeof(level_job_t));
+        pthread_t* tids = (pthread_t*)calloc((size_t)nt, sizeof(pthread_t));
+        for (int w = 0; w < nt; ++w) {
+            level_job_t* j = &jobs[w];
+            j->x = x; j->b = b; j->t = t; j->d = d; j->v = v; j->l = l;
+            j->strides = strides; j->codebooks = codebooks; j->csq = csq;
+            j->resid_codes = resid; j->codes = codes; j->gap = gap; j->total = total;
+            j->row_begin = rows * w / nt;
+            j->row_end = rows * (w + 1) / nt;
+        }
+        if (nt == 1) {
+            level_worker(&jobs[0]);
+        } else {
+            for (int w = 0; w < nt; ++w) pthread_create(&tids[w], NULL, level_worker, &jobs[w]);
+            for (int w = 0; w < nt; ++w) pthread_join(tids[w], NULL);
+        }
+        free(jobs);
+        free(tids);
+    }
+    if (recon) return ncmo_rvq_decode(forced ? forced : codes, b, t, d, levels, strides,
+                                      codebooks, v, recon);
+    return 0;
+}
+
+int ncmo_rvq_level_rows(const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
+                        const int32_t* strides, const uint16_t* codebooks, const float* csq,
+                        int64_t v, const int32_t* codes, int64_t level, const int64_t* rows,
+                        int64_t n_rows, int32_t* out_codes, float* out_gap, float* out_u) {
+    int rc = ncmo_rvq_check_strides(t, levels, strides);
+    if (rc) return rc;
+    if (level < 0 || level >= levels) return -6;
+    int64_t s = strides[level];
+    int64_t per_b = t / s;
+    int64_t total = ncmo_rvq_codes_per_batch(t, levels, strides);
+    float* u = (float*)malloc((size_t)d * sizeof(float));
+    float* dacc = (float*)malloc((size_t)d * sizeof(float));
+    float* scratch = (float*)malloc((size_t)(s * d) * sizeof(float));
+    for (int64_t i = 0; i < n_rows; ++i) {
+        int64_t r = rows[i];
+        if (r < 0 || r >= b * per_b) { rc = -7; break; }
+        int64_t bb = r / per_b, tp = r % per_b;
+        residual_row(x + bb * t * d, t, d, strides, codebooks, v, codes + bb * total, level, tp,
+                     u, dacc, scratch);
+        if (out_u) memcpy(out_u + i * d, u, (size_t)d * sizeof(float));
+        nearest_code(u, d, codebooks + level * v * d, csq + level * v, v, &out_codes[i],
+                     out_gap ? &out_gap[i] : NULL);
+    }
+    free(u);
+    free(dacc);
+    free(scratch);
+    return rc;
+}
+
+int ncmo_rvq_decode(const int32_t* codes, int64_t b, int64_t t, int64_t d, int64_t levels,
+                    const int32_t* strides, const uint16_t* codebooks, int64_t v,
+                    float* recon) {
+    int rc = ncmo_rvq_check_strides(t, levels, strides);
+    if (rc) return rc;
+    int64_t total = ncmo_rvq_codes_per_batch(t, levels, strides);
+    for (int64_t bb = 0; bb < b; ++bb)
+        for (int64_t tt = 0; tt < t; ++tt) {
+            float* out = recon + (bb * t + tt) * d;
+            for (int64_t i = 0; i < d; ++i) out[i] = 0.0f;
+            int64_t off = 0;
+            for (int64_t l = 0; l < levels; ++l) {
+                int32_t k = codes[bb * total + off + tt / strides[l]];
+                if (k < 0 || k >= v) return -8;
+                const uint16_t* c = codebooks + (l * v + k) * d;
+                for (int64_t i = 0; i < d; ++i) out[i] = out[i] + ncmo_bf16_to_f32(c[i]);
+                off += t / strides[l];
+            }
+        }
+    return 0;
+}
+
+int ncmo_rvq_encode_f64(const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
+                        const int32_t* strides, const uint16_t* codebooks, int64_t v,
+                        int32_t* codes, double* gap, const int32_t* forced) {
+    /* Strides need only divide t here: the residual is materialized. */
+    if (levels < 1) return -1;
+    for (int64_t l = 0; l < levels; ++l)
+        if (strides[l] < 1 || t % strides[l] != 0) return -4;
+    int64_t total = 0;
+    for (int64_t l = 0; l < levels; ++l) total += t / strides[l];
+    double* r = (double*)malloc((size_t)(b * t * d) * sizeof(double));
+    double* u = (double*)malloc((size_t)d * sizeof(double));
+    double* cn = (double*)malloc((size_t)v * sizeof(double));
+    for (int64_t i = 0; i < b * t * d; ++i) r[i] = (double)x[i];
+    int64_t off = 0;
+    for (int64_t l = 0; l < levels; ++l) {
+        int64_t s = strides[l], per_b = t / s;
+        const uint16_t* cbl = codebooks + l * v * d;
+        for (int64_t k = 0; k < v; ++k) {
+            double a = 0.0;
+            for (int64_t i = 0; i < d; ++i) {
+                double c = (double)ncmo_bf16_to_f32(cbl[k * d + i]);
+                a += c * c;
+            }
+            cn[k] = a;
+        }
+        for (int64_t bb = 0; bb < b; ++bb)
+            for (int64_t tp = 0; tp < per_b; ++tp) {
+                for (int64_t i = 0; i < d; ++i) {
+                    double a = 0.0;
+                    for (int64_t q = 0; q < s; ++q) a += r[(bb * t + tp * s + q) * d + i];
+                    u[i] = a / (double)s;
+                }
+                double un = 0.0;
+                for (int64_t i = 0; i < d; ++i) un += u[i] * u[i];
+                double best = INFINITY, second = INFINITY;
+                int32_t bk = 0;
+                for (int64_t k = 0; k < v; ++k) {
+                    double dot = 0.0;
+                    for (int64_t i = 0; i < d; ++i)
+                        dot += u[i] * (double)ncmo_bf16_to_f32(cbl[k * d + i]);
+                    double e = un + cn[k] - 2.0 * dot;
+                    if (e < best) {
+                        second = best;
+                        best = e;
+                        bk = (int32_t)k;
+                    } else if (e < second) {
+                        second = e;
+                    }
+                }
+                int64_t ci = bb * total + off + tp;
+                codes[ci] = bk;
+                if (gap) gap[ci] = (v < 2) ? INFINITY : (second - best) / fmax(fabs(best), 1e-300);
+            }
+        for (int64_t bb = 0; bb < b; ++bb)
+            for (int64_t tt = 0; tt < t; ++tt) {
+                int64_t ci = bb * total + off + tt / s;
+                int32_t k = forced ? forced[ci] : codes[ci];
+                for (int64_t i = 0; i < d; ++i)
+                    r[(bb * t + tt) * d + i] -= (double)ncmo_bf16_to_f32(cbl[k * d + i]);
+            }
+        off += per_b;
+    }
+    free(r);
+    free(u);
+    free(cn);
+    return 0;
+}

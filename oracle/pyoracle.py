@@ -1,0 +1,233 @@
+"""ctypes wrapper of the C oracle (libncm_oracle.so). TEST INFRASTRUCTURE ONLY.
+
+Imported by the test suite, the smoke check and the benchmark's CPU-baseline
+leg. The product path never imports this module.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libncm_oracle.so")
+_lib = None
+
+f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+i64p = np.ctypeslib.ndpointer(dtype=np.int64, flags="C_CONTIGUOUS")
+vp = C.c_void_p
+sz = C.c_size_t
+i64 = C.c_int64
+
+
+def build() -> str:
+    """Compile the oracle with its Makefile (gcc)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = C.CDLL(_LIB_PATH)
+        L.ncmo_bf16_from_f32.argtypes = [C.c_float]
+        L.ncmo_bf16_from_f32.restype = C.c_uint16
+        L.ncmo_bf16_to_f32.argtypes = [C.c_uint16]
+        L.ncmo_bf16_to_f32.restype = C.c_float
+        L.ncmo_round_bf16.argtypes = [C.c_float]
+        L.ncmo_round_bf16.restype = C.c_float
+        L.ncmo_flush_f32_subnormal.argtypes = [C.c_float]
+        L.ncmo_flush_f32_subnormal.restype = C.c_float
+        L.ncmo_bf16_from_f32_array.argtypes = [f32p, u16p, sz]
+        L.ncmo_widen_little_endian.argtypes = [f32p, u8p, sz]
+        L.ncmo_matmul_bf16.argtypes = [f32p, f32p, vp, f32p, vp, sz, sz, sz]
+        L.ncmo_matmul_bf16_rows.argtypes = [f32p, f32p, vp, f32p, vp, sz, sz, sz, sz, sz]
+        L.ncmo_matmul_bf16_u16_rows.argtypes = [u16p, u16p, vp, f32p, vp, sz, sz, sz, sz, sz]
+        L.ncmo_matmul_reference.argtypes = [f32p, f32p, f32p, sz, sz, sz]
+        L.ncmo_matmul_f64.argtypes = [f32p, f32p, f64p, vp, sz, sz, sz]
+        L.ncmo_fnv1a_bf16_digest.argtypes = [f32p, sz]
+        L.ncmo_fnv1a_bf16_digest.restype = C.c_uint64
+        L.ncmo_dot_fixed.argtypes = [f32p, u16p, i64]
+        L.ncmo_dot_fixed.restype = C.c_float
+        L.ncmo_sumsq_bf16_fixed.argtypes = [u16p, i64]
+        L.ncmo_sumsq_bf16_fixed.restype = C.c_float
+        L.ncmo_rvq_csq.argtypes = [u16p, i64, i64, i64, f32p]
+        L.ncmo_rvq_check_strides.argtypes = [i64, i64, i32p]
+        L.ncmo_rvq_codes_per_batch.argtypes = [i64, i64, i32p]
+        L.ncmo_rvq_codes_per_batch.restype = i64
+        L.ncmo_rvq_encode.argtypes = [f32p, i64, i64, i64, i64, i32p, u16p, f32p, i64, i32p,
+                                      vp, vp, vp, C.c_int]
+        L.ncmo_rvq_level_rows.argtypes = [f32p, i64, i64, i64, i64, i32p, u16p, f32p, i64,
+                                          i32p, i64, i64p, i64, i32p, vp, vp]
+        L.ncmo_rvq_decode.argtypes = [i32p, i64, i64, i64, i64, i32p, u16p, i64, f32p]
+        L.ncmo_rvq_encode_f64.argtypes = [f32p, i64, i64, i64, i64, i32p, u16p, i64, i32p,
+                                          vp, vp]
+        _lib = L
+    return _lib
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
+
+
+# ---------------------------------------------------------------- bf16
+def bf16_from_f32(values) -> np.ndarray:
+    a = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    out = np.empty(a.shape, np.uint16)
+    lib().ncmo_bf16_from_f32_array(a, out, a.size)
+    return out.reshape(np.shape(values))
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    b = np.ascontiguousarray(bits, dtype=np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(values) -> np.ndarray:
+    return bf16_to_f32(bf16_from_f32(values))
+
+
+# ---------------------------------------------------------------- linear
+def matmul_bf16(x, w, bias=None, token_count=None, input_width=None, output_width=None,
+                want_sum=False):
+    """Reference matmul_bf16 / matmul_bf16_bias (root.zig:96-142).
+    x: f32 [T, in]; w: f32 [out, in]; bias: f32 [out] or None."""
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    T = x.shape[0] if token_count is None else token_count
+    K = x.shape[-1] if input_width is None else input_width
+    N = w.shape[0] if output_width is None else output_width
+    out = np.empty((T, N), np.float32)
+    s = np.empty((T, N), np.float32) if want_sum else None
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    lib().ncmo_matmul_bf16(x.ravel(), w.ravel(), _ptr(b), out, _ptr(s), T, K, N)
+    return (out, s) if want_sum else out
+
+
+def matmul_bf16_u16_rows(x_bits, w_bits, row_begin, row_end, bias_bits=None):
+    """Same arithmetic on bf16 bit patterns; rows [row_begin, row_end) only.
+    Returns (bf16-rounded output rows, fp32 pre-rounding sums)."""
+    x_bits = np.ascontiguousarray(x_bits, np.uint16)
+    w_bits = np.ascontiguousarray(w_bits, np.uint16)
+    T, K = x_bits.shape
+    N = w_bits.shape[0]
+    out = np.zeros((T, N), np.float32)
+    s = np.zeros((T, N), np.float32)
+    b = None if bias_bits is None else np.ascontiguousarray(bias_bits, np.uint16)
+    lib().ncmo_matmul_bf16_u16_rows(x_bits, w_bits, _ptr(b), out, _ptr(s), T, K, N,
+                                    row_begin, row_end)
+    return out[row_begin:row_end], s[row_begin:row_end]
+
+
+def matmul_reference(x, w):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty((x.shape[0], w.shape[0]), np.float32)
+    lib().ncmo_matmul_reference(x, w, out, x.shape[0], x.shape[1], w.shape[0])
+    return out
+
+
+def matmul_f64(x, w):
+    x = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(w, np.float32)
+    out = np.empty((x.shape[0], w.shape[0]), np.float64)
+    a = np.empty_like(out)
+    lib().ncmo_matmul_f64(x, w, out, _ptr(a), x.shape[0], x.shape[1], w.shape[0])
+    return out, a
+
+
+def digest(values) -> int:
+    v = np.ascontiguousarray(values, np.float32).ravel()
+    return int(lib().ncmo_fnv1a_bf16_digest(v, v.size))
+
+
+# ---------------------------------------------------------------- RVQ
+def rvq_csq(codebooks_bits):
+    cb = np.ascontiguousarray(codebooks_bits, np.uint16)
+    L, V, D = cb.shape
+    csq = np.empty((L, V), np.float32)
+    lib().ncmo_rvq_csq(cb, L, V, D, csq)
+    return csq
+
+
+def codes_per_batch(t, strides):
+    s = np.ascontiguousarray(strides, np.int32)
+    return int(lib().ncmo_rvq_codes_per_batch(t, len(s), s))
+
+
+def rvq_encode(x, codebooks_bits, strides, csq=None, forced=None, want_recon=True,
+               want_gap=True, threads=1):
+    """x: f32 [B, T, d]; codebooks: bf16 bits [L, V, d]. Returns dict."""
+    x = np.ascontiguousarray(x, np.float32)
+    cb = np.ascontiguousarray(codebooks_bits, np.uint16)
+    B, T, D = x.shape
+    L, V, _ = cb.shape
+    s = np.ascontiguousarray(strides, np.int32)
+    if csq is None:
+        csq = rvq_csq(cb)
+    csq = np.ascontiguousarray(csq, np.float32)
+    total = codes_per_batch(T, s)
+    codes = np.zeros((B, total), np.int32)
+    recon = np.empty((B, T, D), np.float32) if want_recon else None
+    gap = np.empty((B, total), np.float32) if want_gap else None
+    fr = None if forced is None else np.ascontiguousarray(forced, np.int32)
+    rc = lib().ncmo_rvq_encode(x, B, T, D, L, s, cb, csq, V, codes, _ptr(recon), _ptr(gap),
+                               _ptr(fr), threads)
+    if rc != 0:
+        raise ValueError(f"ncmo_rvq_encode failed: {rc}")
+    return {"codes": codes, "recon": recon, "gap": gap, "csq": csq}
+
+
+def rvq_level_rows(x, codebooks_bits, strides, csq, codes, level, rows, want_u=False):
+    x = np.ascontiguousarray(x, np.float32)
+    cb = np.ascontiguousarray(codebooks_bits, np.uint16)
+    B, T, D = x.shape
+    L, V, _ = cb.shape
+    s = np.ascontiguousarray(strides, np.int32)
+    rows = np.ascontiguousarray(rows, np.int64)
+    out = np.empty(rows.shape[0], np.int32)
+    gap = np.empty(rows.shape[0], np.float32)
+    u = np.empty((rows.shape[0], D), np.float32) if want_u else None
+    rc = lib().ncmo_rvq_level_rows(x, B, T, D, L, s, cb, np.ascontiguousarray(csq, np.float32),
+                                   V, np.ascontiguousarray(codes, np.int32), level, rows,
+                                   rows.shape[0], out, _ptr(gap), _ptr(u))
+    if rc != 0:
+        raise ValueError(f"ncmo_rvq_level_rows failed: {rc}")
+    return (out, gap, u) if want_u else (out, gap)
+
+
+def rvq_decode(codes, codebooks_bits, strides, t):
+    cb = np.ascontiguousarray(codebooks_bits, np.uint16)
+    L, V, D = cb.shape
+    codes = np.ascontiguousarray(codes, np.int32)
+    B = codes.shape[0]
+    s = np.ascontiguousarray(strides, np.int32)
+    recon = np.empty((B, t, D), np.float32)
+    rc = lib().ncmo_rvq_decode(codes, B, t, D, L, s, cb, V, recon)
+    if rc != 0:
+        raise ValueError(f"ncmo_rvq_decode failed: {rc}")
+    return recon
+
+
+def rvq_encode_f64(x, codebooks_bits, strides, forced=None):
+    x = np.ascontiguousarray(x, np.float32)
+    cb = np.ascontiguousarray(codebooks_bits, np.uint16)
+    B, T, D = x.shape
+    L, V, _ = cb.shape
+    s = np.ascontiguousarray(strides, np.int32)
+    total = int(sum(T // int(v) for v in s))
+    codes = np.zeros((B, total), np.int32)
+    gap = np.empty((B, total), np.float64)
+    fr = None if forced is None else np.ascontiguousarray(forced, np.int32)
+    rc = lib().ncmo_rvq_encode_f64(x, B, T, D, L, s, cb, V, codes, _ptr(gap), _ptr(fr))
+    if rc != 0:
+        raise ValueError(f"ncmo_rvq_encode_f64 failed: {rc}")
+    return codes, gap

@@ -1,0 +1,145 @@
+"""GPU parity of the bf16 linear against the oracle (restatement of
+packages/kernels/root.zig:96-148).
+
+Tolerance (fp32 output vs the oracle's pre-rounding fp32 sum):
+|y - ref| <= 1e-3 + 1e-2 |ref|. Every output is additionally held to the
+D53 form |y - y_f64| <= (K + 1) 2^-24 sum|x w| (PROJECT.md:506), which any
+RNE fp32 summation order of exact bf16 products satisfies.
+"""
+import numpy as np
+import pytest
+
+from ncmorph_amd import synth
+
+RTOL, ATOL = 1e-2, 1e-3
+pytestmark = pytest.mark.gpu
+
+
+def _to_dev(bits, cuda):
+    import torch
+
+    return torch.from_numpy(bits.view(np.int16).copy()).to(cuda).view(torch.bfloat16)
+
+
+def _run(x_bits, w_bits, cuda, bias_bits=None, out_mode="f32"):
+    import torch
+    from ncmorph_amd import kernels
+
+    x = _to_dev(x_bits, cuda)
+    w = _to_dev(w_bits, cuda)
+    b = None if bias_bits is None else _to_dev(bias_bits, cuda)
+    y = kernels.linear_bf16(x, w, bias=b, out_mode=out_mode)
+    torch.cuda.synchronize()
+    out = y.cpu().numpy()
+    return out.view(np.uint16) if out_mode == "bf16" else out
+
+
+def test_dropin_kats(ncm, oracle, cuda):
+    """The reference KAT inputs through the host drop-in (root.zig:707-770)."""
+    from ncmorph_amd import kernels
+
+    from .test_oracle_linear import kat_inputs
+
+    x, w = kat_inputs()
+    out = np.zeros((4, 576), np.float32)
+    kernels.matmul_bf16(x.ravel(), w.ravel(), out.ravel(), 4, 1536, 576)
+    ref, s = oracle.matmul_bf16(x, w, want_sum=True)
+    assert np.all(np.abs(out - s) <= ATOL + RTOL * np.abs(s))
+    # Output is bf16-valued.
+    assert np.array_equal(out, oracle.round_bf16(out))
+    agree = np.mean(out == ref)
+    assert agree > 0.97, agree
+    # Flush KAT (root.zig:746-755): exactly zero.
+    v = np.float32(5.421010862427522e-20)
+    o1 = np.zeros(1, np.float32)
+    kernels.matmul_bf16(np.array([v, v], np.float32), np.array([v, v], np.float32), o1, 1, 2, 1)
+    assert o1[0] == 0.0
+    # K-block KAT (root.zig:757-770): within tolerance of 1.0078125.
+    xi = np.full(576, 5.960464477539063e-8, np.float32)
+    xi[0] = 1.0
+    xi[-1] = 0.00390625
+    o2 = np.zeros(1, np.float32)
+    kernels.matmul_bf16(xi, np.ones(576, np.float32), o2, 1, 576, 1)
+    assert abs(o2[0] - 1.0078125) <= ATOL + RTOL * 1.0078125
+
+
+def test_dropin_bias_and_ragged(ncm, oracle, cuda):
+    from ncmorph_amd import kernels
+
+    rng = np.random.default_rng(11)
+    for T, K, N in [(1, 1, 1), (3, 7, 5), (17, 130, 33), (65, 1030, 257), (300, 64, 129)]:
+        x = rng.standard_normal((T, K)).astype(np.float32)
+        w = (rng.standard_normal((N, K)) * 0.1).astype(np.float32)
+        b = rng.standard_normal(N).astype(np.float32)
+        out = np.zeros((T, N), np.float32)
+        kernels.matmul_bf16_bias(x.ravel(), w.ravel(), b, out.ravel(), T, K, N)
+        ref, s = oracle.matmul_bf16(x, w, bias=b, want_sum=True)
+        assert np.all(np.abs(out - s) <= ATOL + RTOL * np.abs(s)), (T, K, N)
+        out2 = np.zeros((T, N), np.float32)
+        kernels.matmul_bf16(x.ravel(), w.ravel(), out2.ravel(), T, K, N)
+        ref2, s2 = oracle.matmul_bf16(x, w, want_sum=True)
+        assert np.all(np.abs(out2 - s2) <= ATOL + RTOL * np.abs(s2)), (T, K, N)
+
+
+def test_round_bf16_device_matches_reference_vectors(ncm, cuda):
+    import os
+
+    from ncmorph_amd import kernels
+
+    pairs = np.load(os.path.join(os.path.dirname(__file__), "golden", "bf16_pairs.npy"))
+    f = pairs[:, 0].astype(np.uint32).view(np.float32)
+    got = kernels.round_bf16(f).view(np.uint32) >> 16
+    assert np.array_equal(got.astype(np.uint16), pairs[:, 1].astype(np.uint16))
+
+
+@pytest.mark.parametrize("n,k", [(2048, 2048), (8192, 2048), (2048, 8192)])
+def test_linear_1b_shapes(ncm, oracle, cuda, n, k):
+    """Config shapes: x [2048, k] ~N(0,1), W [n, k] ~N(0, 0.02^2), bf16."""
+    m = 2048
+    xb = synth.normal_bf16(synth.LINEAR_SEED_X + k, (m, k))
+    wb = synth.normal_bf16(synth.LINEAR_SEED_W + n * 7 + k, (n, k), std=0.02)
+    y = _run(xb, wb, cuda)
+    x64 = synth.bf16_to_f32(xb).astype(np.float64)
+    w64 = synth.bf16_to_f32(wb).astype(np.float64)
+    ref = x64 @ w64.T
+    asum = np.abs(x64) @ np.abs(w64).T
+    err = np.abs(y - ref)
+    assert np.all(err <= (k + 1) * 2.0**-24 * asum), float(np.max(err / asum))
+    # Oracle rows (exact reference arithmetic) on a sample of rows.
+    rows = [0, 1, 777, m - 1]
+    for r in rows:
+        yb, s = oracle.matmul_bf16_u16_rows(xb[r:r + 1], wb, 0, 1)
+        assert np.all(np.abs(y[r] - s[0]) <= ATOL + RTOL * np.abs(s[0]))
+        yb16 = synth.bf16_bits(y[r:r + 1])
+        agree = np.mean(synth.bf16_to_f32(yb16) == yb)
+        assert agree > 0.99, agree
+
+
+def test_linear_out_modes_and_bias(ncm, cuda):
+    rng = np.random.default_rng(5)
+    m, k, n = 300, 520, 260
+    xb = synth.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    wb = synth.bf16_bits((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    bb = synth.bf16_bits(rng.standard_normal(n).astype(np.float32))
+    y32 = _run(xb, wb, cuda, bias_bits=bb)
+    ybf = _run(xb, wb, cuda, bias_bits=bb, out_mode="bf16_f32")
+    y16 = _run(xb, wb, cuda, bias_bits=bb, out_mode="bf16")
+    assert np.array_equal(ybf, synth.bf16_to_f32(synth.bf16_bits(y32)))
+    assert np.array_equal(y16, synth.bf16_bits(y32))
+    ref = (synth.bf16_to_f32(xb).astype(np.float64) @ synth.bf16_to_f32(wb).astype(np.float64).T
+           + synth.bf16_to_f32(bb).astype(np.float64))
+    assert np.all(np.abs(y32 - ref) <= ATOL + RTOL * np.abs(ref))
+
+
+def test_linear_zero_k_and_empty(ncm, cuda):
+    import torch
+    from ncmorph_amd import kernels
+
+    x = torch.zeros((4, 0), dtype=torch.bfloat16, device=cuda)
+    w = torch.zeros((3, 0), dtype=torch.bfloat16, device=cuda)
+    y = kernels.linear_bf16(x, w)
+    torch.cuda.synchronize()
+    assert torch.all(y == 0)
+    x = torch.zeros((0, 8), dtype=torch.bfloat16, device=cuda)
+    w = torch.zeros((3, 8), dtype=torch.bfloat16, device=cuda)
+    assert kernels.linear_bf16(x, w).shape == (0, 3)
