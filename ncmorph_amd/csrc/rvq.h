@@ -1,4 +1,4 @@
-// Host-side RVQ launchers (internal to the library).
+// Host-side RVQ launchers and device-side argument blocks (internal).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -12,12 +12,20 @@ hipStream_t ncm_ctx_stream(ncm_ctx_t* ctx);
 namespace ncm {
 
 constexpr int kMaxLevels = 32;
+constexpr int kMaxPyr = 24;  // pyramid strides 2^1 .. 2^23
 
 struct LevelTable {
     int32_t stride[kMaxLevels];
     int64_t offset[kMaxLevels];  // code offset of each level inside a batch row
     int32_t levels;
     int64_t total;               // codes per batch row
+};
+
+// Everything a per-row RVQ kernel needs to locate its data.
+struct RvqGeom {
+    int64_t b, t, d, v;
+    LevelTable L;
+    int64_t pyr_off[kMaxPyr];  // float offset of the stride-2^j pool (j >= 1)
 };
 
 int rvq_check_shape(int64_t b, int64_t t, int64_t d, int64_t levels, const int32_t* strides,

@@ -1,13 +1,875 @@
-// Multiscale RVQ encode (placeholder until the MFMA distance path lands).
-#include "common.h"
+// Multiscale residual vector quantization (encode) on gfx950.
+//
+// Semantics follow the multiscale residual quantizer of
+// research/reference/vq_forward_semantics.md:59-82 (nearest code by
+// ||u||^2 + ||c||^2 - 2 u.c, lowest index on ties, codes concatenated level 0
+// first, PROJECT.md:279) in its average-pool / nearest-repeat variant, with
+// one fixed fp32 operation order that the CPU oracle restates:
+//   P_1 = x, P_2s[t] = (P_s[2t] + P_s[2t+1]) * 0.5
+//   D_l[t'] = sum over j < l, in order, of C_j[code_j]   (coarse reconstruction)
+//   u_l = P_{s_l} - D_l                                  (pooled residual)
+//   dist_k = fmaf(-2, dot_fixed(u, c_k), csq_k), code = lowest argmin
+// pool(r_l) equals P_{s_l} - D_l in exact arithmetic because the strides are
+// non-increasing powers of two, so the full-resolution residual is never
+// materialized.
+//
+// Per level:
+//   1. rvq_dist_kernel: bf16 MFMA of the codebook (A, M = codes) against the
+//      bf16-rounded residual rows (B, N = rows); the epilogue forms
+//      offset + csq_k - 2 S and keeps, per row and per lane chunk of codes,
+//      the four smallest as 32-bit keys (distance bits | local code index).
+//   2. rvq_rescore_kernel (one wavefront per row): rebuilds u in fp32, bounds
+//      the MFMA pass's error rigorously, rescores every candidate that could
+//      be the exact argmin in the fixed fp32 order (bit-identical to the
+//      oracle), and writes code, gap and the next level's bf16 rows. A row
+//      whose candidate list cannot be proven complete is queued instead.
+//   3. rvq_fallback_kernel: exhaustive exact search for queued rows.
+#include <algorithm>
+
+#include "gemm_core.h"
 #include "rvq.h"
 
 namespace ncm {
 
-int rvq_encode(ncm_ctx_t*, const float*, int64_t, int64_t, int64_t, int64_t, const int32_t*,
-               const uint16_t*, const float*, int64_t, int32_t*, float*, float*, const int32_t*,
-               int64_t*) {
-    return NCM_E_SHAPE;
+// ---------------------------------------------------------------- helpers
+
+template <int NCH>
+struct RowVec {
+    float v[NCH][4];
+};
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm volatile("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
+// Sorted top-4 of 32-bit keys: insert v, keep the four smallest.
+__device__ __forceinline__ void top4_insert(uint32_t (&k)[4], uint32_t v) {
+    k[3] = med3_u32(k[2], k[3], v);
+    k[2] = med3_u32(k[1], k[2], v);
+    k[1] = med3_u32(k[0], k[1], v);
+    k[0] = min(k[0], v);
+}
+
+__device__ __forceinline__ bool lane_chunk_valid(int64_t d, int m, int lane) {
+    return (int64_t)m * 256 + 4 * lane < d;
+}
+
+template <int NCH>
+__device__ __forceinline__ void load_f32_row(const float* row, int64_t d, int lane,
+                                             RowVec<NCH>& r) {
+#pragma unroll
+    for (int m = 0; m < NCH; ++m) {
+        if (lane_chunk_valid(d, m, lane)) {
+            const f32x4_t q = *(const f32x4_t*)(row + m * 256 + 4 * lane);
+            r.v[m][0] = q[0]; r.v[m][1] = q[1]; r.v[m][2] = q[2]; r.v[m][3] = q[3];
+        } else {
+            r.v[m][0] = r.v[m][1] = r.v[m][2] = r.v[m][3] = 0.0f;
+        }
+    }
+}
+
+// acc += widen(bf16 row) elementwise (fp32 adds, one per element).
+template <int NCH>
+__device__ __forceinline__ void add_bf16_row(const uint16_t* row, int64_t d, int lane,
+                                             RowVec<NCH>& acc) {
+#pragma unroll
+    for (int m = 0; m < NCH; ++m) {
+        if (lane_chunk_valid(d, m, lane)) {
+            const u32x2_t p = *(const u32x2_t*)(row + m * 256 + 4 * lane);
+            acc.v[m][0] = acc.v[m][0] + bf16_lo_to_f32(p[0]);
+            acc.v[m][1] = acc.v[m][1] + bf16_hi_to_f32(p[0]);
+            acc.v[m][2] = acc.v[m][2] + bf16_lo_to_f32(p[1]);
+            acc.v[m][3] = acc.v[m][3] + bf16_hi_to_f32(p[1]);
+        }
+    }
+}
+
+// The oracle's ncmo_dot_fixed: lane j accumulates elements 256 m + 4 j + e
+// (m ascending, then e) with fmaf from +0, then an xor butterfly (same bits
+// in every lane, fp32 addition being commutative).
+template <int NCH>
+__device__ __forceinline__ float dot_fixed(const RowVec<NCH>& u, const uint16_t* c, int64_t d,
+                                           int lane) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NCH; ++m) {
+        if (lane_chunk_valid(d, m, lane)) {
+            const u32x2_t p = *(const u32x2_t*)(c + m * 256 + 4 * lane);
+            acc = __builtin_fmaf(u.v[m][0], bf16_lo_to_f32(p[0]), acc);
+            acc = __builtin_fmaf(u.v[m][1], bf16_hi_to_f32(p[0]), acc);
+            acc = __builtin_fmaf(u.v[m][2], bf16_lo_to_f32(p[1]), acc);
+            acc = __builtin_fmaf(u.v[m][3], bf16_hi_to_f32(p[1]), acc);
+        }
+    }
+    return wave_sum(acc);
+}
+
+__device__ __forceinline__ int ilog2_pow2(int64_t s) { return 63 - __builtin_clzll((uint64_t)s); }
+
+__device__ __forceinline__ const float* pooled_row_ptr(const RvqGeom& g, const float* x,
+                                                       const float* pyr, int level,
+                                                       int64_t row) {
+    const int64_t s = g.L.stride[level];
+    if (s == 1) return x + row * g.d;
+    return pyr + g.pyr_off[ilog2_pow2(s)] + row * g.d;
+}
+
+// D = sum over j < level (in order, from +0) of C_j[code_j] for one row.
+template <int NCH>
+__device__ __forceinline__ void coarse_recon(const RvqGeom& g, const uint16_t* cb,
+                                             const int32_t* codes, int level, int64_t row,
+                                             int lane, RowVec<NCH>& D) {
+#pragma unroll
+    for (int m = 0; m < NCH; ++m) D.v[m][0] = D.v[m][1] = D.v[m][2] = D.v[m][3] = 0.0f;
+    const int64_t s = g.L.stride[level];
+    const int64_t per_b = g.t / s;
+    const int64_t bb = row / per_b, tp = row % per_b;
+    for (int j = 0; j < level; ++j) {
+        int32_t k = codes[bb * g.L.total + g.L.offset[j] + (tp * s) / g.L.stride[j]];
+        k = k < 0 ? 0 : (k >= g.v ? (int32_t)(g.v - 1) : k);
+        add_bf16_row<NCH>(cb + ((int64_t)j * g.v + k) * g.d, g.d, lane, D);
+    }
+}
+
+struct RowStats {
+    float unorm;   // ||u|| (rounded up)
+    float dnorm;   // ||u - bf16(u)|| (rounded up)
+    double unorm2; // ||u||^2 in f64 (gap reporting)
+};
+
+// Writes bf16(u) and returns the norms of u and of its rounding error.
+template <int NCH>
+__device__ __forceinline__ RowStats write_bf16_row(const RowVec<NCH>& u, int64_t d, int lane,
+                                                   uint16_t* dst) {
+    float su = 0.0f, sd = 0.0f;
+    double su2 = 0.0;
+#pragma unroll
+    for (int m = 0; m < NCH; ++m) {
+        if (lane_chunk_valid(d, m, lane)) {
+            uint32_t b[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float v = u.v[m][e];
+                b[e] = bf16_bits_rne(v);
+                const float r = v - __uint_as_float(b[e] << 16);
+                su = __builtin_fmaf(v, v, su);
+                sd = __builtin_fmaf(r, r, sd);
+                su2 = __builtin_fma((double)v, (double)v, su2);
+            }
+            if (dst) {
+                u32x2_t o;
+                o[0] = b[0] | (b[1] << 16);
+                o[1] = b[2] | (b[3] << 16);
+                *(u32x2_t*)(dst + m * 256 + 4 * lane) = o;
+            }
+        }
+    }
+    RowStats s;
+    // 1e-4 relative head-room covers the rounding of the sums.
+    s.unorm = sqrtf(wave_sum(su) * 1.0001f);
+    s.dnorm = sqrtf(wave_sum(sd) * 1.0001f);
+    s.unorm2 = wave_sum_d(su2);
+    return s;
+}
+
+// Offset that keeps offset + csq_k - 2 S_k >= 0 for every code:
+// |S_k| <= ||bf16(u)|| ||c_k|| (1 + d 2^-23) and ||bf16(u)|| <= unorm + dnorm.
+__device__ __forceinline__ float row_offset(const RowStats& s, float cmax) {
+    return 2.0f * (s.unorm + s.dnorm) * cmax * (1.0f + 1.0f / 1024.0f) + 1e-30f;
+}
+
+// ------------------------------------------------------------- pyramid
+
+// Pools `src` rows [R, d] by 2, 4, ..., 2^DEPTH in one pass; dst[k] receives
+// the stride-2^(k+1) pool relative to src. A thread owns 4 columns of one
+// group of 2^DEPTH consecutive rows (groups never straddle a batch row,
+// because t is a multiple of the largest stride).
+template <int DEPTH>
+__global__ void rvq_pyramid_kernel(const float* __restrict__ src, int64_t rows, int64_t d,
+                                   float* __restrict__ dst0, float* __restrict__ dst1,
+                                   float* __restrict__ dst2, float* __restrict__ dst3) {
+    constexpr int N = 1 << DEPTH;
+    const int64_t q = d / 4;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t groups = rows >> DEPTH;
+    if (idx >= groups * q) return;
+    const int64_t g = idx / q, c = (idx % q) * 4;
+    float* dst[4] = {dst0, dst1, dst2, dst3};
+    f32x4_t stk[DEPTH];
+    f32x4_t in[N];
+#pragma unroll
+    for (int r = 0; r < N; ++r) in[r] = *(const f32x4_t*)(src + ((g << DEPTH) + r) * d + c);
+#pragma unroll
+    for (int r = 0; r < N; ++r) {
+        f32x4_t v = in[r];
+#pragma unroll
+        for (int k = 0; k < DEPTH; ++k) {
+            if ((r >> k) & 1) {
+                f32x4_t s;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) s[e] = (stk[k][e] + v[e]) * 0.5f;
+                v = s;
+                *(f32x4_t*)(dst[k] + (((g << DEPTH) + r) >> (k + 1)) * d + c) = v;
+            } else {
+                stk[k] = v;
+                break;
+            }
+        }
+    }
+}
+
+// ------------------------------------------------- per-encode set-up kernel
+
+// cmax[l] = sqrt(max_k csq[l, k]) (rounded up); zeroes the flag counters.
+__global__ void rvq_setup_kernel(const float* __restrict__ csq, int64_t v, float* cmax,
+                                 int32_t* flag_count, int levels) {
+    const int l = blockIdx.x;
+    float m = 0.0f;
+    for (int64_t k = threadIdx.x; k < v; k += blockDim.x) m = fmaxf(m, csq[l * v + k]);
+    __shared__ float red[256];
+    red[threadIdx.x] = m;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        cmax[l] = sqrtf(red[0]) * 1.00001f;
+        flag_count[l] = 0;
+    }
+    (void)levels;
+}
+
+// ------------------------------------------------------ level-0 prep kernel
+
+struct PrepArgs {
+    RvqGeom g;
+    const float* x;
+    const float* pyr;
+    const uint16_t* cb;
+    const int32_t* resid_codes;
+    const float* cmax;
+    uint16_t* ubuf;
+    float* rowc;
+    int level;
+    int64_t n_rows;
+};
+
+// u = P - D for every row of a level; bf16(u) and the row offset.
+template <int NCH>
+__global__ __launch_bounds__(256) void rvq_prep_kernel(PrepArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.n_rows) return;
+    RowVec<NCH> D, u;
+    coarse_recon<NCH>(a.g, a.cb, a.resid_codes, a.level, row, lane, D);
+    load_f32_row<NCH>(pooled_row_ptr(a.g, a.x, a.pyr, a.level, row), a.g.d, lane, u);
+#pragma unroll
+    for (int m = 0; m < NCH; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
+    const RowStats s = write_bf16_row<NCH>(u, a.g.d, lane, a.ubuf + row * a.g.d);
+    if (lane == 0) a.rowc[row] = row_offset(s, a.cmax[a.level]);
+}
+
+// ------------------------------------------------------- distance kernel
+
+// Candidate key layout: the distance bits (offset + csq - 2S >= 0, so the
+// fp32 pattern orders like the value) with the low `ib` bits replaced by the
+// code's index inside its lane chunk. Lane chunk = (range, wave row wm, lane
+// half h); local index = (tile * MB + mb) * 16 + i for accumulator element i
+// of block mb in tile `tile` of the range.
+struct CandGeom {
+    int bm;       // codes per tile
+    int wm_codes; // codes per wave along M
+    int mb;       // 32-code blocks per wave
+    int wgm;      // waves along M
+    int ntv;      // tiles per range
+    int nranges;
+    int ib;       // index bits
+    int nchunk;   // chunks per row = nranges * wgm * 2
+};
+
+struct DistArgs {
+    const uint16_t* cb;   // level codebook [v, d]
+    const uint16_t* ubuf; // [n_rows, d]
+    const float* csq;     // level [v]
+    const float* rowc;    // [n_rows]
+    uint32_t* cand;       // [n_rows, nchunk, 4]
+    int64_t n_rows, v, d;
+    CandGeom cg;
+};
+
+// Folds one finished code tile into the running per-row top-4 keys.
+// FULL: every code of the tile is < v (no per-value guard).
+template <class S, bool FULL>
+__device__ __forceinline__ void dist_epilogue(const GemmAcc<S>& acc, const DistArgs& a,
+                                              int64_t code0, int tile, int wm, int half,
+                                              const float (&rowc)[S::NB], uint32_t imask,
+                                              uint32_t (&top)[S::NB][4]) {
+#pragma unroll
+    for (int mb = 0; mb < S::MB; ++mb) {
+        const int64_t cbase = code0 + wm * S::WM + mb * 32 + 4 * half;
+        float cs[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int64_t code = cbase + 8 * (i >> 2) + (i & 3);
+            cs[i] = (FULL || code < a.v) ? a.csq[code] : 0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const uint32_t local = (uint32_t)((tile * S::MB + mb) * 16 + i);
+            const bool ok = FULL || (cbase + 8 * (i >> 2) + (i & 3) < a.v);
+#pragma unroll
+            for (int nb = 0; nb < S::NB; ++nb) {
+                const float dist = __builtin_fmaf(acc.v[mb][nb][i], -2.0f, cs[i] + rowc[nb]);
+                uint32_t key = (__float_as_uint(dist) & ~imask) | local;
+                if (!FULL) key = ok ? key : 0xFFFFFFFFu;
+                top4_insert(top[nb], key);
+            }
+        }
+    }
+}
+
+template <class S>
+__global__ __launch_bounds__(S::NT, 1) void rvq_dist_kernel(DistArgs a) {
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+    const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int range = logical % a.cg.nranges;
+    const int rt = logical / a.cg.nranges;
+    const int64_t row0 = (int64_t)rt * S::BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int wm = wave % S::WGM;
+    const int wn = wave / S::WGM;
+    const int half = lane >> 5;
+    const uint32_t imask = (1u << a.cg.ib) - 1u;
+
+    float rowc[S::NB];
+#pragma unroll
+    for (int nb = 0; nb < S::NB; ++nb) {
+        const int64_t r = row0 + wn * S::WN + nb * 32 + (lane & 31);
+        rowc[nb] = r < a.n_rows ? a.rowc[r] : 0.0f;
+    }
+    uint32_t top[S::NB][4];
+#pragma unroll
+    for (int nb = 0; nb < S::NB; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) top[nb][j] = 0xFFFFFFFFu;
+
+    const uint32_t b_bytes = operand_bytes(a.n_rows, row0, a.d);
+    for (int tile = 0; tile < a.cg.ntv; ++tile) {
+        const int64_t code0 = ((int64_t)range * a.cg.ntv + tile) * S::BM;
+        if (code0 >= a.v) break;
+        GemmAcc<S> acc;
+        acc.zero();
+        gemm_mainloop<S>(a.cb + code0 * a.d, a.d, operand_bytes(a.v, code0, a.d),
+                         a.ubuf + row0 * a.d, a.d, b_bytes, a.d, lds, acc);
+        if (code0 + S::BM <= a.v)
+            dist_epilogue<S, true>(acc, a, code0, tile, wm, half, rowc, imask, top);
+        else
+            dist_epilogue<S, false>(acc, a, code0, tile, wm, half, rowc, imask, top);
+    }
+    const int chunk = (range * S::WGM + wm) * 2 + half;
+#pragma unroll
+    for (int nb = 0; nb < S::NB; ++nb) {
+        const int64_t r = row0 + wn * S::WN + nb * 32 + (lane & 31);
+        if (r < a.n_rows) {
+            u32x4_t o;
+            o[0] = top[nb][0]; o[1] = top[nb][1]; o[2] = top[nb][2]; o[3] = top[nb][3];
+            *(u32x4_t*)(a.cand + (r * a.cg.nchunk + chunk) * 4) = o;
+        }
+    }
+}
+
+// --------------------------------------------------------- rescore kernel
+
+struct RescoreArgs {
+    RvqGeom g;
+    const float* x;
+    const float* pyr;
+    const uint16_t* cb;          // all codebooks [levels, v, d]
+    const float* csq;            // all levels [levels, v]
+    const int32_t* resid_codes;  // codes that build residuals (forced or own)
+    const int32_t* force_codes;  // nullable
+    int32_t* codes;
+    float* gap;                  // nullable
+    const uint32_t* cand;
+    const float* rowc_in;
+    const float* cmax;
+    uint16_t* ubuf;              // next level's bf16 rows
+    float* rowc_out;             // next level's offsets
+    int32_t* flag_count;         // this level's counter
+    int32_t* flag_rows;
+    int32_t* fb_done;
+    int level;
+    int64_t n_rows;
+    CandGeom cg;
+};
+
+__device__ __forceinline__ int64_t decode_code(const CandGeom& cg, int chunk, uint32_t local) {
+    const int half = chunk & 1;
+    const int wm = (chunk >> 1) % cg.wgm;
+    const int range = (chunk >> 1) / cg.wgm;
+    const int i = (int)(local & 15u);
+    const int mb = (int)((local >> 4) % (uint32_t)cg.mb);
+    const int tile = (int)((local >> 4) / (uint32_t)cg.mb);
+    return ((int64_t)range * cg.ntv + tile) * cg.bm + wm * cg.wm_codes + mb * 32 +
+           8 * (i >> 2) + 4 * half + (i & 3);
+}
+
+struct Best {
+    float best, second;
+    int32_t code;
+};
+
+__device__ __forceinline__ void best_update(Best& b, float dist, int32_t code) {
+    if (dist < b.best || (dist == b.best && code < b.code)) {
+        b.second = b.best;
+        b.best = dist;
+        b.code = code;
+    } else if (dist < b.second) {
+        b.second = dist;
+    }
+}
+
+__device__ __forceinline__ float rel_gap(const Best& b, double unorm2) {
+    if (!(b.second < INFINITY)) return INFINITY;
+    const double e1 = unorm2 + (double)b.best, e2 = unorm2 + (double)b.second;
+    return (float)((e2 - e1) / fmax(fabs(e1), 1e-300));
+}
+
+// Code write, gap write and the next level's rows for one finished row.
+template <int NCH>
+__device__ __forceinline__ void finish_row(const RescoreArgs& a, int64_t row, const Best& b,
+                                          double unorm2, RowVec<NCH>& D, int lane) {
+    const RvqGeom& g = a.g;
+    const int l = a.level;
+    const int64_t s = g.L.stride[l];
+    const int64_t per_b = g.t / s;
+    const int64_t bb = row / per_b, tp = row % per_b;
+    const int64_t ci = bb * g.L.total + g.L.offset[l] + tp;
+    if (lane == 0) {
+        a.codes[ci] = b.code;
+        if (a.gap) a.gap[ci] = rel_gap(b, unorm2);
+    }
+    if (l + 1 >= g.L.levels) return;
+    int32_t k = a.force_codes ? a.force_codes[ci] : b.code;
+    k = k < 0 ? 0 : (k >= g.v ? (int32_t)(g.v - 1) : k);
+    add_bf16_row<NCH>(a.cb + ((int64_t)l * g.v + k) * g.d, g.d, lane, D);  // D_{l+1}
+    const int64_t ratio = s / g.L.stride[l + 1];
+    for (int64_t c = 0; c < ratio; ++c) {
+        const int64_t child = row * ratio + c;
+        RowVec<NCH> u;
+        load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l + 1, child), g.d, lane, u);
+#pragma unroll
+        for (int m = 0; m < NCH; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
+        const RowStats st = write_bf16_row<NCH>(u, g.d, lane, a.ubuf + child * g.d);
+        if (lane == 0) a.rowc_out[child] = row_offset(st, a.cmax[l + 1]);
+    }
+}
+
+template <int NCH>
+__device__ __forceinline__ void residual(const RescoreArgs& a, int64_t row, int lane,
+                                         RowVec<NCH>& D, RowVec<NCH>& u) {
+    coarse_recon<NCH>(a.g, a.cb, a.resid_codes, a.level, row, lane, D);
+    load_f32_row<NCH>(pooled_row_ptr(a.g, a.x, a.pyr, a.level, row), a.g.d, lane, u);
+#pragma unroll
+    for (int m = 0; m < NCH; ++m)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
+}
+
+template <int NCH>
+__global__ __launch_bounds__(256) void rvq_rescore_kernel(RescoreArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.n_rows) return;
+    const RvqGeom& g = a.g;
+    const int l = a.level;
+    const int64_t d = g.d;
+
+    RowVec<NCH> D, u;
+    residual<NCH>(a, row, lane, D, u);
+    const RowStats st = write_bf16_row<NCH>(u, d, lane, nullptr);
+
+    // Rigorous bound E on |key distance - (offset + exact dist)|:
+    //   bf16 rounding of u:     2 cmax ||u - bf16(u)||
+    //   MFMA fp32 accumulation: 2 cmax d 2^-23 ||bf16(u)||
+    //   fixed-order rescore:    2 cmax (d/64 + 7) 2^-23 ||u||
+    //   epilogue / final ops:   2^-21 of the largest magnitude involved.
+    const float cmax = a.cmax[l];
+    const float rowc = a.rowc_in[row];
+    const float ub = st.unorm + st.dnorm;
+    const float dmag = cmax * cmax + rowc + 2.0f * ub * cmax;
+    const float E = 2.0f * cmax *
+                        (st.dnorm + (float)d * 0x1p-23f * ub +
+                         ((float)(d / 64) + 7.0f) * 0x1p-23f * st.unorm) +
+                    dmag * 0x1p-21f + 1e-30f;
+    const uint32_t imask = (1u << a.cg.ib) - 1u;
+
+    const int nk = a.cg.nchunk * 4;
+    const uint32_t* ck = a.cand + row * (int64_t)nk;
+    uint32_t key[4];
+    uint32_t mn = 0xFFFFFFFFu;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int idx = lane + 64 * s;
+        key[s] = idx < nk ? ck[idx] : 0xFFFFFFFFu;
+        mn = min(mn, key[s]);
+    }
+    mn = wave_min_u32(mn);
+    const float m_f = __uint_as_float(mn & ~imask);
+    const float eps_q = __uint_as_float((uint32_t)(127 + a.cg.ib - 23) << 23);  // 2^(ib-23)
+    const float tau = 1e-4f * (st.unorm * st.unorm + fabsf(m_f - rowc) + 2.0f * E);
+    const float thr = (m_f * (1.0f + eps_q) + 2.0f * E + tau) * (1.0f + 0x1p-20f);
+
+    // Incomplete chunk: its fourth key is still under the threshold.
+    bool incomplete = false;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int idx = lane + 64 * s;
+        if (idx < nk && (idx & 3) == 3 && key[s] != 0xFFFFFFFFu &&
+            __uint_as_float(key[s] & ~imask) <= thr)
+            incomplete = true;
+    }
+    if (__ballot(incomplete) != 0) {
+        if (lane == 0) {
+            const int f = atomicAdd(a.flag_count, 1);
+            a.flag_rows[f] = (int32_t)row;
+            a.fb_done[f] = 0;
+        }
+        return;
+    }
+
+    const uint16_t* cbl = a.cb + (int64_t)l * g.v * d;
+    const float* csql = a.csq + (int64_t)l * g.v;
+    Best b{INFINITY, INFINITY, 0x7FFFFFFF};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int idx = lane + 64 * s;
+        const bool sel = idx < nk && key[s] != 0xFFFFFFFFu &&
+                         __uint_as_float(key[s] & ~imask) <= thr;
+        uint64_t mask = __ballot(sel);
+        while (mask) {
+            const int src = __builtin_ctzll(mask);
+            mask &= mask - 1;
+            const uint32_t kk = (uint32_t)__shfl((int)key[s], src, 64);
+            const int cidx = src + 64 * s;
+            const int64_t code = decode_code(a.cg, cidx >> 2, kk & imask);
+            const float dot = dot_fixed<NCH>(u, cbl + code * d, d, lane);
+            const float dist = __builtin_fmaf(-2.0f, dot, csql[code]);
+            best_update(b, dist, (int32_t)code);
+        }
+    }
+    finish_row<NCH>(a, row, b, st.unorm2, D, lane);
+}
+
+// -------------------------------------------------------- fallback kernel
+
+struct FbPart {
+    float best, second;
+    int32_t code, pad;
+};
+
+// Exhaustive exact search for queued rows: work item = (queued row, chunk of
+// 256 codes); the block that completes a row's last chunk merges the chunk
+// results and finishes the row.
+template <int NCH>
+__global__ __launch_bounds__(256) void rvq_fallback_kernel(RescoreArgs a, FbPart* part,
+                                                           int nvch) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int count = *a.flag_count;
+    const int64_t items = (int64_t)count * nvch;
+    const RvqGeom& g = a.g;
+    const int64_t d = g.d;
+    const uint16_t* cbl = a.cb + (int64_t)a.level * g.v * d;
+    const float* csql = a.csq + (int64_t)a.level * g.v;
+    __shared__ Best wb[4];
+    __shared__ int last;
+    for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
+        const int f = (int)(item / nvch);
+        const int ch = (int)(item % nvch);
+        const int64_t row = a.flag_rows[f];
+        RowVec<NCH> D, u;
+        residual<NCH>(a, row, lane, D, u);
+        Best b{INFINITY, INFINITY, 0x7FFFFFFF};
+        const int64_t c0 = (int64_t)ch * 256 + wave * 64;
+        for (int j = 0; j < 64; ++j) {
+            const int64_t code = c0 + j;
+            if (code >= g.v) break;
+            const float dot = dot_fixed<NCH>(u, cbl + code * d, d, lane);
+            best_update(b, __builtin_fmaf(-2.0f, dot, csql[code]), (int32_t)code);
+        }
+        if (lane == 0) wb[wave] = b;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            Best m = wb[0];
+            for (int w = 1; w < 4; ++w) {
+                if (wb[w].best < INFINITY) {
+                    best_update(m, wb[w].best, wb[w].code);
+                    if (wb[w].second < m.second) m.second = wb[w].second;
+                }
+            }
+            FbPart p{m.best, m.second, m.code, 0};
+            part[(int64_t)f * nvch + ch] = p;
+            __threadfence();
+            last = atomicAdd(&a.fb_done[f], 1) == nvch - 1;
+        }
+        __syncthreads();
+        if (last && wave == 0) {
+            __threadfence();
+            Best m{INFINITY, INFINITY, 0x7FFFFFFF};
+            for (int c = 0; c < nvch; ++c) {
+                const FbPart* pp = part + (int64_t)f * nvch + c;
+                const float pb = __hip_atomic_load(&pp->best, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                const float ps = __hip_atomic_load(&pp->second, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+                const int32_t pc = __hip_atomic_load(&pp->code, __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT);
+                if (pb < INFINITY) {
+                    best_update(m, pb, pc);
+                    if (ps < m.second) m.second = ps;
+                }
+            }
+            const RowStats st = write_bf16_row<NCH>(u, d, lane, nullptr);
+            finish_row<NCH>(a, row, m, st.unorm2, D, lane);
+        }
+        __syncthreads();
+    }
+}
+
+// ------------------------------------------------------------ host side
+
+using DistShape = GemmShape<256, 128, 64, 2, 2>;
+
+static int nch_for(int64_t d) {
+    const int64_t n = (d + 255) / 256;
+    if (n <= 1) return 1;
+    if (n <= 2) return 2;
+    if (n <= 4) return 4;
+    if (n <= 8) return 8;
+    return 16;
+}
+
+template <int NCH>
+static hipError_t launch_row_kernels(int which, const PrepArgs* pa, const RescoreArgs* ra,
+                                     FbPart* part, int nvch, int64_t rows, hipStream_t st) {
+    const dim3 grid((unsigned)((rows + 3) / 4));
+    if (which == 0)
+        hipLaunchKernelGGL(rvq_prep_kernel<NCH>, grid, dim3(256), 0, st, *pa);
+    else if (which == 1)
+        hipLaunchKernelGGL(rvq_rescore_kernel<NCH>, grid, dim3(256), 0, st, *ra);
+    else
+        hipLaunchKernelGGL(rvq_fallback_kernel<NCH>, dim3(512), dim3(256), 0, st, *ra, part,
+                           nvch);
+    return hipGetLastError();
+}
+
+static hipError_t launch_rows(int nch, int which, const PrepArgs* pa, const RescoreArgs* ra,
+                              FbPart* part, int nvch, int64_t rows, hipStream_t st) {
+    switch (nch) {
+        case 1: return launch_row_kernels<1>(which, pa, ra, part, nvch, rows, st);
+        case 2: return launch_row_kernels<2>(which, pa, ra, part, nvch, rows, st);
+        case 4: return launch_row_kernels<4>(which, pa, ra, part, nvch, rows, st);
+        case 8: return launch_row_kernels<8>(which, pa, ra, part, nvch, rows, st);
+        default: return launch_row_kernels<16>(which, pa, ra, part, nvch, rows, st);
+    }
+}
+
+static CandGeom cand_geom(int64_t n_rows, int64_t v) {
+    using S = DistShape;
+    CandGeom cg{};
+    cg.bm = S::BM;
+    cg.wm_codes = S::WM;
+    cg.mb = S::MB;
+    cg.wgm = S::WGM;
+    const int64_t tiles_v = (v + S::BM - 1) / S::BM;
+    const int64_t rt = (n_rows + S::BN - 1) / S::BN;
+    int64_t nr = std::min<int64_t>(16, tiles_v);
+    if (rt * tiles_v >= 2048) nr = std::min<int64_t>(8, tiles_v);
+    cg.ntv = (int)((tiles_v + nr - 1) / nr);
+    cg.nranges = (int)((tiles_v + cg.ntv - 1) / cg.ntv);
+    const int locals = cg.ntv * S::MB * 16;
+    int ib = 0;
+    while ((1 << ib) < locals) ++ib;
+    cg.ib = ib;
+    cg.nchunk = cg.nranges * S::WGM * 2;
+    return cg;
+}
+
+static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
+               const int32_t* strides, const uint16_t* codebooks, const float* csq, int64_t v,
+               int32_t* codes, float* recon, float* gap, const int32_t* force_codes,
+               int64_t* n_flagged) {
+    using S = DistShape;
+    hipStream_t st = ncm_ctx_stream(ctx);
+    RvqGeom g{};
+    g.b = b; g.t = t; g.d = d; g.v = v;
+    g.L = make_level_table(t, levels, strides);
+    const int64_t smax = strides[0];
+    int jmax = 0;
+    while ((int64_t(1) << jmax) < smax) ++jmax;
+    if (jmax >= kMaxPyr) return NCM_E_SHAPE;
+
+    // Workspace layout.
+    size_t off = 0;
+    auto carve = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
+    int64_t pyr_floats = 0;
+    for (int j = 1; j <= jmax; ++j) {
+        g.pyr_off[j] = pyr_floats;
+        pyr_floats += b * (t >> j) * d;
+    }
+    int64_t max_rows = 0, max_cand = 0;
+    for (int64_t l = 0; l < levels; ++l) {
+        const int64_t n = b * (t / strides[l]);
+        max_rows = std::max(max_rows, n);
+        max_cand = std::max(max_cand, n * (int64_t)cand_geom(n, v).nchunk * 4);
+    }
+    const int nvch = (int)((v + 255) / 256);
+    const size_t o_pyr = carve((size_t)pyr_floats * 4);
+    const size_t o_u = carve((size_t)max_rows * d * 2);
+    const size_t o_rc0 = carve((size_t)max_rows * 4);
+    const size_t o_rc1 = carve((size_t)max_rows * 4);
+    const size_t o_cand = carve((size_t)max_cand * 4);
+    const size_t o_cmax = carve((size_t)levels * 4);
+    const size_t o_fc = carve((size_t)levels * 4);
+    const size_t o_fr = carve((size_t)max_rows * 4);
+    const size_t o_fd = carve((size_t)max_rows * 4);
+    const size_t o_fp = carve((size_t)max_rows * nvch * sizeof(FbPart));
+    void* ws = nullptr;
+    int rc = ncm_ctx_workspace(ctx, off, &ws);
+    if (rc) return rc;
+    char* W = (char*)ws;
+    float* pyr = (float*)(W + o_pyr);
+    uint16_t* ubuf = (uint16_t*)(W + o_u);
+    float* rowc[2] = {(float*)(W + o_rc0), (float*)(W + o_rc1)};
+    uint32_t* cand = (uint32_t*)(W + o_cand);
+    float* cmax = (float*)(W + o_cmax);
+    int32_t* fcount = (int32_t*)(W + o_fc);
+    int32_t* frows = (int32_t*)(W + o_fr);
+    int32_t* fdone = (int32_t*)(W + o_fd);
+    FbPart* fpart = (FbPart*)(W + o_fp);
+
+    hipLaunchKernelGGL(rvq_setup_kernel, dim3((unsigned)levels), dim3(256), 0, st, csq, v, cmax,
+                       fcount, (int)levels);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return NCM_E_HIP;
+
+    // Pyramid, in passes of up to four halvings.
+    {
+        int j0 = 0;
+        while (j0 < jmax) {
+            const int depth = std::min(4, jmax - j0);
+            const float* src = j0 == 0 ? x : pyr + g.pyr_off[j0];
+            const int64_t rows = b * (t >> j0);
+            float* dst[4] = {nullptr, nullptr, nullptr, nullptr};
+            for (int k = 0; k < depth; ++k) dst[k] = pyr + g.pyr_off[j0 + k + 1];
+            const int64_t work = (rows >> depth) * (d / 4);
+            const dim3 grid((unsigned)((work + 255) / 256));
+            switch (depth) {
+                case 1: hipLaunchKernelGGL(rvq_pyramid_kernel<1>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3]); break;
+                case 2: hipLaunchKernelGGL(rvq_pyramid_kernel<2>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3]); break;
+                case 3: hipLaunchKernelGGL(rvq_pyramid_kernel<3>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3]); break;
+                default: hipLaunchKernelGGL(rvq_pyramid_kernel<4>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3]); break;
+            }
+            e = hipGetLastError();
+            if (e != hipSuccess) return NCM_E_HIP;
+            j0 += depth;
+        }
+    }
+
+    const int nch = nch_for(d);
+    const int32_t* resid = force_codes ? force_codes : codes;
+
+    // Level 0 rows.
+    {
+        PrepArgs pa{};
+        pa.g = g; pa.x = x; pa.pyr = pyr; pa.cb = codebooks; pa.resid_codes = resid;
+        pa.cmax = cmax; pa.ubuf = ubuf; pa.rowc = rowc[0]; pa.level = 0;
+        pa.n_rows = b * (t / strides[0]);
+        e = launch_rows(nch, 0, &pa, nullptr, nullptr, 0, pa.n_rows, st);
+        if (e != hipSuccess) return NCM_E_HIP;
+    }
+
+    static bool attr_set = false;
+    if (!attr_set) {
+        e = hipFuncSetAttribute((const void*)rvq_dist_kernel<S>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS_BYTES);
+        if (e != hipSuccess) return NCM_E_HIP;
+        attr_set = true;
+    }
+
+    for (int64_t l = 0; l < levels; ++l) {
+        const int64_t n = b * (t / strides[l]);
+        const CandGeom cg = cand_geom(n, v);
+        DistArgs da{};
+        da.cb = codebooks + l * v * d;
+        da.ubuf = ubuf;
+        da.csq = csq + l * v;
+        da.rowc = rowc[l & 1];
+        da.cand = cand;
+        da.n_rows = n; da.v = v; da.d = d;
+        da.cg = cg;
+        const int64_t rt = (n + S::BN - 1) / S::BN;
+        hipLaunchKernelGGL(rvq_dist_kernel<S>, dim3((unsigned)(rt * cg.nranges)), dim3(S::NT),
+                           S::LDS_BYTES, st, da);
+        e = hipGetLastError();
+        if (e != hipSuccess) return NCM_E_HIP;
+
+        RescoreArgs ra{};
+        ra.g = g; ra.x = x; ra.pyr = pyr; ra.cb = codebooks; ra.csq = csq;
+        ra.resid_codes = resid; ra.force_codes = force_codes; ra.codes = codes; ra.gap = gap;
+        ra.cand = cand; ra.rowc_in = rowc[l & 1]; ra.cmax = cmax;
+        ra.ubuf = ubuf; ra.rowc_out = rowc[(l + 1) & 1];
+        ra.flag_count = fcount + l; ra.flag_rows = frows; ra.fb_done = fdone;
+        ra.level = (int)l; ra.n_rows = n; ra.cg = cg;
+        e = launch_rows(nch, 1, nullptr, &ra, nullptr, nvch, n, st);
+        if (e != hipSuccess) return NCM_E_HIP;
+        e = launch_rows(nch, 2, nullptr, &ra, fpart, nvch, n, st);
+        if (e != hipSuccess) return NCM_E_HIP;
+    }
+
+    if (recon) {
+        e = launch_rvq_decode(resid, b, t, d, levels, strides, codebooks, v, recon, st);
+        if (e != hipSuccess) return NCM_E_HIP;
+    }
+    if (n_flagged) {
+        int32_t host[kMaxLevels];
+        e = hipMemcpyAsync(host, fcount, levels * 4, hipMemcpyDeviceToHost, st);
+        if (e == hipSuccess) e = hipStreamSynchronize(st);
+        if (e != hipSuccess) return NCM_E_HIP;
+        int64_t s = 0;
+        for (int64_t l = 0; l < levels; ++l) s += host[l];
+        *n_flagged = s;
+    }
+    return NCM_OK;
 }
 
 }  // namespace ncm

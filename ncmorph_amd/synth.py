@@ -63,3 +63,21 @@ def normal_bf16(seed: int, shape, std: float = 1.0) -> np.ndarray:
 # Seeds of the linear shapes (none are given by the configuration; fixed here).
 LINEAR_SEED_X = 0x11E4_0001
 LINEAR_SEED_W = 0x11E4_0002
+
+# Codebook seed = input seed + this offset (the configuration names only the
+# input seed).
+RVQ_CODEBOOK_SEED_OFFSET = 0xC0DE_B00C
+
+
+def rvq_inputs(seed: int, b: int, t: int, d: int, levels: int, v: int):
+    """x f32 [b, t, d] ~N(0, 1); codebooks bf16 bits [levels, v, d] ~N(0, 1/d)."""
+    x = normal_f32(seed, (b, t, d))
+    cb = normal_bf16(seed + RVQ_CODEBOOK_SEED_OFFSET, (levels, v, d), std=1.0 / np.sqrt(d))
+    return x, cb
+
+
+# The two RVQ configurations: encode+decode of one sequence at full
+# resolution, and the multiscale encode at scale.
+RVQ_SMALL = dict(seed=0, b=1, t=128, d=256, levels=4, v=512, strides=(1, 1, 1, 1))
+RVQ_LARGE = dict(seed=1, b=16, t=2048, d=2048, levels=8, v=4096,
+                 strides=(128, 64, 32, 16, 8, 4, 2, 1))

@@ -299,7 +299,10 @@ int ncmo_rvq_check_strides(int64_t t, int64_t levels, const int32_t* strides) {
 
 int64_t ncmo_rvq_codes_per_batch(int64_t t, int64_t levels, const int32_t* strides) {
     int64_t n = 0;
-    for (int64_t l = 0; l < levels; ++l) n += t / strides[l];
+    for (int64_t l = 0; l < levels; ++l) {
+        if (strides[l] < 1) return -1;
+        n += t / strides[l];
+    }
     return n;
 }
 

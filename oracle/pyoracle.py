@@ -171,6 +171,9 @@ def rvq_encode(x, codebooks_bits, strides, csq=None, forced=None, want_recon=Tru
     B, T, D = x.shape
     L, V, _ = cb.shape
     s = np.ascontiguousarray(strides, np.int32)
+    rc = lib().ncmo_rvq_check_strides(T, len(s), s)
+    if rc != 0:
+        raise ValueError(f"invalid strides {tuple(strides)} for t={T}: {rc}")
     if csq is None:
         csq = rvq_csq(cb)
     csq = np.ascontiguousarray(csq, np.float32)
