@@ -1,0 +1,244 @@
+"""Benchmark of the ncmorph hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only linear|rvq]
+
+A step is one pass of the bf16-weight linear over the three Llama-3.2-1B
+shapes: x bf16 [2048, K] ~N(0,1) times W^T with W bf16 [N, K] ~N(0, 0.02^2),
+(N, K) in {(2048, 2048), (8192, 2048), (2048, 8192)}, fp32 accumulation and
+fp32 output. `value` is the whole step's TFLOP/s (algorithmic 2*M*N*K per
+linear) with inputs resident in HBM.
+
+The same JSON line carries the multiscale RVQ encode at 16 x 2048 positions,
+d = 2048, 8 levels (strides 128..1), 4096 codes per level (input seed 1),
+timed separately and reported as tokens/s (input positions per second of a
+full encode including the reconstruction), plus the roofline fractions and
+CPU baselines of both.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+BF16_PEAK_TFLOPS = 2516.6  # MI355X dense bf16 MFMA
+HBM_PEAK_GBS = 8000.0
+METRIC = "RVQ-encode tokens/s & bf16-linear TFLOP/s (1B shape), % of MI355X roofline"
+LINEAR_M = 2048
+LINEAR_NK = [(2048, 2048), (8192, 2048), (2048, 8192)]
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def linear_inputs(torch, dev):
+    from ncmorph_amd import synth
+
+    xs, ws = {}, {}
+    for (n, k) in LINEAR_NK:
+        if k not in xs:
+            xb = synth.normal_bf16(synth.LINEAR_SEED_X + k, (LINEAR_M, k))
+            xs[k] = torch.from_numpy(xb.view(np.int16)).to(dev).view(torch.bfloat16)
+        wb = synth.normal_bf16(synth.LINEAR_SEED_W + n * 7 + k, (n, k), std=0.02)
+        ws[(n, k)] = torch.from_numpy(wb.view(np.int16)).to(dev).view(torch.bfloat16)
+    ys = {nk: torch.empty((LINEAR_M, nk[0]), dtype=torch.float32, device=dev) for nk in LINEAR_NK}
+    return xs, ws, ys
+
+
+def run_linear(torch, steps, warmup):
+    from ncmorph_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    xs, ws, ys = linear_inputs(torch, dev)
+
+    def step():
+        for (n, k) in LINEAR_NK:
+            kernels.linear_bf16(xs[k], ws[(n, k)], out=ys[(n, k)])
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    # Per-shape launch durations (events on the launch stream).
+    per_shape = {}
+    for (n, k) in LINEAR_NK:
+        e0, e1 = _events(torch)
+        reps = 20
+        e0.record()
+        for _ in range(reps):
+            kernels.linear_bf16(xs[k], ws[(n, k)], out=ys[(n, k)])
+        e1.record()
+        torch.cuda.synchronize()
+        per_shape[(n, k)] = e0.elapsed_time(e1) / reps * 1e-3
+    # Timed region: exactly `steps` steps, synchronized on both sides.
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_s = e0.elapsed_time(e1) * 1e-3
+    flops = sum(2.0 * LINEAR_M * n * k for (n, k) in LINEAR_NK)
+    # Sanity: one output against torch's fp32 product.
+    n, k = LINEAR_NK[0]
+    ref = xs[k].float() @ ws[(n, k)].float().T
+    err = float((ys[(n, k)] - ref).abs().max())
+    return {"step_s": gpu_s / steps, "wall_s": wall, "flops_per_step": flops,
+            "per_shape_s": per_shape, "max_abs_err_vs_fp32": err}
+
+
+def run_rvq(torch, reps, warmup):
+    from ncmorph_amd import synth, vq
+
+    dev = torch.device("cuda", 0)
+    c = synth.RVQ_LARGE
+    x, cb = synth.rvq_inputs(c["seed"], c["b"], c["t"], c["d"], c["levels"], c["v"])
+    xd = torch.from_numpy(x).to(dev)
+    cbd = torch.from_numpy(cb.view(np.int16)).to(dev).view(torch.bfloat16)
+    del x
+    csq = vq.prepare(cbd)
+    out = {}
+    r = vq.encode(xd, cbd, c["strides"], csq=csq, want_gap=False, count_flagged=True)
+    n_flagged = r["n_flagged"]
+    out = {"codes": r["codes"], "recon": r["recon"]}
+    for _ in range(warmup):
+        vq.encode(xd, cbd, c["strides"], csq=csq, want_gap=False, out=out)
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        vq.encode(xd, cbd, c["strides"], csq=csq, want_gap=False, out=out)
+    e1.record()
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3 / reps
+    rows = sum(c["b"] * c["t"] // s for s in c["strides"])
+    flops = 2.0 * c["v"] * c["d"] * rows
+    # x read once, codebooks read once, codes and reconstruction written once.
+    bytes_alg = (c["b"] * c["t"] * c["d"] * 4 + c["levels"] * c["v"] * c["d"] * 2 +
+                 rows * 4 + c["b"] * c["t"] * c["d"] * 4)
+    return {"encode_s": t, "tokens": c["b"] * c["t"], "flops": flops, "bytes": bytes_alg,
+            "n_flagged": n_flagged}
+
+
+def cpu_linear_baseline():
+    """Oracle (scalar restatement of matmul_bf16, 1 thread) on a 24-row slice
+    of each shape, extrapolated linearly in M."""
+    from ncmorph_amd import synth
+    from oracle import pyoracle
+
+    rows = 24
+    t_total = 0.0
+    for (n, k) in LINEAR_NK:
+        xb = synth.normal_bf16(synth.LINEAR_SEED_X + k, (rows, k))
+        wb = synth.normal_bf16(synth.LINEAR_SEED_W + n * 7 + k, (n, k), std=0.02)
+        t0 = time.perf_counter()
+        pyoracle.matmul_bf16_u16_rows(xb, wb, 0, rows)
+        t_total += (time.perf_counter() - t0) * (LINEAR_M / rows)
+    flops = sum(2.0 * LINEAR_M * n * k for (n, k) in LINEAR_NK)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": "port",
+            "sample": f"first {rows} rows of x for each of the 3 shapes, oracle matmul_bf16 "
+                      "(pair-FMA, FTZ, K-blocks), 1 thread, extrapolated to M=2048"}
+
+
+def cpu_rvq_baseline():
+    """Oracle encode (exhaustive fp32 search, 1 thread) of the first 256
+    positions of sequence 0, all 8 levels."""
+    from ncmorph_amd import synth
+    from oracle import pyoracle
+
+    c = synth.RVQ_LARGE
+    t = 256
+    x, cb = synth.rvq_inputs(c["seed"], c["b"], c["t"], c["d"], c["levels"], c["v"])
+    xs = np.ascontiguousarray(x[:1, :t])
+    del x
+    csq = pyoracle.rvq_csq(cb)
+    t0 = time.perf_counter()
+    pyoracle.rvq_encode(xs, cb, c["strides"], csq=csq, want_gap=False, threads=1)
+    dt = time.perf_counter() - t0
+    return {"value": t / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"sequence 0, positions 0..{t - 1}, all 8 levels (strides 128..1), "
+                      "4096 codes/level, d=2048, oracle exhaustive search, 1 thread"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--only", choices=["linear", "rvq", "all"], default="all")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1"}))
+        sys.exit(2)
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(1)
+    import ncmorph_amd  # noqa: F401  (raises if the HIP library is missing)
+
+    torch.cuda.init()
+    res = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (SplitMix64 + Box-Muller normals, fixed seeds)"}
+    if args.only in ("linear", "all"):
+        lin = run_linear(torch, args.steps, args.warmup)
+        tflops = lin["flops_per_step"] / lin["step_s"] / 1e12
+        res.update({"value": round(tflops, 2), "unit": "TFLOP/s",
+                    "ms_per_step": round(lin["step_s"] * 1e3, 4)})
+        res["config"] = {"workload": "bf16-weight linear y = x W^T at Llama-3.2-1B shapes",
+                         "m": LINEAR_M, "nk": [list(nk) for nk in LINEAR_NK],
+                         "accumulate": "fp32", "output": "fp32"}
+        res["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2),
+                           "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                           "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None}
+        res["linear_per_shape"] = {
+            f"{LINEAR_M}x{n}x{k}": {
+                "us": round(t * 1e6, 2),
+                "tflops": round(2.0 * LINEAR_M * n * k / t / 1e12, 2),
+                "frac": round(2.0 * LINEAR_M * n * k / t / 1e12 / BF16_PEAK_TFLOPS, 4)}
+            for (n, k), t in lin["per_shape_s"].items()}
+        res["linear_max_abs_err_vs_fp32"] = lin["max_abs_err_vs_fp32"]
+        if not args.no_cpu:
+            res["cpu_baseline"] = cpu_linear_baseline()
+    if args.only in ("rvq", "all"):
+        rv = run_rvq(torch, max(3, args.steps // 10), max(1, args.warmup // 5))
+        tps = rv["tokens"] / rv["encode_s"]
+        tf = rv["flops"] / rv["encode_s"] / 1e12
+        gbs = rv["bytes"] / rv["encode_s"] / 1e9
+        rvq = {"metric": "RVQ-encode tokens/s", "value": round(tps, 1), "unit": "tokens/s",
+               "ms_per_encode": round(rv["encode_s"] * 1e3, 4),
+               "config": {"workload": "multiscale RVQ encode + reconstruction",
+                          "b": 16, "t": 2048, "d": 2048, "levels": 8, "v": 4096,
+                          "strides": [128, 64, 32, 16, 8, 4, 2, 1]},
+               "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                            "hbm_gbs_algorithmic": round(gbs, 1),
+                            "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
+               "flagged_rows": rv["n_flagged"]}
+        if not args.no_cpu:
+            rvq["cpu_baseline"] = cpu_rvq_baseline()
+        res["rvq_encode"] = rvq
+        if "value" not in res:
+            res.update({"value": rvq["value"], "unit": "tokens/s",
+                        "ms_per_step": rvq["ms_per_encode"], "config": rvq["config"],
+                        "roofline": rvq["roofline"]})
+            if "cpu_baseline" in rvq:
+                res["cpu_baseline"] = rvq["cpu_baseline"]
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

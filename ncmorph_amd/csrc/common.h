@@ -40,9 +40,16 @@ __device__ __forceinline__ float bf16_hi_to_f32(uint32_t packed) {
 
 // Raw buffer resource over [base, base + bytes). Loads past `bytes` return
 // zero, which is how partial tiles are zero-filled without branches.
+// `base` and `bytes` must be wavefront-uniform; readfirstlane makes that
+// explicit so the descriptor lives in SGPRs (a VGPR descriptor would force a
+// waterfall loop around every load).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
-                                             0x00020000);
+    const uint64_t p = (uint64_t)base;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+    const uint32_t n = __builtin_amdgcn_readfirstlane(bytes);
+    void* up = (void*)(((uint64_t)hi << 32) | lo);
+    return __builtin_amdgcn_make_buffer_rsrc(up, (short)0, (int)n, 0x00020000);
 }
 
 // An offset that is always outside any resource built above.
@@ -50,6 +57,19 @@ constexpr uint32_t kOobOffset = 0x80000000u;
 
 __device__ __forceinline__ u32x4_t buffer_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+}
+
+// Workgroup barrier for LDS hand-off that leaves global loads in flight.
+// __syncthreads() also waits for every outstanding vector-memory load
+// (vmcnt(0)), which would drain the register prefetch of the next K tiles at
+// each barrier. Here: wait for this wave's LDS operations (lgkmcnt(0)), then
+// s_barrier; the empty asm statements keep the compiler from moving memory
+// operations across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt, expcnt unconstrained
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
 }
 
 // Remap a linear workgroup id so that consecutive logical tiles land on the

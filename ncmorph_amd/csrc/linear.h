@@ -6,8 +6,8 @@
 
 namespace ncm {
 
-// Tile configuration chosen for an M x N output: 0 = 256x256, 1 = 256x128,
-// 2 = 128x128. `forced` in [0, 2] overrides the choice.
+// Tile configuration chosen for an M x N output (see the table in
+// linear.hip); a valid `forced` index overrides the choice.
 int linear_tile_config(int64_t M, int64_t N, int forced);
 
 hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, void* y,

@@ -352,7 +352,8 @@ __device__ __forceinline__ void dist_epilogue(const GemmAcc<S>& acc, const DistA
 }
 
 template <class S>
-__global__ __launch_bounds__(S::NT, 1) void rvq_dist_kernel(DistArgs a) {
+__global__ __launch_bounds__(S::NT)
+__attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void rvq_dist_kernel(DistArgs a) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
     const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
     const int range = logical % a.cg.nranges;
@@ -403,6 +404,10 @@ __global__ __launch_bounds__(S::NT, 1) void rvq_dist_kernel(DistArgs a) {
 }
 
 // --------------------------------------------------------- rescore kernel
+
+// Candidate keys per row are read 64 per lane slot: at most 512 per row.
+constexpr int kKeySlots = 8;
+constexpr int kMaxChunks = kKeySlots * 64 / 4;
 
 struct RescoreArgs {
     RvqGeom g;
@@ -532,10 +537,10 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RescoreArgs a) {
 
     const int nk = a.cg.nchunk * 4;
     const uint32_t* ck = a.cand + row * (int64_t)nk;
-    uint32_t key[4];
+    uint32_t key[kKeySlots];
     uint32_t mn = 0xFFFFFFFFu;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < kKeySlots; ++s) {
         const int idx = lane + 64 * s;
         key[s] = idx < nk ? ck[idx] : 0xFFFFFFFFu;
         mn = min(mn, key[s]);
@@ -549,7 +554,7 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RescoreArgs a) {
     // Incomplete chunk: its fourth key is still under the threshold.
     bool incomplete = false;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < kKeySlots; ++s) {
         const int idx = lane + 64 * s;
         if (idx < nk && (idx & 3) == 3 && key[s] != 0xFFFFFFFFu &&
             __uint_as_float(key[s] & ~imask) <= thr)
@@ -568,7 +573,7 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RescoreArgs a) {
     const float* csql = a.csq + (int64_t)l * g.v;
     Best b{INFINITY, INFINITY, 0x7FFFFFFF};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s = 0; s < kKeySlots; ++s) {
         const int idx = lane + 64 * s;
         const bool sel = idx < nk && key[s] != 0xFFFFFFFFu &&
                          __uint_as_float(key[s] & ~imask) <= thr;
@@ -665,7 +670,12 @@ __global__ __launch_bounds__(256) void rvq_fallback_kernel(RescoreArgs a, FbPart
 
 // ------------------------------------------------------------ host side
 
-using DistShape = GemmShape<256, 128, 64, 2, 2>;
+// Distance GEMM tiles (codes x rows): 256 x 256 with 8 wavefronts for the
+// large levels, 128 x 128 with 4 for the small ones; both load global ->
+// LDS directly and run two wavefronts per SIMD.
+using DistBig = GemmShape<256, 256, 64, 4, 2, 1, 2, true, 4, true>;
+using DistSmall = GemmShape<128, 128, 64, 2, 2, 1, 2, true, 4, true>;
+constexpr int64_t kDistBigRows = 8192;
 
 static int nch_for(int64_t d) {
     const int64_t n = (d + 255) / 256;
@@ -701,8 +711,8 @@ static hipError_t launch_rows(int nch, int which, const PrepArgs* pa, const Resc
     }
 }
 
-static CandGeom cand_geom(int64_t n_rows, int64_t v) {
-    using S = DistShape;
+template <class S>
+static CandGeom cand_geom_t(int64_t n_rows, int64_t v) {
     CandGeom cg{};
     cg.bm = S::BM;
     cg.wm_codes = S::WM;
@@ -710,8 +720,10 @@ static CandGeom cand_geom(int64_t n_rows, int64_t v) {
     cg.wgm = S::WGM;
     const int64_t tiles_v = (v + S::BM - 1) / S::BM;
     const int64_t rt = (n_rows + S::BN - 1) / S::BN;
-    int64_t nr = std::min<int64_t>(16, tiles_v);
-    if (rt * tiles_v >= 2048) nr = std::min<int64_t>(8, tiles_v);
+    const int64_t max_ranges = kMaxChunks / (S::WGM * 2);
+    int64_t nr = std::min<int64_t>(max_ranges, tiles_v);
+    // Large levels: fewer, longer ranges (less candidate traffic).
+    while (nr > 8 && rt * nr > 2048) nr /= 2;
     cg.ntv = (int)((tiles_v + nr - 1) / nr);
     cg.nranges = (int)((tiles_v + cg.ntv - 1) / cg.ntv);
     const int locals = cg.ntv * S::MB * 16;
@@ -722,13 +734,33 @@ static CandGeom cand_geom(int64_t n_rows, int64_t v) {
     return cg;
 }
 
+static CandGeom cand_geom(int64_t n_rows, int64_t v) {
+    return n_rows >= kDistBigRows ? cand_geom_t<DistBig>(n_rows, v)
+                                  : cand_geom_t<DistSmall>(n_rows, v);
+}
+
+template <class S>
+static hipError_t launch_dist(const DistArgs& da, hipStream_t st) {
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)rvq_dist_kernel<S>,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           S::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int64_t rt = (da.n_rows + S::BN - 1) / S::BN;
+    hipLaunchKernelGGL(rvq_dist_kernel<S>, dim3((unsigned)(rt * da.cg.nranges)), dim3(S::NT),
+                       S::LDS_BYTES, st, da);
+    return hipGetLastError();
+}
+
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
                const int32_t* strides, const uint16_t* codebooks, const float* csq, int64_t v,
                int32_t* codes, float* recon, float* gap, const int32_t* force_codes,
                int64_t* n_flagged) {
-    using S = DistShape;
     hipStream_t st = ncm_ctx_stream(ctx);
     RvqGeom g{};
     g.b = b; g.t = t; g.d = d; g.v = v;
@@ -818,14 +850,6 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         if (e != hipSuccess) return NCM_E_HIP;
     }
 
-    static bool attr_set = false;
-    if (!attr_set) {
-        e = hipFuncSetAttribute((const void*)rvq_dist_kernel<S>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, S::LDS_BYTES);
-        if (e != hipSuccess) return NCM_E_HIP;
-        attr_set = true;
-    }
-
     for (int64_t l = 0; l < levels; ++l) {
         const int64_t n = b * (t / strides[l]);
         const CandGeom cg = cand_geom(n, v);
@@ -837,10 +861,7 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         da.cand = cand;
         da.n_rows = n; da.v = v; da.d = d;
         da.cg = cg;
-        const int64_t rt = (n + S::BN - 1) / S::BN;
-        hipLaunchKernelGGL(rvq_dist_kernel<S>, dim3((unsigned)(rt * cg.nranges)), dim3(S::NT),
-                           S::LDS_BYTES, st, da);
-        e = hipGetLastError();
+        e = n >= kDistBigRows ? launch_dist<DistBig>(da, st) : launch_dist<DistSmall>(da, st);
         if (e != hipSuccess) return NCM_E_HIP;
 
         RescoreArgs ra{};
