@@ -56,6 +56,13 @@ __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
     return v;
 }
 
+// Makes this wavefront's LDS writes visible to its own later LDS reads by
+// other lanes: the writes complete (lgkmcnt(0)) and the compiler may not
+// move memory operations across this point.
+__device__ __forceinline__ void wave_lds_sync() {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+}
+
 __device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
     uint32_t r;
     asm volatile("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
@@ -409,26 +416,30 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void rvq_dist_kernel(DistAr
 constexpr int kKeySlots = 8;
 constexpr int kMaxChunks = kKeySlots * 64 / 4;
 
-struct RescoreArgs {
+// Per-level arguments of the row kernels (rescore and fallback).
+struct RowArgs {
     RvqGeom g;
     const float* x;
     const float* pyr;
     const uint16_t* cb;          // all codebooks [levels, v, d]
     const float* csq;            // all levels [levels, v]
-    const int32_t* resid_codes;  // codes that build residuals (forced or own)
-    const int32_t* force_codes;  // nullable
+    const int32_t* force_codes;  // nullable: codes that build later residuals
     int32_t* codes;
     float* gap;                  // nullable
     const uint32_t* cand;
     const float* rowc_in;
     const float* cmax;
-    uint16_t* ubuf;              // next level's bf16 rows
-    float* rowc_out;             // next level's offsets
+    const float* d_in;           // D_l, one row per level l-1 row (level > 0)
+    float* d_out;                // D_{l+1}, one row per level-l row (not last level)
+    uint16_t* ubuf;              // level l+1 bf16 rows
+    float* rowc_out;             // level l+1 offsets
+    float* recon;                // last level only, nullable
     int32_t* flag_count;         // this level's counter
     int32_t* flag_rows;
     int32_t* fb_done;
     int level;
     int64_t n_rows;
+    int64_t d_div;               // level-l rows per D_l row (s_{l-1} / s_l)
     CandGeom cg;
 };
 
@@ -464,42 +475,83 @@ __device__ __forceinline__ float rel_gap(const Best& b, double unorm2) {
     return (float)((e2 - e1) / fmax(fabs(e1), 1e-300));
 }
 
-// Code write, gap write and the next level's rows for one finished row.
+// kDotBatch fixed-order dot products at once (all code rows loaded before
+// any arithmetic, so one memory round trip serves the batch). Each result
+// has the bits of the oracle's ncmo_dot_fixed.
+constexpr int kDotBatch = 2;
+
 template <int NCH>
-__device__ __forceinline__ void finish_row(const RescoreArgs& a, int64_t row, const Best& b,
-                                          double unorm2, RowVec<NCH>& D, int lane) {
-    const RvqGeom& g = a.g;
-    const int l = a.level;
-    const int64_t s = g.L.stride[l];
-    const int64_t per_b = g.t / s;
-    const int64_t bb = row / per_b, tp = row % per_b;
-    const int64_t ci = bb * g.L.total + g.L.offset[l] + tp;
-    if (lane == 0) {
-        a.codes[ci] = b.code;
-        if (a.gap) a.gap[ci] = rel_gap(b, unorm2);
-    }
-    if (l + 1 >= g.L.levels) return;
-    int32_t k = a.force_codes ? a.force_codes[ci] : b.code;
-    k = k < 0 ? 0 : (k >= g.v ? (int32_t)(g.v - 1) : k);
-    add_bf16_row<NCH>(a.cb + ((int64_t)l * g.v + k) * g.d, g.d, lane, D);  // D_{l+1}
-    const int64_t ratio = s / g.L.stride[l + 1];
-    for (int64_t c = 0; c < ratio; ++c) {
-        const int64_t child = row * ratio + c;
-        RowVec<NCH> u;
-        load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l + 1, child), g.d, lane, u);
+__device__ __forceinline__ void dotn_fixed(const RowVec<NCH>& u,
+                                           const uint16_t* const (&c)[kDotBatch], int64_t d,
+                                           int lane, float (&out)[kDotBatch]) {
+    u32x2_t p[kDotBatch][NCH];
+#pragma unroll
+    for (int j = 0; j < kDotBatch; ++j)
 #pragma unroll
         for (int m = 0; m < NCH; ++m)
+            if (lane_chunk_valid(d, m, lane)) p[j][m] = *(const u32x2_t*)(c[j] + m * 256 + 4 * lane);
+    float acc[kDotBatch];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
-        const RowStats st = write_bf16_row<NCH>(u, g.d, lane, a.ubuf + child * g.d);
-        if (lane == 0) a.rowc_out[child] = row_offset(st, a.cmax[l + 1]);
+    for (int j = 0; j < kDotBatch; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int m = 0; m < NCH; ++m) {
+        if (lane_chunk_valid(d, m, lane)) {
+#pragma unroll
+            for (int j = 0; j < kDotBatch; ++j) {
+                acc[j] = __builtin_fmaf(u.v[m][0], bf16_lo_to_f32(p[j][m][0]), acc[j]);
+                acc[j] = __builtin_fmaf(u.v[m][1], bf16_hi_to_f32(p[j][m][0]), acc[j]);
+                acc[j] = __builtin_fmaf(u.v[m][2], bf16_lo_to_f32(p[j][m][1]), acc[j]);
+                acc[j] = __builtin_fmaf(u.v[m][3], bf16_hi_to_f32(p[j][m][1]), acc[j]);
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+        for (int j = 0; j < kDotBatch; ++j) acc[j] = acc[j] + __shfl_xor(acc[j], off, 64);
+#pragma unroll
+    for (int j = 0; j < kDotBatch; ++j) out[j] = acc[j];
+}
+
+// Exact distances of `n` codes listed in `list` (wave-uniform), folded into b.
+template <int NCH>
+__device__ __forceinline__ void score_list(const RowVec<NCH>& u, const uint16_t* cbl,
+                                           const float* csql, const int32_t* list, int n,
+                                           int64_t d, int lane, Best& b) {
+    for (int i = 0; i < n; i += kDotBatch) {
+        int32_t k[kDotBatch];
+        const uint16_t* c[kDotBatch];
+#pragma unroll
+        for (int j = 0; j < kDotBatch; ++j) {
+            k[j] = list[i + j < n ? i + j : i];
+            c[j] = cbl + (int64_t)k[j] * d;
+        }
+        float dots[kDotBatch];
+        dotn_fixed<NCH>(u, c, d, lane, dots);
+#pragma unroll
+        for (int j = 0; j < kDotBatch; ++j)
+            if (i + j < n) best_update(b, __builtin_fmaf(-2.0f, dots[j], csql[k[j]]), k[j]);
     }
 }
 
+// D_l for one row (zero at level 0).
 template <int NCH>
-__device__ __forceinline__ void residual(const RescoreArgs& a, int64_t row, int lane,
-                                         RowVec<NCH>& D, RowVec<NCH>& u) {
-    coarse_recon<NCH>(a.g, a.cb, a.resid_codes, a.level, row, lane, D);
+__device__ __forceinline__ void load_coarse(const RowArgs& a, int64_t row, int lane,
+                                            RowVec<NCH>& D) {
+    if (a.level == 0) {
+#pragma unroll
+        for (int m = 0; m < NCH; ++m) D.v[m][0] = D.v[m][1] = D.v[m][2] = D.v[m][3] = 0.0f;
+    } else {
+        load_f32_row<NCH>(a.d_in + (row / a.d_div) * a.g.d, a.g.d, lane, D);
+    }
+}
+
+// u = P_l - D_l for one row.
+template <int NCH>
+__device__ __forceinline__ void load_residual(const RowArgs& a, int64_t row, int lane,
+                                              RowVec<NCH>& u) {
+    RowVec<NCH> D;
+    load_coarse<NCH>(a, row, lane, D);
     load_f32_row<NCH>(pooled_row_ptr(a.g, a.x, a.pyr, a.level, row), a.g.d, lane, u);
 #pragma unroll
     for (int m = 0; m < NCH; ++m)
@@ -507,17 +559,88 @@ __device__ __forceinline__ void residual(const RescoreArgs& a, int64_t row, int 
         for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
 }
 
+// Code and gap of a finished row; D_{l+1} and the next level's bf16 rows, or
+// the reconstruction at the last level.
 template <int NCH>
-__global__ __launch_bounds__(256) void rvq_rescore_kernel(RescoreArgs a) {
+__device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const Best& b,
+                                          double unorm2, int lane) {
+    const RvqGeom& g = a.g;
+    const int l = a.level;
+    const int64_t d = g.d;
+    const int64_t s = g.L.stride[l];
+    const int64_t per_b = g.t / s;
+    const int64_t bb = row / per_b, tp = row - bb * per_b;
+    const int64_t ci = bb * g.L.total + g.L.offset[l] + tp;
+    if (lane == 0) {
+        a.codes[ci] = b.code;
+        if (a.gap) a.gap[ci] = rel_gap(b, unorm2);
+    }
+    const bool last = l + 1 >= g.L.levels;
+    if (last && !a.recon) return;
+    int32_t k = a.force_codes ? a.force_codes[ci] : b.code;
+    k = k < 0 ? 0 : (k >= g.v ? (int32_t)(g.v - 1) : k);
+    RowVec<NCH> D;
+    load_coarse<NCH>(a, row, lane, D);
+    add_bf16_row<NCH>(a.cb + ((int64_t)l * g.v + k) * d, d, lane, D);  // D_{l+1}
+    if (last) {
+        // recon[bb, tp * s .. tp * s + s - 1] = D_L
+        for (int64_t r = 0; r < s; ++r) {
+            float* dst = a.recon + (bb * g.t + tp * s + r) * d;
+#pragma unroll
+            for (int m = 0; m < NCH; ++m)
+                if (lane_chunk_valid(d, m, lane)) {
+                    f32x4_t o;
+                    o[0] = D.v[m][0]; o[1] = D.v[m][1]; o[2] = D.v[m][2]; o[3] = D.v[m][3];
+                    *(f32x4_t*)(dst + m * 256 + 4 * lane) = o;
+                }
+        }
+        return;
+    }
+    {
+        float* dst = a.d_out + row * d;
+#pragma unroll
+        for (int m = 0; m < NCH; ++m)
+            if (lane_chunk_valid(d, m, lane)) {
+                f32x4_t o;
+                o[0] = D.v[m][0]; o[1] = D.v[m][1]; o[2] = D.v[m][2]; o[3] = D.v[m][3];
+                *(f32x4_t*)(dst + m * 256 + 4 * lane) = o;
+            }
+    }
+    const int64_t ratio = s / g.L.stride[l + 1];
+    for (int64_t c = 0; c < ratio; ++c) {
+        const int64_t child = row * ratio + c;
+        RowVec<NCH> u;
+        load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l + 1, child), d, lane, u);
+#pragma unroll
+        for (int m = 0; m < NCH; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
+        const RowStats st = write_bf16_row<NCH>(u, d, lane, a.ubuf + child * d);
+        if (lane == 0) a.rowc_out[child] = row_offset(st, a.cmax[l + 1]);
+    }
+}
+
+template <int NCH>
+__global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
+    __shared__ int32_t cand_list[4][kKeySlots * 64];
     const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int wave = threadIdx.x >> 6;
+    const int64_t row = (int64_t)blockIdx.x * 4 + wave;
     if (row >= a.n_rows) return;
     const RvqGeom& g = a.g;
     const int l = a.level;
     const int64_t d = g.d;
 
-    RowVec<NCH> D, u;
-    residual<NCH>(a, row, lane, D, u);
+    RowVec<NCH> u;
+    load_residual<NCH>(a, row, lane, u);
+    const int nk = a.cg.nchunk * 4;
+    const uint32_t* ck = a.cand + row * (int64_t)nk;
+    uint32_t key[kKeySlots];
+#pragma unroll
+    for (int s = 0; s < kKeySlots; ++s) {
+        const int idx = lane + 64 * s;
+        key[s] = idx < nk ? ck[idx] : 0xFFFFFFFFu;
+    }
     const RowStats st = write_bf16_row<NCH>(u, d, lane, nullptr);
 
     // Rigorous bound E on |key distance - (offset + exact dist)|:
@@ -534,31 +657,34 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RescoreArgs a) {
                          ((float)(d / 64) + 7.0f) * 0x1p-23f * st.unorm) +
                     dmag * 0x1p-21f + 1e-30f;
     const uint32_t imask = (1u << a.cg.ib) - 1u;
-
-    const int nk = a.cg.nchunk * 4;
-    const uint32_t* ck = a.cand + row * (int64_t)nk;
-    uint32_t key[kKeySlots];
     uint32_t mn = 0xFFFFFFFFu;
 #pragma unroll
-    for (int s = 0; s < kKeySlots; ++s) {
-        const int idx = lane + 64 * s;
-        key[s] = idx < nk ? ck[idx] : 0xFFFFFFFFu;
-        mn = min(mn, key[s]);
-    }
+    for (int s = 0; s < kKeySlots; ++s) mn = min(mn, key[s]);
     mn = wave_min_u32(mn);
     const float m_f = __uint_as_float(mn & ~imask);
     const float eps_q = __uint_as_float((uint32_t)(127 + a.cg.ib - 23) << 23);  // 2^(ib-23)
-    const float tau = 1e-4f * (st.unorm * st.unorm + fabsf(m_f - rowc) + 2.0f * E);
+    // Codes whose exact relative gap to the best is below ~2e-5 are always
+    // rescored, so the reported gap is exact for near-ties.
+    const float tau = 2e-5f * (st.unorm * st.unorm + fabsf(m_f - rowc) + 2.0f * E);
     const float thr = (m_f * (1.0f + eps_q) + 2.0f * E + tau) * (1.0f + 0x1p-20f);
 
     // Incomplete chunk: its fourth key is still under the threshold.
     bool incomplete = false;
+    int nsel = 0;
+    int32_t* list = cand_list[wave];
 #pragma unroll
     for (int s = 0; s < kKeySlots; ++s) {
         const int idx = lane + 64 * s;
-        if (idx < nk && (idx & 3) == 3 && key[s] != 0xFFFFFFFFu &&
-            __uint_as_float(key[s] & ~imask) <= thr)
-            incomplete = true;
+        const bool valid = idx < nk && key[s] != 0xFFFFFFFFu;
+        const bool under = valid && __uint_as_float(key[s] & ~imask) <= thr;
+        if (under && (idx & 3) == 3) incomplete = true;
+        const uint64_t mask = __ballot(under);
+        if (under) {
+            const int pos = nsel + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
+                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
+            list[pos] = (int32_t)decode_code(a.cg, idx >> 2, key[s] & imask);
+        }
+        nsel += __popcll(mask);
     }
     if (__ballot(incomplete) != 0) {
         if (lane == 0) {
@@ -568,28 +694,12 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RescoreArgs a) {
         }
         return;
     }
+    wave_lds_sync();
 
-    const uint16_t* cbl = a.cb + (int64_t)l * g.v * d;
-    const float* csql = a.csq + (int64_t)l * g.v;
     Best b{INFINITY, INFINITY, 0x7FFFFFFF};
-#pragma unroll
-    for (int s = 0; s < kKeySlots; ++s) {
-        const int idx = lane + 64 * s;
-        const bool sel = idx < nk && key[s] != 0xFFFFFFFFu &&
-                         __uint_as_float(key[s] & ~imask) <= thr;
-        uint64_t mask = __ballot(sel);
-        while (mask) {
-            const int src = __builtin_ctzll(mask);
-            mask &= mask - 1;
-            const uint32_t kk = (uint32_t)__shfl((int)key[s], src, 64);
-            const int cidx = src + 64 * s;
-            const int64_t code = decode_code(a.cg, cidx >> 2, kk & imask);
-            const float dot = dot_fixed<NCH>(u, cbl + code * d, d, lane);
-            const float dist = __builtin_fmaf(-2.0f, dot, csql[code]);
-            best_update(b, dist, (int32_t)code);
-        }
-    }
-    finish_row<NCH>(a, row, b, st.unorm2, D, lane);
+    score_list<NCH>(u, a.cb + (int64_t)l * g.v * d, a.csq + (int64_t)l * g.v, list, nsel, d, lane,
+                    b);
+    finish_row<NCH>(a, row, b, st.unorm2, lane);
 }
 
 // -------------------------------------------------------- fallback kernel
@@ -599,12 +709,16 @@ struct FbPart {
     int32_t code, pad;
 };
 
+constexpr int kFbChunk = 64;  // codes per fallback work item
+
 // Exhaustive exact search for queued rows: work item = (queued row, chunk of
-// 256 codes); the block that completes a row's last chunk merges the chunk
-// results and finishes the row.
+// 64 codes, 16 per wavefront in batches of four); the block that completes a
+// row's last chunk merges the chunk results and finishes the row.
 template <int NCH>
-__global__ __launch_bounds__(256) void rvq_fallback_kernel(RescoreArgs a, FbPart* part,
-                                                           int nvch) {
+__global__ __launch_bounds__(256) void rvq_fallback_kernel(RowArgs a, FbPart* part, int nvch) {
+    __shared__ int32_t codes_l[4][16];
+    __shared__ Best wb[4];
+    __shared__ int last;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int count = *a.flag_count;
@@ -613,22 +727,18 @@ __global__ __launch_bounds__(256) void rvq_fallback_kernel(RescoreArgs a, FbPart
     const int64_t d = g.d;
     const uint16_t* cbl = a.cb + (int64_t)a.level * g.v * d;
     const float* csql = a.csq + (int64_t)a.level * g.v;
-    __shared__ Best wb[4];
-    __shared__ int last;
     for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
         const int f = (int)(item / nvch);
         const int ch = (int)(item % nvch);
         const int64_t row = a.flag_rows[f];
-        RowVec<NCH> D, u;
-        residual<NCH>(a, row, lane, D, u);
+        RowVec<NCH> u;
+        load_residual<NCH>(a, row, lane, u);
+        const int64_t c0 = (int64_t)ch * kFbChunk + wave * 16;
+        const int n = (int)max<int64_t>(0, min<int64_t>(16, g.v - c0));
+        if (lane < 16) codes_l[wave][lane] = (int32_t)(c0 + lane);
+        wave_lds_sync();
         Best b{INFINITY, INFINITY, 0x7FFFFFFF};
-        const int64_t c0 = (int64_t)ch * 256 + wave * 64;
-        for (int j = 0; j < 64; ++j) {
-            const int64_t code = c0 + j;
-            if (code >= g.v) break;
-            const float dot = dot_fixed<NCH>(u, cbl + code * d, d, lane);
-            best_update(b, __builtin_fmaf(-2.0f, dot, csql[code]), (int32_t)code);
-        }
+        score_list<NCH>(u, cbl, csql, codes_l[wave], n, d, lane, b);
         if (lane == 0) wb[wave] = b;
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -662,7 +772,7 @@ __global__ __launch_bounds__(256) void rvq_fallback_kernel(RescoreArgs a, FbPart
                 }
             }
             const RowStats st = write_bf16_row<NCH>(u, d, lane, nullptr);
-            finish_row<NCH>(a, row, m, st.unorm2, D, lane);
+            finish_row<NCH>(a, row, m, st.unorm2, lane);
         }
         __syncthreads();
     }
@@ -687,7 +797,7 @@ static int nch_for(int64_t d) {
 }
 
 template <int NCH>
-static hipError_t launch_row_kernels(int which, const PrepArgs* pa, const RescoreArgs* ra,
+static hipError_t launch_row_kernels(int which, const PrepArgs* pa, const RowArgs* ra,
                                      FbPart* part, int nvch, int64_t rows, hipStream_t st) {
     const dim3 grid((unsigned)((rows + 3) / 4));
     if (which == 0)
@@ -700,7 +810,7 @@ static hipError_t launch_row_kernels(int which, const PrepArgs* pa, const Rescor
     return hipGetLastError();
 }
 
-static hipError_t launch_rows(int nch, int which, const PrepArgs* pa, const RescoreArgs* ra,
+static hipError_t launch_rows(int nch, int which, const PrepArgs* pa, const RowArgs* ra,
                               FbPart* part, int nvch, int64_t rows, hipStream_t st) {
     switch (nch) {
         case 1: return launch_row_kernels<1>(which, pa, ra, part, nvch, rows, st);
@@ -784,9 +894,13 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         max_rows = std::max(max_rows, n);
         max_cand = std::max(max_cand, n * (int64_t)cand_geom(n, v).nchunk * 4);
     }
-    const int nvch = (int)((v + 255) / 256);
+    const int nvch = (int)((v + kFbChunk - 1) / kFbChunk);
     const size_t o_pyr = carve((size_t)pyr_floats * 4);
     const size_t o_u = carve((size_t)max_rows * d * 2);
+    // Level l (l + 1 < levels) writes D_{l+1} to dbuf[(l + 1) & 1]: dbuf[1]
+    // from level 0 on (two or more levels), dbuf[0] from level 1 on.
+    const size_t o_d0 = carve(levels > 2 ? (size_t)max_rows * d * 4 : 0);
+    const size_t o_d1 = carve(levels > 1 ? (size_t)max_rows * d * 4 : 0);
     const size_t o_rc0 = carve((size_t)max_rows * 4);
     const size_t o_rc1 = carve((size_t)max_rows * 4);
     const size_t o_cand = carve((size_t)max_cand * 4);
@@ -808,6 +922,8 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
     int32_t* frows = (int32_t*)(W + o_fr);
     int32_t* fdone = (int32_t*)(W + o_fd);
     FbPart* fpart = (FbPart*)(W + o_fp);
+    // D_{l+1} (coarse reconstruction) is written by level l into dbuf[(l+1)&1].
+    float* dbuf[2] = {(float*)(W + o_d0), (float*)(W + o_d1)};
 
     hipLaunchKernelGGL(rvq_setup_kernel, dim3((unsigned)levels), dim3(256), 0, st, csq, v, cmax,
                        fcount, (int)levels);
@@ -838,12 +954,11 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
     }
 
     const int nch = nch_for(d);
-    const int32_t* resid = force_codes ? force_codes : codes;
 
     // Level 0 rows.
     {
         PrepArgs pa{};
-        pa.g = g; pa.x = x; pa.pyr = pyr; pa.cb = codebooks; pa.resid_codes = resid;
+        pa.g = g; pa.x = x; pa.pyr = pyr; pa.cb = codebooks; pa.resid_codes = codes;
         pa.cmax = cmax; pa.ubuf = ubuf; pa.rowc = rowc[0]; pa.level = 0;
         pa.n_rows = b * (t / strides[0]);
         e = launch_rows(nch, 0, &pa, nullptr, nullptr, 0, pa.n_rows, st);
@@ -864,11 +979,15 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         e = n >= kDistBigRows ? launch_dist<DistBig>(da, st) : launch_dist<DistSmall>(da, st);
         if (e != hipSuccess) return NCM_E_HIP;
 
-        RescoreArgs ra{};
+        RowArgs ra{};
         ra.g = g; ra.x = x; ra.pyr = pyr; ra.cb = codebooks; ra.csq = csq;
-        ra.resid_codes = resid; ra.force_codes = force_codes; ra.codes = codes; ra.gap = gap;
+        ra.force_codes = force_codes; ra.codes = codes; ra.gap = gap;
         ra.cand = cand; ra.rowc_in = rowc[l & 1]; ra.cmax = cmax;
+        ra.d_in = l > 0 ? dbuf[l & 1] : nullptr;
+        ra.d_out = l + 1 < levels ? dbuf[(l + 1) & 1] : nullptr;
+        ra.d_div = l > 0 ? strides[l - 1] / strides[l] : 1;
         ra.ubuf = ubuf; ra.rowc_out = rowc[(l + 1) & 1];
+        ra.recon = l + 1 == levels ? recon : nullptr;
         ra.flag_count = fcount + l; ra.flag_rows = frows; ra.fb_done = fdone;
         ra.level = (int)l; ra.n_rows = n; ra.cg = cg;
         e = launch_rows(nch, 1, nullptr, &ra, nullptr, nvch, n, st);
@@ -877,10 +996,6 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         if (e != hipSuccess) return NCM_E_HIP;
     }
 
-    if (recon) {
-        e = launch_rvq_decode(resid, b, t, d, levels, strides, codebooks, v, recon, st);
-        if (e != hipSuccess) return NCM_E_HIP;
-    }
     if (n_flagged) {
         int32_t host[kMaxLevels];
         e = hipMemcpyAsync(host, fcount, levels * 4, hipMemcpyDeviceToHost, st);
