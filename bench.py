@@ -32,6 +32,12 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "RVQ-encode tokens/s & bf16-linear TFLOP/s (1B shape), % of MI355X roofline"
 LINEAR_M = 2048
 LINEAR_NK = [(2048, 2048), (8192, 2048), (2048, 8192)]
+# HBM-side bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+# (each in its own run, fetch scaled by the factor a plain copy shows); the
+# summaries and commands are in profiles/linear_bf16_1b_shapes.md and
+# profiles/rvq_encode_b16_t2048_d2048_l8_v4096.md.
+LINEAR_TRAFFIC_BYTES_PER_LAUNCH = 151.3e6
+RVQ_TRAFFIC_BYTES_PER_ENCODE = 6743e6
 
 
 def _events(torch):
@@ -174,7 +180,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["linear", "rvq", "all"], default="all")
+    ap.add_argument("--only", choices=["linear", "rvq", "all", "copy"], default="all",
+                    help="copy: a plain 256 MiB device copy, the reference point for "
+                         "the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -189,6 +197,15 @@ def main():
     import ncmorph_amd  # noqa: F401  (raises if the HIP library is missing)
 
     torch.cuda.init()
+    if args.only == "copy":
+        n = 64 * 1024 * 1024
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_per_launch": n * 4, "launches": 5}))
+        return
     res = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
            "data": "synthetic (SplitMix64 + Box-Muller normals, fixed seeds)"}
@@ -202,7 +219,10 @@ def main():
                          "accumulate": "fp32", "output": "fp32"}
         res["roofline"] = {"bound": "mfma", "achieved": round(tflops, 2),
                            "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                           "frac": round(tflops / BF16_PEAK_TFLOPS, 4), "traffic": None}
+                           "frac": round(tflops / BF16_PEAK_TFLOPS, 4),
+                           "traffic": LINEAR_TRAFFIC_BYTES_PER_LAUNCH,
+                           "flops_per_launch": lin["flops_per_step"] / len(LINEAR_NK),
+                           "avg_launch_us": round(lin["step_s"] / len(LINEAR_NK) * 1e6, 3)}
         res["linear_per_shape"] = {
             f"{LINEAR_M}x{n}x{k}": {
                 "us": round(t * 1e6, 2),
@@ -224,7 +244,8 @@ def main():
                           "strides": [128, 64, 32, 16, 8, 4, 2, 1]},
                "roofline": {"bound": "mfma", "achieved": round(tf, 2),
                             "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
-                            "frac": round(tf / BF16_PEAK_TFLOPS, 4), "traffic": None,
+                            "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                            "traffic": RVQ_TRAFFIC_BYTES_PER_ENCODE,
                             "hbm_gbs_algorithmic": round(gbs, 1),
                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
                "flagged_rows": rv["n_flagged"]}
