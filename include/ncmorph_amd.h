@@ -87,6 +87,16 @@ int ncm_matmul_bf16_bias(const float* input, size_t input_len, const float* weig
                          float* output, size_t output_len, size_t token_count,
                          size_t input_width, size_t output_width);
 
+/* Replaces `kernels.matmul` (packages/kernels/root.zig:25-65): fp32
+ * output[t, o] = sum_k input[t, k] * weights[o, k] on the fp32 MFMA. The
+ * reference accumulates in increasing k (root.zig:55-58); the MFMA order
+ * differs, and both meet the reference's own contract
+ * |y - y_f64| <= (input_width + 1) 2^-24 sum |x w| (root.zig:836-865).
+ * Host pointers; lengths as in root.zig:32-34. */
+int ncm_matmul_f32(const float* input, size_t input_len, const float* weights,
+                   size_t weights_len, float* output, size_t output_len, size_t token_count,
+                   size_t input_width, size_t output_width);
+
 /* Replaces `kernels.round_bf16` (packages/kernels/root.zig:10-12) and
  * `bf16_t.from_f32` (packages/bf16/root.zig:17-22) for whole buffers:
  * RNE, every NaN -> 0x7FC0, no flush. Host pointers. */
@@ -106,6 +116,12 @@ int ncm_round_bf16(const float* values, float* out, size_t n);
 int ncm_linear_bf16(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
                     const uint16_t* bias, void* y, int64_t m, int64_t k, int64_t n,
                     int out_mode);
+
+/* y[m, n] = sum_k x[m, k] * w[n, k], fp32 operands and accumulation on the
+ * fp32 MFMA (device counterpart of packages/kernels/root.zig:25-65).
+ * Requires k % 4 == 0 and 16-byte aligned x and w. Device pointers. */
+int ncm_linear_f32(ncm_ctx_t* ctx, const float* x, const float* w, float* y, int64_t m,
+                   int64_t k, int64_t n);
 
 /* f32 -> bf16 bits, RNE, NaN -> 0x7FC0 (packages/bf16/root.zig:17-22).
  * flush != 0 additionally flushes subnormal results to signed zero (the

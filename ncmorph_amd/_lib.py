@@ -35,10 +35,12 @@ SIGNATURES = [
     ("ncm_set_stream", i32, [vp, vp]),
     ("ncm_get_stream", vp, [vp]),
     ("ncm_synchronize", i32, [vp]),
+    ("ncm_matmul_f32", i32, [vp, sz, vp, sz, vp, sz, sz, sz, sz]),
     ("ncm_matmul_bf16", i32, [vp, sz, vp, sz, vp, sz, sz, sz, sz]),
     ("ncm_matmul_bf16_bias", i32, [vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz]),
     ("ncm_round_bf16", i32, [vp, vp, sz]),
     ("ncm_linear_bf16", i32, [vp, vp, vp, vp, vp, i64, i64, i64, i32]),
+    ("ncm_linear_f32", i32, [vp, vp, vp, vp, i64, i64, i64]),
     ("ncm_bf16_from_f32_dev", i32, [vp, vp, vp, i64, i32]),
     ("ncm_bf16_widen_dev", i32, [vp, vp, vp, i64]),
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),

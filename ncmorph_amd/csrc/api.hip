@@ -166,6 +166,22 @@ int ncm_linear_bf16(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w, const 
     return NCM_OK;
 }
 
+int ncm_linear_f32(ncm_ctx_t* ctx, const float* x, const float* w, float* y, int64_t m,
+                   int64_t k, int64_t n) {
+    if (!ctx) return NCM_E_NULL;
+    if (m < 0 || n < 0 || k < 0) return NCM_E_SHAPE;
+    if (m == 0 || n == 0) return NCM_OK;
+    if (!y || (k > 0 && (!x || !w))) return NCM_E_NULL;
+    if (k % 4 != 0 || k > (int64_t(1) << 20)) return NCM_E_SHAPE;
+    if ((uintptr_t)x % 16 || (uintptr_t)w % 16) return NCM_E_ARG;
+    if (m > (int64_t(1) << 31) || n > (int64_t(1) << 31)) return NCM_E_SHAPE;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_linear_f32(x, w, y, m, k, n, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "f32 linear kernel launch");
+    return NCM_OK;
+}
+
 int ncm_bf16_from_f32_dev(ncm_ctx_t* ctx, const float* src, uint16_t* dst, int64_t n,
                           int flush) {
     if (!ctx) return NCM_E_NULL;
@@ -213,7 +229,7 @@ int host_linear(const float* input, size_t input_len, const float* weights, size
     if (input_len != T * K || weights_len != N * K || output_len != T * N) return NCM_E_LENGTH;
     if (bias && bias_len != N) return NCM_E_LENGTH;
     if (T == 0 || N == 0) return NCM_OK;
-    if (!input || !weights || !output) return NCM_E_NULL;
+    if (!output || (K > 0 && (!input || !weights))) return NCM_E_NULL;
     if (K > (size_t(1) << 21) || T > (size_t(1) << 31) || N > (size_t(1) << 31))
         return NCM_E_SHAPE;
     int rc = 0;
@@ -263,6 +279,46 @@ int host_linear(const float* input, size_t input_len, const float* weights, size
 }
 
 }  // namespace
+
+int ncm_matmul_f32(const float* input, size_t input_len, const float* weights,
+                   size_t weights_len, float* output, size_t output_len, size_t token_count,
+                   size_t input_width, size_t output_width) {
+    const size_t T = token_count, K = input_width, N = output_width;
+    // root.zig:32-34: the slice lengths must match the dimensions.
+    if (input_len != T * K || weights_len != N * K || output_len != T * N) return NCM_E_LENGTH;
+    if (T == 0 || N == 0) return NCM_OK;
+    if (!output || (K > 0 && (!input || !weights))) return NCM_E_NULL;
+    if (K > (size_t(1) << 20) || T > (size_t(1) << 31) || N > (size_t(1) << 31))
+        return NCM_E_SHAPE;
+    int rc = 0;
+    ncm_ctx_t* ctx = default_ctx(&rc);
+    if (rc) return rc;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    // Rows padded with zeros to K4 = K rounded up to 4 (16-byte rows).
+    const size_t K4 = align_up(K, 4);
+    const size_t o_x = 0, o_w = align_up(T * K4 * 4, 256), o_y = o_w + align_up(N * K4 * 4, 256);
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, o_y + T * N * 4, &ws);
+    if (rc) return rc;
+    char* base = (char*)ws;
+    hipStream_t st = ctx->stream;
+    float* x = (float*)(base + o_x);
+    float* w = (float*)(base + o_w);
+    float* y = (float*)(base + o_y);
+    if (K4 != K) {
+        NCM_HIP(hipMemsetAsync(x, 0, T * K4 * 4, st));
+        NCM_HIP(hipMemsetAsync(w, 0, N * K4 * 4, st));
+    }
+    if (K > 0) {
+        NCM_HIP(hipMemcpy2DAsync(x, K4 * 4, input, K * 4, K * 4, T, hipMemcpyHostToDevice, st));
+        NCM_HIP(hipMemcpy2DAsync(w, K4 * 4, weights, K * 4, K * 4, N, hipMemcpyHostToDevice, st));
+    }
+    NCM_HIP(ncm::launch_linear_f32(x, w, y, T, K4, N, st));
+    NCM_HIP(hipMemcpyAsync(output, y, T * N * 4, hipMemcpyDeviceToHost, st));
+    NCM_HIP(hipStreamSynchronize(st));
+    return NCM_OK;
+}
 
 int ncm_matmul_bf16(const float* input, size_t input_len, const float* weights,
                     size_t weights_len, float* output, size_t output_len, size_t token_count,

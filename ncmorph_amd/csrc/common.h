@@ -72,6 +72,27 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("" ::: "memory");
 }
 
+// 4 x 4 transpose inside each quad of lanes (DPP quad permutes). Before:
+// lane q of a quad holds M[j][q] in v[j]; after: lane q holds M[q][j].
+// Applied to an MFMA D fragment (lane = column, element = row), it leaves
+// each lane with four consecutive columns of one row.
+__device__ __forceinline__ float dpp_quad_xor1(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float dpp_quad_xor2(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+}
+__device__ __forceinline__ void quad_transpose4(float (&v)[4], int q) {
+    const bool odd = (q & 1) != 0;
+    float r0 = dpp_quad_xor1(odd ? v[0] : v[1]);
+    float r1 = dpp_quad_xor1(odd ? v[2] : v[3]);
+    if (odd) { v[0] = r0; v[2] = r1; } else { v[1] = r0; v[3] = r1; }
+    const bool hi = (q & 2) != 0;
+    r0 = dpp_quad_xor2(hi ? v[0] : v[2]);
+    r1 = dpp_quad_xor2(hi ? v[1] : v[3]);
+    if (hi) { v[0] = r0; v[1] = r1; } else { v[2] = r0; v[3] = r1; }
+}
+
 // Remap a linear workgroup id so that consecutive logical tiles land on the
 // same XCD (workgroups are dispatched round-robin over the 8 XCDs).
 __device__ __forceinline__ int xcd_remap(int bid, int nblk) {

@@ -14,6 +14,10 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
                          int64_t M, int64_t K, int64_t N, int out_mode, int config,
                          hipStream_t stream);
 
+// fp32 operands, fp32 output; K % 4 == 0, 16-byte aligned x and w.
+hipError_t launch_linear_f32(const float* x, const float* w, float* y, int64_t M, int64_t K,
+                             int64_t N, hipStream_t stream);
+
 hipError_t launch_bf16_from_f32(const float* src, uint16_t* dst, int64_t n, int flush,
                                 hipStream_t stream);
 // Row-padded variant: src [rows, cols] -> dst [rows, ld] (ld >= cols),

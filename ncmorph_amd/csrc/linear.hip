@@ -1,7 +1,10 @@
-// bf16-weight linear y = x * W^T on gfx950 bf16 MFMA, fp32 accumulation.
-// Device counterpart of matmul_bf16_impl (packages/kernels/root.zig:106-142)
-// and of the f32 widen that feeds it at load time (packages/bf16/root.zig:31-37
-// via src/loader.zig:339-342): the MFMA consumes the bf16 bits directly.
+// Linear y = x * W^T on gfx950 MFMA, fp32 accumulation.
+// bf16 operands: device counterpart of matmul_bf16_impl
+// (packages/kernels/root.zig:106-142) and of the f32 widen that feeds it at
+// load time (packages/bf16/root.zig:31-37 via src/loader.zig:339-342): the
+// MFMA consumes the bf16 bits directly.
+// fp32 operands: device counterpart of matmul (packages/kernels/root.zig:25-65)
+// on the fp32 MFMA.
 #include <cstdlib>
 
 #include "gemm_core.h"
@@ -11,8 +14,8 @@ namespace ncm {
 
 template <class S, int OUT_MODE, bool HAS_BIAS>
 __global__ __launch_bounds__(S::NT)
-__attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const uint16_t* __restrict__ x,
-                                                          const uint16_t* __restrict__ w,
+__attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const void* __restrict__ x,
+                                                          const void* __restrict__ w,
                                                           const uint16_t* __restrict__ bias,
                                                           void* __restrict__ y, int64_t M,
                                                           int64_t K, int64_t N, int tiles_n,
@@ -35,13 +38,62 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const ui
 
     GemmAcc<S> acc;
     acc.zero();
-    gemm_mainloop<S>(x + m0 * K, K, operand_bytes(M, m0, K), w + n0 * K, K,
-                     operand_bytes(N, n0, K), K, lds, acc);
+    gemm_mainloop<S>((const char*)x + m0 * K * S::ESZ, K, operand_bytes(M, m0, K, S::ESZ),
+                     (const char*)w + n0 * K * S::ESZ, K, operand_bytes(N, n0, K, S::ESZ), K, lds,
+                     acc);
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave % S::WGM;
     const int wn = wave / S::WGM;
+    if (m0 + S::BM <= M && n0 + S::BN <= N && (N & 3) == 0 && ((uintptr_t)y & 15) == 0) {
+        // Whole tile in range: transpose each 4-row group of the D fragment
+        // inside lane quads so that every lane stores 4 consecutive columns
+        // of one row (16-byte stores; 8 lanes cover 128 contiguous bytes).
+        const int q = lane & 3;
+        const int col4 = (lane & 31) & ~3;
+        const int hrow = 4 * (lane >> 5) + q;
+#pragma unroll
+        for (int nb = 0; nb < S::NB; ++nb) {
+            float bv = 0.0f;
+            if (HAS_BIAS) bv = __uint_as_float((uint32_t)bias[n0 + wn * S::WN + nb * 32 + (lane & 31)] << 16);
+            const int64_t ncol = n0 + wn * S::WN + nb * 32 + col4;
+#pragma unroll
+            for (int mb = 0; mb < S::MB; ++mb) {
+#pragma unroll
+                for (int blk = 0; blk < 4; ++blk) {
+                    float v[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        v[j] = acc.v[mb][nb][4 * blk + j];
+                        if (HAS_BIAS) v[j] = v[j] + bv;
+                    }
+                    quad_transpose4(v, q);
+                    const int64_t m = m0 + wm * S::WM + mb * 32 + 8 * blk + hrow;
+                    if (OUT_MODE == NCM_OUT_F32) {
+                        f32x4_t o;
+                        o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; o[3] = v[3];
+                        *(f32x4_t*)((float*)y + m * N + ncol) = o;
+                    } else {
+                        uint32_t b[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) b[j] = bf16_bits_rne(flush_subnormal(v[j]));
+                        if (OUT_MODE == NCM_OUT_BF16_F32) {
+                            u32x4_t o;
+                            o[0] = b[0] << 16; o[1] = b[1] << 16; o[2] = b[2] << 16; o[3] = b[3] << 16;
+                            *(u32x4_t*)((float*)y + m * N + ncol) = o;
+                        } else {
+                            u32x2_t o;
+                            o[0] = b[0] | (b[1] << 16);
+                            o[1] = b[2] | (b[3] << 16);
+                            *(u32x2_t*)((uint16_t*)y + m * N + ncol) = o;
+                        }
+                    }
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int nb = 0; nb < S::NB; ++nb) {
         const int64_t n = n0 + wn * S::WN + nb * 32 + (lane & 31);
@@ -72,9 +124,8 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const ui
 }
 
 template <class S, int OUT_MODE, bool HAS_BIAS>
-static hipError_t launch_linear_t(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
-                                  void* y, int64_t M, int64_t K, int64_t N,
-                                  hipStream_t stream) {
+static hipError_t launch_linear_t(const void* x, const void* w, const uint16_t* bias, void* y,
+                                  int64_t M, int64_t K, int64_t N, hipStream_t stream) {
     auto kern = linear_kernel<S, OUT_MODE, HAS_BIAS>;
     static bool attr_set = false;
     if (!attr_set) {
@@ -110,73 +161,43 @@ static hipError_t launch_linear_s(const uint16_t* x, const uint16_t* w, const ui
     }
 }
 
-// Tile configurations (index = NCM_LINEAR_TILE):
-//  0: 256x256x64, 4 waves (128x128 each), 1 wave/SIMD
-//  1: 256x128x32, 4 waves (128x64), 2 waves/SIMD
-//  2: 128x128x64, 4 waves (64x64), 2 waves/SIMD
-//  3: 128x128x64, fragment double buffering, 2 waves/SIMD
-//  4: 256x128x64, 4 waves (128x64), 1 wave/SIMD, two prefetch sets
-//  5: 128x64x64, 4 waves (64x32), 2 waves/SIMD
-//  6: 256x256x64, two prefetch sets
-//  7: 256x256x64, fragment double buffering
-//  8: 256x256x32, two prefetch sets, fragment double buffering
-//  9: 256x256x64, fragment double buffering, explicit DS/MFMA interleave
-// 10: 256x256x64, iglp_opt(0)
-// 11: 256x256x64, iglp_opt(1)
-// 12: 256x256x64, two prefetch sets, FDB, explicit interleave
-// 13: 256x256x64, FDB, scheduling fences
-// 14: 256x256x64, two prefetch sets, FDB, scheduling fences
-// 15: 256x128x64, FDB, scheduling fences, 1 wave/SIMD
-// 16: 256x256x64, 8 waves (128x64 each, 2 per SIMD), FDB, fences
-// 17: 256x256x64, 8 waves, FDB, compiler order
-// 18: 256x256x32, 8 waves, FDB, fences
-// 19: 256x256x64, 8 waves (64x128 each), FDB, fences
-// 20: 256x128x32, 2 waves/SIMD (two workgroups per CU), FDB, fences
-// 21: 128x128x64, 2 waves/SIMD, FDB, fences
-// 22: 256x128x32, 2 waves/SIMD, two prefetch sets, FDB, fences
-// 23: 128x256x32, 2 waves/SIMD, FDB, fences
-// 24: 256x256x64, direct-to-LDS loads, FDB, fences
-// 25: 256x256x64, 8 waves (64x128), direct-to-LDS loads, FDB, fences
-// 26: 128x128x64, direct-to-LDS loads, FDB, fences, 2 waves/SIMD
-// 27: 256x128x64, direct-to-LDS loads, FDB, fences
-using Lin0 = GemmShape<256, 256, 64, 2, 2, 1, 1, false>;
-using Lin1 = GemmShape<256, 128, 32, 2, 2, 1, 2, false>;
-using Lin2 = GemmShape<128, 128, 64, 2, 2, 1, 2, false>;
-using Lin3 = GemmShape<128, 128, 64, 2, 2, 1, 2, true>;
-using Lin4 = GemmShape<256, 128, 64, 2, 2, 2, 1, true>;
-using Lin5 = GemmShape<128, 64, 64, 2, 2, 1, 2, false>;
-using Lin6 = GemmShape<256, 256, 64, 2, 2, 2, 1, false>;
-using Lin7 = GemmShape<256, 256, 64, 2, 2, 1, 1, true>;
-using Lin8 = GemmShape<256, 256, 32, 2, 2, 2, 1, true>;
-using Lin9 = GemmShape<256, 256, 64, 2, 2, 1, 1, true, 3>;
-using Lin10 = GemmShape<256, 256, 64, 2, 2, 1, 1, false, 1>;
-using Lin11 = GemmShape<256, 256, 64, 2, 2, 1, 1, false, 2>;
-using Lin12 = GemmShape<256, 256, 64, 2, 2, 2, 1, true, 3>;
-using Lin13 = GemmShape<256, 256, 64, 2, 2, 1, 1, true, 4>;
-using Lin14 = GemmShape<256, 256, 64, 2, 2, 2, 1, true, 4>;
-using Lin15 = GemmShape<256, 128, 64, 2, 2, 1, 1, true, 4>;
-using Lin16 = GemmShape<256, 256, 64, 2, 4, 1, 2, true, 4>;
-using Lin17 = GemmShape<256, 256, 64, 2, 4, 1, 2, true, 0>;
-using Lin18 = GemmShape<256, 256, 32, 2, 4, 1, 2, true, 4>;
-using Lin19 = GemmShape<256, 256, 64, 4, 2, 1, 2, true, 4>;
-using Lin20 = GemmShape<256, 128, 32, 2, 2, 1, 2, true, 4>;
-using Lin21 = GemmShape<128, 128, 64, 2, 2, 1, 2, true, 4>;
-using Lin22 = GemmShape<256, 128, 32, 2, 2, 2, 2, true, 4>;
-using Lin23 = GemmShape<128, 256, 32, 2, 2, 1, 2, true, 4>;
-using Lin24 = GemmShape<256, 256, 64, 2, 2, 1, 1, true, 4, true>;
-using Lin25 = GemmShape<256, 256, 64, 4, 2, 1, 2, true, 4, true>;
-using Lin26 = GemmShape<128, 128, 64, 2, 2, 1, 2, true, 4, true>;
-using Lin27 = GemmShape<256, 128, 64, 2, 2, 1, 1, true, 4, true>;
-constexpr int kLinConfigs = 28;
+// Tile configurations of the bf16 linear (index = NCM_LINEAR_TILE):
+//  0: 256x256x64, 8 waves (64x128 each, 2 per SIMD), direct-to-LDS loads,
+//     barrier in the middle of the last k-step (SCHED 5), 2 LDS stages
+//  1: 128x128x64, 4 waves (64x64), DMA, SCHED 5, 4 LDS stages
+//  2: 128x128x64, 4 waves, DMA, fences (SCHED 4), 2 stages: two workgroups
+//     per CU
+//  3: 256x256x32, 8 waves, DMA, ping-pong (SCHED 6), 4 LDS stages
+//  4: 256x256x64, 4 waves (128x128, 1 per SIMD), DMA, SCHED 5
+//  5: 256x128x64, 8 waves (64x64), DMA, SCHED 5, 3 LDS stages
+//  6: 256x256x64, 8 waves, register-staged loads, fences
+//  7: 128x128x64, 4 waves, register-staged loads, fences
+using Lin0 = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
+using Lin1 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
+using Lin2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
+using Lin3 = GemmShape<256, 256, 32, 4, 2, 2, 6, true, 4>;
+using Lin4 = GemmShape<256, 256, 64, 2, 2, 1, 5, true>;
+using Lin5 = GemmShape<256, 128, 64, 4, 2, 2, 5, true, 3>;
+using Lin6 = GemmShape<256, 256, 64, 4, 2, 2, 4, false>;
+using Lin7 = GemmShape<128, 128, 64, 2, 2, 2, 4, false>;
+constexpr int kLinConfigs = 8;
+
+// fp32 linear: 128x128x32 (128-byte rows), 4 waves, DMA, SCHED 5, two
+// stages (64 KB: two workgroups per CU). The fp32 MFMA has 1/16 of the bf16
+// rate, so this tile is MFMA-bound with a wide margin.
+using LinF32 = GemmShape<128, 128, 32, 2, 2, 2, 5, true, 2, true>;
 
 int linear_tile_config(int64_t M, int64_t N, int forced) {
     if (forced >= 0 && forced < kLinConfigs) return forced;
     const int64_t cus = 256;
     auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    // 256x256 with 8 waves when it fills every CU, else 128x128 (two
-    // workgroups per CU); both with direct-to-LDS loads.
-    if (tiles(256, 256) >= cus) return 25;
-    return 26;
+    // 256x256 with 8 waves when it fills every CU; 128x128 with four LDS
+    // stages when that gives at most one tile per CU (latency-bound: deeper
+    // prefetch pays), else 128x128 with two stages (two workgroups per CU).
+    // All with direct-to-LDS loads.
+    if (tiles(256, 256) >= cus) return 0;
+    if (tiles(128, 128) <= cus) return 1;
+    return 2;
 }
 
 hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, void* y,
@@ -196,28 +217,13 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
         case 4: return launch_linear_s<Lin4>(x, w, bias, y, M, K, N, out_mode, stream);
         case 5: return launch_linear_s<Lin5>(x, w, bias, y, M, K, N, out_mode, stream);
         case 6: return launch_linear_s<Lin6>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 7: return launch_linear_s<Lin7>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 8: return launch_linear_s<Lin8>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 9: return launch_linear_s<Lin9>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 10: return launch_linear_s<Lin10>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 11: return launch_linear_s<Lin11>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 12: return launch_linear_s<Lin12>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 13: return launch_linear_s<Lin13>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 14: return launch_linear_s<Lin14>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 15: return launch_linear_s<Lin15>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 16: return launch_linear_s<Lin16>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 17: return launch_linear_s<Lin17>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 18: return launch_linear_s<Lin18>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 19: return launch_linear_s<Lin19>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 20: return launch_linear_s<Lin20>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 21: return launch_linear_s<Lin21>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 22: return launch_linear_s<Lin22>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 23: return launch_linear_s<Lin23>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 24: return launch_linear_s<Lin24>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 25: return launch_linear_s<Lin25>(x, w, bias, y, M, K, N, out_mode, stream);
-        case 26: return launch_linear_s<Lin26>(x, w, bias, y, M, K, N, out_mode, stream);
-        default: return launch_linear_s<Lin27>(x, w, bias, y, M, K, N, out_mode, stream);
+        default: return launch_linear_s<Lin7>(x, w, bias, y, M, K, N, out_mode, stream);
     }
+}
+
+hipError_t launch_linear_f32(const float* x, const float* w, float* y, int64_t M, int64_t K,
+                             int64_t N, hipStream_t stream) {
+    return launch_linear_t<LinF32, NCM_OUT_F32, false>(x, w, nullptr, y, M, K, N, stream);
 }
 
 }  // namespace ncm

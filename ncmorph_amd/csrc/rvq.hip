@@ -780,11 +780,12 @@ __global__ __launch_bounds__(256) void rvq_fallback_kernel(RowArgs a, FbPart* pa
 
 // ------------------------------------------------------------ host side
 
-// Distance GEMM tiles (codes x rows): 256 x 256 with 8 wavefronts for the
-// large levels, 128 x 128 with 4 for the small ones; both load global ->
-// LDS directly and run two wavefronts per SIMD.
-using DistBig = GemmShape<256, 256, 64, 4, 2, 1, 2, true, 4, true>;
-using DistSmall = GemmShape<128, 128, 64, 2, 2, 1, 2, true, 4, true>;
+// Distance GEMM tiles (codes x rows): 256 x 256 with 8 wavefronts and two
+// LDS stages for the large levels, 128 x 128 with 4 wavefronts and four
+// stages (deeper prefetch for the latency-bound small grids) for the small
+// ones; both load global -> LDS directly and run two wavefronts per SIMD.
+using DistBig = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
+using DistSmall = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
 constexpr int64_t kDistBigRows = 8192;
 
 static int nch_for(int64_t d) {

@@ -1,14 +1,14 @@
 """Mirror of the reference's Zig `kernels` operator surface for the linear.
 
 Host-slice functions keep the reference signatures and argument meaning
-(packages/kernels/root.zig:10-12, :96-104): flat float32 buffers, explicit
+(packages/kernels/root.zig:10-12, :25-65, :96-104): flat float32 buffers, explicit
 dimensions, caller-owned output. Where the reference asserts
 (root.zig:107-110) these raise NcmError. They run on the GPU through the C
 ABI; nothing here computes on the CPU.
 
-`linear_bf16` is the device-resident path: torch tensors already in HBM,
-bf16 operands, fp32 (or bf16) output, stream-ordered on torch's current
-stream.
+`linear_bf16` / `linear_f32` are the device-resident paths: torch tensors
+already in HBM, bf16 (or fp32) operands, fp32 (or bf16) output,
+stream-ordered on torch's current stream.
 """
 from __future__ import annotations
 
@@ -30,6 +30,17 @@ def _host_f32(a, name):
 
 def _p(a):
     return C.c_void_p(a.ctypes.data) if a is not None and a.size else None
+
+
+def matmul(input, weights, output, token_count, input_width, output_width):
+    """kernels.matmul (root.zig:25-65): fp32 output = input * weightsT on the
+    GPU's fp32 MFMA (accumulation order differs from the reference's
+    increasing k; both meet |y - y_f64| <= (K + 1) 2^-24 sum|x w|)."""
+    for a, n in ((input, "input"), (weights, "weights"), (output, "output")):
+        _host_f32(a, n)
+    check(lib().ncm_matmul_f32(_p(input), input.size, _p(weights), weights.size, _p(output),
+                               output.size, token_count, input_width, output_width),
+          "matmul")
 
 
 def matmul_bf16(input, weights, output, token_count, input_width, output_width):
@@ -91,6 +102,24 @@ def linear_bf16(x, w, bias=None, out=None, out_mode: str = "f32", ctx=None):
     check(lib().ncm_linear_bf16(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
                                 _dev_ptr(bias, "bias"), _dev_ptr(out, "out"), m, k, n, mode),
           "linear_bf16")
+    return out
+
+
+def linear_f32(x, w, out=None, ctx=None):
+    """y = x @ w.T with float32 operands [m, k] and [n, k] (k % 4 == 0) on
+    the fp32 MFMA, on torch's current stream."""
+    import torch
+
+    m, k = x.shape
+    n, k2 = w.shape
+    if k != k2:
+        raise NcmError(-2, "linear_f32")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float32, device=x.device)
+    ctx = ctx or default_context(x.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_linear_f32(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"), _dev_ptr(out, "out"),
+                               m, k, n), "linear_f32")
     return out
 
 
