@@ -93,6 +93,70 @@ __device__ __forceinline__ void quad_transpose4(float (&v)[4], int q) {
     if (hi) { v[0] = r0; v[1] = r1; } else { v[2] = r0; v[3] = r1; }
 }
 
+// Wavefront butterfly reductions in VALU (no LDS round trip): permlane32 /
+// permlane16 swaps for the xor-32 and xor-16 stages, DPP for the others.
+// Every stage combines the same two values as v op shfl_xor(v, off) does
+// (after the xor-8 stage the values repeat with period 8 inside each row, so
+// row_ror:4 meets the xor-4 partner's value), so for a commutative op the
+// result has, in every lane, the bits of the xor butterfly with offsets
+// 32, 16, 8, 4, 2, 1.
+__device__ __forceinline__ u32x2_t swap32(uint32_t v) {
+    auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    u32x2_t o; o[0] = r[0]; o[1] = r[1];
+    return o;
+}
+__device__ __forceinline__ u32x2_t swap16(uint32_t v) {
+    auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    u32x2_t o; o[0] = r[0]; o[1] = r[1];
+    return o;
+}
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppRor8 = 0x128, kDppRor4 = 0x124, kDppXor2 = 0x4E, kDppXor1 = 0xB1;
+
+__device__ __forceinline__ float wave_sum_xor(float v) {
+    u32x2_t p = swap32(__float_as_uint(v));
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    p = swap16(__float_as_uint(v));
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    v = v + __uint_as_float(dpp_u32<kDppRor8>(__float_as_uint(v)));
+    v = v + __uint_as_float(dpp_u32<kDppRor4>(__float_as_uint(v)));
+    v = v + __uint_as_float(dpp_u32<kDppXor2>(__float_as_uint(v)));
+    v = v + __uint_as_float(dpp_u32<kDppXor1>(__float_as_uint(v)));
+    return v;
+}
+
+__device__ __forceinline__ uint32_t wave_min_xor(uint32_t v) {
+    u32x2_t p = swap32(v);
+    v = min(p[0], p[1]);
+    p = swap16(v);
+    v = min(p[0], p[1]);
+    v = min(v, dpp_u32<kDppRor8>(v));
+    v = min(v, dpp_u32<kDppRor4>(v));
+    v = min(v, dpp_u32<kDppXor2>(v));
+    v = min(v, dpp_u32<kDppXor1>(v));
+    return v;
+}
+
+__device__ __forceinline__ double wave_sum_xor_d(double v) {
+    auto join = [](uint32_t lo, uint32_t hi) {
+        return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+    };
+    auto lo = [](double x) { return (uint32_t)__double_as_longlong(x); };
+    auto hi = [](double x) { return (uint32_t)((uint64_t)__double_as_longlong(x) >> 32); };
+    u32x2_t pl = swap32(lo(v)), ph = swap32(hi(v));
+    v = join(pl[0], ph[0]) + join(pl[1], ph[1]);
+    pl = swap16(lo(v)); ph = swap16(hi(v));
+    v = join(pl[0], ph[0]) + join(pl[1], ph[1]);
+    v = v + join(dpp_u32<kDppRor8>(lo(v)), dpp_u32<kDppRor8>(hi(v)));
+    v = v + join(dpp_u32<kDppRor4>(lo(v)), dpp_u32<kDppRor4>(hi(v)));
+    v = v + join(dpp_u32<kDppXor2>(lo(v)), dpp_u32<kDppXor2>(hi(v)));
+    v = v + join(dpp_u32<kDppXor1>(lo(v)), dpp_u32<kDppXor1>(hi(v)));
+    return v;
+}
+
 // Remap a linear workgroup id so that consecutive logical tiles land on the
 // same XCD (workgroups are dispatched round-robin over the 8 XCDs).
 __device__ __forceinline__ int xcd_remap(int bid, int nblk) {

@@ -50,6 +50,7 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
         // Whole tile in range: transpose each 4-row group of the D fragment
         // inside lane quads so that every lane stores 4 consecutive columns
         // of one row (16-byte stores; 8 lanes cover 128 contiguous bytes).
+        // The output is not read again by this kernel: non-temporal stores.
         const int q = lane & 3;
         const int col4 = (lane & 31) & ~3;
         const int hrow = 4 * (lane >> 5) + q;
@@ -73,7 +74,7 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
                     if (OUT_MODE == NCM_OUT_F32) {
                         f32x4_t o;
                         o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; o[3] = v[3];
-                        *(f32x4_t*)((float*)y + m * N + ncol) = o;
+                        __builtin_nontemporal_store(o, (f32x4_t*)((float*)y + m * N + ncol));
                     } else {
                         uint32_t b[4];
 #pragma unroll
@@ -81,12 +82,12 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
                         if (OUT_MODE == NCM_OUT_BF16_F32) {
                             u32x4_t o;
                             o[0] = b[0] << 16; o[1] = b[1] << 16; o[2] = b[2] << 16; o[3] = b[3] << 16;
-                            *(u32x4_t*)((float*)y + m * N + ncol) = o;
+                            __builtin_nontemporal_store(o, (u32x4_t*)((float*)y + m * N + ncol));
                         } else {
                             u32x2_t o;
                             o[0] = b[0] | (b[1] << 16);
                             o[1] = b[2] | (b[3] << 16);
-                            *(u32x2_t*)((uint16_t*)y + m * N + ncol) = o;
+                            __builtin_nontemporal_store(o, (u32x2_t*)((uint16_t*)y + m * N + ncol));
                         }
                     }
                 }

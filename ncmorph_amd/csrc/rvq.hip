@@ -38,23 +38,11 @@ struct RowVec {
     float v[NCH][4];
 };
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = v + __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, off, 64));
-    return v;
-}
+// Xor-butterfly reductions (offsets 32, 16, 8, 4, 2, 1; same bits in every
+// lane), done in VALU.
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_xor(v); }
+__device__ __forceinline__ double wave_sum_d(double v) { return wave_sum_xor_d(v); }
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) { return wave_min_xor(v); }
 
 // Makes this wavefront's LDS writes visible to its own later LDS reads by
 // other lanes: the writes complete (lgkmcnt(0)) and the compiler may not
@@ -506,11 +494,7 @@ __device__ __forceinline__ void dotn_fixed(const RowVec<NCH>& u,
         }
     }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-        for (int j = 0; j < kDotBatch; ++j) acc[j] = acc[j] + __shfl_xor(acc[j], off, 64);
-#pragma unroll
-    for (int j = 0; j < kDotBatch; ++j) out[j] = acc[j];
+    for (int j = 0; j < kDotBatch; ++j) out[j] = wave_sum(acc[j]);
 }
 
 // Exact distances of `n` codes listed in `list` (wave-uniform), folded into b.

@@ -51,9 +51,7 @@ __device__ __forceinline__ float wave_sumsq_bf16(const uint16_t* c, int64_t d, i
             acc = __builtin_fmaf(c3, c3, acc);
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) acc = acc + __shfl_xor(acc, off, 64);
-    return acc;
+    return wave_sum_xor(acc);  // xor butterfly 32, 16, ..., 1
 }
 
 __global__ void rvq_csq_kernel(const uint16_t* __restrict__ cb, int64_t rows, int64_t d,
