@@ -149,8 +149,9 @@ int ncm_rvq_prepare(ncm_ctx_t* ctx, const uint16_t* codebooks, int64_t levels, i
  * teacher forcing; when given, later levels' residuals are built from these
  * codes while `codes` still receives this library's own argmin.
  * Requires d % 64 == 0, v <= 65536. n_flagged (host, nullable) receives the
- * number of rows whose candidate list could not be proven complete and that
- * were searched exhaustively (a synchronizing read). */
+ * number of rows for which some group of codes had more near-best members
+ * than the approximate pass kept, so that every code of the group was
+ * rescored exactly (a synchronizing read). */
 int ncm_rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d,
                    int64_t levels, const int32_t* strides, const uint16_t* codebooks,
                    const float* csq, int64_t v, int32_t* codes, float* recon, float* gap,

@@ -21,9 +21,9 @@
 //   2. rvq_rescore_kernel (one wavefront per row): rebuilds u in fp32, bounds
 //      the MFMA pass's error rigorously, rescores every candidate that could
 //      be the exact argmin in the fixed fp32 order (bit-identical to the
-//      oracle), and writes code, gap and the next level's bf16 rows. A row
-//      whose candidate list cannot be proven complete is queued instead.
-//   3. rvq_fallback_kernel: exhaustive exact search for queued rows.
+//      oracle), and writes code, gap and the next level's bf16 rows. A lane
+//      chunk whose kept keys cannot be proven to cover every code under the
+//      threshold has all of its codes rescored.
 #include <algorithm>
 
 #include "gemm_core.h"
@@ -404,7 +404,7 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void rvq_dist_kernel(DistAr
 constexpr int kKeySlots = 8;
 constexpr int kMaxChunks = kKeySlots * 64 / 4;
 
-// Per-level arguments of the row kernels (rescore and fallback).
+// Per-level arguments of the rescore kernel.
 struct RowArgs {
     RvqGeom g;
     const float* x;
@@ -423,8 +423,6 @@ struct RowArgs {
     float* rowc_out;             // level l+1 offsets
     float* recon;                // last level only, nullable
     int32_t* flag_count;         // this level's counter
-    int32_t* flag_rows;
-    int32_t* fb_done;
     int level;
     int64_t n_rows;
     int64_t d_div;               // level-l rows per D_l row (s_{l-1} / s_l)
@@ -607,6 +605,7 @@ __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const 
 template <int NCH>
 __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     __shared__ int32_t cand_list[4][kKeySlots * 64];
+    __shared__ int32_t inc_list[4][kMaxChunks];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -652,114 +651,72 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     const float tau = 2e-5f * (st.unorm * st.unorm + fabsf(m_f - rowc) + 2.0f * E);
     const float thr = (m_f * (1.0f + eps_q) + 2.0f * E + tau) * (1.0f + 0x1p-20f);
 
-    // Incomplete chunk: its fourth key is still under the threshold.
-    bool incomplete = false;
-    int nsel = 0;
+    // Candidates: keys under the threshold. A chunk whose fourth (largest
+    // kept) key is under the threshold may hold more codes under it than it
+    // kept ("incomplete"): all of its codes are rescored instead of its
+    // keys. The four keys of a chunk sit in one lane quad of one slot.
     int32_t* list = cand_list[wave];
+    int32_t* inc = inc_list[wave];
+    int nsel = 0, ninc = 0;
 #pragma unroll
     for (int s = 0; s < kKeySlots; ++s) {
         const int idx = lane + 64 * s;
         const bool valid = idx < nk && key[s] != 0xFFFFFFFFu;
         const bool under = valid && __uint_as_float(key[s] & ~imask) <= thr;
-        if (under && (idx & 3) == 3) incomplete = true;
-        const uint64_t mask = __ballot(under);
-        if (under) {
+        const bool head = under && (idx & 3) == 3;
+        const bool chunk_inc =
+            __builtin_amdgcn_update_dpp(0, head ? 1 : 0, 0xFF, 0xF, 0xF, false) != 0;  // quad lane 3
+        const bool take = under && !chunk_inc;
+        const uint64_t mask = __ballot(take);
+        if (take) {
             const int pos = nsel + __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32),
                                                               __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0));
             list[pos] = (int32_t)decode_code(a.cg, idx >> 2, key[s] & imask);
         }
         nsel += __popcll(mask);
-    }
-    if (__ballot(incomplete) != 0) {
-        if (lane == 0) {
-            const int f = atomicAdd(a.flag_count, 1);
-            a.flag_rows[f] = (int32_t)row;
-            a.fb_done[f] = 0;
+        const uint64_t hmask = __ballot(head);
+        if (head) {
+            const int pos = ninc + __builtin_amdgcn_mbcnt_hi((uint32_t)(hmask >> 32),
+                                                              __builtin_amdgcn_mbcnt_lo((uint32_t)hmask, 0));
+            inc[pos] = idx >> 2;
         }
-        return;
+        ninc += __popcll(hmask);
     }
     wave_lds_sync();
 
+    const uint16_t* cbl = a.cb + (int64_t)l * g.v * d;
+    const float* csql = a.csq + (int64_t)l * g.v;
     Best b{INFINITY, INFINITY, 0x7FFFFFFF};
-    score_list<NCH>(u, a.cb + (int64_t)l * g.v * d, a.csq + (int64_t)l * g.v, list, nsel, d, lane,
-                    b);
-    finish_row<NCH>(a, row, b, st.unorm2, lane);
-}
-
-// -------------------------------------------------------- fallback kernel
-
-struct FbPart {
-    float best, second;
-    int32_t code, pad;
-};
-
-constexpr int kFbChunk = 64;  // codes per fallback work item
-
-// Exhaustive exact search for queued rows: work item = (queued row, chunk of
-// 64 codes, 16 per wavefront in batches of four); the block that completes a
-// row's last chunk merges the chunk results and finishes the row.
-template <int NCH>
-__global__ __launch_bounds__(256) void rvq_fallback_kernel(RowArgs a, FbPart* part, int nvch) {
-    __shared__ int32_t codes_l[4][16];
-    __shared__ Best wb[4];
-    __shared__ int last;
-    const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
-    const int count = *a.flag_count;
-    const int64_t items = (int64_t)count * nvch;
-    const RvqGeom& g = a.g;
-    const int64_t d = g.d;
-    const uint16_t* cbl = a.cb + (int64_t)a.level * g.v * d;
-    const float* csql = a.csq + (int64_t)a.level * g.v;
-    for (int64_t item = blockIdx.x; item < items; item += gridDim.x) {
-        const int f = (int)(item / nvch);
-        const int ch = (int)(item % nvch);
-        const int64_t row = a.flag_rows[f];
-        RowVec<NCH> u;
-        load_residual<NCH>(a, row, lane, u);
-        const int64_t c0 = (int64_t)ch * kFbChunk + wave * 16;
-        const int n = (int)max<int64_t>(0, min<int64_t>(16, g.v - c0));
-        if (lane < 16) codes_l[wave][lane] = (int32_t)(c0 + lane);
-        wave_lds_sync();
-        Best b{INFINITY, INFINITY, 0x7FFFFFFF};
-        score_list<NCH>(u, cbl, csql, codes_l[wave], n, d, lane, b);
-        if (lane == 0) wb[wave] = b;
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            Best m = wb[0];
-            for (int w = 1; w < 4; ++w) {
-                if (wb[w].best < INFINITY) {
-                    best_update(m, wb[w].best, wb[w].code);
-                    if (wb[w].second < m.second) m.second = wb[w].second;
+    score_list<NCH>(u, cbl, csql, list, nsel, d, lane, b);
+    if (ninc > 0) {
+        if (lane == 0) atomicAdd(a.flag_count, 1);
+        // Every code of each incomplete chunk, listed in LDS then rescored.
+        const int nloc = a.cg.ntv * a.cg.mb * 16;
+        for (int c = 0; c < ninc; ++c) {
+            const int chunk = inc[c];
+            for (int base = 0; base < nloc; base += kKeySlots * 64) {
+                wave_lds_sync();  // the previous list has been read
+                int n = 0;
+                for (int off = 0; off < kKeySlots * 64 && base + off < nloc; off += 64) {
+                    const int local = base + off + lane;
+                    const int64_t code =
+                        local < nloc ? decode_code(a.cg, chunk, (uint32_t)local) : g.v;
+                    const bool ok = code < g.v;
+                    const uint64_t m = __ballot(ok);
+                    if (ok) {
+                        const int pos = n + __builtin_amdgcn_mbcnt_hi(
+                                                (uint32_t)(m >> 32),
+                                                __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+                        list[pos] = (int32_t)code;
+                    }
+                    n += __popcll(m);
                 }
+                wave_lds_sync();
+                score_list<NCH>(u, cbl, csql, list, n, d, lane, b);
             }
-            FbPart p{m.best, m.second, m.code, 0};
-            part[(int64_t)f * nvch + ch] = p;
-            __threadfence();
-            last = atomicAdd(&a.fb_done[f], 1) == nvch - 1;
         }
-        __syncthreads();
-        if (last && wave == 0) {
-            __threadfence();
-            Best m{INFINITY, INFINITY, 0x7FFFFFFF};
-            for (int c = 0; c < nvch; ++c) {
-                const FbPart* pp = part + (int64_t)f * nvch + c;
-                const float pb = __hip_atomic_load(&pp->best, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-                const float ps = __hip_atomic_load(&pp->second, __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT);
-                const int32_t pc = __hip_atomic_load(&pp->code, __ATOMIC_RELAXED,
-                                                     __HIP_MEMORY_SCOPE_AGENT);
-                if (pb < INFINITY) {
-                    best_update(m, pb, pc);
-                    if (ps < m.second) m.second = ps;
-                }
-            }
-            const RowStats st = write_bf16_row<NCH>(u, d, lane, nullptr);
-            finish_row<NCH>(a, row, m, st.unorm2, lane);
-        }
-        __syncthreads();
     }
+    finish_row<NCH>(a, row, b, st.unorm2, lane);
 }
 
 // ------------------------------------------------------------ host side
@@ -782,27 +739,25 @@ static int nch_for(int64_t d) {
 }
 
 template <int NCH>
-static hipError_t launch_row_kernels(int which, const PrepArgs* pa, const RowArgs* ra,
-                                     FbPart* part, int nvch, int64_t rows, hipStream_t st) {
+static hipError_t launch_row_kernels(const PrepArgs* pa, const RowArgs* ra, int64_t rows,
+                                     hipStream_t st) {
     const dim3 grid((unsigned)((rows + 3) / 4));
-    if (which == 0)
+    if (pa)
         hipLaunchKernelGGL(rvq_prep_kernel<NCH>, grid, dim3(256), 0, st, *pa);
-    else if (which == 1)
-        hipLaunchKernelGGL(rvq_rescore_kernel<NCH>, grid, dim3(256), 0, st, *ra);
     else
-        hipLaunchKernelGGL(rvq_fallback_kernel<NCH>, dim3(512), dim3(256), 0, st, *ra, part,
-                           nvch);
+        hipLaunchKernelGGL(rvq_rescore_kernel<NCH>, grid, dim3(256), 0, st, *ra);
     return hipGetLastError();
 }
 
-static hipError_t launch_rows(int nch, int which, const PrepArgs* pa, const RowArgs* ra,
-                              FbPart* part, int nvch, int64_t rows, hipStream_t st) {
+// Level-0 prep (pa) or a level's rescore (ra).
+static hipError_t launch_rows(int nch, const PrepArgs* pa, const RowArgs* ra, int64_t rows,
+                              hipStream_t st) {
     switch (nch) {
-        case 1: return launch_row_kernels<1>(which, pa, ra, part, nvch, rows, st);
-        case 2: return launch_row_kernels<2>(which, pa, ra, part, nvch, rows, st);
-        case 4: return launch_row_kernels<4>(which, pa, ra, part, nvch, rows, st);
-        case 8: return launch_row_kernels<8>(which, pa, ra, part, nvch, rows, st);
-        default: return launch_row_kernels<16>(which, pa, ra, part, nvch, rows, st);
+        case 1: return launch_row_kernels<1>(pa, ra, rows, st);
+        case 2: return launch_row_kernels<2>(pa, ra, rows, st);
+        case 4: return launch_row_kernels<4>(pa, ra, rows, st);
+        case 8: return launch_row_kernels<8>(pa, ra, rows, st);
+        default: return launch_row_kernels<16>(pa, ra, rows, st);
     }
 }
 
@@ -879,7 +834,6 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         max_rows = std::max(max_rows, n);
         max_cand = std::max(max_cand, n * (int64_t)cand_geom(n, v).nchunk * 4);
     }
-    const int nvch = (int)((v + kFbChunk - 1) / kFbChunk);
     const size_t o_pyr = carve((size_t)pyr_floats * 4);
     const size_t o_u = carve((size_t)max_rows * d * 2);
     // Level l (l + 1 < levels) writes D_{l+1} to dbuf[(l + 1) & 1]: dbuf[1]
@@ -891,9 +845,6 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
     const size_t o_cand = carve((size_t)max_cand * 4);
     const size_t o_cmax = carve((size_t)levels * 4);
     const size_t o_fc = carve((size_t)levels * 4);
-    const size_t o_fr = carve((size_t)max_rows * 4);
-    const size_t o_fd = carve((size_t)max_rows * 4);
-    const size_t o_fp = carve((size_t)max_rows * nvch * sizeof(FbPart));
     void* ws = nullptr;
     int rc = ncm_ctx_workspace(ctx, off, &ws);
     if (rc) return rc;
@@ -904,9 +855,6 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
     uint32_t* cand = (uint32_t*)(W + o_cand);
     float* cmax = (float*)(W + o_cmax);
     int32_t* fcount = (int32_t*)(W + o_fc);
-    int32_t* frows = (int32_t*)(W + o_fr);
-    int32_t* fdone = (int32_t*)(W + o_fd);
-    FbPart* fpart = (FbPart*)(W + o_fp);
     // D_{l+1} (coarse reconstruction) is written by level l into dbuf[(l+1)&1].
     float* dbuf[2] = {(float*)(W + o_d0), (float*)(W + o_d1)};
 
@@ -946,7 +894,7 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         pa.g = g; pa.x = x; pa.pyr = pyr; pa.cb = codebooks; pa.resid_codes = codes;
         pa.cmax = cmax; pa.ubuf = ubuf; pa.rowc = rowc[0]; pa.level = 0;
         pa.n_rows = b * (t / strides[0]);
-        e = launch_rows(nch, 0, &pa, nullptr, nullptr, 0, pa.n_rows, st);
+        e = launch_rows(nch, &pa, nullptr, pa.n_rows, st);
         if (e != hipSuccess) return NCM_E_HIP;
     }
 
@@ -973,11 +921,9 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         ra.d_div = l > 0 ? strides[l - 1] / strides[l] : 1;
         ra.ubuf = ubuf; ra.rowc_out = rowc[(l + 1) & 1];
         ra.recon = l + 1 == levels ? recon : nullptr;
-        ra.flag_count = fcount + l; ra.flag_rows = frows; ra.fb_done = fdone;
+        ra.flag_count = fcount + l;
         ra.level = (int)l; ra.n_rows = n; ra.cg = cg;
-        e = launch_rows(nch, 1, nullptr, &ra, nullptr, nvch, n, st);
-        if (e != hipSuccess) return NCM_E_HIP;
-        e = launch_rows(nch, 2, nullptr, &ra, fpart, nvch, n, st);
+        e = launch_rows(nch, nullptr, &ra, n, st);
         if (e != hipSuccess) return NCM_E_HIP;
     }
 

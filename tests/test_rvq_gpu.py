@@ -81,8 +81,9 @@ def test_multiscale_matches_oracle(ncm, oracle, cuda, case):
 
 
 def test_duplicate_codewords_take_lowest_index(ncm, oracle, cuda):
-    # Identical codewords tie exactly; the flagged / exhaustive path must
-    # still return the lowest index, as the oracle does.
+    # Identical codewords tie exactly; the flagged path (every code of an
+    # incomplete group rescored) must still return the lowest index, as the
+    # oracle does.
     rng = np.random.default_rng(31)
     d, V = 256, 300
     x, cb = synth.rvq_inputs(31, 1, 64, d, 2, V)
@@ -96,7 +97,7 @@ def test_duplicate_codewords_take_lowest_index(ncm, oracle, cuda):
     assert r["n_flagged"] >= 1
 
 
-def test_all_equal_codebook_uses_fallback(ncm, oracle, cuda):
+def test_all_equal_codebook_rescores_every_code(ncm, oracle, cuda):
     d, V = 128, 600
     x, cb = synth.rvq_inputs(32, 1, 16, d, 1, V)
     cb[0, :] = cb[0, 0]
