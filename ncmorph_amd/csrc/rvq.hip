@@ -721,13 +721,18 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
 
 // ------------------------------------------------------------ host side
 
-// Distance GEMM tiles (codes x rows): 256 x 256 with 8 wavefronts and two
-// LDS stages for the large levels, 128 x 128 with 4 wavefronts and four
-// stages (deeper prefetch for the latency-bound small grids) for the small
-// ones; both load global -> LDS directly and run two wavefronts per SIMD.
+// Distance GEMM tiles (codes x rows), all loading global -> LDS directly
+// with two wavefronts per SIMD:
+//   DistBig    256 x 256, 8 wavefronts, 2 LDS stages: when it gives at least
+//              one workgroup per CU;
+//   DistSmall  128 x 128, 4 wavefronts, 4 stages (deeper prefetch for the
+//              latency-bound small grids): at most one workgroup per CU;
+//   DistSmall2 128 x 128, 2 stages (64 KB: two workgroups per CU) between.
+// DistSmall and DistSmall2 share the candidate layout.
 using DistBig = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
 using DistSmall = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
-constexpr int64_t kDistBigRows = 8192;
+using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 2>;
+constexpr int64_t kCus = 256;
 
 static int nch_for(int64_t d) {
     const int64_t n = (d + 255) / 256;
@@ -784,9 +789,22 @@ static CandGeom cand_geom_t(int64_t n_rows, int64_t v) {
     return cg;
 }
 
+enum DistKind { kDistBig, kDistSmall, kDistSmall2 };
+
+static int64_t dist_grid(const CandGeom& cg, int64_t n_rows, int64_t bn) {
+    return (n_rows + bn - 1) / bn * cg.nranges;
+}
+
+static DistKind dist_kind(int64_t n_rows, int64_t v) {
+    if (dist_grid(cand_geom_t<DistBig>(n_rows, v), n_rows, DistBig::BN) >= kCus) return kDistBig;
+    if (dist_grid(cand_geom_t<DistSmall>(n_rows, v), n_rows, DistSmall::BN) <= kCus)
+        return kDistSmall;
+    return kDistSmall2;
+}
+
 static CandGeom cand_geom(int64_t n_rows, int64_t v) {
-    return n_rows >= kDistBigRows ? cand_geom_t<DistBig>(n_rows, v)
-                                  : cand_geom_t<DistSmall>(n_rows, v);
+    return dist_kind(n_rows, v) == kDistBig ? cand_geom_t<DistBig>(n_rows, v)
+                                            : cand_geom_t<DistSmall>(n_rows, v);
 }
 
 template <class S>
@@ -909,7 +927,11 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         da.cand = cand;
         da.n_rows = n; da.v = v; da.d = d;
         da.cg = cg;
-        e = n >= kDistBigRows ? launch_dist<DistBig>(da, st) : launch_dist<DistSmall>(da, st);
+        switch (dist_kind(n, v)) {
+            case kDistBig: e = launch_dist<DistBig>(da, st); break;
+            case kDistSmall: e = launch_dist<DistSmall>(da, st); break;
+            default: e = launch_dist<DistSmall2>(da, st); break;
+        }
         if (e != hipSuccess) return NCM_E_HIP;
 
         RowArgs ra{};
