@@ -16,6 +16,7 @@ class Context:
         h = C.c_void_p()
         check(lib().ncm_init(device, C.byref(h)), "ncm_init")
         self.handle = h
+        self._bound = None  # stream handle last passed to ncm_set_stream
 
     def bind_stream(self, stream=None) -> None:
         """Route library work to `stream` (a torch.cuda.Stream) or to torch's
@@ -24,8 +25,10 @@ class Context:
 
         if stream is None:
             stream = torch.cuda.current_stream(self.device)
-        check(lib().ncm_set_stream(self.handle, C.c_void_p(stream.cuda_stream)),
-              "ncm_set_stream")
+        h = stream.cuda_stream
+        if h != self._bound:
+            check(lib().ncm_set_stream(self.handle, C.c_void_p(h)), "ncm_set_stream")
+            self._bound = h
 
     def synchronize(self) -> None:
         check(lib().ncm_synchronize(self.handle), "ncm_synchronize")
