@@ -4,11 +4,11 @@
 // Computes acc += A_tile * B_tile^T where both operands are row-major with
 // the reduction dimension contiguous ("NT"): A rows are the M dimension,
 // B rows the N dimension. A K tile is RB = BK * element-size bytes per row
-// (64 or 128). Each 16-byte chunk c of LDS row r is stored at chunk slot
-// c ^ ((r / 2) % 8) (RB = 128) or c ^ ((r / 4) % 4) (RB = 64): a 16-lane
-// phase of a ds_read_b128 covers 16 consecutive rows at one K offset, and
-// this gives those 16 rows 16 distinct 16-byte bank groups of the 64-bank
-// LDS.
+// (64, 128 or 256). Each 16-byte chunk c of LDS row r is stored at chunk
+// slot c ^ (r % 16) (RB = 256), c ^ ((r / 2) % 8) (RB = 128) or
+// c ^ ((r / 4) % 4) (RB = 64): a 16-lane phase of a ds_read_b128 covers 16
+// consecutive rows at one K offset, and this gives those 16 rows 16 distinct
+// 16-byte bank groups of the 64-bank LDS.
 //
 // A k-step consumes two 16-byte chunks of every row: lanes 0-31 read chunk
 // 2 kk, lanes 32-63 chunk 2 kk + 1, of row (lane % 32) of a 32-row block.
@@ -39,25 +39,32 @@ namespace ncm {
 //      wavefront of each per SIMD) that run half a K tile apart. Between
 //      two barriers one group issues all MFMAs of a tile from registers
 //      while the other reads the next tile's fragments from LDS and issues
-//      its share of the direct-to-LDS loads.
+//      its share of the direct-to-LDS loads;
+//   7  (DMA, KG = 2, NST even >= 4) K groups: two groups of WGM x WGN
+//      wavefronts (one wavefront of each per SIMD) each accumulate the whole
+//      output tile over alternate K tiles (group g takes tiles 2i + g) from
+//      one shared pipeline, NST / 2 - 1 tile pairs ahead; at the end group 1
+//      hands its accumulators to group 0 through LDS and group 0 holds
+//      acc(group 0) + acc(group 1).
 // DMA: global -> LDS directly (buffer_load ... lds), no staging registers
 // and no ds_write instructions; this path waits for its own loads (vmcnt)
 // explicitly at each barrier. Without DMA, one K tile is staged through
 // registers while the previous one feeds the MFMAs.
 // NST: LDS stages of the DMA path; K tiles up to NST - 1 ahead are in flight.
-// F32: fp32 operands (else bf16).
+// F32: fp32 operands (else bf16). KG: K groups (SCHED 7).
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int OCC_, int SCHED_, bool DMA_,
-          int NST_ = 2, bool F32_ = false>
+          int NST_ = 2, bool F32_ = false, int KG_ = 1>
 struct GemmShape {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_;
-    static constexpr int OCC = OCC_, SCHED = SCHED_, NST = NST_;
+    static constexpr int OCC = OCC_, SCHED = SCHED_, NST = NST_, KG = KG_;
     static constexpr bool DMA = DMA_, F32 = F32_;
     static constexpr bool FDB = SCHED >= 4;
     static constexpr int ESZ = F32 ? 4 : 2;
     static constexpr int EPC = 16 / ESZ;  // elements per 16-byte chunk
     static constexpr int RB = BK * ESZ;   // bytes per tile row
-    static constexpr int NT = kWave * WGM * WGN;
-    static constexpr int NW = WGM * WGN;
+    static constexpr int NT = kWave * WGM * WGN * KG;
+    static constexpr int NW = WGM * WGN * KG;
+    static constexpr int NWG = WGM * WGN;  // wavefronts per K group
     static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int MB = WM / 32, NB = WN / 32;
     static constexpr int CH = RB / 16;
@@ -69,21 +76,24 @@ struct GemmShape {
     static constexpr int LDS_B = BN * RB;
     static constexpr int LDS_STAGE = LDS_A + LDS_B;
     static constexpr int LDS_BYTES = NST * LDS_STAGE;
-    // Rows sharing a swizzle pattern: 2 for 128-byte rows, 4 for 64-byte rows.
-    static constexpr int SWZ_SHIFT = RB == 128 ? 1 : 2;
+    // Rows sharing a swizzle pattern: 1, 2 or 4 for 256-, 128- or 64-byte rows.
+    static constexpr int SWZ_SHIFT = RB == 256 ? 0 : (RB == 128 ? 1 : 2);
     // Direct-to-LDS: one wave instruction fills 1 KB = RPI rows.
     static constexpr int RPI = 1024 / RB;
     static constexpr int A_DMA = BM / (NW * RPI);
     static constexpr int B_DMA = BN / (NW * RPI);
     static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tile must be 32-aligned");
-    static_assert(RB == 64 || RB == 128, "a K tile row is 64 or 128 bytes");
+    static_assert(RB == 64 || RB == 128 || RB == 256, "a K tile row is 64, 128 or 256 bytes");
     static_assert(NT % CH == 0 && BM % RPP == 0 && BN % RPP == 0, "loader shape");
     static_assert(RPP % (CH << SWZ_SHIFT) == 0, "swizzle must not depend on the pass");
-    static_assert(SCHED == 0 || SCHED == 4 || SCHED == 5 || SCHED == 6, "schedule");
-    static_assert(DMA || SCHED <= 4, "SCHED 5 and 6 need direct-to-LDS loads");
+    static_assert(SCHED == 0 || SCHED == 4 || SCHED == 5 || SCHED == 6 || SCHED == 7,
+                  "schedule");
+    static_assert((KG == 2) == (SCHED == 7), "K groups go with SCHED 7");
+    static_assert(SCHED != 7 || (NST % 2 == 0 && NST >= 4), "SCHED 7 stages come in pairs");
+    static_assert(DMA || SCHED <= 4, "SCHED 5, 6 and 7 need direct-to-LDS loads");
     static_assert(!DMA || SCHED >= 4, "direct-to-LDS loads need fragment double buffering");
     static_assert(!DMA || (BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0), "DMA loader shape");
-    static_assert(NST == 2 || SCHED >= 5, "more than two stages: SCHED 5 or 6 only");
+    static_assert(NST == 2 || SCHED >= 5, "more than two stages: SCHED 5, 6 or 7 only");
     static_assert(SCHED != 6 || (NST >= 3 && NW % 2 == 0), "ping-pong layout");
     static_assert(SCHED != 5 || KSTEPS % 2 == 0, "SCHED 5 splits the last k-step pair");
     static_assert(NST >= 2 && (NST - 2) * (A_DMA + B_DMA) <= 63, "vmcnt range");
@@ -142,8 +152,9 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wm = wave % S::WGM;
-    const int wn = wave / S::WGM;
+    const int wl = wave % S::NWG;  // wavefront inside its K group
+    const int wm = wl % S::WGM;
+    const int wn = wl / S::WGM;
 
     const __amdgpu_buffer_rsrc_t rsa = make_rsrc(A, a_bytes);
     const __amdgpu_buffer_rsrc_t rsb = make_rsrc(B, b_bytes);
@@ -187,9 +198,9 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
             } else {
                 fload(0, base, kk);
             }
-            if (S::SCHED == 4) __builtin_amdgcn_sched_barrier(0);
+            if (S::SCHED == 4 || S::SCHED == 7) __builtin_amdgcn_sched_barrier(0);
             mfma_range(fs, 0, NMF);
-            if (S::SCHED == 4) __builtin_amdgcn_sched_barrier(0);
+            if (S::SCHED == 4 || S::SCHED == 7) __builtin_amdgcn_sched_barrier(0);
         }
     };
 
@@ -316,6 +327,55 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
             wait_barrier<VM>();
         }
         if (group == 0) wait_barrier<VM>();
+    } else if constexpr (S::SCHED == 7) {
+        // Pair i = tiles 2i (group 0) and 2i + 1 (group 1) in stages 2i % NST
+        // and (2i + 1) % NST. Iteration i loads pair i + PA into the stages of
+        // pair i - 1; its closing barrier sees pair i + 1 landed.
+        constexpr int PA = S::NST / 2 - 1;
+        constexpr int VMP = (PA - 1) * 2 * (S::A_DMA + S::B_DMA);
+        const int group = wave / S::NWG;
+        const int NP = (KT + 1) / 2;
+#pragma unroll
+        for (int p = 0; p < PA; ++p) {
+            dma(2 * p, (int64_t)(2 * p) * S::BK);
+            dma(2 * p + 1, (int64_t)(2 * p + 1) * S::BK);
+        }
+        wait_barrier<VMP>();
+        for (int i = 0; i < NP; ++i) {
+            const int sp = (2 * (i + PA)) % S::NST;
+            dma(sp, (int64_t)(2 * (i + PA)) * S::BK);
+            dma(sp + 1, (int64_t)(2 * (i + PA) + 1) * S::BK);
+            compute((2 * i + group) % S::NST);
+            wait_barrier<VMP>();
+        }
+        // Every load has landed and every fragment read is done; the stages
+        // now carry group 1's accumulators to group 0 (vector j of lane l of
+        // wavefront wl at ((wl * NV + j) * 64 + l) * 16 bytes).
+        constexpr int NV = S::MB * S::NB * 4;
+        static_assert(S::NWG * NV * 64 * 16 <= S::LDS_BYTES, "reduction fits the stages");
+        wait_barrier<0>();
+        f32x4_t* red = (f32x4_t*)lds + (wl * NV) * 64 + lane;
+        if (group == 1) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                f32x4_t v;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) v[e] = acc.v[j / 4 / S::NB][(j / 4) % S::NB][(j % 4) * 4 + e];
+                red[j * 64] = v;
+            }
+        }
+        wait_barrier<0>();
+        if (group == 0) {
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                const f32x4_t v = red[j * 64];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    acc.v[j / 4 / S::NB][(j / 4) % S::NB][(j % 4) * 4 + e] =
+                        acc.v[j / 4 / S::NB][(j / 4) % S::NB][(j % 4) * 4 + e] + v[e];
+            }
+        }
+        return;
     } else if (S::SCHED == 5) {
         // Tile kt + NST - 1 goes to the stage tile kt - 1 used; the barrier
         // in the middle of tile kt's last k-step sees tile kt + 1 landed

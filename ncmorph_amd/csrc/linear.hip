@@ -44,6 +44,7 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
+    if (wave >= S::NWG) return;  // K group 1: its sums were handed to group 0
     const int wm = wave % S::WGM;
     const int wn = wave / S::WGM;
     if (m0 + S::BM <= M && n0 + S::BN <= N && (N & 3) == 0 && ((uintptr_t)y & 15) == 0) {
@@ -173,6 +174,10 @@ static hipError_t launch_linear_s(const uint16_t* x, const uint16_t* w, const ui
 //  5: 256x128x64, 8 waves (64x64), DMA, SCHED 5, 3 LDS stages
 //  6: 256x256x64, 8 waves, register-staged loads, fences
 //  7: 128x128x64, 4 waves, register-staged loads, fences
+//  8: 128x128x32, two K groups of 4 waves (SCHED 7: 8 waves, two per SIMD,
+//     alternate K tiles from 8 LDS stages, summed through LDS at the end)
+//  9: as 8 with 128x128x64 tiles and 4 LDS stages
+// 10: 128x128x128 (256-byte rows), 4 waves, DMA, SCHED 5, 2 stages
 using Lin0 = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
 using Lin1 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
 using Lin2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
@@ -181,7 +186,10 @@ using Lin4 = GemmShape<256, 256, 64, 2, 2, 1, 5, true>;
 using Lin5 = GemmShape<256, 128, 64, 4, 2, 2, 5, true, 3>;
 using Lin6 = GemmShape<256, 256, 64, 4, 2, 2, 4, false>;
 using Lin7 = GemmShape<128, 128, 64, 2, 2, 2, 4, false>;
-constexpr int kLinConfigs = 8;
+using Lin8 = GemmShape<128, 128, 32, 2, 2, 2, 7, true, 8, false, 2>;
+using Lin9 = GemmShape<128, 128, 64, 2, 2, 2, 7, true, 4, false, 2>;
+using Lin10 = GemmShape<128, 128, 128, 2, 2, 2, 5, true, 2>;
+constexpr int kLinConfigs = 11;
 
 // fp32 linear: 128x128x32 (128-byte rows), 4 waves, DMA, SCHED 5, two
 // stages (64 KB: two workgroups per CU). The fp32 MFMA has 1/16 of the bf16
@@ -218,7 +226,10 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
         case 4: return launch_linear_s<Lin4>(x, w, bias, y, M, K, N, out_mode, stream);
         case 5: return launch_linear_s<Lin5>(x, w, bias, y, M, K, N, out_mode, stream);
         case 6: return launch_linear_s<Lin6>(x, w, bias, y, M, K, N, out_mode, stream);
-        default: return launch_linear_s<Lin7>(x, w, bias, y, M, K, N, out_mode, stream);
+        case 7: return launch_linear_s<Lin7>(x, w, bias, y, M, K, N, out_mode, stream);
+        case 8: return launch_linear_s<Lin8>(x, w, bias, y, M, K, N, out_mode, stream);
+        case 9: return launch_linear_s<Lin9>(x, w, bias, y, M, K, N, out_mode, stream);
+        default: return launch_linear_s<Lin10>(x, w, bias, y, M, K, N, out_mode, stream);
     }
 }
 

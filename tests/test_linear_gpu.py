@@ -143,3 +143,35 @@ def test_linear_zero_k_and_empty(ncm, cuda):
     x = torch.zeros((0, 8), dtype=torch.bfloat16, device=cuda)
     w = torch.zeros((3, 8), dtype=torch.bfloat16, device=cuda)
     assert kernels.linear_bf16(x, w).shape == (0, 3)
+
+
+def test_linear_ragged_long_k_bias_modes_repeatable(ncm, cuda):
+    """Ragged M and N, K not a multiple of the 64-wide K tile (partial last
+    tile), bias, every output mode against the D53 bound and each other, and
+    identical bits over repeated launches."""
+    import torch
+    from ncmorph_amd import kernels
+
+    rng = np.random.default_rng(77)
+    m, k, n = 200, 1096, 300
+    xb = synth.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    wb = synth.bf16_bits((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    bb = synth.bf16_bits(rng.standard_normal(n).astype(np.float32))
+    y32 = _run(xb, wb, cuda, bias_bits=bb)
+    x64 = synth.bf16_to_f32(xb).astype(np.float64)
+    w64 = synth.bf16_to_f32(wb).astype(np.float64)
+    ref = x64 @ w64.T + synth.bf16_to_f32(bb).astype(np.float64)
+    asum = np.abs(x64) @ np.abs(w64).T + np.abs(synth.bf16_to_f32(bb))
+    assert np.all(np.abs(y32 - ref) <= (k + 2) * 2.0**-24 * asum)
+    assert np.array_equal(_run(xb, wb, cuda, bias_bits=bb, out_mode="bf16"), synth.bf16_bits(y32))
+    ybf = _run(xb, wb, cuda, bias_bits=bb, out_mode="bf16_f32")
+    assert np.array_equal(ybf, synth.bf16_to_f32(synth.bf16_bits(y32)))
+    # Repeated launches give identical bits.
+    x = _to_dev(xb, cuda)
+    w = _to_dev(wb, cuda)
+    b = _to_dev(bb, cuda)
+    outs = [kernels.linear_bf16(x, w, bias=b) for _ in range(5)]
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    assert np.array_equal(outs[0].cpu().numpy(), y32)
