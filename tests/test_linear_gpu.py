@@ -175,3 +175,22 @@ def test_linear_ragged_long_k_bias_modes_repeatable(ncm, cuda):
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     assert np.array_equal(outs[0].cpu().numpy(), y32)
+
+
+@pytest.mark.parametrize("m,n,k", [(96, 512, 2048), (64, 128256, 2048)])
+def test_linear_decoder_caller_shapes(ncm, oracle, cuda, m, n, k):
+    """The other shapes the reference's callers pass (decoder.project k/v:
+    out 512; the LM head tied to the 128256-row embedding, decoder.zig:219-227)
+    at a few tokens: partial row tiles, wide grids."""
+    rng = np.random.default_rng(n + m)
+    xb = synth.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    wb = synth.bf16_bits((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    y = _run(xb, wb, cuda)
+    x64 = synth.bf16_to_f32(xb).astype(np.float64)
+    w64 = synth.bf16_to_f32(wb).astype(np.float64)
+    ref = x64 @ w64.T
+    asum = np.abs(x64) @ np.abs(w64).T
+    assert np.all(np.abs(y - ref) <= (k + 1) * 2.0**-24 * asum)
+    for r in (0, m - 1):
+        _, s = oracle.matmul_bf16_u16_rows(xb[r:r + 1], wb, 0, 1)
+        assert np.all(np.abs(y[r] - s[0]) <= ATOL + RTOL * np.abs(s[0]))
