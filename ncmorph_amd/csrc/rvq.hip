@@ -303,6 +303,8 @@ struct CandGeom {
     int nranges;
     int ib;       // index bits
     int nchunk;   // chunks per row = nranges * wgm * 2
+    int mb_log2;  // log2(mb), log2(wgm): both are powers of two
+    int wgm_log2;
 };
 
 struct DistArgs {
@@ -431,11 +433,11 @@ struct RowArgs {
 
 __device__ __forceinline__ int64_t decode_code(const CandGeom& cg, int chunk, uint32_t local) {
     const int half = chunk & 1;
-    const int wm = (chunk >> 1) % cg.wgm;
-    const int range = (chunk >> 1) / cg.wgm;
+    const int wm = (chunk >> 1) & (cg.wgm - 1);
+    const int range = (chunk >> 1) >> cg.wgm_log2;
     const int i = (int)(local & 15u);
-    const int mb = (int)((local >> 4) % (uint32_t)cg.mb);
-    const int tile = (int)((local >> 4) / (uint32_t)cg.mb);
+    const int mb = (int)((local >> 4) & (uint32_t)(cg.mb - 1));
+    const int tile = (int)((local >> 4) >> cg.mb_log2);
     return ((int64_t)range * cg.ntv + tile) * cg.bm + wm * cg.wm_codes + mb * 32 +
            8 * (i >> 2) + 4 * half + (i & 3);
 }
@@ -786,6 +788,10 @@ static CandGeom cand_geom_t(int64_t n_rows, int64_t v) {
     while ((1 << ib) < locals) ++ib;
     cg.ib = ib;
     cg.nchunk = cg.nranges * S::WGM * 2;
+    static_assert((S::MB & (S::MB - 1)) == 0 && (S::WGM & (S::WGM - 1)) == 0,
+                  "candidate decoding shifts by log2(MB) and log2(WGM)");
+    cg.mb_log2 = __builtin_ctz(S::MB);
+    cg.wgm_log2 = __builtin_ctz(S::WGM);
     return cg;
 }
 

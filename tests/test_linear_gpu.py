@@ -92,6 +92,36 @@ def test_round_bf16_device_matches_reference_vectors(ncm, cuda):
     assert np.array_equal(got.astype(np.uint16), pairs[:, 1].astype(np.uint16))
 
 
+def test_device_conversions_against_oracle(ncm, oracle, cuda):
+    """Device bf16 conversions: every bf16 pattern widens exactly and
+    rounds back to itself (bf16/root.zig:50-59; NaN payloads -> 0x7FC0);
+    f32 -> bf16 agrees with the oracle's RNE on rounding-critical patterns,
+    with and without the operand flush (kernels/root.zig:144-148)."""
+    import torch
+    from ncmorph_amd import kernels
+
+    bits = np.arange(65536, dtype=np.uint16)
+    wide = kernels.bf16_widen(torch.from_numpy(bits.view(np.int16)).to(cuda).view(torch.bfloat16))
+    w = wide.cpu().numpy()
+    assert np.array_equal(w.view(np.uint32), bits.astype(np.uint32) << 16)
+    back = kernels.bf16_from_f32(wide).cpu().view(torch.int16).numpy().view(np.uint16)
+    nan = (bits & 0x7F80) == 0x7F80
+    nan &= (bits & 0x007F) != 0
+    assert np.array_equal(back[~nan], bits[~nan])
+    assert np.all(back[nan] == 0x7FC0)
+    rng = np.random.default_rng(11)
+    hi = rng.integers(0, 1 << 16, 1 << 18, dtype=np.uint32) << 16
+    lo = np.array([0x0000, 0x7FFF, 0x8000, 0x8001, 0xFFFF], np.uint32)
+    f32 = (hi[:, None] | lo[None, :]).ravel().view(np.float32)
+    fd = torch.from_numpy(f32).to(cuda)
+    for flush in (False, True):
+        got = kernels.bf16_from_f32(fd, flush=flush).cpu().view(torch.int16).numpy().view(np.uint16)
+        ref = oracle.bf16_from_f32(f32)
+        if flush:
+            ref = np.where((ref & 0x7F80) == 0, ref & 0x8000, ref).astype(np.uint16)
+        assert np.array_equal(got, ref), flush
+
+
 @pytest.mark.parametrize("n,k", [(2048, 2048), (8192, 2048), (2048, 8192)])
 def test_linear_1b_shapes(ncm, oracle, cuda, n, k):
     """Config shapes: x [2048, k] ~N(0,1), W [n, k] ~N(0, 0.02^2), bf16."""
