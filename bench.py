@@ -136,6 +136,46 @@ def run_rvq(torch, reps, warmup):
             "n_flagged": n_flagged}
 
 
+def run_decoder_ops(torch, reps=20):
+    """The bf16 decoder's ops around the linear at the Llama-3.2-1B layer shape
+    (4096 tokens, hidden 2048, intermediate 8192): RMSNorm rows (f32 in, bf16
+    out) and the MLP activation round_bf16(silu(gate) * up) (f32 in, bf16
+    out). HBM-bound: bytes = inputs read once + output written once."""
+    from ncmorph_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(7)
+    t, h, inter = 4096, 2048, 8192
+    x = torch.randn(t, h, device=dev, generator=g)
+    w = torch.randn(h, device=dev, generator=g) * 0.1 + 1
+    gate = torch.randn(t, inter, device=dev, generator=g)
+    up = torch.randn(t, inter, device=dev, generator=g)
+    y_n = torch.empty(t, h, dtype=torch.bfloat16, device=dev)
+    y_m = torch.empty(t, inter, dtype=torch.bfloat16, device=dev)
+    out = {}
+    for name, fn, nbytes in (
+            ("rms_norm_bf16_rows", lambda: kernels.rms_norm_rows(x, w, 1e-5, "bf16", out=y_n),
+             t * h * 4 + h * 4 + t * h * 2),
+            ("silu_mul_bf16", lambda: kernels.silu_mul(gate, up, "bf16", out=y_m),
+             2 * t * inter * 4 + t * inter * 2)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / reps
+        gbs = nbytes / sec / 1e9
+        out[name] = {"shape": [t, h] if "norm" in name else [t, inter], "us": round(sec * 1e6, 2),
+                     "bytes": nbytes,
+                     "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                                  "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)}}
+    return out
+
+
 def cpu_linear_baseline():
     """Oracle (scalar restatement of matmul_bf16, 1 thread) on a 24-row slice
     of each shape, extrapolated linearly in M."""
@@ -233,6 +273,8 @@ def main():
         res["linear_max_abs_err_vs_fp32"] = lin["max_abs_err_vs_fp32"]
         if not args.no_cpu:
             res["cpu_baseline"] = cpu_linear_baseline()
+    if args.only in ("linear", "all"):
+        res["decoder_ops"] = run_decoder_ops(torch)
     if args.only in ("rvq", "all"):
         rv = run_rvq(torch, max(3, args.steps // 10), max(1, args.warmup // 5))
         tps = rv["tokens"] / rv["encode_s"]

@@ -102,6 +102,19 @@ int ncm_matmul_f32(const float* input, size_t input_len, const float* weights,
  * RNE, every NaN -> 0x7FC0, no flush. Host pointers. */
 int ncm_round_bf16(const float* values, float* out, size_t n);
 
+/* Replaces `kernels.rms_norm_bf16` (packages/kernels/root.zig:246-254): the
+ * sum of squares in the reference's pinned order (root.zig:152-227), then
+ * round_bf16(round_bf16(x * inverse_rms) * round_bf16(weight)); bit-identical
+ * to the reference. One nonempty vector; lengths as root.zig:247. */
+int ncm_rms_norm_bf16(const float* input, size_t input_len, const float* weight,
+                      size_t weight_len, float* output, size_t output_len, float epsilon);
+
+/* Replaces `kernels.silu_bf16` (packages/kernels/root.zig:265-270):
+ * round_bf16(v / (1 + exp(-v))). exp is the device's expf, so a result can
+ * differ from the reference's by one bf16 step where the f32 quotient lies
+ * next to a rounding boundary. */
+int ncm_silu_bf16(const float* input, size_t input_len, float* output, size_t output_len);
+
 /* ===================================================================== */
 /* 2. Device-resident entry points (stream-ordered)                        */
 /* ===================================================================== */
@@ -130,6 +143,21 @@ int ncm_bf16_from_f32_dev(ncm_ctx_t* ctx, const float* src, uint16_t* dst, int64
                           int flush);
 /* bf16 bits -> f32, exact (packages/bf16/root.zig:25-37). Device pointers. */
 int ncm_bf16_widen_dev(ncm_ctx_t* ctx, const uint16_t* src, float* dst, int64_t n);
+
+/* Device RMSNorm, bf16 mode, of each of `rows` rows of x [rows, width] (f32)
+ * with weight [width] (f32): the decoder's normalize_rows
+ * (src/decoder.zig:168, root.zig:246-254), one row per wavefront, same bits
+ * as ncm_rms_norm_bf16. out_mode NCM_OUT_BF16_F32 (y float) or NCM_OUT_BF16
+ * (y uint16 bits, ready for ncm_linear_bf16). When width % 4 == 0, x and
+ * weight must be 16-byte aligned. */
+int ncm_rms_norm_rows_dev(ncm_ctx_t* ctx, const float* x, const float* weight, void* y,
+                          int64_t rows, int64_t width, float epsilon, int out_mode);
+
+/* Device MLP activation, bf16 mode (src/decoder.zig:210-211):
+ * y[i] = round_bf16(silu_bf16(gate[i]) * up[i]); up NULL gives silu_bf16
+ * alone. out_mode NCM_OUT_BF16_F32 or NCM_OUT_BF16. */
+int ncm_silu_mul_dev(ncm_ctx_t* ctx, const float* gate, const float* up, void* y, int64_t n,
+                     int out_mode);
 
 /* ---- multiscale residual vector quantization ---- */
 

@@ -207,6 +207,39 @@ int ncm_bf16_widen_dev(ncm_ctx_t* ctx, const uint16_t* src, float* dst, int64_t 
     return NCM_OK;
 }
 
+// ------------------------------------------------------------------ decoder ops
+
+int ncm_rms_norm_rows_dev(ncm_ctx_t* ctx, const float* x, const float* weight, void* y,
+                          int64_t rows, int64_t width, float epsilon, int out_mode) {
+    if (!ctx) return NCM_E_NULL;
+    if (rows < 0 || width < 0) return NCM_E_SHAPE;
+    if (out_mode != NCM_OUT_BF16_F32 && out_mode != NCM_OUT_BF16) return NCM_E_ARG;
+    if (rows == 0) return NCM_OK;
+    if (width == 0) return NCM_E_SHAPE;  // root.zig:247: nonempty rows
+    if (!x || !weight || !y) return NCM_E_NULL;
+    if (width % 4 == 0 && ((uintptr_t)x % 16 || (uintptr_t)weight % 16)) return NCM_E_ARG;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_rms_norm_rows(x, weight, y, rows, width, epsilon, out_mode,
+                                             ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "rms_norm launch");
+    return NCM_OK;
+}
+
+int ncm_silu_mul_dev(ncm_ctx_t* ctx, const float* gate, const float* up, void* y, int64_t n,
+                     int out_mode) {
+    if (!ctx) return NCM_E_NULL;
+    if (n < 0) return NCM_E_SHAPE;
+    if (out_mode != NCM_OUT_BF16_F32 && out_mode != NCM_OUT_BF16) return NCM_E_ARG;
+    if (n == 0) return NCM_OK;
+    if (!gate || !y) return NCM_E_NULL;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_silu_mul(gate, up, y, n, out_mode, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "silu_mul launch");
+    return NCM_OK;
+}
+
 // ------------------------------------------------------------------ drop-ins
 
 namespace {
@@ -334,6 +367,57 @@ int ncm_matmul_bf16_bias(const float* input, size_t input_len, const float* weig
     if (!bias) return NCM_E_NULL;
     return host_linear(input, input_len, weights, weights_len, bias, bias_len, output,
                        output_len, token_count, input_width, output_width);
+}
+
+int ncm_rms_norm_bf16(const float* input, size_t input_len, const float* weight,
+                      size_t weight_len, float* output, size_t output_len, float epsilon) {
+    // root.zig:247: nonempty, equal lengths.
+    if (input_len == 0 || weight_len != input_len || output_len != input_len)
+        return NCM_E_LENGTH;
+    if (!input || !weight || !output) return NCM_E_NULL;
+    int rc = 0;
+    ncm_ctx_t* ctx = default_ctx(&rc);
+    if (rc) return rc;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    const size_t n = input_len;
+    const size_t o_w = align_up(n * 4, 256), o_y = o_w + align_up(n * 4, 256);
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, o_y + n * 4, &ws);
+    if (rc) return rc;
+    char* base = (char*)ws;
+    hipStream_t st = ctx->stream;
+    NCM_HIP(hipMemcpyAsync(base, input, n * 4, hipMemcpyHostToDevice, st));
+    NCM_HIP(hipMemcpyAsync(base + o_w, weight, n * 4, hipMemcpyHostToDevice, st));
+    NCM_HIP(ncm::launch_rms_norm_rows((const float*)base, (const float*)(base + o_w), base + o_y,
+                                      1, (int64_t)n, epsilon, NCM_OUT_BF16_F32, st));
+    NCM_HIP(hipMemcpyAsync(output, base + o_y, n * 4, hipMemcpyDeviceToHost, st));
+    NCM_HIP(hipStreamSynchronize(st));
+    return NCM_OK;
+}
+
+int ncm_silu_bf16(const float* input, size_t input_len, float* output, size_t output_len) {
+    if (output_len != input_len) return NCM_E_LENGTH;  // root.zig:266
+    if (input_len == 0) return NCM_OK;
+    if (!input || !output) return NCM_E_NULL;
+    int rc = 0;
+    ncm_ctx_t* ctx = default_ctx(&rc);
+    if (rc) return rc;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    const size_t n = input_len;
+    const size_t o_y = align_up(n * 4, 256);
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, o_y + n * 4, &ws);
+    if (rc) return rc;
+    char* base = (char*)ws;
+    hipStream_t st = ctx->stream;
+    NCM_HIP(hipMemcpyAsync(base, input, n * 4, hipMemcpyHostToDevice, st));
+    NCM_HIP(ncm::launch_silu_mul((const float*)base, nullptr, base + o_y, (int64_t)n,
+                                 NCM_OUT_BF16_F32, st));
+    NCM_HIP(hipMemcpyAsync(output, base + o_y, n * 4, hipMemcpyDeviceToHost, st));
+    NCM_HIP(hipStreamSynchronize(st));
+    return NCM_OK;
 }
 
 int ncm_round_bf16(const float* values, float* out, size_t n) {

@@ -1,0 +1,200 @@
+// Decoder ops around the bf16 linear (packages/kernels/root.zig:150-270,
+// src/decoder.zig:168-216): RMSNorm rows with the reference's pinned
+// sum-of-squares cascade, and the MLP activation round_bf16(silu_bf16(gate) *
+// up). Memory-bound: each kernel reads its inputs and writes its output once.
+#include "common.h"
+#include "linear.h"
+
+namespace ncm {
+
+// One wavefront per row. The pinned cascade of root.zig:152-227 keeps 4 x 4 x
+// 8 accumulators acc[level][r][l]; every (r, l) chain sees the same sequence
+// of operations, so lane c < 32 runs chain (r = c / 8, l = c % 8) with its
+// four levels in registers, and the merges that cross chains (rows into the
+// vector sum, lanes into the scalar sum) run in the reference's order on
+// values gathered by shuffles. Every product and sum is a separate fp32 op
+// (built with -ffp-contract=off), as in the reference.
+// STAGE: the row is first copied to LDS with 16-byte loads by all 64 lanes
+// (n % 4 == 0, n <= kRmsStageMax), and both passes read it from there.
+constexpr int64_t kRmsStageMax = 8192;
+
+template <int OUT_MODE, bool STAGE>
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ weight,
+                                                            void* __restrict__ y, int64_t rows,
+                                                            int64_t n, float epsilon) {
+    extern __shared__ __attribute__((aligned(16))) float stage[];
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + row * n;
+    if (STAGE) {
+        float* sr = stage + (threadIdx.x >> 6) * n;
+        for (int64_t i = 4 * lane; i < n; i += 256) *(f32x4_t*)(sr + i) = *(const f32x4_t*)(xr + i);
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // this wave's row is in LDS
+        xr = sr;
+    }
+    const bool chain = lane < 32;
+    const int r = (lane >> 3) & 3, l = lane & 7;
+
+    const int64_t vectors = n / 8, groups = vectors / 4;
+    int lg = 0;
+    for (int64_t lim = 1; lim < groups; lim *= 2) ++lg;
+    const int power = lg / 4 > 4 ? lg / 4 : 4;
+    const int64_t step = (int64_t)1 << power, mask = step - 1;
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    auto sq = [&](int64_t vi) {
+        const float v = chain ? xr[vi * 8 + l] : 0.0f;
+        return v * v;
+    };
+    int64_t g = 0;
+    while (g + step <= groups) {
+        for (int64_t s = 0; s < step; ++s) a0 = a0 + sq((g + s) * 4 + r);
+        g += step;
+        a1 = a1 + a0;
+        a0 = 0.0f;
+        if ((g & (mask << power)) == 0) {
+            a2 = a2 + a1;
+            a1 = 0.0f;
+            if ((g & (mask << (2 * power))) == 0) {
+                a3 = a3 + a2;
+                a2 = 0.0f;
+            }
+        }
+    }
+    for (; g < groups; ++g) a0 = a0 + sq(g * 4 + r);
+    a0 = a0 + a1;
+    a0 = a0 + a2;
+    a0 = a0 + a3;
+    if (r == 0)  // vector tail, into row 0's chains
+        for (int64_t vi = groups * 4; vi < vectors; ++vi) a0 = a0 + sq(vi);
+    // vector_sum[l] = ((acc[0][0][l] + acc[0][1][l]) + acc[0][2][l]) + acc[0][3][l]
+    const float r1 = __shfl(a0, l + 8, 64), r2 = __shfl(a0, l + 16, 64), r3 = __shfl(a0, l + 24, 64);
+    float vs = a0;
+    vs = vs + r1;
+    vs = vs + r2;
+    vs = vs + r3;
+    float sum = 0.0f;
+    for (int64_t i = vectors * 8; i < n; ++i) {
+        const float v = xr[i];
+        sum = sum + v * v;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sum = sum + __shfl(vs, k, 64);
+    const float mean = sum / (float)n;
+    const float inv = 1.0f / sqrtf(mean + epsilon);
+
+    // round_bf16(round_bf16(x * inv) * round_bf16(weight)) (root.zig:250-252).
+    auto out1 = [&](int64_t i, float v, float wv) {
+        const float normalized = __uint_as_float(bf16_bits_rne(v * inv) << 16);
+        const uint32_t bits = bf16_bits_rne(normalized * __uint_as_float(bf16_bits_rne(wv) << 16));
+        if (OUT_MODE == NCM_OUT_BF16)
+            ((uint16_t*)y)[row * n + i] = (uint16_t)bits;
+        else
+            ((float*)y)[row * n + i] = __uint_as_float(bits << 16);
+    };
+    if ((n & 3) == 0) {
+        for (int64_t i = 4 * lane; i < n; i += 256) {
+            const f32x4_t v = *(const f32x4_t*)(xr + i);
+            const f32x4_t wv = *(const f32x4_t*)(weight + i);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) out1(i + e, v[e], wv[e]);
+        }
+    } else {
+        for (int64_t i = lane; i < n; i += 64) out1(i, xr[i], weight[i]);
+    }
+}
+
+// round_bf16(round_bf16(g / (1 + exp(-g))) * up) (root.zig:265-270,
+// src/decoder.zig:210-211), four elements per thread (16-byte loads when the
+// four are in range and aligned).
+template <int OUT_MODE>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gate,
+                                                       const float* __restrict__ up,
+                                                       void* __restrict__ y, int64_t n) {
+    auto act = [](float v, float u) {
+        const float a = __uint_as_float(bf16_bits_rne(v / (1.0f + expf(-v))) << 16);
+        return bf16_bits_rne(a * u);
+    };
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (i0 >= n) return;
+    const bool vec = i0 + 4 <= n && ((uintptr_t)gate & 15) == 0 && (!up || ((uintptr_t)up & 15) == 0);
+    uint32_t b[4];
+    if (vec) {
+        const f32x4_t g = *(const f32x4_t*)(gate + i0);
+        f32x4_t u = {1.0f, 1.0f, 1.0f, 1.0f};
+        if (up) u = *(const f32x4_t*)(up + i0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) b[e] = act(g[e], u[e]);
+        if (OUT_MODE == NCM_OUT_BF16 && ((uintptr_t)y & 7) == 0) {
+            u32x2_t o;
+            o[0] = b[0] | (b[1] << 16);
+            o[1] = b[2] | (b[3] << 16);
+            *(u32x2_t*)((uint16_t*)y + i0) = o;
+            return;
+        }
+        if (OUT_MODE != NCM_OUT_BF16 && ((uintptr_t)y & 15) == 0) {
+            u32x4_t o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = b[e] << 16;
+            *(u32x4_t*)((float*)y + i0) = o;
+            return;
+        }
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            b[e] = i0 + e < n ? act(gate[i0 + e], up ? up[i0 + e] : 1.0f) : 0u;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        if (i0 + e >= n) break;
+        if (OUT_MODE == NCM_OUT_BF16)
+            ((uint16_t*)y)[i0 + e] = (uint16_t)b[e];
+        else
+            ((float*)y)[i0 + e] = __uint_as_float(b[e] << 16);
+    }
+}
+
+template <int OUT_MODE, bool STAGE>
+static hipError_t launch_rms_t(const float* x, const float* weight, void* y, int64_t rows,
+                               int64_t n, float epsilon, hipStream_t stream) {
+    auto kern = rms_norm_rows_kernel<OUT_MODE, STAGE>;
+    const size_t lds = STAGE ? (size_t)4 * n * sizeof(float) : 0;
+    if (STAGE && lds > 64 * 1024) {
+        static bool attr_set = false;
+        if (!attr_set) {
+            hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                               hipFuncAttributeMaxDynamicSharedMemorySize,
+                                               (int)(4 * kRmsStageMax * sizeof(float)));
+            if (e != hipSuccess) return e;
+            attr_set = true;
+        }
+    }
+    hipLaunchKernelGGL(kern, dim3((unsigned)((rows + 3) / 4)), dim3(256), lds, stream, x, weight,
+                       y, rows, n, epsilon);
+    return hipGetLastError();
+}
+
+hipError_t launch_rms_norm_rows(const float* x, const float* weight, void* y, int64_t rows,
+                                int64_t n, float epsilon, int out_mode, hipStream_t stream) {
+    const bool stage = n % 4 == 0 && n <= kRmsStageMax;
+    if (out_mode == NCM_OUT_BF16)
+        return stage ? launch_rms_t<NCM_OUT_BF16, true>(x, weight, y, rows, n, epsilon, stream)
+                     : launch_rms_t<NCM_OUT_BF16, false>(x, weight, y, rows, n, epsilon, stream);
+    return stage ? launch_rms_t<NCM_OUT_BF16_F32, true>(x, weight, y, rows, n, epsilon, stream)
+                 : launch_rms_t<NCM_OUT_BF16_F32, false>(x, weight, y, rows, n, epsilon, stream);
+}
+
+hipError_t launch_silu_mul(const float* gate, const float* up, void* y, int64_t n, int out_mode,
+                           hipStream_t stream) {
+    const dim3 grid((unsigned)((n + 1023) / 1024));
+    if (out_mode == NCM_OUT_BF16)
+        hipLaunchKernelGGL(silu_mul_kernel<NCM_OUT_BF16>, grid, dim3(256), 0, stream, gate, up, y,
+                           n);
+    else
+        hipLaunchKernelGGL(silu_mul_kernel<NCM_OUT_BF16_F32>, grid, dim3(256), 0, stream, gate,
+                           up, y, n);
+    return hipGetLastError();
+}
+
+}  // namespace ncm

@@ -65,6 +65,22 @@ def matmul_bf16_bias(input, weights, bias, output, token_count, input_width, out
           "matmul_bf16_bias")
 
 
+def rms_norm_bf16(input, weight, output, epsilon):
+    """kernels.rms_norm_bf16 (root.zig:246-254) of one vector, on the GPU,
+    bit-identical to the reference."""
+    for a, n in ((input, "input"), (weight, "weight"), (output, "output")):
+        _host_f32(a, n)
+    check(lib().ncm_rms_norm_bf16(_p(input), input.size, _p(weight), weight.size, _p(output),
+                                  output.size, float(epsilon)), "rms_norm_bf16")
+
+
+def silu_bf16(input, output):
+    """kernels.silu_bf16 (root.zig:265-270) on the GPU."""
+    for a, n in ((input, "input"), (output, "output")):
+        _host_f32(a, n)
+    check(lib().ncm_silu_bf16(_p(input), input.size, _p(output), output.size), "silu_bf16")
+
+
 def round_bf16(value):
     """kernels.round_bf16 (root.zig:10-12) on a scalar or a float32 array,
     RNE with every NaN -> 0x7FC0, computed on the GPU."""
@@ -144,4 +160,39 @@ def bf16_widen(src, ctx=None):
     ctx.bind_stream()
     check(lib().ncm_bf16_widen_dev(ctx.handle, _dev_ptr(src, "src"), _dev_ptr(out, "out"),
                                    src.numel()), "bf16_widen")
+    return out
+
+
+def rms_norm_rows(x, weight, epsilon: float, out_mode: str = "bf16_f32", out=None, ctx=None):
+    """RMSNorm (bf16 mode) of every row of x (float32 [rows, width]) with
+    weight (float32 [width]) on torch's current stream; out_mode "bf16_f32"
+    (float32 holding bf16 values) or "bf16" (torch.bfloat16)."""
+    import torch
+
+    rows, width = x.shape
+    mode = _OUT_MODES[out_mode]
+    if out is None:
+        dt = torch.bfloat16 if mode == NCM_OUT_BF16 else torch.float32
+        out = torch.empty((rows, width), dtype=dt, device=x.device)
+    ctx = ctx or default_context(x.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_rms_norm_rows_dev(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(weight, "weight"),
+                                      _dev_ptr(out, "out"), rows, width, float(epsilon), mode),
+          "rms_norm_rows")
+    return out
+
+
+def silu_mul(gate, up=None, out_mode: str = "bf16_f32", out=None, ctx=None):
+    """round_bf16(silu_bf16(gate) * up) elementwise (up None: silu_bf16) on
+    torch's current stream."""
+    import torch
+
+    mode = _OUT_MODES[out_mode]
+    if out is None:
+        dt = torch.bfloat16 if mode == NCM_OUT_BF16 else torch.float32
+        out = torch.empty(gate.shape, dtype=dt, device=gate.device)
+    ctx = ctx or default_context(gate.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_silu_mul_dev(ctx.handle, _dev_ptr(gate, "gate"), _dev_ptr(up, "up"),
+                                 _dev_ptr(out, "out"), gate.numel(), mode), "silu_mul")
     return out

@@ -565,3 +565,100 @@ int ncmo_rvq_encode_f64(const float* x, int64_t b, int64_t t, int64_t d, int64_t
     free(cn);
     return 0;
 }
+
+/* ------------------------------------------------------------------ */
+/* Decoder ops around the linear                                      */
+/* ------------------------------------------------------------------ */
+
+float ncmo_sum_squares_pinned(const float* x, size_t n) {
+    enum { W = 8 };
+    const size_t vectors = n / W;
+    const size_t groups = vectors / 4; /* row groups of four vectors */
+    size_t lg = 0, lim = 1;
+    while (lim < groups) {
+        ++lg;
+        lim *= 2;
+    }
+    const size_t power = lg / 4 > 4 ? lg / 4 : 4;
+    const size_t step = (size_t)1 << power;
+    const size_t mask = step - 1;
+    float acc[4][4][W];
+    memset(acc, 0, sizeof(acc));
+    size_t g = 0;
+    while (g + step <= groups) {
+        for (size_t s = 0; s < step; ++s)
+            for (int r = 0; r < 4; ++r)
+                for (int l = 0; l < W; ++l) {
+                    const float v = x[((g + s) * 4 + r) * W + l];
+                    const float sq = v * v;
+                    acc[0][r][l] = acc[0][r][l] + sq;
+                }
+        g += step;
+        for (int lev = 1; lev < 4; ++lev) {
+            for (int r = 0; r < 4; ++r)
+                for (int l = 0; l < W; ++l) {
+                    acc[lev][r][l] = acc[lev][r][l] + acc[lev - 1][r][l];
+                    acc[lev - 1][r][l] = 0.0f;
+                }
+            if ((g & (mask << (lev * power))) != 0) break;
+        }
+    }
+    for (; g < groups; ++g)
+        for (int r = 0; r < 4; ++r)
+            for (int l = 0; l < W; ++l) {
+                const float v = x[(g * 4 + r) * W + l];
+                const float sq = v * v;
+                acc[0][r][l] = acc[0][r][l] + sq;
+            }
+    for (int lev = 1; lev < 4; ++lev)
+        for (int r = 0; r < 4; ++r)
+            for (int l = 0; l < W; ++l) acc[0][r][l] = acc[0][r][l] + acc[lev][r][l];
+    for (size_t vi = groups * 4; vi < vectors; ++vi)
+        for (int l = 0; l < W; ++l) {
+            const float v = x[vi * W + l];
+            const float sq = v * v;
+            acc[0][0][l] = acc[0][0][l] + sq;
+        }
+    float vs[W];
+    for (int l = 0; l < W; ++l) vs[l] = acc[0][0][l];
+    for (int r = 1; r < 4; ++r)
+        for (int l = 0; l < W; ++l) vs[l] = vs[l] + acc[0][r][l];
+    float sum = 0.0f;
+    for (size_t i = vectors * W; i < n; ++i) {
+        const float sq = x[i] * x[i];
+        sum = sum + sq;
+    }
+    for (int l = 0; l < W; ++l) sum = sum + vs[l];
+    return sum;
+}
+
+void ncmo_rms_norm(const float* x, const float* weight, float* out, size_t n, float epsilon,
+                   int bf16) {
+    const float ss = ncmo_sum_squares_pinned(x, n);
+    const float mean = ss / (float)n;
+    const float inv = 1.0f / sqrtf(mean + epsilon);
+    for (size_t i = 0; i < n; ++i) {
+        if (bf16) {
+            const float normalized = ncmo_round_bf16(x[i] * inv);
+            out[i] = ncmo_round_bf16(normalized * ncmo_round_bf16(weight[i]));
+        } else {
+            const float normalized = x[i] * inv;
+            out[i] = normalized * weight[i];
+        }
+    }
+}
+
+void ncmo_silu_bf16(const float* x, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        out[i] = ncmo_round_bf16(v / (1.0f + expf(-v)));
+    }
+}
+
+void ncmo_silu_mul_bf16(const float* gate, const float* up, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float v = gate[i];
+        const float a = ncmo_round_bf16(v / (1.0f + expf(-v)));
+        out[i] = ncmo_round_bf16(a * up[i]);
+    }
+}

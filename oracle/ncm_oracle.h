@@ -107,6 +107,23 @@ int ncmo_rvq_encode_f64(const float* x, int64_t b, int64_t t, int64_t d, int64_t
                         const int32_t* strides, const uint16_t* codebooks, int64_t v,
                         int32_t* codes, double* gap, const int32_t* forced);
 
+/* ---- decoder ops around the linear (packages/kernels/root.zig:150-270) ---- */
+/* pinned_torch_sum_squares_f32 (root.zig:152-227): 8-lane vectors grouped in
+ * rows of four, 4 x 4 x 8 accumulators flushed level by level every
+ * 2^level_power row groups, then the row-group tail, the level merge, the
+ * vector tail, the row merge and the scalar tail, each a separate fp32
+ * product and add in that order. */
+float ncmo_sum_squares_pinned(const float* x, size_t n);
+/* rms_norm (root.zig:229-242, bf16 = 0) and rms_norm_bf16 (root.zig:246-254,
+ * bf16 = 1). n > 0. */
+void ncmo_rms_norm(const float* x, const float* weight, float* out, size_t n, float epsilon,
+                   int bf16);
+/* silu_bf16 (root.zig:265-270): round_bf16(v / (1 + exp(-v))), libm expf. */
+void ncmo_silu_bf16(const float* x, float* out, size_t n);
+/* The decoder's MLP activation in bf16 mode (src/decoder.zig:210-211):
+ * round_bf16(silu_bf16(gate) * up). */
+void ncmo_silu_mul_bf16(const float* gate, const float* up, float* out, size_t n);
+
 #ifdef __cplusplus
 }
 #endif

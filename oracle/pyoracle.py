@@ -70,6 +70,11 @@ def lib():
         L.ncmo_rvq_decode.argtypes = [i32p, i64, i64, i64, i64, i32p, u16p, i64, f32p]
         L.ncmo_rvq_encode_f64.argtypes = [f32p, i64, i64, i64, i64, i32p, u16p, i64, i32p,
                                           vp, vp]
+        L.ncmo_sum_squares_pinned.argtypes = [f32p, sz]
+        L.ncmo_sum_squares_pinned.restype = C.c_float
+        L.ncmo_rms_norm.argtypes = [f32p, f32p, f32p, sz, C.c_float, C.c_int]
+        L.ncmo_silu_bf16.argtypes = [f32p, f32p, sz]
+        L.ncmo_silu_mul_bf16.argtypes = [f32p, f32p, f32p, sz]
         _lib = L
     return _lib
 
@@ -234,3 +239,37 @@ def rvq_encode_f64(x, codebooks_bits, strides, forced=None):
     if rc != 0:
         raise ValueError(f"ncmo_rvq_encode_f64 failed: {rc}")
     return codes, gap
+
+
+# ------------------------------------------------------------ decoder ops
+def sum_squares_pinned(x) -> np.float32:
+    """pinned_torch_sum_squares_f32 (packages/kernels/root.zig:152-227)."""
+    a = np.ascontiguousarray(x, np.float32).ravel()
+    return np.float32(lib().ncmo_sum_squares_pinned(a, a.size))
+
+
+def rms_norm(x, weight, epsilon: float, bf16: bool = True) -> np.ndarray:
+    """rms_norm / rms_norm_bf16 (root.zig:229-254) of every row of x [.., n]."""
+    a = np.ascontiguousarray(x, np.float32)
+    w = np.ascontiguousarray(weight, np.float32).ravel()
+    n = a.shape[-1]
+    rows = a.reshape(-1, n)
+    out = np.empty_like(rows)
+    for r in range(rows.shape[0]):
+        lib().ncmo_rms_norm(np.ascontiguousarray(rows[r]), w, out[r], n, epsilon, 1 if bf16 else 0)
+    return out.reshape(a.shape)
+
+
+def silu_bf16(x) -> np.ndarray:
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    lib().ncmo_silu_bf16(a.ravel(), out.ravel(), a.size)
+    return out
+
+
+def silu_mul_bf16(gate, up) -> np.ndarray:
+    g = np.ascontiguousarray(gate, np.float32)
+    u = np.ascontiguousarray(up, np.float32)
+    out = np.empty_like(g)
+    lib().ncmo_silu_mul_bf16(g.ravel(), u.ravel(), out.ravel(), g.size)
+    return out
