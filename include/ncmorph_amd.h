@@ -130,6 +130,19 @@ int ncm_linear_bf16(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
                     const uint16_t* bias, void* y, int64_t m, int64_t k, int64_t n,
                     int out_mode);
 
+/* y = residual + ncm_linear_bf16(x, w, bias): the projection and the
+ * residual add that follows it in the decoder layer (add_rows,
+ * src/decoder.zig:279-282, after the o and down projections at
+ * src/decoder.zig:199-200 and 213-214) in one pass. residual: float [m, n].
+ * out_mode F32: residual + value in fp32 (the reference's fp32 mode).
+ * BF16_F32 / BF16: round_bf16(residual + round_bf16(value)), the bf16 mode's
+ * add of the bf16-rounded projection. residual may equal y for F32 and
+ * BF16_F32 (in-place update of the hidden state), not for BF16. Same shape and
+ * alignment rules as ncm_linear_bf16. Device pointers. */
+int ncm_linear_bf16_residual(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                             const uint16_t* bias, const float* residual, void* y,
+                             int64_t m, int64_t k, int64_t n, int out_mode);
+
 /* y[m, n] = sum_k x[m, k] * w[n, k], fp32 operands and accumulation on the
  * fp32 MFMA (device counterpart of packages/kernels/root.zig:25-65).
  * Requires k % 4 == 0 and 16-byte aligned x and w. Device pointers. */
@@ -158,6 +171,35 @@ int ncm_rms_norm_rows_dev(ncm_ctx_t* ctx, const float* x, const float* weight, v
  * alone. out_mode NCM_OUT_BF16_F32 or NCM_OUT_BF16. */
 int ncm_silu_mul_dev(ncm_ctx_t* ctx, const float* gate, const float* up, void* y, int64_t n,
                      int out_mode);
+
+/* Device RoPE rotation, bf16 mode: rotate_head (packages/kernels/root.zig:
+ * 615-634) applied in place to every head of every row, as attention_impl
+ * does for queries and keys (root.zig:497-530). x: uint16 bf16 bits, row r
+ * holds `heads` heads of head_dim values at x[r * row_stride + h * head_dim];
+ * row r rotates by table row r % seq_len of cosine/sine (float
+ * [seq_len, head_dim], the rope_tables layout, root.zig:328-348). Table
+ * entries, products and sums are rounded to bf16 in the reference's order:
+ * bit-identical to the reference. Device pointers. */
+int ncm_rope_rotate_dev(ncm_ctx_t* ctx, uint16_t* x, int64_t rows, int64_t row_stride,
+                        int heads, int head_dim, int64_t seq_len, const float* cosine,
+                        const float* sine);
+
+/* Device causal attention, bf16 mode: the scores, softmax and context of
+ * attention_impl (root.zig:536-578) with the causal_mask of the decoder
+ * (root.zig:380-399, src/decoder.zig:155) for `batch` sequences of seq_len
+ * tokens each (positions 0 .. seq_len - 1; window 0 = no sliding window).
+ * q: uint16 bits [batch * seq_len, q_stride] (head h at column h * head_dim);
+ * k, v: uint16 bits [batch * seq_len, kv_stride]; query head h reads key/value
+ * head h / (q_heads / kv_heads). out: [batch * seq_len, out_stride], float
+ * holding bf16 values (NCM_OUT_BF16_F32) or uint16 bits (NCM_OUT_BF16,
+ * ready for the output projection). head_dim 64 or 128; strides multiples of
+ * 8 elements; q, k, v 16-byte aligned. Scores and P V are summed on the MFMA
+ * in its own order (the reference sums in key order), so results agree with
+ * the reference within a few bf16 steps rather than bit for bit. */
+int ncm_attention_bf16_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
+                           const uint16_t* v, void* out, int64_t batch, int64_t seq_len,
+                           int q_heads, int kv_heads, int head_dim, int64_t q_stride,
+                           int64_t kv_stride, int64_t out_stride, int64_t window, int out_mode);
 
 /* ---- multiscale residual vector quantization ---- */
 

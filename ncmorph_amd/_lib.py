@@ -42,11 +42,15 @@ SIGNATURES = [
     ("ncm_rms_norm_bf16", i32, [vp, sz, vp, sz, vp, sz, C.c_float]),
     ("ncm_silu_bf16", i32, [vp, sz, vp, sz]),
     ("ncm_linear_bf16", i32, [vp, vp, vp, vp, vp, i64, i64, i64, i32]),
+    ("ncm_linear_bf16_residual", i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32]),
     ("ncm_linear_f32", i32, [vp, vp, vp, vp, i64, i64, i64]),
     ("ncm_bf16_from_f32_dev", i32, [vp, vp, vp, i64, i32]),
     ("ncm_bf16_widen_dev", i32, [vp, vp, vp, i64]),
     ("ncm_rms_norm_rows_dev", i32, [vp, vp, vp, vp, i64, i64, C.c_float, i32]),
     ("ncm_silu_mul_dev", i32, [vp, vp, vp, vp, i64, i32]),
+    ("ncm_rope_rotate_dev", i32, [vp, vp, i64, i64, i32, i32, i64, vp, vp]),
+    ("ncm_attention_bf16_dev", i32, [vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, i64, i64, i64,
+                                     i64, i32]),
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
     ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
     ("ncm_rvq_decode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, i64, vp]),

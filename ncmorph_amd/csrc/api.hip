@@ -166,6 +166,27 @@ int ncm_linear_bf16(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w, const 
     return NCM_OK;
 }
 
+int ncm_linear_bf16_residual(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                             const uint16_t* bias, const float* residual, void* y, int64_t m,
+                             int64_t k, int64_t n, int out_mode) {
+    if (!ctx) return NCM_E_NULL;
+    if (m < 0 || n < 0 || k < 0) return NCM_E_SHAPE;
+    if (out_mode < NCM_OUT_F32 || out_mode > NCM_OUT_BF16) return NCM_E_ARG;
+    if (m == 0 || n == 0) return NCM_OK;
+    if (!y || !residual || (k > 0 && (!x || !w))) return NCM_E_NULL;
+    if (k % 8 != 0 || k > (int64_t(1) << 21)) return NCM_E_SHAPE;
+    if ((uintptr_t)x % 16 || (uintptr_t)w % 16) return NCM_E_ARG;
+    // In place only where y holds fp32 values at the residual's addresses.
+    if (out_mode == NCM_OUT_BF16 && (const void*)residual == y) return NCM_E_ARG;
+    if (m > (int64_t(1) << 31) || n > (int64_t(1) << 31)) return NCM_E_SHAPE;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_linear_residual(x, w, bias, residual, y, m, k, n, out_mode,
+                                               ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "residual linear kernel launch");
+    return NCM_OK;
+}
+
 int ncm_linear_f32(ncm_ctx_t* ctx, const float* x, const float* w, float* y, int64_t m,
                    int64_t k, int64_t n) {
     if (!ctx) return NCM_E_NULL;
@@ -237,6 +258,52 @@ int ncm_silu_mul_dev(ncm_ctx_t* ctx, const float* gate, const float* up, void* y
     if (rc) return rc;
     hipError_t e = ncm::launch_silu_mul(gate, up, y, n, out_mode, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "silu_mul launch");
+    return NCM_OK;
+}
+
+int ncm_rope_rotate_dev(ncm_ctx_t* ctx, uint16_t* x, int64_t rows, int64_t row_stride,
+                        int heads, int head_dim, int64_t seq_len, const float* cosine,
+                        const float* sine) {
+    if (!ctx) return NCM_E_NULL;
+    if (rows < 0 || heads < 0 || head_dim <= 0 || head_dim % 2 || seq_len <= 0)
+        return NCM_E_SHAPE;
+    if (row_stride < (int64_t)heads * head_dim) return NCM_E_SHAPE;
+    if (rows == 0 || heads == 0) return NCM_OK;
+    if (!x || !cosine || !sine) return NCM_E_NULL;
+    if (rows * heads * (int64_t)(head_dim / 2) > (int64_t(1) << 40)) return NCM_E_SHAPE;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_rope_rotate(x, rows, row_stride, heads, head_dim, seq_len, cosine,
+                                           sine, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "rope rotate launch");
+    return NCM_OK;
+}
+
+int ncm_attention_bf16_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
+                           const uint16_t* v, void* out, int64_t batch, int64_t seq_len,
+                           int q_heads, int kv_heads, int head_dim, int64_t q_stride,
+                           int64_t kv_stride, int64_t out_stride, int64_t window, int out_mode) {
+    if (!ctx) return NCM_E_NULL;
+    if (batch < 0 || seq_len < 0 || q_heads <= 0 || kv_heads <= 0 || window < 0)
+        return NCM_E_SHAPE;
+    if (head_dim != 64 && head_dim != 128) return NCM_E_SHAPE;
+    if (q_heads % kv_heads) return NCM_E_SHAPE;
+    if (out_mode != NCM_OUT_BF16_F32 && out_mode != NCM_OUT_BF16) return NCM_E_ARG;
+    if (q_stride < (int64_t)q_heads * head_dim || kv_stride < (int64_t)kv_heads * head_dim ||
+        out_stride < (int64_t)q_heads * head_dim)
+        return NCM_E_SHAPE;
+    if (batch == 0 || seq_len == 0) return NCM_OK;
+    if (!q || !k || !v || !out) return NCM_E_NULL;
+    // 16-byte row segments for the vector loads.
+    if (q_stride % 8 || kv_stride % 8) return NCM_E_ARG;
+    if ((uintptr_t)q % 16 || (uintptr_t)k % 16 || (uintptr_t)v % 16) return NCM_E_ARG;
+    if (batch > 65535 || q_heads > 65535 || seq_len > (int64_t(1) << 31)) return NCM_E_SHAPE;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_attention_bf16(q, k, v, out, batch, seq_len, q_heads, kv_heads,
+                                              head_dim, q_stride, kv_stride, out_stride, window,
+                                              out_mode, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "attention launch");
     return NCM_OK;
 }
 

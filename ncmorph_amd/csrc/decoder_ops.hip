@@ -155,6 +155,49 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
     }
 }
 
+// rotate_head in bf16 mode (root.zig:615-634) over every head of every row,
+// in place on bf16 bits: row r, head h occupies x[r * row_stride + h * hd ..
+// + hd); its table row is position r % seq_len of cosine/sine [seq_len, hd].
+// Each table entry, product and sum is rounded to bf16, in the reference's
+// order; one thread per (row, head, i < hd / 2) pair of elements.
+__global__ __launch_bounds__(256) void rope_rotate_kernel(uint16_t* __restrict__ x, int64_t rows,
+                                                          int64_t row_stride, int heads, int hd,
+                                                          int64_t seq_len,
+                                                          const float* __restrict__ cosine,
+                                                          const float* __restrict__ sine) {
+    const int half = hd >> 1;
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * heads * half) return;
+    const int i = (int)(idx % half);
+    const int64_t rh = idx / half;
+    const int h = (int)(rh % heads);
+    const int64_t r = rh / heads;
+    const int64_t pos = r % seq_len;
+    auto rb = [](float v) { return __uint_as_float(bf16_bits_rne(v) << 16); };
+    uint16_t* e = x + r * row_stride + (int64_t)h * hd + i;
+    const float first = __uint_as_float((uint32_t)e[0] << 16);
+    const float second = __uint_as_float((uint32_t)e[half] << 16);
+    const float* ct = cosine + pos * hd + i;
+    const float* st = sine + pos * hd + i;
+    const float cos_first = rb(ct[0]), sin_first = rb(st[0]);
+    const float cos_second = rb(ct[half]), sin_second = rb(st[half]);
+    const float left = rb(first * cos_first);
+    const float right = rb(-second * sin_first);
+    const float right2 = rb(first * sin_second);
+    const float left2 = rb(second * cos_second);
+    e[0] = (uint16_t)bf16_bits_rne(left + right);
+    e[half] = (uint16_t)bf16_bits_rne(left2 + right2);
+}
+
+hipError_t launch_rope_rotate(uint16_t* x, int64_t rows, int64_t row_stride, int heads, int hd,
+                              int64_t seq_len, const float* cosine, const float* sine,
+                              hipStream_t stream) {
+    const int64_t n = rows * heads * (hd / 2);
+    hipLaunchKernelGGL(rope_rotate_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
+                       x, rows, row_stride, heads, hd, seq_len, cosine, sine);
+    return hipGetLastError();
+}
+
 template <int OUT_MODE, bool STAGE>
 static hipError_t launch_rms_t(const float* x, const float* weight, void* y, int64_t rows,
                                int64_t n, float epsilon, hipStream_t stream) {

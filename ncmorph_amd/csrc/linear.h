@@ -14,6 +14,12 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
                          int64_t M, int64_t K, int64_t N, int out_mode, int config,
                          hipStream_t stream);
 
+// y = residual + linear (bf16 modes: round_bf16(residual + round_bf16(linear)));
+// residual fp32 [M, N], may equal y for the fp32 output mode.
+hipError_t launch_linear_residual(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                  const float* residual, void* y, int64_t M, int64_t K,
+                                  int64_t N, int out_mode, hipStream_t stream);
+
 // fp32 operands, fp32 output; K % 4 == 0, 16-byte aligned x and w.
 hipError_t launch_linear_f32(const float* x, const float* w, float* y, int64_t M, int64_t K,
                              int64_t N, hipStream_t stream);
@@ -25,6 +31,18 @@ hipError_t launch_rms_norm_rows(const float* x, const float* weight, void* y, in
 // y = round_bf16(silu_bf16(gate) * up) (up NULL: silu_bf16(gate) alone).
 hipError_t launch_silu_mul(const float* gate, const float* up, void* y, int64_t n, int out_mode,
                            hipStream_t stream);
+
+// RoPE rotate-half (bf16 mode) in place on bf16 bits; see decoder_ops.hip.
+hipError_t launch_rope_rotate(uint16_t* x, int64_t rows, int64_t row_stride, int heads, int hd,
+                              int64_t seq_len, const float* cosine, const float* sine,
+                              hipStream_t stream);
+// Causal (optionally windowed) bf16 attention over `batch` sequences of
+// seq_len tokens; see attention.hip.
+hipError_t launch_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                 void* out, int64_t batch, int64_t seq_len, int q_heads,
+                                 int kv_heads, int head_dim, int64_t q_stride, int64_t kv_stride,
+                                 int64_t out_stride, int64_t window, int out_mode,
+                                 hipStream_t stream);
 
 hipError_t launch_bf16_from_f32(const float* src, uint16_t* dst, int64_t n, int flush,
                                 hipStream_t stream);

@@ -12,14 +12,19 @@
 
 namespace ncm {
 
-template <class S, int OUT_MODE, bool HAS_BIAS>
+// HAS_RES: y = residual + result (the decoder's add_rows, src/decoder.zig:279-282):
+// fp32 output adds in fp32; the bf16 modes round the linear's result to bf16
+// first (its own output contract) and then round the sum to bf16. residual
+// [M, N] fp32 may be y itself (each element is read, then written, by one
+// thread).
+template <class S, int OUT_MODE, bool HAS_BIAS, bool HAS_RES = false>
 __global__ __launch_bounds__(S::NT)
 __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const void* __restrict__ x,
                                                           const void* __restrict__ w,
                                                           const uint16_t* __restrict__ bias,
-                                                          void* __restrict__ y, int64_t M,
+                                                          void* y, int64_t M,
                                                           int64_t K, int64_t N, int tiles_n,
-                                                          int group_m) {
+                                                          int group_m, const float* residual) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
 
     // XCD-aware grouped tile order: a run of consecutive logical ids covers a
@@ -47,7 +52,8 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
     if (wave >= S::NWG) return;  // K group 1: its sums were handed to group 0
     const int wm = wave % S::WGM;
     const int wn = wave / S::WGM;
-    if (m0 + S::BM <= M && n0 + S::BN <= N && (N & 3) == 0 && ((uintptr_t)y & 15) == 0) {
+    if (m0 + S::BM <= M && n0 + S::BN <= N && (N & 3) == 0 && ((uintptr_t)y & 15) == 0 &&
+        (!HAS_RES || ((uintptr_t)residual & 15) == 0)) {
         // Whole tile in range: transpose each 4-row group of the D fragment
         // inside lane quads so that every lane stores 4 consecutive columns
         // of one row (16-byte stores; 8 lanes cover 128 contiguous bytes).
@@ -72,14 +78,22 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
                     }
                     quad_transpose4(v, q);
                     const int64_t m = m0 + wm * S::WM + mb * 32 + 8 * blk + hrow;
+                    f32x4_t rv;
+                    if (HAS_RES) rv = *(const f32x4_t*)(residual + m * N + ncol);
                     if (OUT_MODE == NCM_OUT_F32) {
                         f32x4_t o;
                         o[0] = v[0]; o[1] = v[1]; o[2] = v[2]; o[3] = v[3];
+                        if (HAS_RES)
+#pragma unroll
+                            for (int j = 0; j < 4; ++j) o[j] = rv[j] + o[j];
                         __builtin_nontemporal_store(o, (f32x4_t*)((float*)y + m * N + ncol));
                     } else {
                         uint32_t b[4];
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) b[j] = bf16_bits_rne(flush_subnormal(v[j]));
+                        for (int j = 0; j < 4; ++j) {
+                            b[j] = bf16_bits_rne(flush_subnormal(v[j]));
+                            if (HAS_RES) b[j] = bf16_bits_rne(rv[j] + __uint_as_float(b[j] << 16));
+                        }
                         if (OUT_MODE == NCM_OUT_BF16_F32) {
                             u32x4_t o;
                             o[0] = b[0] << 16; o[1] = b[1] << 16; o[2] = b[2] << 16; o[3] = b[3] << 16;
@@ -112,9 +126,10 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
                 float v = acc.v[mb][nb][i];
                 if (HAS_BIAS) v = v + bv;
                 if (OUT_MODE == NCM_OUT_F32) {
-                    ((float*)y)[m * N + n] = v;
+                    ((float*)y)[m * N + n] = HAS_RES ? residual[m * N + n] + v : v;
                 } else {
-                    const uint32_t bits = bf16_bits_rne(flush_subnormal(v));
+                    uint32_t bits = bf16_bits_rne(flush_subnormal(v));
+                    if (HAS_RES) bits = bf16_bits_rne(residual[m * N + n] + __uint_as_float(bits << 16));
                     if (OUT_MODE == NCM_OUT_BF16_F32)
                         ((float*)y)[m * N + n] = __uint_as_float(bits << 16);
                     else
@@ -125,10 +140,11 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
     }
 }
 
-template <class S, int OUT_MODE, bool HAS_BIAS>
+template <class S, int OUT_MODE, bool HAS_BIAS, bool HAS_RES = false>
 static hipError_t launch_linear_t(const void* x, const void* w, const uint16_t* bias, void* y,
-                                  int64_t M, int64_t K, int64_t N, hipStream_t stream) {
-    auto kern = linear_kernel<S, OUT_MODE, HAS_BIAS>;
+                                  int64_t M, int64_t K, int64_t N, hipStream_t stream,
+                                  const float* residual = nullptr) {
+    auto kern = linear_kernel<S, OUT_MODE, HAS_BIAS, HAS_RES>;
     static bool attr_set = false;
     if (!attr_set) {
         hipError_t e = hipFuncSetAttribute((const void*)kern,
@@ -141,7 +157,7 @@ static hipError_t launch_linear_t(const void* x, const void* w, const uint16_t* 
     const int tiles_n = (int)((N + S::BN - 1) / S::BN);
     const int group_m = tiles_m < 4 ? tiles_m : 4;
     hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(S::NT), S::LDS_BYTES, stream, x, w,
-                       bias, y, M, K, N, tiles_n, group_m);
+                       bias, y, M, K, N, tiles_n, group_m, residual);
     return hipGetLastError();
 }
 
@@ -230,6 +246,32 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
         case 8: return launch_linear_s<Lin8>(x, w, bias, y, M, K, N, out_mode, stream);
         case 9: return launch_linear_s<Lin9>(x, w, bias, y, M, K, N, out_mode, stream);
         default: return launch_linear_s<Lin10>(x, w, bias, y, M, K, N, out_mode, stream);
+    }
+}
+
+template <class S>
+static hipError_t launch_linear_res_s(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                      const float* res, void* y, int64_t M, int64_t K, int64_t N,
+                                      int out_mode, hipStream_t st) {
+    const bool hb = bias != nullptr;
+#define NCM_LINR(MODE, HB) launch_linear_t<S, MODE, HB, true>(x, w, bias, y, M, K, N, st, res)
+    switch (out_mode) {
+        case NCM_OUT_F32: return hb ? NCM_LINR(NCM_OUT_F32, true) : NCM_LINR(NCM_OUT_F32, false);
+        case NCM_OUT_BF16_F32:
+            return hb ? NCM_LINR(NCM_OUT_BF16_F32, true) : NCM_LINR(NCM_OUT_BF16_F32, false);
+        default: return hb ? NCM_LINR(NCM_OUT_BF16, true) : NCM_LINR(NCM_OUT_BF16, false);
+    }
+#undef NCM_LINR
+}
+
+hipError_t launch_linear_residual(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                  const float* residual, void* y, int64_t M, int64_t K,
+                                  int64_t N, int out_mode, hipStream_t stream) {
+    // The automatic tile choice only (configurations 0-2).
+    switch (linear_tile_config(M, N, -1)) {
+        case 0: return launch_linear_res_s<Lin0>(x, w, bias, residual, y, M, K, N, out_mode, stream);
+        case 1: return launch_linear_res_s<Lin1>(x, w, bias, residual, y, M, K, N, out_mode, stream);
+        default: return launch_linear_res_s<Lin2>(x, w, bias, residual, y, M, K, N, out_mode, stream);
     }
 }
 

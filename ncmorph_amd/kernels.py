@@ -121,6 +121,30 @@ def linear_bf16(x, w, bias=None, out=None, out_mode: str = "f32", ctx=None):
     return out
 
 
+def linear_bf16_residual(x, w, residual, bias=None, out=None, out_mode: str = "bf16_f32",
+                         ctx=None):
+    """y = residual + x @ w.T (+ bias) in one pass: the projection followed by
+    the decoder's residual add (src/decoder.zig:279-282). residual: float32
+    [m, n]; out may be residual itself for the "f32" and "bf16_f32" modes."""
+    import torch
+
+    m, k = x.shape
+    n, k2 = w.shape
+    if k != k2 or tuple(residual.shape) != (m, n) or residual.dtype != torch.float32:
+        raise NcmError(-2, "linear_bf16_residual")
+    mode = _OUT_MODES[out_mode]
+    if out is None:
+        dt = torch.int16 if mode == NCM_OUT_BF16 else torch.float32
+        out = torch.empty((m, n), dtype=dt, device=x.device)
+    ctx = ctx or default_context(x.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_linear_bf16_residual(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
+                                         _dev_ptr(bias, "bias"), _dev_ptr(residual, "residual"),
+                                         _dev_ptr(out, "out"), m, k, n, mode),
+          "linear_bf16_residual")
+    return out
+
+
 def linear_f32(x, w, out=None, ctx=None):
     """y = x @ w.T with float32 operands [m, k] and [n, k] (k % 4 == 0) on
     the fp32 MFMA, on torch's current stream."""
@@ -195,4 +219,53 @@ def silu_mul(gate, up=None, out_mode: str = "bf16_f32", out=None, ctx=None):
     ctx.bind_stream()
     check(lib().ncm_silu_mul_dev(ctx.handle, _dev_ptr(gate, "gate"), _dev_ptr(up, "up"),
                                  _dev_ptr(out, "out"), gate.numel(), mode), "silu_mul")
+    return out
+
+
+def _rows_ptr(t, name):
+    """Pointer and row stride of a 2-D GPU tensor whose rows are contiguous
+    (a column slice of a wider buffer is allowed)."""
+    if not t.is_cuda or t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be a 2-D GPU tensor with contiguous rows")
+    return C.c_void_p(t.data_ptr()), t.stride(0)
+
+
+def rope_rotate(x, heads: int, head_dim: int, seq_len: int, cosine, sine, ctx=None):
+    """In-place bf16 RoPE (rotate_head, root.zig:615-634) of every head of
+    every row of x (torch.bfloat16 [rows, >= heads * head_dim], rows may be
+    strided); row r uses table row r % seq_len of cosine/sine (float32
+    [seq_len, head_dim])."""
+    ptr, stride = _rows_ptr(x, "x")
+    ctx = ctx or default_context(x.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_rope_rotate_dev(ctx.handle, ptr, x.shape[0], stride, heads, head_dim, seq_len,
+                                    _dev_ptr(cosine, "cosine"), _dev_ptr(sine, "sine")),
+          "rope_rotate")
+    return x
+
+
+def attention_bf16(q, k, v, batch: int, seq_len: int, q_heads: int, kv_heads: int,
+                   head_dim: int, window: int = 0, out_mode: str = "bf16_f32", out=None,
+                   ctx=None):
+    """Causal bf16 attention (root.zig:536-578) of `batch` sequences: q
+    [batch * seq_len, >= q_heads * head_dim], k and v [batch * seq_len,
+    >= kv_heads * head_dim], torch.bfloat16 with contiguous rows (column
+    slices of one q|k|v buffer are allowed)."""
+    import torch
+
+    qp, qs = _rows_ptr(q, "q")
+    kp, ks = _rows_ptr(k, "k")
+    vp_, vs = _rows_ptr(v, "v")
+    if ks != vs:
+        raise NcmError(-2, "attention_bf16: k and v row strides differ")
+    mode = _OUT_MODES[out_mode]
+    if out is None:
+        dt = torch.bfloat16 if mode == NCM_OUT_BF16 else torch.float32
+        out = torch.empty((batch * seq_len, q_heads * head_dim), dtype=dt, device=q.device)
+    op, os_ = _rows_ptr(out, "out")
+    ctx = ctx or default_context(q.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_attention_bf16_dev(ctx.handle, qp, kp, vp_, op, batch, seq_len, q_heads,
+                                       kv_heads, head_dim, qs, ks, os_, window, mode),
+          "attention_bf16")
     return out

@@ -662,3 +662,134 @@ void ncmo_silu_mul_bf16(const float* gate, const float* up, float* out, size_t n
         out[i] = ncmo_round_bf16(a * up[i]);
     }
 }
+
+static float maybe_round(float v, int bf16) { return bf16 ? ncmo_round_bf16(v) : v; }
+
+void ncmo_rotate_head(float* values, const float* cosine, const float* sine, size_t head_dim,
+                      int bf16) {
+    const size_t half = head_dim / 2;
+    for (size_t i = 0; i < half; ++i) {
+        const float first = values[i];
+        const float second = values[i + half];
+        const float cos_first = maybe_round(cosine[i], bf16);
+        const float sin_first = maybe_round(sine[i], bf16);
+        const float cos_second = maybe_round(cosine[i + half], bf16);
+        const float sin_second = maybe_round(sine[i + half], bf16);
+        const float left = maybe_round(first * cos_first, bf16);
+        const float right = maybe_round(-second * sin_first, bf16);
+        const float right2 = maybe_round(first * sin_second, bf16);
+        const float left2 = maybe_round(second * cos_second, bf16);
+        values[i] = maybe_round(left + right, bf16);
+        values[i + half] = maybe_round(left2 + right2, bf16);
+    }
+}
+
+void ncmo_causal_mask(size_t query_count, size_t key_count, size_t window, uint8_t* out) {
+    for (size_t q = 0; q < query_count; ++q)
+        for (size_t k = 0; k < key_count; ++k) {
+            const int causal = k <= q;
+            const int in_window = window == 0 || q < window || k > q - window;
+            out[q * key_count + k] = (uint8_t)(causal && in_window);
+        }
+}
+
+void ncmo_attention_core(const float* queries, const float* keys, const float* values,
+                         const uint8_t* mask, float* context, size_t tokens, size_t q_heads,
+                         size_t kv_heads, size_t head_dim, int bf16) {
+    const size_t qw = q_heads * head_dim, kvw = kv_heads * head_dim;
+    const size_t group = q_heads / kv_heads;
+    const float scale = 1.0f / sqrtf((float)head_dim);
+    float* scores = (float*)malloc(tokens * sizeof(float));
+    float* probs = (float*)malloc(tokens * sizeof(float));
+    for (size_t qi = 0; qi < tokens; ++qi)
+        for (size_t h = 0; h < q_heads; ++h) {
+            const float* q = queries + qi * qw + h * head_dim;
+            const size_t kvh = h / group;
+            int any = 0;
+            for (size_t ki = 0; ki < tokens; ++ki) {
+                if (!mask[qi * tokens + ki]) {
+                    scores[ki] = -INFINITY;
+                    continue;
+                }
+                any = 1;
+                const float* k = keys + ki * kvw + kvh * head_dim;
+                float score = 0.0f;
+                for (size_t d = 0; d < head_dim; ++d) {
+                    const float p = q[d] * k[d];
+                    score = score + p;
+                }
+                const float sv = maybe_round(score, bf16);
+                scores[ki] = maybe_round(sv * scale, bf16);
+            }
+            if (any) {
+                float mx = scores[0];
+                for (size_t ki = 1; ki < tokens; ++ki) mx = scores[ki] > mx ? scores[ki] : mx;
+                float sum = 0.0f;
+                for (size_t ki = 0; ki < tokens; ++ki) {
+                    probs[ki] = expf(scores[ki] - mx);
+                    sum = sum + probs[ki];
+                }
+                for (size_t ki = 0; ki < tokens; ++ki) probs[ki] = probs[ki] / sum;
+                if (bf16)
+                    for (size_t ki = 0; ki < tokens; ++ki) probs[ki] = ncmo_round_bf16(probs[ki]);
+            } else {
+                for (size_t ki = 0; ki < tokens; ++ki) probs[ki] = 0.0f;
+            }
+            float* out = context + qi * qw + h * head_dim;
+            for (size_t d = 0; d < head_dim; ++d) {
+                float sum = 0.0f;
+                for (size_t ki = 0; ki < tokens; ++ki) {
+                    const float p = probs[ki] * values[ki * kvw + kvh * head_dim + d];
+                    sum = sum + p;
+                }
+                out[d] = maybe_round(sum, bf16);
+            }
+        }
+    free(scores);
+    free(probs);
+}
+
+void ncmo_rope_default_frequencies(size_t head_dim, float theta, float* inv) {
+    const float hd = (float)head_dim;
+    for (size_t i = 0; i < head_dim / 2; ++i) {
+        const float exponent = (float)(2 * i) / hd;
+        inv[i] = 1.0f / powf(theta, exponent);
+    }
+}
+
+void ncmo_rope_llama3(size_t head_dim, float theta, float factor, float low_freq_factor,
+                      float high_freq_factor, size_t original_max_positions, float* inv) {
+    ncmo_rope_default_frequencies(head_dim, theta, inv);
+    const float old_context_len = (float)original_max_positions;
+    const float low_wavelen = (float)((double)original_max_positions / (double)low_freq_factor);
+    const float high_wavelen = (float)((double)original_max_positions / (double)high_freq_factor);
+    const float two_pi = (float)(2.0 * 3.14159265358979323846);
+    for (size_t i = 0; i < head_dim / 2; ++i) {
+        const float f = inv[i];
+        const float wavelen = two_pi / f;
+        const float llama = wavelen > low_wavelen ? f / factor : f;
+        const float smooth =
+            (old_context_len / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor);
+        const float a = (1.0f - smooth) * llama;
+        const float b = smooth * llama;
+        const float smoothed = a / factor + b;
+        const int medium = !(wavelen < high_wavelen) && !(wavelen > low_wavelen);
+        inv[i] = medium ? smoothed : llama;
+    }
+}
+
+void ncmo_rope_tables(const float* inv, size_t half, size_t positions, float* cosine,
+                      float* sine) {
+    const size_t hd = 2 * half;
+    for (size_t p = 0; p < positions; ++p) {
+        const float pf = (float)p;
+        for (size_t i = 0; i < half; ++i) {
+            const float angle = pf * inv[i];
+            const float c = cosf(angle), s = sinf(angle);
+            cosine[p * hd + i] = c;
+            cosine[p * hd + half + i] = c;
+            sine[p * hd + i] = s;
+            sine[p * hd + half + i] = s;
+        }
+    }
+}

@@ -124,6 +124,34 @@ void ncmo_silu_bf16(const float* x, float* out, size_t n);
  * round_bf16(silu_bf16(gate) * up). */
 void ncmo_silu_mul_bf16(const float* gate, const float* up, float* out, size_t n);
 
+/* rotate_head (root.zig:615-634): rotate-half RoPE of one head in place;
+ * bf16 != 0 rounds the table entries, each product and each sum to bf16. */
+void ncmo_rotate_head(float* values, const float* cosine, const float* sine, size_t head_dim,
+                      int bf16);
+/* causal_mask (root.zig:380-399) for positions 0..count-1; window 0 = none.
+ * out[q * key_count + k] = 1 where key k may contribute to query q. */
+void ncmo_causal_mask(size_t query_count, size_t key_count, size_t window, uint8_t* out);
+/* The attention of attention_impl (root.zig:536-578) after the projections,
+ * the optional QK norm and the rotation: per query and head, scores
+ * round(round(q.k) * 1/sqrt(head_dim)) (sequential fp32 dot), masked keys
+ * -inf, softmax (root.zig:272-284: max, exp(s - max), sequential sum,
+ * divide), probabilities rounded to bf16, context round(sum_k p v)
+ * (sequential in key order). Key/value head = query head / (q_heads /
+ * kv_heads). bf16 = 0: no roundings (the f32 path). Rows of queries and
+ * context are [q_heads * head_dim], of keys and values [kv_heads * head_dim]. */
+/* RoPE tables, host libm (root.zig:305-348, 636-682; system powf, cosf and
+ * sinf as the reference links them). inv has head_dim / 2 entries; the
+ * tables are [positions, 2 * half] with each angle's value duplicated into
+ * both halves. */
+void ncmo_rope_default_frequencies(size_t head_dim, float theta, float* inv);
+void ncmo_rope_llama3(size_t head_dim, float theta, float factor, float low_freq_factor,
+                      float high_freq_factor, size_t original_max_positions, float* inv);
+void ncmo_rope_tables(const float* inv, size_t half, size_t positions, float* cosine,
+                      float* sine);
+void ncmo_attention_core(const float* queries, const float* keys, const float* values,
+                         const uint8_t* mask, float* context, size_t tokens, size_t q_heads,
+                         size_t kv_heads, size_t head_dim, int bf16);
+
 #ifdef __cplusplus
 }
 #endif

@@ -75,6 +75,12 @@ def lib():
         L.ncmo_rms_norm.argtypes = [f32p, f32p, f32p, sz, C.c_float, C.c_int]
         L.ncmo_silu_bf16.argtypes = [f32p, f32p, sz]
         L.ncmo_silu_mul_bf16.argtypes = [f32p, f32p, f32p, sz]
+        L.ncmo_rotate_head.argtypes = [f32p, f32p, f32p, sz, C.c_int]
+        L.ncmo_causal_mask.argtypes = [sz, sz, sz, u8p]
+        L.ncmo_rope_default_frequencies.argtypes = [sz, C.c_float, f32p]
+        L.ncmo_rope_llama3.argtypes = [sz, C.c_float, C.c_float, C.c_float, C.c_float, sz, f32p]
+        L.ncmo_rope_tables.argtypes = [f32p, sz, sz, f32p, f32p]
+        L.ncmo_attention_core.argtypes = [f32p, f32p, f32p, u8p, f32p, sz, sz, sz, sz, C.c_int]
         _lib = L
     return _lib
 
@@ -273,3 +279,67 @@ def silu_mul_bf16(gate, up) -> np.ndarray:
     out = np.empty_like(g)
     lib().ncmo_silu_mul_bf16(g.ravel(), u.ravel(), out.ravel(), g.size)
     return out
+
+
+def rotate_heads(x, cosine, sine, heads: int, head_dim: int, bf16: bool = True) -> np.ndarray:
+    """rotate_head (root.zig:615-634) applied to every head of every row of
+    x [rows, heads * head_dim]; row r uses table row r of cosine/sine
+    [rows, head_dim]. Returns a new array."""
+    out = np.array(x, np.float32, copy=True).reshape(-1, heads * head_dim)
+    cos = np.ascontiguousarray(cosine, np.float32).reshape(-1, head_dim)
+    sin = np.ascontiguousarray(sine, np.float32).reshape(-1, head_dim)
+    for r in range(out.shape[0]):
+        for h in range(heads):
+            seg = np.ascontiguousarray(out[r, h * head_dim:(h + 1) * head_dim])
+            lib().ncmo_rotate_head(seg, np.ascontiguousarray(cos[r]), np.ascontiguousarray(sin[r]),
+                                   head_dim, 1 if bf16 else 0)
+            out[r, h * head_dim:(h + 1) * head_dim] = seg
+    return out
+
+
+def causal_mask(count: int, window: int = 0) -> np.ndarray:
+    """causal_mask (root.zig:380-399) for positions 0..count-1, uint8 [count, count]."""
+    out = np.empty((count, count), np.uint8)
+    lib().ncmo_causal_mask(count, count, window, out)
+    return out
+
+
+def attention_core(q, k, v, mask, q_heads: int, kv_heads: int, head_dim: int,
+                   bf16: bool = True) -> np.ndarray:
+    """Scores, softmax and context of attention_impl (root.zig:536-578) for
+    one sequence: q [T, q_heads * head_dim], k/v [T, kv_heads * head_dim]."""
+    q = np.ascontiguousarray(q, np.float32)
+    k = np.ascontiguousarray(k, np.float32)
+    v = np.ascontiguousarray(v, np.float32)
+    t = q.shape[0]
+    m = np.ascontiguousarray(mask, np.uint8)
+    out = np.empty((t, q_heads * head_dim), np.float32)
+    lib().ncmo_attention_core(q, k, v, m, out, t, q_heads, kv_heads, head_dim, 1 if bf16 else 0)
+    return out
+
+
+def rope_default_frequencies(head_dim: int, theta: float) -> np.ndarray:
+    """Inverse frequencies of rope_default (root.zig:305-326, 676-682)."""
+    out = np.empty(head_dim // 2, np.float32)
+    lib().ncmo_rope_default_frequencies(head_dim, theta, out)
+    return out
+
+
+def rope_llama3(head_dim: int, theta: float, factor: float, low_freq_factor: float,
+                high_freq_factor: float, original_max_positions: int) -> np.ndarray:
+    """Llama 3 adjusted inverse frequencies (root.zig:636-674)."""
+    out = np.empty(head_dim // 2, np.float32)
+    lib().ncmo_rope_llama3(head_dim, theta, factor, low_freq_factor, high_freq_factor,
+                           original_max_positions, out)
+    return out
+
+
+def rope_tables(inv, positions: int):
+    """Duplicated rotate-half cosine and sine tables (root.zig:328-348),
+    each [positions, 2 * len(inv)]."""
+    inv = np.ascontiguousarray(inv, np.float32)
+    half = inv.size
+    cos = np.empty((positions, 2 * half), np.float32)
+    sin = np.empty((positions, 2 * half), np.float32)
+    lib().ncmo_rope_tables(inv, half, positions, cos, sin)
+    return cos, sin
