@@ -201,6 +201,61 @@ int ncm_attention_bf16_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
                            int q_heads, int kv_heads, int head_dim, int64_t q_stride,
                            int64_t kv_stride, int64_t out_stride, int64_t window, int out_mode);
 
+/* ---- bf16 decoder prefill forward (src/decoder.zig:62-228) ---- */
+
+/* Model shape (config.spec_t fields the forward reads). window: sliding
+ * window, 0 = none. */
+typedef struct ncm_decoder_shape {
+    int64_t hidden;        /* hidden_size */
+    int64_t intermediate;  /* intermediate_size */
+    int64_t vocab;         /* vocab_size */
+    int32_t q_heads;       /* num_attention_heads */
+    int32_t kv_heads;      /* num_key_value_heads */
+    int32_t head_dim;      /* 64 or 128 */
+    int32_t layers;        /* num_hidden_layers */
+    int64_t window;        /* sliding_window, 0 = none */
+    float rms_eps;         /* rms_norm_eps */
+} ncm_decoder_shape_t;
+
+/* One layer's device weights (bf16 bits unless stated). The projections the
+ * reference keeps separate (attention_weights_t, root.zig:351-362; the MLP
+ * weights of decoder.zig) are row-concatenated: qkv_weight holds the q rows
+ * [q_heads * head_dim], then the k rows, then the v rows [kv_heads *
+ * head_dim each], each row `hidden` wide; gate_up_weight holds the gate rows
+ * [intermediate] then the up rows. Biases follow the same row order; NULL =
+ * no bias. */
+typedef struct ncm_decoder_layer {
+    const float* input_norm;           /* [hidden] */
+    const uint16_t* qkv_weight;        /* [(q_heads + 2 kv_heads) head_dim, hidden] */
+    const uint16_t* qkv_bias;          /* [(q_heads + 2 kv_heads) head_dim] or NULL */
+    const uint16_t* o_weight;          /* [hidden, q_heads head_dim] */
+    const uint16_t* o_bias;            /* [hidden] or NULL */
+    const float* post_attention_norm;  /* [hidden] */
+    const uint16_t* gate_up_weight;    /* [2 intermediate, hidden] */
+    const uint16_t* gate_up_bias;      /* [2 intermediate] or NULL */
+    const uint16_t* down_weight;       /* [hidden, intermediate] */
+    const uint16_t* down_bias;         /* [hidden] or NULL */
+} ncm_decoder_layer_t;
+
+/* Bf16 prefill forward of `batch` sequences of seq_len tokens each (the
+ * reference's forward, decoder.zig:62-228 with bf16_compute, applied to each
+ * sequence; positions restart at 0 in every sequence). token_ids: HOST int64
+ * [batch * seq_len], each < vocab (else NCM_E_ARG, the reference's
+ * TokenIdOutOfRange). layers: HOST array [shape->layers] of device weight
+ * pointers. embed: bf16 [vocab, hidden]; lm_head: bf16 [vocab, hidden] or
+ * NULL for tied embeddings; final_norm: float [hidden]; cosine, sine: float
+ * [seq_len, head_dim] RoPE tables (rope_tables layout, root.zig:328-348,
+ * built on the host with the system libm as the reference does). logits:
+ * float [batch * seq_len, vocab] (bf16 values, token-major). Intermediates
+ * live in the context's workspace. No QK norm (Llama / Mistral / Qwen2
+ * layouts). Linear outputs, scores and P V are summed in MFMA order, so
+ * logits agree with the reference within bf16 tolerance, not bit for bit. */
+int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
+                            const ncm_decoder_layer_t* layers, const uint16_t* embed,
+                            const float* final_norm, const uint16_t* lm_head,
+                            const float* cosine, const float* sine, const int64_t* token_ids,
+                            int64_t batch, int64_t seq_len, float* logits);
+
 /* ---- multiscale residual vector quantization ---- */
 
 /* csq[l * v + k] = squared norm of codebook row (l, k), in the fixed fp32

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "../../include/ncmorph_amd.h"
+#include "decoder.h"
 #include "linear.h"
 #include "rvq.h"
 
@@ -304,6 +305,49 @@ int ncm_attention_bf16_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
                                               head_dim, q_stride, kv_stride, out_stride, window,
                                               out_mode, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "attention launch");
+    return NCM_OK;
+}
+
+int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
+                            const ncm_decoder_layer_t* layers, const uint16_t* embed,
+                            const float* final_norm, const uint16_t* lm_head,
+                            const float* cosine, const float* sine, const int64_t* token_ids,
+                            int64_t batch, int64_t seq_len, float* logits) {
+    if (!ctx || !shape) return NCM_E_NULL;
+    const ncm_decoder_shape_t& s = *shape;
+    if (batch < 0 || seq_len < 0) return NCM_E_SHAPE;
+    if (batch == 0 || seq_len == 0) return NCM_E_ARG;  // EmptyInput
+    if (s.hidden <= 0 || s.intermediate <= 0 || s.vocab <= 0 || s.layers < 0 || s.window < 0)
+        return NCM_E_SHAPE;
+    if (s.q_heads <= 0 || s.kv_heads <= 0 || s.q_heads % s.kv_heads) return NCM_E_SHAPE;
+    if (s.head_dim != 64 && s.head_dim != 128) return NCM_E_SHAPE;
+    if (s.hidden % 8 || s.intermediate % 8) return NCM_E_SHAPE;
+    if (s.hidden > (int64_t(1) << 21) || s.intermediate > (int64_t(1) << 20) ||
+        s.vocab > (int64_t(1) << 31) || (int64_t)s.q_heads * s.head_dim > (int64_t(1) << 21))
+        return NCM_E_SHAPE;
+    if (batch > 65535 || batch * seq_len > (int64_t(1) << 31)) return NCM_E_SHAPE;
+    if (!embed || !final_norm || !cosine || !sine || !token_ids || !logits) return NCM_E_NULL;
+    if (s.layers > 0 && !layers) return NCM_E_NULL;
+    if ((uintptr_t)embed % 16 || (lm_head && (uintptr_t)lm_head % 16)) return NCM_E_ARG;
+    for (int l = 0; l < s.layers; ++l) {
+        const ncm_decoder_layer_t& L = layers[l];
+        if (!L.input_norm || !L.qkv_weight || !L.o_weight || !L.post_attention_norm ||
+            !L.gate_up_weight || !L.down_weight)
+            return NCM_E_NULL;
+        if ((uintptr_t)L.qkv_weight % 16 || (uintptr_t)L.o_weight % 16 ||
+            (uintptr_t)L.gate_up_weight % 16 || (uintptr_t)L.down_weight % 16)
+            return NCM_E_ARG;
+    }
+    for (int64_t i = 0; i < batch * seq_len; ++i)
+        if (token_ids[i] < 0 || token_ids[i] >= s.vocab) return NCM_E_ARG;  // TokenIdOutOfRange
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::decoder_workspace_bytes(s, batch, seq_len), &ws);
+    if (rc) return rc;
+    hipError_t e = ncm::decoder_forward(s, layers, embed, final_norm, lm_head, cosine, sine,
+                                        token_ids, batch, seq_len, logits, ws, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "decoder forward");
     return NCM_OK;
 }
 

@@ -1,0 +1,172 @@
+// The bf16 decoder prefill forward of src/decoder.zig:62-228 on one GPU:
+// stream-ordered launches of the linear, RMSNorm, RoPE, attention and MLP
+// kernels over a batch of equal-length sequences, with every intermediate
+// resident in the context's workspace. Per layer (bf16 mode):
+//   n   = rms_norm_bf16(h, input_norm)                 -> bf16 bits
+//   qkv = n W_qkv^T (+ b)                              -> bf16 bits, one GEMM
+//   rotate q and k heads (RoPE tables row = position in the sequence)
+//   c   = attention(q, k, v)                           -> bf16 bits
+//   h   = round(h + round(c W_o^T (+ b)))              (fused residual)
+//   n   = rms_norm_bf16(h, post_attention_norm)
+//   gu  = n W_gate_up^T (+ b)                          -> bf16 bits, one GEMM
+//   a   = round(silu_bf16(gate) * up)
+//   h   = round(h + round(a W_down^T (+ b)))           (fused residual)
+// then logits = round(rms_norm_bf16(h, final_norm) W_head^T).
+// The reference runs q, k and v (and gate and up) as separate projections of
+// the same input; one GEMM over the row-concatenated weights computes each
+// output column by the same dot product.
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+#include "decoder.h"
+#include "linear.h"
+
+namespace ncm {
+
+// hidden[r] = widened embed[ids[r]] (bf16 -> f32 is exact, so the
+// reference's round_bf16 of the embedding rows is the identity here).
+__global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* __restrict__ ids,
+                                                         const uint16_t* __restrict__ table,
+                                                         float* __restrict__ hidden,
+                                                         int64_t width) {
+    const int64_t r = blockIdx.y;
+    const uint16_t* src = table + ids[r] * width;
+    float* dst = hidden + r * width;
+    for (int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 2; i < width;
+         i += (int64_t)gridDim.x * 512) {
+        if (i + 1 < width) {
+            const uint32_t p = *(const uint32_t*)(src + i);
+            dst[i] = __uint_as_float(p << 16);
+            dst[i + 1] = __uint_as_float(p & 0xFFFF0000u);
+        } else {
+            dst[i] = __uint_as_float((uint32_t)src[i] << 16);
+        }
+    }
+}
+
+// act[r, j] = round(round(silu(g)) * u), g = gu[r, j], u = gu[r, inter + j]
+// (src/decoder.zig:210-211 on the bf16 gate and up projections).
+__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t* __restrict__ gu,
+                                                            uint16_t* __restrict__ act,
+                                                            int64_t rows, int64_t inter) {
+    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
+    if (idx >= rows * inter) return;
+    const int64_t r = idx / inter, j = idx % inter;
+    const uint16_t* g = gu + r * 2 * inter + j;
+    const uint16_t* u = g + inter;
+    auto act1 = [](uint32_t gb, uint32_t ub) {
+        const float v = __uint_as_float(gb << 16);
+        const float a = __uint_as_float(bf16_bits_rne(v / (1.0f + expf(-v))) << 16);
+        return bf16_bits_rne(a * __uint_as_float(ub << 16));
+    };
+    if (j + 4 <= inter && (inter & 3) == 0) {
+        const u32x2_t gv = *(const u32x2_t*)g, uv = *(const u32x2_t*)u;
+        u32x2_t o;
+        o[0] = act1(gv[0] & 0xFFFFu, uv[0] & 0xFFFFu) | (act1(gv[0] >> 16, uv[0] >> 16) << 16);
+        o[1] = act1(gv[1] & 0xFFFFu, uv[1] & 0xFFFFu) | (act1(gv[1] >> 16, uv[1] >> 16) << 16);
+        *(u32x2_t*)(act + idx) = o;
+    } else {
+        for (int e = 0; e < 4 && idx + e < rows * inter; ++e) {
+            const int64_t re = (idx + e) / inter, je = (idx + e) % inter;
+            const uint16_t* ge = gu + re * 2 * inter + je;
+            act[idx + e] = (uint16_t)act1(ge[0], ge[inter]);
+        }
+    }
+}
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+struct Plan {
+    int64_t T, qkv_w, q_w;
+    size_t o_hidden, o_normed, o_qkv, o_ctx, o_gu, o_act, o_ids, total;
+};
+
+Plan plan(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq) {
+    Plan p;
+    p.T = batch * seq;
+    p.q_w = (int64_t)s.q_heads * s.head_dim;
+    p.qkv_w = (int64_t)(s.q_heads + 2 * s.kv_heads) * s.head_dim;
+    size_t off = 0;
+    p.o_hidden = off; off += up((size_t)p.T * s.hidden * 4);
+    p.o_normed = off; off += up((size_t)p.T * s.hidden * 2);
+    p.o_qkv = off;    off += up((size_t)p.T * p.qkv_w * 2);
+    p.o_ctx = off;    off += up((size_t)p.T * p.q_w * 2);
+    p.o_gu = off;     off += up((size_t)p.T * 2 * s.intermediate * 2);
+    p.o_act = off;    off += up((size_t)p.T * s.intermediate * 2);
+    p.o_ids = off;    off += up((size_t)p.T * 8);
+    p.total = off;
+    return p;
+}
+
+}  // namespace
+
+size_t decoder_workspace_bytes(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq) {
+    return plan(s, batch, seq).total;
+}
+
+#define NCM_TRY(call)                                  \
+    do {                                               \
+        hipError_t e_ = (call);                        \
+        if (e_ != hipSuccess) return e_;               \
+    } while (0)
+
+hipError_t decoder_forward(const ncm_decoder_shape_t& s, const ncm_decoder_layer_t* layers,
+                           const uint16_t* embed, const float* final_norm,
+                           const uint16_t* lm_head, const float* cosine, const float* sine,
+                           const int64_t* host_ids, int64_t batch, int64_t seq, float* logits,
+                           void* ws, hipStream_t st) {
+    const Plan p = plan(s, batch, seq);
+    char* w = (char*)ws;
+    float* hidden = (float*)(w + p.o_hidden);
+    uint16_t* normed = (uint16_t*)(w + p.o_normed);
+    uint16_t* qkv = (uint16_t*)(w + p.o_qkv);
+    uint16_t* ctxb = (uint16_t*)(w + p.o_ctx);
+    uint16_t* gu = (uint16_t*)(w + p.o_gu);
+    uint16_t* act = (uint16_t*)(w + p.o_act);
+    int64_t* ids = (int64_t*)(w + p.o_ids);
+    const int64_t T = p.T, H = s.hidden, I = s.intermediate;
+    const int hd = s.head_dim;
+
+    NCM_TRY(hipMemcpyAsync(ids, host_ids, (size_t)T * 8, hipMemcpyHostToDevice, st));
+    {
+        const unsigned gx = (unsigned)((H + 511) / 512 < 8 ? (H + 511) / 512 : 8);
+        hipLaunchKernelGGL(embed_rows_kernel, dim3(gx, (unsigned)T), dim3(256), 0, st, ids, embed,
+                           hidden, H);
+        NCM_TRY(hipGetLastError());
+    }
+    for (int l = 0; l < s.layers; ++l) {
+        const ncm_decoder_layer_t& L = layers[l];
+        NCM_TRY(launch_rms_norm_rows(hidden, L.input_norm, normed, T, H, s.rms_eps, NCM_OUT_BF16,
+                                     st));
+        NCM_TRY(launch_linear(normed, L.qkv_weight, L.qkv_bias, qkv, T, H, p.qkv_w, NCM_OUT_BF16,
+                              -1, st));
+        NCM_TRY(launch_rope_rotate(qkv, T, p.qkv_w, s.q_heads, hd, seq, cosine, sine, st));
+        NCM_TRY(launch_rope_rotate(qkv + p.q_w, T, p.qkv_w, s.kv_heads, hd, seq, cosine, sine,
+                                   st));
+        NCM_TRY(launch_attention_bf16(qkv, qkv + p.q_w, qkv + p.q_w + (int64_t)s.kv_heads * hd,
+                                      ctxb, batch, seq, s.q_heads, s.kv_heads, hd, p.qkv_w,
+                                      p.qkv_w, p.q_w, s.window, NCM_OUT_BF16, st));
+        NCM_TRY(launch_linear_residual(ctxb, L.o_weight, L.o_bias, hidden, hidden, T, p.q_w, H,
+                                       NCM_OUT_BF16_F32, st));
+        NCM_TRY(launch_rms_norm_rows(hidden, L.post_attention_norm, normed, T, H, s.rms_eps,
+                                     NCM_OUT_BF16, st));
+        NCM_TRY(launch_linear(normed, L.gate_up_weight, L.gate_up_bias, gu, T, H, 2 * I,
+                              NCM_OUT_BF16, -1, st));
+        {
+            const int64_t n4 = (T * I + 3) / 4;
+            hipLaunchKernelGGL(silu_mul_rows_kernel, dim3((unsigned)((n4 + 255) / 256)),
+                               dim3(256), 0, st, gu, act, T, I);
+            NCM_TRY(hipGetLastError());
+        }
+        NCM_TRY(launch_linear_residual(act, L.down_weight, L.down_bias, hidden, hidden, T, I, H,
+                                       NCM_OUT_BF16_F32, st));
+    }
+    NCM_TRY(launch_rms_norm_rows(hidden, final_norm, normed, T, H, s.rms_eps, NCM_OUT_BF16, st));
+    return launch_linear(normed, lm_head ? lm_head : embed, nullptr, logits, T, H, s.vocab,
+                         NCM_OUT_BF16_F32, -1, st);
+}
+
+}  // namespace ncm

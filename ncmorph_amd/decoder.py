@@ -1,0 +1,205 @@
+"""Bf16 decoder prefill forward on the GPU (src/decoder.zig:62-228).
+
+The forward itself is one C-ABI call (ncm_decoder_forward_dev) that
+stream-orders the device kernels; this module holds the model description,
+device weights in the layout that call reads (q|k|v and gate|up rows
+concatenated), random initialisation for synthetic runs, and the RoPE
+tables, which the reference builds on the host with the system libm
+(packages/kernels/root.zig:305-348, 636-682) and which are built the same
+way here.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import ctypes.util
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from ._lib import check, lib
+from .context import default_context
+
+
+@dataclass
+class DecoderSpec:
+    """The config.spec_t fields the bf16 forward reads."""
+
+    hidden: int
+    intermediate: int
+    vocab: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    layers: int
+    rms_eps: float = 1e-5
+    window: int = 0
+    rope_theta: float = 500000.0
+    # Llama 3 RoPE scaling (factor, low_freq_factor, high_freq_factor,
+    # original_max_position_embeddings); None = default RoPE.
+    rope_llama3: tuple | None = (32.0, 1.0, 4.0, 8192)
+    tie_word_embeddings: bool = True
+
+    @property
+    def qkv_width(self) -> int:
+        return (self.q_heads + 2 * self.kv_heads) * self.head_dim
+
+
+LLAMA_3_2_1B = DecoderSpec(hidden=2048, intermediate=8192, vocab=128256, q_heads=32, kv_heads=8,
+                           head_dim=64, layers=16)
+
+
+class _Shape(C.Structure):
+    _fields_ = [("hidden", C.c_int64), ("intermediate", C.c_int64), ("vocab", C.c_int64),
+                ("q_heads", C.c_int32), ("kv_heads", C.c_int32), ("head_dim", C.c_int32),
+                ("layers", C.c_int32), ("window", C.c_int64), ("rms_eps", C.c_float)]
+
+
+_LAYER_FIELDS = ("input_norm", "qkv_weight", "qkv_bias", "o_weight", "o_bias",
+                 "post_attention_norm", "gate_up_weight", "gate_up_bias", "down_weight",
+                 "down_bias")
+
+
+class _Layer(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _LAYER_FIELDS]
+
+
+@dataclass
+class DecoderWeights:
+    """Device weights: bf16 tensors for projections and embeddings, float32
+    for norm scales. layers[i] maps the _LAYER_FIELDS names to tensors (the
+    bias entries may be None)."""
+
+    embed: object
+    final_norm: object
+    layers: list = field(default_factory=list)
+    lm_head: object = None
+
+
+def random_weights(spec: DecoderSpec, device, seed: int = 0, std: float = 0.02,
+                   norm_std: float = 0.0, bias_std: float = 0.0) -> DecoderWeights:
+    """Random-init weights of spec's shape, ~N(0, std) in bf16, on device.
+    Norm scales are 1 (+ N(0, norm_std)); biases are present when bias_std > 0."""
+    import torch
+
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+
+    def w(*shape, s=std):
+        return (torch.randn(*shape, generator=g, device=device) * s).to(torch.bfloat16)
+
+    def norm():
+        v = torch.ones(spec.hidden, device=device)
+        if norm_std:
+            v = v + torch.randn(spec.hidden, generator=g, device=device) * norm_std
+        return v.contiguous()
+
+    layers = []
+    for _ in range(spec.layers):
+        layer = {
+            "input_norm": norm(),
+            "qkv_weight": w(spec.qkv_width, spec.hidden),
+            "qkv_bias": w(spec.qkv_width, s=bias_std) if bias_std else None,
+            "o_weight": w(spec.hidden, spec.q_heads * spec.head_dim),
+            "o_bias": w(spec.hidden, s=bias_std) if bias_std else None,
+            "post_attention_norm": norm(),
+            "gate_up_weight": w(2 * spec.intermediate, spec.hidden),
+            "gate_up_bias": w(2 * spec.intermediate, s=bias_std) if bias_std else None,
+            "down_weight": w(spec.hidden, spec.intermediate),
+            "down_bias": w(spec.hidden, s=bias_std) if bias_std else None,
+        }
+        layers.append(layer)
+    embed = w(spec.vocab, spec.hidden)
+    lm_head = None if spec.tie_word_embeddings else w(spec.vocab, spec.hidden)
+    return DecoderWeights(embed=embed, final_norm=norm(), layers=layers, lm_head=lm_head)
+
+
+_libm = None
+
+
+def _math_lib():
+    global _libm
+    if _libm is None:
+        m = C.CDLL(ctypes.util.find_library("m") or "libm.so.6")
+        for name, args in (("powf", [C.c_float, C.c_float]), ("cosf", [C.c_float]),
+                           ("sinf", [C.c_float])):
+            fn = getattr(m, name)
+            fn.restype = C.c_float
+            fn.argtypes = args
+        _libm = m
+    return _libm
+
+
+def rope_inverse_frequencies(spec: DecoderSpec) -> np.ndarray:
+    """Inverse frequencies in the reference's f32 operation order with the
+    system powf (root.zig:305-326, 636-682)."""
+    m = _math_lib()
+    f32 = np.float32
+    hd = spec.head_dim
+    inv = np.array([f32(1.0) / f32(m.powf(f32(spec.rope_theta), f32(2 * i) / f32(hd)))
+                    for i in range(hd // 2)], np.float32)
+    if spec.rope_llama3 is None:
+        return inv
+    factor, low, high, orig = (f32(spec.rope_llama3[0]), f32(spec.rope_llama3[1]),
+                               f32(spec.rope_llama3[2]), int(spec.rope_llama3[3]))
+    old_len = f32(orig)
+    low_wl = f32(orig / float(low))
+    high_wl = f32(orig / float(high))
+    two_pi = f32(2.0 * math.pi)
+    out = np.empty_like(inv)
+    for i, f in enumerate(inv):
+        wl = two_pi / f
+        llama = f / factor if wl > low_wl else f
+        smooth = (old_len / wl - low) / (high - low)
+        smoothed = (f32(1.0) - smooth) * llama / factor + smooth * llama
+        medium = not (wl < high_wl) and not (wl > low_wl)
+        out[i] = smoothed if medium else llama
+    return out
+
+
+def rope_tables(spec: DecoderSpec, positions: int):
+    """cosine, sine float32 [positions, head_dim] (root.zig:328-348), system
+    cosf / sinf of the f32 angle position * inverse frequency."""
+    m = _math_lib()
+    inv = rope_inverse_frequencies(spec)
+    half = inv.size
+    ang = np.arange(positions, dtype=np.float32)[:, None] * inv[None, :]
+    flat = ang.ravel()
+    c = np.fromiter((m.cosf(a) for a in flat.tolist()), np.float32, flat.size).reshape(ang.shape)
+    s = np.fromiter((m.sinf(a) for a in flat.tolist()), np.float32, flat.size).reshape(ang.shape)
+    return np.concatenate([c, c], axis=1), np.concatenate([s, s], axis=1)
+
+
+def _ptr(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine, logits=None,
+            ctx=None):
+    """Logits [batch * seq, vocab] (float32 holding bf16 values) of the bf16
+    prefill forward of every row of token_ids (int [batch, seq]); cosine and
+    sine: float32 device tensors [seq, head_dim]. Runs on torch's current
+    stream."""
+    import torch
+
+    ids = np.ascontiguousarray(token_ids, dtype=np.int64)
+    if ids.ndim != 2:
+        raise ValueError("token_ids must be [batch, seq]")
+    batch, seq = ids.shape
+    dev = weights.embed.device
+    if logits is None:
+        logits = torch.empty((batch * seq, spec.vocab), dtype=torch.float32, device=dev)
+    shape = _Shape(spec.hidden, spec.intermediate, spec.vocab, spec.q_heads, spec.kv_heads,
+                   spec.head_dim, spec.layers, spec.window, spec.rms_eps)
+    arr = (_Layer * max(1, spec.layers))()
+    for i, layer in enumerate(weights.layers):
+        arr[i] = _Layer(*[_ptr(layer.get(n)) for n in _LAYER_FIELDS])
+    ctx = ctx or default_context(dev.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_decoder_forward_dev(ctx.handle, C.byref(shape), arr, _ptr(weights.embed),
+                                        _ptr(weights.final_norm), _ptr(weights.lm_head),
+                                        _ptr(cosine), _ptr(sine),
+                                        ids.ctypes.data_as(C.c_void_p), batch, seq,
+                                        _ptr(logits)),
+          "decoder_forward")
+    return logits

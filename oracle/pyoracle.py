@@ -343,3 +343,44 @@ def rope_tables(inv, positions: int):
     sin = np.empty((positions, 2 * half), np.float32)
     lib().ncmo_rope_tables(inv, half, positions, cos, sin)
     return cos, sin
+
+
+def decoder_forward(ids, embed, layers, final_norm, lm_head, cos, sin, q_heads, kv_heads,
+                    head_dim, eps, window=0):
+    """forward_with_trace with bf16_compute (src/decoder.zig:62-228) for one
+    sequence, composed of the restatements above. Weights are float32
+    (bf16 values); each layer is a dict with input_norm, qkv_weight [(q_heads
+    + 2 kv_heads) head_dim, hidden] (the q, k and v projections' rows in that
+    order), qkv_bias, o_weight, o_bias, post_attention_norm, gate_up_weight
+    [2 intermediate, hidden] (gate rows then up rows), gate_up_bias,
+    down_weight, down_bias (biases may be None). lm_head None: tied to embed.
+    cos, sin: [len(ids), head_dim]."""
+    t = len(ids)
+    hidden = round_bf16(embed[np.asarray(ids)])
+    qw, kvw = q_heads * head_dim, kv_heads * head_dim
+    mask = causal_mask(t, window)
+
+    def proj(x, w, b, lo, hi):
+        return matmul_bf16(x, w[lo:hi], None if b is None else b[lo:hi])
+
+    for layer in layers:
+        n = rms_norm(hidden, layer["input_norm"], eps, bf16=True)
+        wq, bq = layer["qkv_weight"], layer.get("qkv_bias")
+        q = proj(n, wq, bq, 0, qw)
+        k = proj(n, wq, bq, qw, qw + kvw)
+        v = proj(n, wq, bq, qw + kvw, qw + 2 * kvw)
+        q = rotate_heads(q, cos, sin, q_heads, head_dim, bf16=True)
+        k = rotate_heads(k, cos, sin, kv_heads, head_dim, bf16=True)
+        ctx = attention_core(q, k, v, mask, q_heads, kv_heads, head_dim, bf16=True)
+        attn = matmul_bf16(ctx, layer["o_weight"], layer.get("o_bias"))
+        hidden = round_bf16(hidden + attn)
+        n = rms_norm(hidden, layer["post_attention_norm"], eps, bf16=True)
+        inter = layer["gate_up_weight"].shape[0] // 2
+        wg, bg = layer["gate_up_weight"], layer.get("gate_up_bias")
+        gate = proj(n, wg, bg, 0, inter)
+        up = proj(n, wg, bg, inter, 2 * inter)
+        act = silu_mul_bf16(gate, up)
+        mlp = matmul_bf16(act, layer["down_weight"], layer.get("down_bias"))
+        hidden = round_bf16(hidden + mlp)
+    n = rms_norm(hidden, final_norm, eps, bf16=True)
+    return matmul_bf16(n, embed if lm_head is None else lm_head)
