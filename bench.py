@@ -1,6 +1,6 @@
 """Benchmark of the ncmorph hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only linear|rvq]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only linear|rvq|decoder]
 
 A step is one pass of the bf16-weight linear over the three Llama-3.2-1B
 shapes: x bf16 [2048, K] ~N(0,1) times W^T with W bf16 [N, K] ~N(0, 0.02^2),
@@ -11,8 +11,9 @@ linear) with inputs resident in HBM.
 The same JSON line carries the multiscale RVQ encode at 16 x 2048 positions,
 d = 2048, 8 levels (strides 128..1), 4096 codes per level (input seed 1),
 timed separately and reported as tokens/s (input positions per second of a
-full encode including the reconstruction), plus the roofline fractions and
-CPU baselines of both.
+full encode including the reconstruction), and the bf16 decoder prefill
+forward of a random-init Llama-3.2-1B over 4 x 1024 tokens (tokens/s), each
+with its roofline fraction and CPU baseline.
 """
 from __future__ import annotations
 
@@ -176,6 +177,103 @@ def run_decoder_ops(torch, reps=20):
     return out
 
 
+DECODER_BATCH, DECODER_SEQ = 4, 1024
+
+
+def decoder_flops(spec, batch, seq):
+    """Algorithmic FLOPs of one bf16 prefill forward: 2 per multiply-add of
+    every projection and the LM head, plus the causal attention's QK^T and
+    PV over the allowed (query, key) pairs."""
+    t = batch * seq
+    per_layer = (spec.qkv_width * spec.hidden + spec.hidden * spec.q_heads * spec.head_dim
+                 + 2 * spec.intermediate * spec.hidden + spec.hidden * spec.intermediate)
+    linear = 2.0 * t * (spec.layers * per_layer + spec.vocab * spec.hidden)
+    pairs = batch * seq * (seq + 1) / 2
+    attention = spec.layers * spec.q_heads * 2 * (2.0 * pairs * spec.head_dim)
+    return linear, attention
+
+
+def run_decoder(torch, reps=10, warmup=3):
+    """Random-init Llama-3.2-1B bf16 prefill forward over 4 x 1024 token ids
+    (16 layers, hidden 2048, 32/8 heads of 64, SwiGLU 8192, vocab 128256,
+    weights ~N(0, 0.02), Llama 3 RoPE theta 500000), logits to HBM."""
+    from ncmorph_amd import decoder
+
+    dev = torch.device("cuda", 0)
+    spec = decoder.LLAMA_3_2_1B
+    w = decoder.random_weights(spec, dev, seed=11)
+    cos, sin = decoder.rope_tables(spec, DECODER_SEQ)
+    cd, sd = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    ids = np.random.default_rng(12).integers(0, spec.vocab, (DECODER_BATCH, DECODER_SEQ))
+    logits = torch.empty((DECODER_BATCH * DECODER_SEQ, spec.vocab), dtype=torch.float32,
+                         device=dev)
+    for _ in range(warmup):
+        decoder.forward(spec, w, ids, cd, sd, logits=logits)
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        decoder.forward(spec, w, ids, cd, sd, logits=logits)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / reps
+    lin, att = decoder_flops(spec, DECODER_BATCH, DECODER_SEQ)
+    tf = (lin + att) / sec / 1e12
+    tokens = DECODER_BATCH * DECODER_SEQ
+    return {"metric": "bf16 decoder prefill tokens/s", "value": round(tokens / sec, 1),
+            "unit": "tokens/s", "ms_per_forward": round(sec * 1e3, 3),
+            "config": {"workload": "random-init Llama-3.2-1B bf16 prefill forward, logits out",
+                       "batch": DECODER_BATCH, "seq_len": DECODER_SEQ, "layers": spec.layers,
+                       "hidden": spec.hidden, "heads": [spec.q_heads, spec.kv_heads],
+                       "head_dim": spec.head_dim, "intermediate": spec.intermediate,
+                       "vocab": spec.vocab},
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4),
+                         "flops_linear": lin, "flops_attention_causal": att}}
+
+
+def cpu_decoder_baseline():
+    """Oracle decoder (scalar restatements, 1 thread) of the same model shape
+    on 4 tokens: once with no layers and an LM head of 8192 vocabulary rows,
+    once with one layer added. The 16-layer, 128256-row forward is
+    extrapolated from the two (attention grows with the sequence and is
+    undercounted at 4 tokens; it is under 6% of the FLOPs at 1024)."""
+    from ncmorph_amd import decoder
+    from oracle import pyoracle
+
+    spec = decoder.LLAMA_3_2_1B
+    rng = np.random.default_rng(13)
+    rb = pyoracle.round_bf16
+
+    def w(*shape):
+        return rb((rng.standard_normal(shape, dtype=np.float32) * np.float32(0.02)))
+
+    tok, vocab_rows = 4, 8192
+    layer = dict(input_norm=np.ones(spec.hidden, np.float32),
+                 qkv_weight=w(spec.qkv_width, spec.hidden), qkv_bias=None,
+                 o_weight=w(spec.hidden, spec.q_heads * spec.head_dim), o_bias=None,
+                 post_attention_norm=np.ones(spec.hidden, np.float32),
+                 gate_up_weight=w(2 * spec.intermediate, spec.hidden), gate_up_bias=None,
+                 down_weight=w(spec.hidden, spec.intermediate), down_bias=None)
+    embed = w(vocab_rows, spec.hidden)
+    fn = np.ones(spec.hidden, np.float32)
+    cos, sin = decoder.rope_tables(spec, tok)
+    ids = rng.integers(0, vocab_rows, tok)
+    args = (spec.q_heads, spec.kv_heads, spec.head_dim, spec.rms_eps)
+    t0 = time.perf_counter()
+    pyoracle.decoder_forward(ids, embed, [], fn, None, cos, sin, *args)
+    t_head = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    pyoracle.decoder_forward(ids, embed, [layer], fn, None, cos, sin, *args)
+    t_layer = max(time.perf_counter() - t0 - t_head, 0.0)
+    per_forward = t_head * spec.vocab / vocab_rows + spec.layers * t_layer
+    return {"value": round(tok / per_forward, 4), "unit": "tokens/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{tok} tokens through the oracle decoder of the 1B shape with 0 and 1 "
+                      f"layers and an LM head of {vocab_rows} rows, 1 thread; 16 layers and "
+                      f"{spec.vocab} rows extrapolated"}
+
+
 def cpu_linear_baseline():
     """Oracle (scalar restatement of matmul_bf16, 1 thread) on a 24-row slice
     of each shape, extrapolated linearly in M."""
@@ -221,7 +319,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["linear", "rvq", "all", "copy"], default="all",
+    ap.add_argument("--only", choices=["linear", "rvq", "decoder", "all", "copy"], default="all",
                     help="copy: a plain 256 MiB device copy, the reference point for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
@@ -301,6 +399,15 @@ def main():
                         "roofline": rvq["roofline"]})
             if "cpu_baseline" in rvq:
                 res["cpu_baseline"] = rvq["cpu_baseline"]
+    if args.only in ("decoder", "all"):
+        dec = run_decoder(torch)
+        if not args.no_cpu:
+            dec["cpu_baseline"] = cpu_decoder_baseline()
+        res["decoder_prefill"] = dec
+        if "value" not in res:
+            res.update({"value": dec["value"], "unit": "tokens/s",
+                        "ms_per_step": dec["ms_per_forward"], "config": dec["config"],
+                        "roofline": dec["roofline"]})
     print(json.dumps(res), flush=True)
 
 

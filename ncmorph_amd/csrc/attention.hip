@@ -6,7 +6,10 @@
 //   context = round(sum_k p_k v_k)
 // Every value entering a product is bf16, so q . k and p v are sums of exact
 // fp32 products; the MFMA sums them in its own order instead of the
-// reference's key order, and the softmax sum is kept online. Results agree
+// reference's key order, and the softmax sum is kept online. exp(x) is
+// computed as exp2(x log2 e) (v_exp_f32, relative error ~2^-20 at |x| ~ 20)
+// and the division as a product with 1 / sum, so a probability can land on
+// the other side of a bf16 rounding boundary now and then. Results agree
 // with the reference within a few bf16 steps, not bit for bit.
 //
 // Two passes over the key blocks of one (sequence, head, 128 queries)
@@ -44,19 +47,37 @@ struct AttnLds {
     static constexpr int V_BYTES = HD * VROW;
 };
 
-// K block [kBk keys][HD] -> LDS rows; keys at or past `valid` are zero.
+// K block [kBk keys][HD] -> registers -> LDS rows; keys at or past `valid`
+// are zero. The load for the next block is issued before the current block's
+// compute and stored to LDS after it, so its latency overlaps the MFMA work.
 template <int HD>
-__device__ __forceinline__ void stage_k(char* kl, const uint16_t* kbase, int64_t kv_stride,
-                                        int64_t key0, int64_t valid) {
-    constexpr int CPR = HD / 8;  // 16-byte chunks per row
+struct KRegs {
+    static constexpr int CPR = HD / 8;  // 16-byte chunks per row
+    static constexpr int N = kBk * CPR / 256;
+    u32x4_t r[N];
+};
+
+template <int HD>
+__device__ __forceinline__ void load_k(KRegs<HD>& R, const uint16_t* kbase, int64_t kv_stride,
+                                       int64_t key0, int64_t valid) {
+    constexpr int CPR = KRegs<HD>::CPR;
 #pragma unroll
-    for (int j = 0; j < kBk * CPR / 256; ++j) {
+    for (int j = 0; j < KRegs<HD>::N; ++j) {
         const int chunk = threadIdx.x + 256 * j;
         const int row = chunk / CPR, cc = chunk % CPR;
-        u32x4_t val = {0u, 0u, 0u, 0u};
-        if (key0 + row < valid)
-            val = *(const u32x4_t*)(kbase + (key0 + row) * kv_stride + 8 * cc);
-        *(u32x4_t*)(kl + row * AttnLds<HD>::KROW + 16 * cc) = val;
+        R.r[j] = u32x4_t{0u, 0u, 0u, 0u};
+        if (key0 + row < valid) R.r[j] = *(const u32x4_t*)(kbase + (key0 + row) * kv_stride + 8 * cc);
+    }
+}
+
+template <int HD>
+__device__ __forceinline__ void store_k(char* kl, const KRegs<HD>& R) {
+    constexpr int CPR = KRegs<HD>::CPR;
+#pragma unroll
+    for (int j = 0; j < KRegs<HD>::N; ++j) {
+        const int chunk = threadIdx.x + 256 * j;
+        const int row = chunk / CPR, cc = chunk % CPR;
+        *(u32x4_t*)(kl + row * AttnLds<HD>::KROW + 16 * cc) = R.r[j];
     }
 }
 
@@ -65,21 +86,36 @@ __device__ __forceinline__ void stage_k(char* kl, const uint16_t* kbase, int64_t
 // LDS stores; consecutive threads take consecutive key pairs, so a wave's
 // stores to one V^T row are contiguous.
 template <int HD>
-__device__ __forceinline__ void stage_v(char* vl, const uint16_t* vbase, int64_t kv_stride,
-                                        int64_t key0, int64_t valid) {
-    constexpr int TASKS = (kBk / 2) * (HD / 8);
+struct VRegs {
+    static constexpr int N = (kBk / 2) * (HD / 8) / 256;
+    u32x4_t a[N], b[N];
+};
+
+template <int HD>
+__device__ __forceinline__ void load_v(VRegs<HD>& R, const uint16_t* vbase, int64_t kv_stride,
+                                       int64_t key0, int64_t valid) {
 #pragma unroll
-    for (int j = 0; j < TASKS / 256; ++j) {
+    for (int j = 0; j < VRegs<HD>::N; ++j) {
         const int task = threadIdx.x + 256 * j;
         const int kp = task % (kBk / 2), dc = task / (kBk / 2);
         const int64_t k0 = key0 + 2 * kp;
-        u32x4_t a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-        if (k0 < valid) a = *(const u32x4_t*)(vbase + k0 * kv_stride + 8 * dc);
-        if (k0 + 1 < valid) b = *(const u32x4_t*)(vbase + (k0 + 1) * kv_stride + 8 * dc);
+        R.a[j] = u32x4_t{0u, 0u, 0u, 0u};
+        R.b[j] = u32x4_t{0u, 0u, 0u, 0u};
+        if (k0 < valid) R.a[j] = *(const u32x4_t*)(vbase + k0 * kv_stride + 8 * dc);
+        if (k0 + 1 < valid) R.b[j] = *(const u32x4_t*)(vbase + (k0 + 1) * kv_stride + 8 * dc);
+    }
+}
+
+template <int HD>
+__device__ __forceinline__ void store_v(char* vl, const VRegs<HD>& R) {
+#pragma unroll
+    for (int j = 0; j < VRegs<HD>::N; ++j) {
+        const int task = threadIdx.x + 256 * j;
+        const int kp = task % (kBk / 2), dc = task / (kBk / 2);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = (a[e] & 0xFFFFu) | (b[e] << 16);
-            const uint32_t hi = (a[e] >> 16) | (b[e] & 0xFFFF0000u);
+            const uint32_t lo = (R.a[j][e] & 0xFFFFu) | (R.b[j][e] << 16);
+            const uint32_t hi = (R.a[j][e] >> 16) | (R.b[j][e] & 0xFFFF0000u);
             *(uint32_t*)(vl + (8 * dc + 2 * e) * AttnLds<HD>::VROW + 4 * kp) = lo;
             *(uint32_t*)(vl + (8 * dc + 2 * e + 1) * AttnLds<HD>::VROW + 4 * kp) = hi;
         }
@@ -108,7 +144,7 @@ __device__ __forceinline__ void scores_t(const char* kl, const u32x4_t (&qf)[HD 
 
 }  // namespace
 
-template <int HD, int OUT_MODE>
+template <int HD, int OUT_MODE, bool POW2 = (HD == 64)>
 __global__ __launch_bounds__(256) void attention_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, void* __restrict__ out, int64_t T, int group,
@@ -121,7 +157,9 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(
     const int c = lane & 31, hl = lane >> 5;
     const int64_t b = blockIdx.z;
     const int h = blockIdx.y, kvh = h / group;
-    const int64_t q0 = (int64_t)blockIdx.x * kBq;
+    // Longest rows of the causal triangle first, so that the short ones fill
+    // the tail of the grid.
+    const int64_t q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * kBq;
     const int64_t qw0 = q0 + 32 * wave;
     const int64_t qq = qw0 + c;  // the query of this lane's score column
     const uint16_t* kbase = k + b * T * kv_stride + (int64_t)kvh * HD;
@@ -148,80 +186,148 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(
     if (wk_lo < 0) wk_lo = 0;
     const bool wave_live = qw0 < T;
 
-    auto allowed = [&](int64_t key) {
-        return key <= qq && key < T && (window <= 0 || key + window > qq);
+    // Masks in block-relative int32 offsets. A block is "full" for this wave
+    // when every key in it is allowed for all 32 of its queries (only
+    // blocks on the diagonal or the window's edge need the per-element test).
+    auto block_full = [&](int64_t key0) {
+        return key0 + kBk - 1 <= qw0 && key0 + kBk <= T &&
+               (window <= 0 || key0 + window > qw0 + 31);
     };
-    auto score = [&](float acc) { return round_bf16_f(round_bf16_f(acc) * scale); };
+    const int koff = 4 * hl;  // + 32 t + 8 (i / 4) + i % 4: the key of element i of tile t
+    // bf16 RNE without the NaN canonicalisation of bf16_bits_rne: exact for
+    // every finite or infinite value (scores and probabilities here; a NaN
+    // input propagates as some NaN or garbage, where the reference's whole
+    // row is NaN).
+    auto rnd = [](float x) {
+        const uint32_t u = __float_as_uint(x);
+        return __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
+    };
+    auto score = [&](float acc) { return rnd(rnd(acc) * scale); };
+    // exp(s - m) as exp2(s log2 e - m log2 e): v_exp_f32 on one FMA.
+    constexpr float kLog2e = 1.4426950408889634f;
+    // The exp2 argument of a raw sum: fma(score, log2 e, -m log2 e). When the
+    // scale is a power of two (head_dim 64: 1/8), round(acc) * scale is exact
+    // and already a bf16 value, so the second rounding is the identity and
+    // the scale folds into the FMA's multiplier without changing its result
+    // (round(acc) * (scale log2e) is the same real product as score * log2e).
+    // The one exception, a product below 2^-126, moves the FMA's addend by
+    // less than 2^-130 and cannot change exp2 of the sum.
+    const float sl = POW2 ? scale * kLog2e : kLog2e;
+    auto expo = [&](float acc, float nm_) {
+        return fmaf(POW2 ? rnd(acc) : score(acc), sl, nm_);
+    };
+    // Per-element mask inside a block: key offset kr (element i of tile t) is
+    // allowed for query offset rq when kr <= rq, kr < rt (keys before T) and
+    // kr > rw (inside the window).
+    auto kr_of = [&](int t, int i) { return 32 * t + 8 * (i / 4) + (i % 4) + koff; };
 
-    // ---- pass 1: running max and softmax sum per query.
+    // ---- pass 1: running max and softmax sum per query. score() is
+    // monotone in the accumulated dot product, so the block maximum is taken
+    // on the raw sums and scored once.
     float m = -INFINITY, lsum = 0.0f;
+    KRegs<HD> kr;
+    load_k<HD>(kr, kbase, kv_stride, kb_begin * kBk, T);
     for (int64_t kb = kb_begin; kb < kb_end; ++kb) {
         const int64_t key0 = kb * kBk;
-        stage_k<HD>(kl, kbase, kv_stride, key0, T);
-        __syncthreads();
+        store_k<HD>(kl, kr);
+        lds_barrier();
+        if (kb + 1 < kb_end) load_k<HD>(kr, kbase, kv_stride, key0 + kBk, T);
         if (wave_live && key0 <= wq_last && key0 + kBk > wk_lo) {
             f32x16_t acc[2];
             scores_t<HD>(kl, qf, acc, lane);
-            float sv[2][16];
+            if (!block_full(key0)) {
+                const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
+                const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int k = kr_of(t, i);
+                        acc[t][i] = (k <= rq && k < rt && k > rw) ? acc[t][i] : -INFINITY;
+                    }
+            }
             float mb = -INFINITY;
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int64_t key = key0 + 32 * t + 8 * (i / 4) + 4 * hl + (i % 4);
-                    sv[t][i] = allowed(key) ? score(acc[t][i]) : -INFINITY;
-                    mb = fmaxf(mb, sv[t][i]);
-                }
+                for (int i = 0; i < 16; ++i) mb = fmaxf(mb, acc[t][i]);
             mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+            mb = POW2 ? rnd(mb) * scale : score(mb);
             const float mn = fmaxf(m, mb);
             if (mn != -INFINITY) {
-                const float alpha = m == -INFINITY ? 0.0f : expf(m - mn);
+                const float nm = -mn * kLog2e;
+                const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(m, kLog2e, nm));
                 float part = 0.0f;
 #pragma unroll
                 for (int t = 0; t < 2; ++t)
 #pragma unroll
-                    for (int i = 0; i < 16; ++i) part = part + expf(sv[t][i] - mn);
-                lsum = lsum * alpha + part;
+                    for (int i = 0; i < 16; ++i)
+                        part = part + __builtin_amdgcn_exp2f(expo(acc[t][i], nm));
+                lsum = fmaf(lsum, alpha, part);
                 m = mn;
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
     const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+    const float inv_l = 1.0f / ltot;
+    const float nm = -m * kLog2e;  // m is a score: -m log2 e as in pass 1
 
     // ---- pass 2: bf16 probabilities and P V.
     constexpr int NT = HD / 32;
     f32x16_t o[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) o[n] = f32x16_t{};
+    VRegs<HD> vr;
+    load_k<HD>(kr, kbase, kv_stride, kb_begin * kBk, T);
+    load_v<HD>(vr, vbase, kv_stride, kb_begin * kBk, T);
     for (int64_t kb = kb_begin; kb < kb_end; ++kb) {
         const int64_t key0 = kb * kBk;
-        stage_k<HD>(kl, kbase, kv_stride, key0, T);
-        stage_v<HD>(vl, vbase, kv_stride, key0, T);
-        __syncthreads();
+        store_k<HD>(kl, kr);
+        store_v<HD>(vl, vr);
+        lds_barrier();
+        if (kb + 1 < kb_end) {
+            load_k<HD>(kr, kbase, kv_stride, key0 + kBk, T);
+            load_v<HD>(vr, vbase, kv_stride, key0 + kBk, T);
+        }
         if (wave_live && key0 <= wq_last && key0 + kBk > wk_lo) {
             f32x16_t acc[2];
             scores_t<HD>(kl, qf, acc, lane);
+            if (!block_full(key0)) {
+                const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
+                const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
+#pragma unroll
+                for (int t = 0; t < 2; ++t)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) {
+                        const int k = kr_of(t, i);
+                        acc[t][i] = (k <= rq && k < rt && k > rw) ? acc[t][i] : -INFINITY;
+                    }
+            }
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                uint32_t pb[16];
+                // p = round_bf16(e / sum): u + 0x7FFF + lsb carries the RNE
+                // result in the high half; v_perm packs two high halves.
+                uint32_t pr[16];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const int64_t key = key0 + 32 * t + 8 * (i / 4) + 4 * hl + (i % 4);
-                    const float p = allowed(key) ? expf(score(acc[t][i]) - m) / ltot : 0.0f;
-                    pb[i] = bf16_bits_rne(p);
+                    const float e = __builtin_amdgcn_exp2f(expo(acc[t][i], nm));
+                    const uint32_t u = __float_as_uint(e * inv_l);
+                    pr[i] = u + 0x7FFFu + ((u >> 16) & 1u);
                 }
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     u32x4_t pa;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) pa[e] = pb[8 * j + 2 * e] | (pb[8 * j + 2 * e + 1] << 16);
+                    for (int e = 0; e < 4; ++e)
+                        pa[e] = __builtin_amdgcn_perm(pr[8 * j + 2 * e + 1], pr[8 * j + 2 * e],
+                                                      0x07060302u);
                     const int kofs = (32 * t + 16 * j + 4 * hl) * 2;
 #pragma unroll
                     for (int n = 0; n < NT; ++n) {
-                        const char* vr = vl + (32 * n + c) * L::VROW + kofs;
-                        const u32x2_t v0 = *(const u32x2_t*)vr;
-                        const u32x2_t v1 = *(const u32x2_t*)(vr + 16);
+                        const char* vp = vl + (32 * n + c) * L::VROW + kofs;
+                        const u32x2_t v0 = *(const u32x2_t*)vp;
+                        const u32x2_t v1 = *(const u32x2_t*)(vp + 16);
                         const u32x4_t vb = {v0[0], v0[1], v1[0], v1[1]};
                         o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                             __builtin_bit_cast(bf16x8_t, pa), __builtin_bit_cast(bf16x8_t, vb),
@@ -230,7 +336,7 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(
                 }
             }
         }
-        __syncthreads();
+        lds_barrier();
     }
 
     // context = round_bf16(sum); D row 8 (i / 4) + 4 hl + i % 4 = query, column = dim.
@@ -273,6 +379,8 @@ hipError_t launch_attention_bf16(const uint16_t* q, const uint16_t* k, const uin
                                  int kv_heads, int head_dim, int64_t q_stride, int64_t kv_stride,
                                  int64_t out_stride, int64_t window, int out_mode,
                                  hipStream_t stream) {
+    // A window of seq_len or more admits every causal key.
+    if (window >= seq_len) window = 0;
     switch (head_dim) {
         case 64:
             return launch_attn_hd<64>(q, k, v, out, batch, seq_len, q_heads, kv_heads, q_stride,
