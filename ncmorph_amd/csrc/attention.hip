@@ -19,7 +19,8 @@
 // transposed (one LDS row per head dimension) so that each lane's eight
 // P-operand keys are two 8-byte LDS reads.
 //
-// Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16:
+// Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16,
+// one 32-key tile at a time (the running max and sum are updated per tile):
 // lane l then holds query l % 32 and keys 8 (i / 4) + 4 (l / 32) + i % 4 of a
 // 32-key tile in element i. Elements 8j .. 8j+7 of that fragment are exactly
 // the A operand of P V for the keys 16j + {4h .. 4h+3, 8+4h .. 8+4h+3}
@@ -122,30 +123,28 @@ __device__ __forceinline__ void store_v(char* vl, const VRegs<HD>& R) {
     }
 }
 
-// S^T tile pair for one wave: keys key0 + [0, 64) x this wave's 32 queries.
+// One S^T tile for one wave: keys key0 + 32 t + [0, 32) x its 32 queries.
 template <int HD>
-__device__ __forceinline__ void scores_t(const char* kl, const u32x4_t (&qf)[HD / 16],
-                                         f32x16_t (&acc)[2], int lane) {
+__device__ __forceinline__ f32x16_t score_tile(const char* kl, const u32x4_t (&qf)[HD / 16],
+                                               int t, int lane) {
     const int c = lane & 31, hl = lane >> 5;
+    f32x16_t a = {};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-        f32x16_t a = {};
-#pragma unroll
-        for (int s = 0; s < HD / 16; ++s) {
-            const u32x4_t kf =
-                *(const u32x4_t*)(kl + (32 * t + c) * AttnLds<HD>::KROW + (16 * s + 8 * hl) * 2);
-            a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
-                                                        __builtin_bit_cast(bf16x8_t, qf[s]), a,
-                                                        0, 0, 0);
-        }
-        acc[t] = a;
+    for (int s = 0; s < HD / 16; ++s) {
+        const u32x4_t kf =
+            *(const u32x4_t*)(kl + (32 * t + c) * AttnLds<HD>::KROW + (16 * s + 8 * hl) * 2);
+        a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                    __builtin_bit_cast(bf16x8_t, qf[s]), a, 0,
+                                                    0, 0);
     }
+    return a;
 }
 
 }  // namespace
 
 template <int HD, int OUT_MODE, bool POW2 = (HD == 64)>
-__global__ __launch_bounds__(256) void attention_bf16_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 2 : 1, 4)))
+void attention_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, void* __restrict__ out, int64_t T, int group,
     int64_t q_stride, int64_t kv_stride, int64_t out_stride, int64_t window, float scale) {
@@ -157,9 +156,15 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(
     const int c = lane & 31, hl = lane >> 5;
     const int64_t b = blockIdx.z;
     const int h = blockIdx.y, kvh = h / group;
-    // Longest rows of the causal triangle first, so that the short ones fill
-    // the tail of the grid.
-    const int64_t q0 = (int64_t)(gridDim.x - 1 - blockIdx.x) * kBq;
+    // Causal balance: workgroup x takes query block nqb - 1 - x (the most
+    // keys) and then block x (the fewest), so every workgroup walks about
+    // the same number of key blocks (the middle block of an odd count is
+    // taken once).
+    const int nqb = (int)((T + kBq - 1) / kBq);
+    for (int part = 0; part < 2; ++part) {
+    const int qbi = part == 0 ? nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    if (part == 1 && qbi == nqb - 1 - (int)blockIdx.x) break;
+    const int64_t q0 = (int64_t)qbi * kBq;
     const int64_t qw0 = q0 + 32 * wave;
     const int64_t qq = qw0 + c;  // the query of this lane's score column
     const uint16_t* kbase = k + b * T * kv_stride + (int64_t)kvh * HD;
@@ -233,38 +238,35 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(
         lds_barrier();
         if (kb + 1 < kb_end) load_k<HD>(kr, kbase, kv_stride, key0 + kBk, T);
         if (wave_live && key0 <= wq_last && key0 + kBk > wk_lo) {
-            f32x16_t acc[2];
-            scores_t<HD>(kl, qf, acc, lane);
-            if (!block_full(key0)) {
-                const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
-                const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
+            const bool full = block_full(key0);
+            const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
+            const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t) {
+                f32x16_t acc = score_tile<HD>(kl, qf, t, lane);
+                if (!full)
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int k = kr_of(t, i);
-                        acc[t][i] = (k <= rq && k < rt && k > rw) ? acc[t][i] : -INFINITY;
+                        acc[i] = (k <= rq && k < rt && k > rw) ? acc[i] : -INFINITY;
                     }
-            }
-            float mb = -INFINITY;
+                float mb = -INFINITY;
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) mb = fmaxf(mb, acc[t][i]);
-            mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
-            mb = POW2 ? rnd(mb) * scale : score(mb);
-            const float mn = fmaxf(m, mb);
-            if (mn != -INFINITY) {
-                const float nm = -mn * kLog2e;
-                const float alpha = m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(m, kLog2e, nm));
-                float part = 0.0f;
-#pragma unroll
-                for (int t = 0; t < 2; ++t)
+                for (int i = 0; i < 16; ++i) mb = fmaxf(mb, acc[i]);
+                mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+                mb = POW2 ? rnd(mb) * scale : score(mb);
+                const float mn = fmaxf(m, mb);
+                if (mn != -INFINITY) {
+                    const float nm = -mn * kLog2e;
+                    const float alpha =
+                        m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(m, kLog2e, nm));
+                    float part = 0.0f;
 #pragma unroll
                     for (int i = 0; i < 16; ++i)
-                        part = part + __builtin_amdgcn_exp2f(expo(acc[t][i], nm));
-                lsum = fmaf(lsum, alpha, part);
-                m = mn;
+                        part = part + __builtin_amdgcn_exp2f(expo(acc[i], nm));
+                    lsum = fmaf(lsum, alpha, part);
+                    m = mn;
+                }
             }
         }
         lds_barrier();
@@ -291,27 +293,24 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(
             load_v<HD>(vr, vbase, kv_stride, key0 + kBk, T);
         }
         if (wave_live && key0 <= wq_last && key0 + kBk > wk_lo) {
-            f32x16_t acc[2];
-            scores_t<HD>(kl, qf, acc, lane);
-            if (!block_full(key0)) {
-                const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
-                const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
+            const bool full = block_full(key0);
+            const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
+            const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
 #pragma unroll
-                for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t) {
+                f32x16_t acc = score_tile<HD>(kl, qf, t, lane);
+                if (!full)
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int k = kr_of(t, i);
-                        acc[t][i] = (k <= rq && k < rt && k > rw) ? acc[t][i] : -INFINITY;
+                        acc[i] = (k <= rq && k < rt && k > rw) ? acc[i] : -INFINITY;
                     }
-            }
-#pragma unroll
-            for (int t = 0; t < 2; ++t) {
                 // p = round_bf16(e / sum): u + 0x7FFF + lsb carries the RNE
                 // result in the high half; v_perm packs two high halves.
                 uint32_t pr[16];
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
-                    const float e = __builtin_amdgcn_exp2f(expo(acc[t][i], nm));
+                    const float e = __builtin_amdgcn_exp2f(expo(acc[i], nm));
                     const uint32_t u = __float_as_uint(e * inv_l);
                     pr[i] = u + 0x7FFFu + ((u >> 16) & 1u);
                 }
@@ -340,20 +339,22 @@ __global__ __launch_bounds__(256) void attention_bf16_kernel(
     }
 
     // context = round_bf16(sum); D row 8 (i / 4) + 4 hl + i % 4 = query, column = dim.
-    if (!wave_live) return;
+    if (wave_live) {
 #pragma unroll
-    for (int n = 0; n < NT; ++n)
+        for (int n = 0; n < NT; ++n)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int64_t qrow = qw0 + 8 * (i / 4) + 4 * hl + (i % 4);
-            if (qrow >= T) continue;
-            const uint32_t bits = bf16_bits_rne(o[n][i]);
-            const int64_t off = (b * T + qrow) * out_stride + (int64_t)h * HD + 32 * n + c;
-            if (OUT_MODE == NCM_OUT_BF16)
-                ((uint16_t*)out)[off] = (uint16_t)bits;
-            else
-                ((float*)out)[off] = __uint_as_float(bits << 16);
-        }
+            for (int i = 0; i < 16; ++i) {
+                const int64_t qrow = qw0 + 8 * (i / 4) + 4 * hl + (i % 4);
+                if (qrow >= T) continue;
+                const uint32_t bits = bf16_bits_rne(o[n][i]);
+                const int64_t off = (b * T + qrow) * out_stride + (int64_t)h * HD + 32 * n + c;
+                if (OUT_MODE == NCM_OUT_BF16)
+                    ((uint16_t*)out)[off] = (uint16_t)bits;
+                else
+                    ((float*)out)[off] = __uint_as_float(bits << 16);
+            }
+    }
+    }  // part
 }
 
 template <int HD>
@@ -361,7 +362,8 @@ static hipError_t launch_attn_hd(const uint16_t* q, const uint16_t* k, const uin
                                  void* out, int64_t batch, int64_t T, int hq, int hkv,
                                  int64_t q_stride, int64_t kv_stride, int64_t out_stride,
                                  int64_t window, int out_mode, hipStream_t stream) {
-    const dim3 grid((unsigned)((T + kBq - 1) / kBq), (unsigned)hq, (unsigned)batch);
+    const int64_t nqb = (T + kBq - 1) / kBq;
+    const dim3 grid((unsigned)((nqb + 1) / 2), (unsigned)hq, (unsigned)batch);
     const float scale = 1.0f / sqrtf((float)HD);
     const int group = hq / hkv;
     if (out_mode == NCM_OUT_BF16)
