@@ -143,6 +143,30 @@ int ncm_linear_bf16_residual(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* 
                              const uint16_t* bias, const float* residual, void* y,
                              int64_t m, int64_t k, int64_t n, int out_mode);
 
+/* The projection and the SwiGLU that follows it in the decoder's MLP
+ * (src/decoder.zig:206-211, bf16 mode) in one pass: y[m, j] =
+ * round(silu_bf16(gate[m, j]) * up[m, j]) with gate and up the bf16 outputs
+ * of the gate and up projections. w: bf16 [n2, k] holding the gate and up
+ * rows interleaved in groups of 32 (rows 64g .. 64g+31 = gate rows
+ * 32g .. 32g+31, rows 64g+32 .. 64g+63 = up rows 32g .. 32g+31; bias, if
+ * given, in the same order); n2 = 2 * intermediate, a multiple of 64.
+ * y: uint16 bf16 bits [m, n2 / 2]. The same bits as ncm_linear_bf16 (BF16)
+ * followed by ncm_silu_mul_dev. Device pointers; y 8-byte aligned. */
+int ncm_linear_bf16_swiglu(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                           const uint16_t* bias, uint16_t* y, int64_t m, int64_t k,
+                           int64_t n2);
+
+/* The q|k|v projection and the RoPE rotation of its q and k heads
+ * (root.zig:497-530) in one pass, for head_dim 64: y = the bf16 output of
+ * ncm_linear_bf16 (BF16), with every 64-wide head in columns [0, rot_cols)
+ * rotated as ncm_rope_rotate_dev does (table row = row % seq_len). n and
+ * rot_cols multiples of 64. The same bits as the two calls in sequence.
+ * Device pointers; y 8-byte aligned. */
+int ncm_linear_bf16_rope64(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                           const uint16_t* bias, uint16_t* y, int64_t m, int64_t k, int64_t n,
+                           int64_t rot_cols, int64_t seq_len, const float* cosine,
+                           const float* sine);
+
 /* y[m, n] = sum_k x[m, k] * w[n, k], fp32 operands and accumulation on the
  * fp32 MFMA (device counterpart of packages/kernels/root.zig:25-65).
  * Requires k % 4 == 0 and 16-byte aligned x and w. Device pointers. */
@@ -221,9 +245,10 @@ typedef struct ncm_decoder_shape {
  * reference keeps separate (attention_weights_t, root.zig:351-362; the MLP
  * weights of decoder.zig) are row-concatenated: qkv_weight holds the q rows
  * [q_heads * head_dim], then the k rows, then the v rows [kv_heads *
- * head_dim each], each row `hidden` wide; gate_up_weight holds the gate rows
- * [intermediate] then the up rows. Biases follow the same row order; NULL =
- * no bias. */
+ * head_dim each], each row `hidden` wide; gate_up_weight holds the gate and
+ * up rows interleaved in groups of 32 as ncm_linear_bf16_swiglu reads them
+ * (intermediate % 32 == 0). Biases follow the same row order; NULL = no
+ * bias. */
 typedef struct ncm_decoder_layer {
     const float* input_norm;           /* [hidden] */
     const uint16_t* qkv_weight;        /* [(q_heads + 2 kv_heads) head_dim, hidden] */
@@ -231,8 +256,8 @@ typedef struct ncm_decoder_layer {
     const uint16_t* o_weight;          /* [hidden, q_heads head_dim] */
     const uint16_t* o_bias;            /* [hidden] or NULL */
     const float* post_attention_norm;  /* [hidden] */
-    const uint16_t* gate_up_weight;    /* [2 intermediate, hidden] */
-    const uint16_t* gate_up_bias;      /* [2 intermediate] or NULL */
+    const uint16_t* gate_up_weight;    /* [2 intermediate, hidden], interleaved */
+    const uint16_t* gate_up_bias;      /* [2 intermediate] or NULL, interleaved */
     const uint16_t* down_weight;       /* [hidden, intermediate] */
     const uint16_t* down_bias;         /* [hidden] or NULL */
 } ncm_decoder_layer_t;

@@ -43,6 +43,8 @@ SIGNATURES = [
     ("ncm_silu_bf16", i32, [vp, sz, vp, sz]),
     ("ncm_linear_bf16", i32, [vp, vp, vp, vp, vp, i64, i64, i64, i32]),
     ("ncm_linear_bf16_residual", i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32]),
+    ("ncm_linear_bf16_swiglu", i32, [vp, vp, vp, vp, vp, i64, i64, i64]),
+    ("ncm_linear_bf16_rope64", i32, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp]),
     ("ncm_linear_f32", i32, [vp, vp, vp, vp, i64, i64, i64]),
     ("ncm_bf16_from_f32_dev", i32, [vp, vp, vp, i64, i32]),
     ("ncm_bf16_widen_dev", i32, [vp, vp, vp, i64]),

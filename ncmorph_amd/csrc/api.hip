@@ -188,6 +188,53 @@ int ncm_linear_bf16_residual(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* 
     return NCM_OK;
 }
 
+namespace {
+int check_linear_args(const void* x, const void* w, const void* y, int64_t m, int64_t k,
+                      int64_t n) {
+    if (m < 0 || n < 0 || k < 0) return NCM_E_SHAPE;
+    if (m == 0 || n == 0) return NCM_OK;
+    if (!y || (k > 0 && (!x || !w))) return NCM_E_NULL;
+    if (k % 8 != 0 || k > (int64_t(1) << 21)) return NCM_E_SHAPE;
+    if ((uintptr_t)x % 16 || (uintptr_t)w % 16 || (uintptr_t)y % 8) return NCM_E_ARG;
+    if (m > (int64_t(1) << 31) || n > (int64_t(1) << 31)) return NCM_E_SHAPE;
+    return NCM_OK;
+}
+}  // namespace
+
+int ncm_linear_bf16_swiglu(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                           const uint16_t* bias, uint16_t* y, int64_t m, int64_t k,
+                           int64_t n2) {
+    if (!ctx) return NCM_E_NULL;
+    int rc = check_linear_args(x, w, y, m, k, n2);
+    if (rc) return rc;
+    if (n2 % 64) return NCM_E_SHAPE;
+    if (m == 0 || n2 == 0) return NCM_OK;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_linear_swiglu(x, w, bias, y, m, k, n2, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "swiglu linear launch");
+    return NCM_OK;
+}
+
+int ncm_linear_bf16_rope64(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                           const uint16_t* bias, uint16_t* y, int64_t m, int64_t k, int64_t n,
+                           int64_t rot_cols, int64_t seq_len, const float* cosine,
+                           const float* sine) {
+    if (!ctx) return NCM_E_NULL;
+    int rc = check_linear_args(x, w, y, m, k, n);
+    if (rc) return rc;
+    if (n % 64 || rot_cols < 0 || rot_cols % 64 || rot_cols > n || seq_len <= 0)
+        return NCM_E_SHAPE;
+    if (m == 0 || n == 0) return NCM_OK;
+    if (rot_cols > 0 && (!cosine || !sine)) return NCM_E_NULL;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_linear_rope64(x, w, bias, y, m, k, n, rot_cols, seq_len, cosine,
+                                             sine, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "rope linear launch");
+    return NCM_OK;
+}
+
 int ncm_linear_f32(ncm_ctx_t* ctx, const float* x, const float* w, float* y, int64_t m,
                    int64_t k, int64_t n) {
     if (!ctx) return NCM_E_NULL;
@@ -321,7 +368,7 @@ int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
         return NCM_E_SHAPE;
     if (s.q_heads <= 0 || s.kv_heads <= 0 || s.q_heads % s.kv_heads) return NCM_E_SHAPE;
     if (s.head_dim != 64 && s.head_dim != 128) return NCM_E_SHAPE;
-    if (s.hidden % 8 || s.intermediate % 8) return NCM_E_SHAPE;
+    if (s.hidden % 8 || s.intermediate % 32) return NCM_E_SHAPE;
     if (s.hidden > (int64_t(1) << 21) || s.intermediate > (int64_t(1) << 20) ||
         s.vocab > (int64_t(1) << 31) || (int64_t)s.q_heads * s.head_dim > (int64_t(1) << 21))
         return NCM_E_SHAPE;

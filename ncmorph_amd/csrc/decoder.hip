@@ -3,13 +3,13 @@
 // kernels over a batch of equal-length sequences, with every intermediate
 // resident in the context's workspace. Per layer (bf16 mode):
 //   n   = rms_norm_bf16(h, input_norm)                 -> bf16 bits
-//   qkv = n W_qkv^T (+ b)                              -> bf16 bits, one GEMM
-//   rotate q and k heads (RoPE tables row = position in the sequence)
+//   qkv = n W_qkv^T (+ b), q and k heads rotated       -> bf16 bits, one GEMM
+//         (RoPE table row = position in the sequence; fused for head_dim 64)
 //   c   = attention(q, k, v)                           -> bf16 bits
 //   h   = round(h + round(c W_o^T (+ b)))              (fused residual)
 //   n   = rms_norm_bf16(h, post_attention_norm)
-//   gu  = n W_gate_up^T (+ b)                          -> bf16 bits, one GEMM
-//   a   = round(silu_bf16(gate) * up)
+//   a   = round(silu_bf16(n W_gate^T) * n W_up^T)      -> bf16 bits, one GEMM
+//         over the interleaved gate/up rows with the SwiGLU in its epilogue
 //   h   = round(h + round(a W_down^T (+ b)))           (fused residual)
 // then logits = round(rms_norm_bf16(h, final_norm) W_head^T).
 // The reference runs q, k and v (and gate and up) as separate projections of
@@ -44,36 +44,6 @@ __global__ __launch_bounds__(256) void embed_rows_kernel(const int64_t* __restri
     }
 }
 
-// act[r, j] = round(round(silu(g)) * u), g = gu[r, j], u = gu[r, inter + j]
-// (src/decoder.zig:210-211 on the bf16 gate and up projections).
-__global__ __launch_bounds__(256) void silu_mul_rows_kernel(const uint16_t* __restrict__ gu,
-                                                            uint16_t* __restrict__ act,
-                                                            int64_t rows, int64_t inter) {
-    const int64_t idx = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 4;
-    if (idx >= rows * inter) return;
-    const int64_t r = idx / inter, j = idx % inter;
-    const uint16_t* g = gu + r * 2 * inter + j;
-    const uint16_t* u = g + inter;
-    auto act1 = [](uint32_t gb, uint32_t ub) {
-        const float v = __uint_as_float(gb << 16);
-        const float a = __uint_as_float(bf16_bits_rne(v / (1.0f + expf(-v))) << 16);
-        return bf16_bits_rne(a * __uint_as_float(ub << 16));
-    };
-    if (j + 4 <= inter && (inter & 3) == 0) {
-        const u32x2_t gv = *(const u32x2_t*)g, uv = *(const u32x2_t*)u;
-        u32x2_t o;
-        o[0] = act1(gv[0] & 0xFFFFu, uv[0] & 0xFFFFu) | (act1(gv[0] >> 16, uv[0] >> 16) << 16);
-        o[1] = act1(gv[1] & 0xFFFFu, uv[1] & 0xFFFFu) | (act1(gv[1] >> 16, uv[1] >> 16) << 16);
-        *(u32x2_t*)(act + idx) = o;
-    } else {
-        for (int e = 0; e < 4 && idx + e < rows * inter; ++e) {
-            const int64_t re = (idx + e) / inter, je = (idx + e) % inter;
-            const uint16_t* ge = gu + re * 2 * inter + je;
-            act[idx + e] = (uint16_t)act1(ge[0], ge[inter]);
-        }
-    }
-}
-
 namespace {
 
 constexpr size_t kAlign = 256;
@@ -81,7 +51,7 @@ size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 
 struct Plan {
     int64_t T, qkv_w, q_w;
-    size_t o_hidden, o_normed, o_qkv, o_ctx, o_gu, o_act, o_ids, total;
+    size_t o_hidden, o_normed, o_qkv, o_ctx, o_act, o_ids, total;
 };
 
 Plan plan(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq) {
@@ -94,7 +64,6 @@ Plan plan(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq) {
     p.o_normed = off; off += up((size_t)p.T * s.hidden * 2);
     p.o_qkv = off;    off += up((size_t)p.T * p.qkv_w * 2);
     p.o_ctx = off;    off += up((size_t)p.T * p.q_w * 2);
-    p.o_gu = off;     off += up((size_t)p.T * 2 * s.intermediate * 2);
     p.o_act = off;    off += up((size_t)p.T * s.intermediate * 2);
     p.o_ids = off;    off += up((size_t)p.T * 8);
     p.total = off;
@@ -124,7 +93,6 @@ hipError_t decoder_forward(const ncm_decoder_shape_t& s, const ncm_decoder_layer
     uint16_t* normed = (uint16_t*)(w + p.o_normed);
     uint16_t* qkv = (uint16_t*)(w + p.o_qkv);
     uint16_t* ctxb = (uint16_t*)(w + p.o_ctx);
-    uint16_t* gu = (uint16_t*)(w + p.o_gu);
     uint16_t* act = (uint16_t*)(w + p.o_act);
     int64_t* ids = (int64_t*)(w + p.o_ids);
     const int64_t T = p.T, H = s.hidden, I = s.intermediate;
@@ -141,11 +109,17 @@ hipError_t decoder_forward(const ncm_decoder_shape_t& s, const ncm_decoder_layer
         const ncm_decoder_layer_t& L = layers[l];
         NCM_TRY(launch_rms_norm_rows(hidden, L.input_norm, normed, T, H, s.rms_eps, NCM_OUT_BF16,
                                      st));
-        NCM_TRY(launch_linear(normed, L.qkv_weight, L.qkv_bias, qkv, T, H, p.qkv_w, NCM_OUT_BF16,
-                              -1, st));
-        NCM_TRY(launch_rope_rotate(qkv, T, p.qkv_w, s.q_heads, hd, seq, cosine, sine, st));
-        NCM_TRY(launch_rope_rotate(qkv + p.q_w, T, p.qkv_w, s.kv_heads, hd, seq, cosine, sine,
-                                   st));
+        if (hd == 64) {  // rotation fused into the projection's epilogue
+            NCM_TRY(launch_linear_rope64(normed, L.qkv_weight, L.qkv_bias, qkv, T, H, p.qkv_w,
+                                         (int64_t)(s.q_heads + s.kv_heads) * hd, seq, cosine,
+                                         sine, st));
+        } else {
+            NCM_TRY(launch_linear(normed, L.qkv_weight, L.qkv_bias, qkv, T, H, p.qkv_w,
+                                  NCM_OUT_BF16, -1, st));
+            NCM_TRY(launch_rope_rotate(qkv, T, p.qkv_w, s.q_heads, hd, seq, cosine, sine, st));
+            NCM_TRY(launch_rope_rotate(qkv + p.q_w, T, p.qkv_w, s.kv_heads, hd, seq, cosine,
+                                       sine, st));
+        }
         NCM_TRY(launch_attention_bf16(qkv, qkv + p.q_w, qkv + p.q_w + (int64_t)s.kv_heads * hd,
                                       ctxb, batch, seq, s.q_heads, s.kv_heads, hd, p.qkv_w,
                                       p.qkv_w, p.q_w, s.window, NCM_OUT_BF16, st));
@@ -153,14 +127,8 @@ hipError_t decoder_forward(const ncm_decoder_shape_t& s, const ncm_decoder_layer
                                        NCM_OUT_BF16_F32, st));
         NCM_TRY(launch_rms_norm_rows(hidden, L.post_attention_norm, normed, T, H, s.rms_eps,
                                      NCM_OUT_BF16, st));
-        NCM_TRY(launch_linear(normed, L.gate_up_weight, L.gate_up_bias, gu, T, H, 2 * I,
-                              NCM_OUT_BF16, -1, st));
-        {
-            const int64_t n4 = (T * I + 3) / 4;
-            hipLaunchKernelGGL(silu_mul_rows_kernel, dim3((unsigned)((n4 + 255) / 256)),
-                               dim3(256), 0, st, gu, act, T, I);
-            NCM_TRY(hipGetLastError());
-        }
+        NCM_TRY(launch_linear_swiglu(normed, L.gate_up_weight, L.gate_up_bias, act, T, H,
+                                     2 * I, st));
         NCM_TRY(launch_linear_residual(act, L.down_weight, L.down_bias, hidden, hidden, T, I, H,
                                        NCM_OUT_BF16_F32, st));
     }

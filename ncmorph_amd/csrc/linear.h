@@ -20,6 +20,18 @@ hipError_t launch_linear_residual(const uint16_t* x, const uint16_t* w, const ui
                                   const float* residual, void* y, int64_t M, int64_t K,
                                   int64_t N, int out_mode, hipStream_t stream);
 
+// Linear + SwiGLU (bf16 bits out, y [M, N2 / 2]); w rows interleaved in
+// groups of 32 (gate, up); N2 % 64 == 0. See linear_fused.hip.
+hipError_t launch_linear_swiglu(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                uint16_t* y, int64_t M, int64_t K, int64_t N2,
+                                hipStream_t stream);
+// Linear + bf16 RoPE of 64-wide heads in columns [0, rot_cols) (bf16 bits out,
+// y [M, N]); N and rot_cols multiples of 64.
+hipError_t launch_linear_rope64(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                uint16_t* y, int64_t M, int64_t K, int64_t N, int64_t rot_cols,
+                                int64_t seq_len, const float* cosine, const float* sine,
+                                hipStream_t stream);
+
 // fp32 operands, fp32 output; K % 4 == 0, 16-byte aligned x and w.
 hipError_t launch_linear_f32(const float* x, const float* w, float* y, int64_t M, int64_t K,
                              int64_t N, hipStream_t stream);

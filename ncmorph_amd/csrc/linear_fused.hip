@@ -1,0 +1,223 @@
+// The bf16 linear with epilogues that pair two 32-column MFMA tiles of one
+// wave, fusing the elementwise op that follows the projection in the
+// decoder (bf16 mode; the projection's own output is rounded to bf16 first,
+// exactly as the unfused path writes it):
+//   SwiGLU: weight rows are interleaved in groups of 32 (rows 64g .. 64g+31
+//     are gate rows 32g .. 32g+31, rows 64g+32 .. 64g+63 the matching up
+//     rows), so tiles 2p and 2p+1 of a wave hold gate and up of the same 32
+//     features; the epilogue writes round(silu_bf16(gate) * up)
+//     (src/decoder.zig:208-211) to y [M, N / 2].
+//   RoPE (head_dim 64): tiles 2p and 2p+1 are the two halves of one head;
+//     columns below rot_cols (the q and k heads) are rotated as rotate_head
+//     does in bf16 mode (packages/kernels/root.zig:615-634) with table row
+//     (row % seq_len), the rest (v) written as projected; y [M, N].
+// Both write bf16 bits only.
+#include "gemm_core.h"
+#include "linear.h"
+
+namespace ncm {
+
+namespace {
+
+constexpr int kEpiSwiGLU = 1;
+constexpr int kEpiRope = 2;
+
+struct PairArgs {
+    const float* cosine;  // RoPE tables [seq_len, 64]
+    const float* sine;
+    int64_t seq_len;
+    int64_t rot_cols;  // columns [0, rot_cols) are rotated
+};
+
+__device__ __forceinline__ float rb(float v) { return __uint_as_float(bf16_bits_rne(v) << 16); }
+
+// The projection's output value of one accumulator: bf16(flush(acc + bias)).
+__device__ __forceinline__ uint32_t proj_bits(float acc, float bias) {
+    return bf16_bits_rne(flush_subnormal(acc + bias));
+}
+
+__device__ __forceinline__ uint32_t swiglu_bits(uint32_t gb, uint32_t ub) {
+    const float g = __uint_as_float(gb << 16);
+    const float a = rb(g / (1.0f + expf(-g)));
+    return bf16_bits_rne(a * __uint_as_float(ub << 16));
+}
+
+}  // namespace
+
+template <class S, int EPI, bool HAS_BIAS>
+__global__ __launch_bounds__(S::NT)
+__attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_pair_kernel(
+    const void* __restrict__ x, const void* __restrict__ w, const uint16_t* __restrict__ bias,
+    uint16_t* __restrict__ y, int64_t M, int64_t K, int64_t N, int tiles_n, int group_m,
+    PairArgs pa) {
+    static_assert(S::NB % 2 == 0 && S::WN % 64 == 0, "pairs of 32-column tiles per wave");
+    extern __shared__ __attribute__((aligned(16))) char lds[];
+
+    const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int per_group = group_m * tiles_n;
+    const int g = logical / per_group;
+    const int tiles_m = (int)((M + S::BM - 1) / S::BM);
+    const int gm = min(group_m, tiles_m - g * group_m);
+    const int in_g = logical % per_group;
+    const int64_t m0 = (int64_t)(g * group_m + in_g % gm) * S::BM;
+    const int64_t n0 = (int64_t)(in_g / gm) * S::BN;
+
+    GemmAcc<S> acc;
+    acc.zero();
+    gemm_mainloop<S>((const char*)x + m0 * K * S::ESZ, K, operand_bytes(M, m0, K, S::ESZ),
+                     (const char*)w + n0 * K * S::ESZ, K, operand_bytes(N, n0, K, S::ESZ), K, lds,
+                     acc);
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    if (wave >= S::NWG) return;
+    const int wm = wave % S::WGM;
+    const int wn = wave / S::WGM;
+    const int c = lane & 31;
+    const int64_t ld = EPI == kEpiSwiGLU ? N / 2 : N;
+    const bool full = m0 + S::BM <= M;
+
+#pragma unroll
+    for (int p = 0; p < S::NB / 2; ++p) {
+        const int64_t col_a = n0 + wn * S::WN + 64 * p + c;  // first tile's column
+        if (col_a >= N) continue;  // N % 64 == 0: the pair is wholly in or out
+        float ba = 0.0f, bb = 0.0f;
+        if (HAS_BIAS) {
+            ba = __uint_as_float((uint32_t)bias[col_a] << 16);
+            bb = __uint_as_float((uint32_t)bias[col_a + 32] << 16);
+        }
+        const bool rotate = EPI == kEpiRope && col_a < pa.rot_cols;
+#pragma unroll
+        for (int mb = 0; mb < S::MB; ++mb) {
+            uint32_t oa[16], ob[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const uint32_t fa = proj_bits(acc.v[mb][2 * p][i], ba);
+                const uint32_t fb = proj_bits(acc.v[mb][2 * p + 1][i], bb);
+                if (EPI == kEpiSwiGLU) {
+                    oa[i] = swiglu_bits(fa, fb);
+                } else if (rotate) {
+                    const int64_t m =
+                        m0 + wm * S::WM + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                    const int64_t t = (m < M ? m : 0) % pa.seq_len;
+                    const float* ct = pa.cosine + t * 64 + c;
+                    const float* st = pa.sine + t * 64 + c;
+                    const float first = __uint_as_float(fa << 16);
+                    const float second = __uint_as_float(fb << 16);
+                    const float left = rb(first * rb(ct[0]));
+                    const float right = rb(-second * rb(st[0]));
+                    const float right2 = rb(first * rb(st[32]));
+                    const float left2 = rb(second * rb(ct[32]));
+                    oa[i] = bf16_bits_rne(left + right);
+                    ob[i] = bf16_bits_rne(left2 + right2);
+                } else {
+                    oa[i] = fa;
+                    ob[i] = fb;
+                }
+            }
+            if (full) {
+                // Quad transpose: each lane then holds 4 consecutive columns
+                // of one row (8-byte stores).
+                const int q = lane & 3;
+                const int hrow = 4 * (lane >> 5) + q;
+                const int64_t ca = EPI == kEpiSwiGLU
+                                       ? (n0 + wn * S::WN) / 2 + 32 * p + (c & ~3)
+                                       : col_a - c + (c & ~3);
+#pragma unroll
+                for (int blk = 0; blk < 4; ++blk) {
+                    const int64_t m = m0 + wm * S::WM + mb * 32 + 8 * blk + hrow;
+                    float v[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(oa[4 * blk + j]);
+                    quad_transpose4(v, q);
+                    u32x2_t o;
+                    o[0] = __float_as_uint(v[0]) | (__float_as_uint(v[1]) << 16);
+                    o[1] = __float_as_uint(v[2]) | (__float_as_uint(v[3]) << 16);
+                    __builtin_nontemporal_store(o, (u32x2_t*)(y + m * ld + ca));
+                    if (EPI == kEpiRope) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(ob[4 * blk + j]);
+                        quad_transpose4(v, q);
+                        o[0] = __float_as_uint(v[0]) | (__float_as_uint(v[1]) << 16);
+                        o[1] = __float_as_uint(v[2]) | (__float_as_uint(v[3]) << 16);
+                        __builtin_nontemporal_store(o, (u32x2_t*)(y + m * ld + ca + 32));
+                    }
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int64_t m =
+                        m0 + wm * S::WM + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+                    if (m >= M) continue;
+                    if (EPI == kEpiSwiGLU) {
+                        y[m * ld + (n0 + wn * S::WN) / 2 + 32 * p + c] = (uint16_t)oa[i];
+                    } else {
+                        y[m * ld + col_a] = (uint16_t)oa[i];
+                        y[m * ld + col_a + 32] = (uint16_t)ob[i];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <class S, int EPI, bool HAS_BIAS>
+static hipError_t launch_pair_t(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                uint16_t* y, int64_t M, int64_t K, int64_t N, PairArgs pa,
+                                hipStream_t stream) {
+    auto kern = linear_pair_kernel<S, EPI, HAS_BIAS>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        hipError_t e = hipFuncSetAttribute((const void*)kern,
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           S::LDS_BYTES);
+        if (e != hipSuccess) return e;
+        attr_set = true;
+    }
+    const int tiles_m = (int)((M + S::BM - 1) / S::BM);
+    const int tiles_n = (int)((N + S::BN - 1) / S::BN);
+    const int group_m = tiles_m < 4 ? tiles_m : 4;
+    hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(S::NT), S::LDS_BYTES, stream, x, w,
+                       bias, y, M, K, N, tiles_n, group_m, pa);
+    return hipGetLastError();
+}
+
+template <int EPI>
+static hipError_t launch_pair(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                              uint16_t* y, int64_t M, int64_t K, int64_t N, PairArgs pa,
+                              hipStream_t st) {
+    using L0 = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
+    using L1 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
+    using L2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
+    const bool hb = bias != nullptr;
+    switch (linear_tile_config(M, N, -1)) {
+        case 0:
+            return hb ? launch_pair_t<L0, EPI, true>(x, w, bias, y, M, K, N, pa, st)
+                      : launch_pair_t<L0, EPI, false>(x, w, bias, y, M, K, N, pa, st);
+        case 1:
+            return hb ? launch_pair_t<L1, EPI, true>(x, w, bias, y, M, K, N, pa, st)
+                      : launch_pair_t<L1, EPI, false>(x, w, bias, y, M, K, N, pa, st);
+        default:
+            return hb ? launch_pair_t<L2, EPI, true>(x, w, bias, y, M, K, N, pa, st)
+                      : launch_pair_t<L2, EPI, false>(x, w, bias, y, M, K, N, pa, st);
+    }
+}
+
+hipError_t launch_linear_swiglu(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                uint16_t* y, int64_t M, int64_t K, int64_t N2,
+                                hipStream_t stream) {
+    if (N2 % 64) return hipErrorInvalidValue;
+    return launch_pair<kEpiSwiGLU>(x, w, bias, y, M, K, N2, PairArgs{nullptr, nullptr, 1, 0},
+                                   stream);
+}
+
+hipError_t launch_linear_rope64(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                                uint16_t* y, int64_t M, int64_t K, int64_t N, int64_t rot_cols,
+                                int64_t seq_len, const float* cosine, const float* sine,
+                                hipStream_t stream) {
+    if (N % 64 || rot_cols % 64 || seq_len <= 0) return hipErrorInvalidValue;
+    return launch_pair<kEpiRope>(x, w, bias, y, M, K, N,
+                                 PairArgs{cosine, sine, seq_len, rot_cols}, stream);
+}
+
+}  // namespace ncm

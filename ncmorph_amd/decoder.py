@@ -68,7 +68,9 @@ class _Layer(C.Structure):
 class DecoderWeights:
     """Device weights: bf16 tensors for projections and embeddings, float32
     for norm scales. layers[i] maps the _LAYER_FIELDS names to tensors (the
-    bias entries may be None)."""
+    bias entries may be None): qkv_weight = rows of q, k, v concatenated;
+    gate_up_weight = gate and up rows interleaved in groups of 32
+    (kernels.interleave_gate_up)."""
 
     embed: object
     final_norm: object

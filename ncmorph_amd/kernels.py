@@ -145,6 +145,67 @@ def linear_bf16_residual(x, w, residual, bias=None, out=None, out_mode: str = "b
     return out
 
 
+def linear_bf16_swiglu(x, w, bias=None, out=None, ctx=None):
+    """round(silu_bf16(gate) * up) of the gate/up projection in one pass: w
+    torch.bfloat16 [2 I, k] with gate and up rows interleaved in groups of
+    32 (see interleave_gate_up); returns torch.bfloat16 [m, I]."""
+    import torch
+
+    m, k = x.shape
+    n2, k2 = w.shape
+    if k != k2:
+        raise NcmError(-2, "linear_bf16_swiglu")
+    if out is None:
+        out = torch.empty((m, n2 // 2), dtype=torch.bfloat16, device=x.device)
+    ctx = ctx or default_context(x.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_linear_bf16_swiglu(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
+                                       _dev_ptr(bias, "bias"), _dev_ptr(out, "out"), m, k, n2),
+          "linear_bf16_swiglu")
+    return out
+
+
+def interleave_gate_up(gate, up):
+    """[2 I, ...] rows in the order linear_bf16_swiglu reads: groups of 32
+    gate rows followed by the matching 32 up rows (I % 32 == 0)."""
+    inter = gate.shape[0]
+    if inter % 32 or up.shape[0] != inter:
+        raise ValueError("gate and up need the same row count, a multiple of 32")
+    rest = tuple(gate.shape[1:])
+    g = gate.reshape((inter // 32, 32) + rest)
+    u = up.reshape((inter // 32, 32) + rest)
+    try:
+        import torch
+
+        if isinstance(gate, torch.Tensor):
+            return torch.stack([g, u], dim=1).reshape((2 * inter,) + rest).contiguous()
+    except ImportError:
+        pass
+    return np.ascontiguousarray(np.stack([g, u], axis=1).reshape((2 * inter,) + rest))
+
+
+def linear_bf16_rope64(x, w, rot_cols: int, seq_len: int, cosine, sine, bias=None, out=None,
+                       ctx=None):
+    """bf16 projection with the RoPE of its 64-wide heads in columns
+    [0, rot_cols) fused (table row = row % seq_len); torch.bfloat16 out."""
+    import torch
+
+    m, k = x.shape
+    n, k2 = w.shape
+    if k != k2:
+        raise NcmError(-2, "linear_bf16_rope64")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    ctx = ctx or default_context(x.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_linear_bf16_rope64(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
+                                       _dev_ptr(bias, "bias"), _dev_ptr(out, "out"), m, k, n,
+                                       rot_cols, seq_len, _dev_ptr(cosine, "cosine"),
+                                       _dev_ptr(sine, "sine")),
+          "linear_bf16_rope64")
+    return out
+
+
 def linear_f32(x, w, out=None, ctx=None):
     """y = x @ w.T with float32 operands [m, k] and [n, k] (k % 4 == 0) on
     the fp32 MFMA, on torch's current stream."""

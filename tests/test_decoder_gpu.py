@@ -40,7 +40,7 @@ def _dev_f32(a, cuda):
                                                         (128, 20, False, 2, 70)])
 def test_decoder_forward_against_oracle(ncm, oracle, cuda, hd, window, biases, batch, seq):
     import torch
-    from ncmorph_amd import decoder
+    from ncmorph_amd import decoder, kernels
 
     rng = np.random.default_rng(hd + window + batch)
     hidden, inter, vocab, hq, hkv, nl = 256, 512, 300, 4, 2, 2
@@ -51,8 +51,14 @@ def test_decoder_forward_against_oracle(ncm, oracle, cuda, hd, window, biases, b
     cos, sin = decoder.rope_tables(spec, seq)
     dl = []
     for L in layers:
-        dl.append({k: (_dev_f32(v, cuda) if k.endswith("norm") else _dev_bf16(v, cuda))
-                   for k, v in L.items()})
+        d = {k: (_dev_f32(v, cuda) if k.endswith("norm") else _dev_bf16(v, cuda))
+             for k, v in L.items()}
+        # The device reads gate and up rows interleaved in groups of 32.
+        for name in ("gate_up_weight", "gate_up_bias"):
+            if L.get(name) is not None:
+                d[name] = _dev_bf16(kernels.interleave_gate_up(L[name][:inter], L[name][inter:]),
+                                    cuda)
+        dl.append(d)
     w = decoder.DecoderWeights(embed=_dev_bf16(embed, cuda), final_norm=_dev_f32(fnorm, cuda),
                                layers=dl)
     ids = rng.integers(0, vocab, (batch, seq))
