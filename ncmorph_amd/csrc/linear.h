@@ -8,7 +8,7 @@ namespace ncm {
 
 // Tile configuration chosen for an M x N output (see the table in
 // linear.hip); a valid `forced` index overrides the choice.
-int linear_tile_config(int64_t M, int64_t N, int forced);
+int linear_tile_config(int64_t M, int64_t N, int64_t K, int forced);
 
 hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, void* y,
                          int64_t M, int64_t K, int64_t N, int out_mode, int config,

@@ -212,16 +212,20 @@ constexpr int kLinConfigs = 11;
 // rate, so this tile is MFMA-bound with a wide margin.
 using LinF32 = GemmShape<128, 128, 32, 2, 2, 2, 5, true, 2, true>;
 
-int linear_tile_config(int64_t M, int64_t N, int forced) {
+int linear_tile_config(int64_t M, int64_t N, int64_t K, int forced) {
     if (forced >= 0 && forced < kLinConfigs) return forced;
     const int64_t cus = 256;
     auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    // 256x256 with 8 waves when it fills every CU; 128x128 with four LDS
-    // stages when that gives at most one tile per CU (latency-bound: deeper
-    // prefetch pays), else 128x128 with two stages (two workgroups per CU).
-    // All with direct-to-LDS loads.
-    if (tiles(256, 256) >= cus) return 0;
+    // 256x256 with 8 waves when it fills at least three quarters of the
+    // CUs; 128x128 with four LDS stages when that gives at most one tile per
+    // CU (latency-bound: deeper prefetch pays); for long K, 256x128 with
+    // three stages when its tiles fill the CUs about once or twice; else
+    // 128x128 with two stages (two workgroups per CU). All with
+    // direct-to-LDS loads. (Measured on the decoder's and the benchmark's
+    // shapes.)
+    if (tiles(256, 256) * 4 >= cus * 3) return 0;
     if (tiles(128, 128) <= cus) return 1;
+    if (K >= 4096 && tiles(256, 128) * 4 >= cus * 3 && tiles(256, 128) <= 2 * cus) return 5;
     return 2;
 }
 
@@ -234,7 +238,7 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
         return e ? atoi(e) : -1;
     }();
     if (config < 0) config = env_cfg;
-    switch (linear_tile_config(M, N, config)) {
+    switch (linear_tile_config(M, N, K, config)) {
         case 0: return launch_linear_s<Lin0>(x, w, bias, y, M, K, N, out_mode, stream);
         case 1: return launch_linear_s<Lin1>(x, w, bias, y, M, K, N, out_mode, stream);
         case 2: return launch_linear_s<Lin2>(x, w, bias, y, M, K, N, out_mode, stream);
@@ -267,10 +271,11 @@ static hipError_t launch_linear_res_s(const uint16_t* x, const uint16_t* w, cons
 hipError_t launch_linear_residual(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                   const float* residual, void* y, int64_t M, int64_t K,
                                   int64_t N, int out_mode, hipStream_t stream) {
-    // The automatic tile choice only (configurations 0-2).
-    switch (linear_tile_config(M, N, -1)) {
+    // The automatic tile choice only (configurations 0, 1, 2 and 5).
+    switch (linear_tile_config(M, N, K, -1)) {
         case 0: return launch_linear_res_s<Lin0>(x, w, bias, residual, y, M, K, N, out_mode, stream);
         case 1: return launch_linear_res_s<Lin1>(x, w, bias, residual, y, M, K, N, out_mode, stream);
+        case 5: return launch_linear_res_s<Lin5>(x, w, bias, residual, y, M, K, N, out_mode, stream);
         default: return launch_linear_res_s<Lin2>(x, w, bias, residual, y, M, K, N, out_mode, stream);
     }
 }

@@ -75,85 +75,78 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_pair_kernel(
     const int wn = wave / S::WGM;
     const int c = lane & 31;
     const int64_t ld = EPI == kEpiSwiGLU ? N / 2 : N;
-    const bool full = m0 + S::BM <= M;
 
 #pragma unroll
     for (int p = 0; p < S::NB / 2; ++p) {
         const int64_t col_a = n0 + wn * S::WN + 64 * p + c;  // first tile's column
-        if (col_a >= N) continue;  // N % 64 == 0: the pair is wholly in or out
+        // N % 64 == 0: the pair is wholly in or out (wave-uniform).
+        const bool in_range = col_a < N;
         float ba = 0.0f, bb = 0.0f;
-        if (HAS_BIAS) {
+        if (HAS_BIAS && in_range) {
             ba = __uint_as_float((uint32_t)bias[col_a] << 16);
             bb = __uint_as_float((uint32_t)bias[col_a + 32] << 16);
         }
         const bool rotate = EPI == kEpiRope && col_a < pa.rot_cols;
 #pragma unroll
         for (int mb = 0; mb < S::MB; ++mb) {
-            uint32_t oa[16], ob[16];
+            if (!in_range) break;
+            // Per group of 4 rows: the projection's bits, a quad transpose
+            // (each lane then holds 4 consecutive columns of one row, so
+            // stores are 8 bytes and each RoPE table half is one 16-byte
+            // load), then the fused op. Rows past M (a partial last row
+            // tile) are computed on table row 0 and not stored.
+            const int q = lane & 3;
+            const int hrow = 4 * (lane >> 5) + q;
+            const int c4 = c & ~3;
+            const int64_t ca = EPI == kEpiSwiGLU ? (n0 + wn * S::WN) / 2 + 32 * p + c4
+                                                 : col_a - c + c4;
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const uint32_t fa = proj_bits(acc.v[mb][2 * p][i], ba);
-                const uint32_t fb = proj_bits(acc.v[mb][2 * p + 1][i], bb);
-                if (EPI == kEpiSwiGLU) {
-                    oa[i] = swiglu_bits(fa, fb);
-                } else if (rotate) {
-                    const int64_t m =
-                        m0 + wm * S::WM + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                    const int64_t t = (m < M ? m : 0) % pa.seq_len;
-                    const float* ct = pa.cosine + t * 64 + c;
-                    const float* st = pa.sine + t * 64 + c;
-                    const float first = __uint_as_float(fa << 16);
-                    const float second = __uint_as_float(fb << 16);
-                    const float left = rb(first * rb(ct[0]));
-                    const float right = rb(-second * rb(st[0]));
-                    const float right2 = rb(first * rb(st[32]));
-                    const float left2 = rb(second * rb(ct[32]));
-                    oa[i] = bf16_bits_rne(left + right);
-                    ob[i] = bf16_bits_rne(left2 + right2);
-                } else {
-                    oa[i] = fa;
-                    ob[i] = fb;
+            for (int blk = 0; blk < 4; ++blk) {
+                const int64_t m = m0 + wm * S::WM + mb * 32 + 8 * blk + hrow;
+                float va[4], vb[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    va[j] = __uint_as_float(proj_bits(acc.v[mb][2 * p][4 * blk + j], ba));
+                    vb[j] = __uint_as_float(proj_bits(acc.v[mb][2 * p + 1][4 * blk + j], bb));
                 }
-            }
-            if (full) {
-                // Quad transpose: each lane then holds 4 consecutive columns
-                // of one row (8-byte stores).
-                const int q = lane & 3;
-                const int hrow = 4 * (lane >> 5) + q;
-                const int64_t ca = EPI == kEpiSwiGLU
-                                       ? (n0 + wn * S::WN) / 2 + 32 * p + (c & ~3)
-                                       : col_a - c + (c & ~3);
+                quad_transpose4(va, q);
+                quad_transpose4(vb, q);
+                uint32_t ra[4], rbits[4];
 #pragma unroll
-                for (int blk = 0; blk < 4; ++blk) {
-                    const int64_t m = m0 + wm * S::WM + mb * 32 + 8 * blk + hrow;
-                    float v[4];
+                for (int j = 0; j < 4; ++j) {
+                    ra[j] = __float_as_uint(va[j]);
+                    rbits[j] = __float_as_uint(vb[j]);
+                }
+                if (EPI == kEpiSwiGLU) {
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(oa[4 * blk + j]);
-                    quad_transpose4(v, q);
-                    u32x2_t o;
-                    o[0] = __float_as_uint(v[0]) | (__float_as_uint(v[1]) << 16);
-                    o[1] = __float_as_uint(v[2]) | (__float_as_uint(v[3]) << 16);
-                    __builtin_nontemporal_store(o, (u32x2_t*)(y + m * ld + ca));
-                    if (EPI == kEpiRope) {
+                    for (int j = 0; j < 4; ++j) ra[j] = swiglu_bits(ra[j], rbits[j]);
+                } else if (rotate) {
+                    const int64_t t = (m < M ? m : 0) % pa.seq_len;
+                    const f32x4_t cf = *(const f32x4_t*)(pa.cosine + t * 64 + c4);
+                    const f32x4_t cs = *(const f32x4_t*)(pa.cosine + t * 64 + 32 + c4);
+                    const f32x4_t sf = *(const f32x4_t*)(pa.sine + t * 64 + c4);
+                    const f32x4_t ss = *(const f32x4_t*)(pa.sine + t * 64 + 32 + c4);
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) v[j] = __uint_as_float(ob[4 * blk + j]);
-                        quad_transpose4(v, q);
-                        o[0] = __float_as_uint(v[0]) | (__float_as_uint(v[1]) << 16);
-                        o[1] = __float_as_uint(v[2]) | (__float_as_uint(v[3]) << 16);
-                        __builtin_nontemporal_store(o, (u32x2_t*)(y + m * ld + ca + 32));
+                    for (int j = 0; j < 4; ++j) {
+                        const float first = __uint_as_float(ra[j] << 16);
+                        const float second = __uint_as_float(rbits[j] << 16);
+                        const float left = rb(first * rb(cf[j]));
+                        const float right = rb(-second * rb(sf[j]));
+                        const float right2 = rb(first * rb(ss[j]));
+                        const float left2 = rb(second * rb(cs[j]));
+                        ra[j] = bf16_bits_rne(left + right);
+                        rbits[j] = bf16_bits_rne(left2 + right2);
                     }
                 }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int64_t m =
-                        m0 + wm * S::WM + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                    if (m >= M) continue;
-                    if (EPI == kEpiSwiGLU) {
-                        y[m * ld + (n0 + wn * S::WN) / 2 + 32 * p + c] = (uint16_t)oa[i];
-                    } else {
-                        y[m * ld + col_a] = (uint16_t)oa[i];
-                        y[m * ld + col_a + 32] = (uint16_t)ob[i];
+                if (m < M) {
+                    u32x2_t o;
+                    o[0] = ra[0] | (ra[1] << 16);
+                    o[1] = ra[2] | (ra[3] << 16);
+                    __builtin_nontemporal_store(o, (u32x2_t*)(y + m * ld + ca));
+                    if (EPI == kEpiRope) {
+                        o[0] = rbits[0] | (rbits[1] << 16);
+                        o[1] = rbits[2] | (rbits[3] << 16);
+                        __builtin_nontemporal_store(o, (u32x2_t*)(y + m * ld + ca + 32));
                     }
                 }
             }
@@ -189,14 +182,18 @@ static hipError_t launch_pair(const uint16_t* x, const uint16_t* w, const uint16
     using L0 = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
     using L1 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
     using L2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
+    using L5 = GemmShape<256, 128, 64, 4, 2, 2, 5, true, 3>;
     const bool hb = bias != nullptr;
-    switch (linear_tile_config(M, N, -1)) {
+    switch (linear_tile_config(M, N, K, -1)) {
         case 0:
             return hb ? launch_pair_t<L0, EPI, true>(x, w, bias, y, M, K, N, pa, st)
                       : launch_pair_t<L0, EPI, false>(x, w, bias, y, M, K, N, pa, st);
         case 1:
             return hb ? launch_pair_t<L1, EPI, true>(x, w, bias, y, M, K, N, pa, st)
                       : launch_pair_t<L1, EPI, false>(x, w, bias, y, M, K, N, pa, st);
+        case 5:
+            return hb ? launch_pair_t<L5, EPI, true>(x, w, bias, y, M, K, N, pa, st)
+                      : launch_pair_t<L5, EPI, false>(x, w, bias, y, M, K, N, pa, st);
         default:
             return hb ? launch_pair_t<L2, EPI, true>(x, w, bias, y, M, K, N, pa, st)
                       : launch_pair_t<L2, EPI, false>(x, w, bias, y, M, K, N, pa, st);
