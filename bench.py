@@ -232,6 +232,39 @@ def run_decoder(torch, reps=10, warmup=3):
                          "flops_linear": lin, "flops_attention_causal": att}}
 
 
+PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
+
+
+def run_weight_upload(torch, mib=512):
+    """Device weight path: one bf16 tensor of `mib` MiB in a safetensors file
+    (written first, so it is in the page cache) copied to HBM as stored
+    through the pinned staging of ncm_st_upload; host-to-device GB/s."""
+    import tempfile
+
+    from ncmorph_amd import safetensors as st
+
+    n = mib * 2**20 // 2
+    raw = np.random.default_rng(14).integers(0, 2**16, n, dtype=np.uint16).tobytes()
+    dev = torch.device("cuda", 0)
+    out = torch.empty(n, dtype=torch.int16, device=dev)
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "w.safetensors")
+        st.write_file(path, {"w": ("BF16", (n,), raw)})
+        with st.SafetensorsFile(path) as f:
+            f.upload("w", out)
+            torch.cuda.synchronize()
+            reps = 3
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                f.upload("w", out)
+            torch.cuda.synchronize()
+            sec = (time.perf_counter() - t0) / reps
+    gbs = n * 2 / sec / 1e9
+    return {"bytes": n * 2, "ms": round(sec * 1e3, 2),
+            "roofline": {"bound": "pcie", "achieved": round(gbs, 1), "peak": PCIE_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / PCIE_PEAK_GBS, 4)}}
+
+
 def cpu_decoder_baseline():
     """Oracle decoder (scalar restatements, 1 thread) of the same model shape
     on 4 tokens: once with no layers and an LM head of 8192 vocabulary rows,
@@ -401,6 +434,7 @@ def main():
                 res["cpu_baseline"] = rvq["cpu_baseline"]
     if args.only in ("decoder", "all"):
         dec = run_decoder(torch)
+        dec["weight_upload"] = run_weight_upload(torch)
         if not args.no_cpu:
             dec["cpu_baseline"] = cpu_decoder_baseline()
         res["decoder_prefill"] = dec

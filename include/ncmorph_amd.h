@@ -36,7 +36,9 @@ enum {
     NCM_E_HIP = -4,       /* a HIP runtime call failed */
     NCM_E_NOMEM = -5,     /* device or host allocation failed */
     NCM_E_DEVICE = -6,    /* no usable gfx950 device */
-    NCM_E_ARG = -7        /* an argument value is out of range */
+    NCM_E_ARG = -7,       /* an argument value is out of range */
+    NCM_E_FORMAT = -8     /* malformed file or header; ncm_last_error() names
+                             the reference's error (e.g. "InvalidOffsets") */
 };
 
 /* Linear output modes. */
@@ -311,6 +313,67 @@ int ncm_rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t
 int ncm_rvq_decode(ncm_ctx_t* ctx, const int32_t* codes, int64_t b, int64_t t, int64_t d,
                    int64_t levels, const int32_t* strides, const uint16_t* codebooks,
                    int64_t v, float* recon);
+
+/* ---- safetensors weights (packages/safetensors/root.zig) ---- */
+
+/* Reader for the safetensors header and the sharded index, with the
+ * reference's checks in its order (root.zig:148-193, 197-228): the 8-byte
+ * little-endian length (>= 8 bytes, <= 100 000 000), valid UTF-8, a JSON
+ * object of tensors {"dtype", "shape", "data_offsets"} and an optional
+ * "__metadata__" of strings, known dtypes, offsets contiguous from 0 in
+ * data-offset order, shape and bit products without overflow, whole bytes,
+ * sizes matching shapes, file = prefix + header + data. Malformed input
+ * returns NCM_E_FORMAT with the reference's error name in ncm_last_error()
+ * ("HeaderTooSmall", "HeaderTooLarge", "InvalidHeaderLength", "InvalidUtf8",
+ * "InvalidHeader", "UnknownDtype", "InvalidOffsets", "ShapeOverflow",
+ * "MisalignedBits", "SizeMismatch", "FileSizeMismatch", "InvalidIndex",
+ * "UnsafeShardName"; "SyntaxError" for JSON that does not parse). */
+#define NCM_ST_MAX_DIMS 8
+typedef struct ncm_st_file ncm_st_file_t;
+typedef struct ncm_st_index ncm_st_index_t;
+typedef struct ncm_st_tensor {
+    const char* name;        /* owned by the file handle */
+    int32_t dtype;           /* index in the reference's Dtype order: BOOL 0, U8, I8,
+                                U16, I16, U32, I32, U64, I64, F4, F6_E2M3, F6_E3M2,
+                                F8_E5M2, F8_E4M3, F8_E8M0, F8_E4M3FNUZ, F8_E5M2FNUZ,
+                                F16 17, BF16 18, F32 19, F64 20, C64 21 */
+    int32_t ndim;
+    uint64_t shape[NCM_ST_MAX_DIMS];
+    uint64_t data_begin;     /* byte range inside the data section */
+    uint64_t data_end;
+} ncm_st_tensor_t;
+
+/* Parses a header held in memory: bytes starts with the 8-byte prefix and
+ * holds at least the JSON header; file_size is the whole file's size
+ * (parse_header, root.zig:148-193). */
+int ncm_st_parse(const void* bytes, size_t len, uint64_t file_size, ncm_st_file_t** out);
+/* Maps a .safetensors file and parses its header. */
+int ncm_st_open(const char* path, ncm_st_file_t** out);
+int ncm_st_close(ncm_st_file_t* f);
+int ncm_st_summary(const ncm_st_file_t* f, uint64_t* header_len, uint64_t* data_len,
+                   int64_t* tensor_count);
+/* Tensor i in data-offset order; NCM_E_SHAPE (info filled, shape cut) when
+ * ndim > NCM_ST_MAX_DIMS. */
+int ncm_st_tensor(const ncm_st_file_t* f, int64_t index, ncm_st_tensor_t* out);
+int ncm_st_find(const ncm_st_file_t* f, const char* name, ncm_st_tensor_t* out);
+const char* ncm_st_dtype_name(int dtype);
+int ncm_st_dtype_bits(int dtype);
+/* Copies a tensor's stored bytes to device memory (dst_bytes must equal its
+ * size), stream-ordered on the context's stream through pinned staging
+ * buffers: bf16 weights reach the device as stored, without the loader's
+ * widen to f32 (src/loader.zig:339-342). The file must come from
+ * ncm_st_open. */
+int ncm_st_upload(ncm_ctx_t* ctx, const ncm_st_file_t* f, const char* name, void* dst,
+                  size_t dst_bytes);
+/* Sharded index (model.safetensors.index.json, parse_index, root.zig:197-228):
+ * weight_map of tensor -> plain shard file name, optional metadata.total_size. */
+int ncm_st_parse_index(const char* json, size_t len, ncm_st_index_t** out);
+int ncm_st_index_close(ncm_st_index_t* ix);
+int64_t ncm_st_index_count(const ncm_st_index_t* ix);
+int ncm_st_index_entry(const ncm_st_index_t* ix, int64_t i, const char** tensor,
+                       const char** shard);
+/* NCM_E_ARG when the index has no metadata.total_size. */
+int ncm_st_index_total_size(const ncm_st_index_t* ix, uint64_t* total);
 
 #ifdef __cplusplus
 }

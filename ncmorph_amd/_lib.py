@@ -20,6 +20,7 @@ NCM_E_HIP = -4
 NCM_E_NOMEM = -5
 NCM_E_DEVICE = -6
 NCM_E_ARG = -7
+NCM_E_FORMAT = -8
 
 NCM_OUT_F32 = 0
 NCM_OUT_BF16_F32 = 1
@@ -57,6 +58,21 @@ SIGNATURES = [
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
     ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
     ("ncm_rvq_decode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, i64, vp]),
+    ("ncm_st_parse", i32, [vp, sz, C.c_uint64, C.POINTER(vp)]),
+    ("ncm_st_open", i32, [C.c_char_p, C.POINTER(vp)]),
+    ("ncm_st_close", i32, [vp]),
+    ("ncm_st_summary", i32, [vp, C.POINTER(C.c_uint64), C.POINTER(C.c_uint64),
+                             C.POINTER(C.c_int64)]),
+    ("ncm_st_tensor", i32, [vp, i64, vp]),
+    ("ncm_st_find", i32, [vp, C.c_char_p, vp]),
+    ("ncm_st_dtype_name", C.c_char_p, [i32]),
+    ("ncm_st_dtype_bits", i32, [i32]),
+    ("ncm_st_upload", i32, [vp, vp, C.c_char_p, vp, sz]),
+    ("ncm_st_parse_index", i32, [C.c_char_p, sz, C.POINTER(vp)]),
+    ("ncm_st_index_close", i32, [vp]),
+    ("ncm_st_index_count", i64, [vp]),
+    ("ncm_st_index_entry", i32, [vp, i64, C.POINTER(C.c_char_p), C.POINTER(C.c_char_p)]),
+    ("ncm_st_index_total_size", i32, [vp, C.POINTER(C.c_uint64)]),
 ]
 
 _lib = None
@@ -73,7 +89,8 @@ class NcmError(RuntimeError):
             text = _lib.ncm_status_string(status).decode()
             detail = _lib.ncm_last_error().decode()
         msg = f"{where}: {text} ({status})"
-        if detail and status in (NCM_E_HIP, NCM_E_NOMEM, NCM_E_DEVICE):
+        self.detail = detail if status == NCM_E_FORMAT else ""
+        if detail and status in (NCM_E_HIP, NCM_E_NOMEM, NCM_E_DEVICE, NCM_E_FORMAT):
             msg += f" [{detail}]"
         super().__init__(msg)
 

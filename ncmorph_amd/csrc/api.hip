@@ -7,11 +7,15 @@
 #include <cstring>
 #include <mutex>
 #include <string>
+#include <thread>
+#include <vector>
+#include <algorithm>
 
 #include "../../include/ncmorph_amd.h"
 #include "decoder.h"
 #include "linear.h"
 #include "rvq.h"
+#include "status.h"
 
 struct ncm_ctx {
     int device = 0;
@@ -75,6 +79,61 @@ int ncm_ctx_workspace(ncm_ctx_t* ctx, size_t bytes, void** out) {
 
 hipStream_t ncm_ctx_stream(ncm_ctx_t* ctx) { return ctx->stream; }
 
+void ncm_set_error_detail(const std::string& what) { g_last_error = what; }
+
+int ncm_upload_host_bytes(ncm_ctx_t* ctx, const void* src, void* dst, size_t n) {
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    // Two pinned staging buffers, refilled from the (mapped, pageable) source
+    // while the previous chunk's copy runs.
+    constexpr size_t kChunk = 64u << 20;
+    constexpr int kCopyThreads = 8;
+    void* stage[2] = {nullptr, nullptr};
+    hipEvent_t done[2] = {nullptr, nullptr};
+    auto cleanup = [&]() {
+        for (int b = 0; b < 2; ++b) {
+            if (done[b]) { (void)hipEventSynchronize(done[b]); (void)hipEventDestroy(done[b]); }
+            if (stage[b]) (void)hipHostFree(stage[b]);
+        }
+    };
+    const size_t chunk = n < kChunk ? n : kChunk;
+    for (int b = 0; b < 2; ++b) {
+        if (hipHostMalloc(&stage[b], chunk, hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&done[b], hipEventDisableTiming) != hipSuccess) {
+            (void)hipGetLastError();
+            cleanup();
+            g_last_error = "pinned staging allocation failed";
+            return NCM_E_NOMEM;
+        }
+    }
+    size_t off = 0;
+    for (int b = 0; off < n; b ^= 1) {
+        const size_t len = n - off < chunk ? n - off : chunk;
+        hipError_t e = hipEventSynchronize(done[b]);  // the buffer's previous copy is done
+        if (e == hipSuccess) {
+            // Page-cache -> pinned copy in parallel slices (one thread moves
+            // ~10-15 GB/s; the host link takes several times that).
+            const char* from = (const char*)src + off;
+            char* to = (char*)stage[b];
+            const size_t slice = (len + kCopyThreads - 1) / kCopyThreads;
+            std::vector<std::thread> pool;
+            for (int t = 1; t < kCopyThreads && t * slice < len; ++t)
+                pool.emplace_back([=] {
+                    const size_t a = t * slice, z = std::min(len, a + slice);
+                    std::memcpy(to + a, from + a, z - a);
+                });
+            std::memcpy(to, from, std::min(len, slice));
+            for (auto& th : pool) th.join();
+            e = hipMemcpyAsync((char*)dst + off, stage[b], len, hipMemcpyHostToDevice, ctx->stream);
+        }
+        if (e == hipSuccess) e = hipEventRecord(done[b], ctx->stream);
+        if (e != hipSuccess) { cleanup(); return fail_hip(e, "upload"); }
+        off += len;
+    }
+    cleanup();  // waits for the last copies: the staging memory is freed
+    return NCM_OK;
+}
+
 extern "C" {
 
 const char* ncm_status_string(int status) {
@@ -87,6 +146,7 @@ const char* ncm_status_string(int status) {
         case NCM_E_NOMEM: return "allocation failed";
         case NCM_E_DEVICE: return "no usable gfx950 device";
         case NCM_E_ARG: return "argument out of range";
+        case NCM_E_FORMAT: return "malformed file or header";
         default: return "unknown status";
     }
 }

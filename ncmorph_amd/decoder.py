@@ -205,3 +205,127 @@ def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine,
                                         _ptr(logits)),
           "decoder_forward")
     return logits
+
+
+def _hf_names(i: int) -> dict:
+    p = f"model.layers.{i}."
+    return {"input_norm": p + "input_layernorm.weight",
+            "q": p + "self_attn.q_proj", "k": p + "self_attn.k_proj", "v": p + "self_attn.v_proj",
+            "o": p + "self_attn.o_proj", "post_attention_norm": p + "post_attention_layernorm.weight",
+            "gate": p + "mlp.gate_proj", "up": p + "mlp.up_proj", "down": p + "mlp.down_proj"}
+
+
+def load_safetensors(spec: DecoderSpec, path: str, device) -> DecoderWeights:
+    """Device weights of a Llama-layout checkpoint (Transformers names:
+    model.embed_tokens, model.layers.N.{input_layernorm, self_attn.{q,k,v,o}_proj,
+    post_attention_layernorm, mlp.{gate,up,down}_proj}, model.norm, lm_head),
+    from one .safetensors file or a directory with model.safetensors or a
+    sharded model.safetensors.index.json (the loader's manifest-first order,
+    src/loader.zig:95-202). BF16 tensors are copied to HBM as stored
+    (ncm_st_upload); F32 projection weights are rounded to bf16 on the device
+    (RNE, the operand rounding of matmul_bf16); norm scales are widened to
+    f32. q|k|v rows are concatenated and gate/up rows interleaved in place."""
+    import os
+
+    import torch
+
+    from . import kernels
+    from .safetensors import SafetensorsFile, parse_index
+
+    files, where = {}, {}
+    if os.path.isdir(path):
+        idx = os.path.join(path, "model.safetensors.index.json")
+        if os.path.exists(idx):
+            entries, _ = parse_index(open(idx).read())
+            for tensor, shard in entries:
+                where[tensor] = os.path.join(path, shard)
+        else:
+            path = os.path.join(path, "model.safetensors")
+    if not where:
+        f = SafetensorsFile(path)
+        files[path] = f
+        for t in f.tensors():
+            where[t.name] = path
+
+    def handle(name):
+        if name not in where:
+            raise KeyError(f"checkpoint has no tensor {name}")
+        p = where[name]
+        if p not in files:
+            files[p] = SafetensorsFile(p)
+        return files[p], files[p].find(name)
+
+    def load_into(name, out):
+        """Tensor `name` into the bf16 device tensor `out` (same element count)."""
+        f, info = handle(name)
+        n = 1
+        for d in info.shape:
+            n *= d
+        if n != out.numel():
+            raise ValueError(f"{name}: {info.shape} does not fit {tuple(out.shape)}")
+        if info.dtype == "BF16":
+            f.upload(name, out)
+        elif info.dtype == "F32":
+            tmp = torch.empty(n, dtype=torch.float32, device=device)
+            f.upload(name, tmp)
+            out.view(-1).copy_(kernels.bf16_from_f32(tmp).view(-1))
+        else:
+            raise ValueError(f"{name}: dtype {info.dtype} is not BF16 or F32")
+        return out
+
+    def bf16(*shape):
+        return torch.empty(*shape, dtype=torch.bfloat16, device=device)
+
+    def norm(name):
+        f, info = handle(name)
+        if info.dtype == "F32":
+            out = torch.empty(spec.hidden, dtype=torch.float32, device=device)
+            f.upload(name, out)
+            return out
+        return load_into(name, bf16(spec.hidden)).float()
+
+    def optional_bias(name, out):
+        return load_into(name, out) if name in where else None
+
+    qw, kw = spec.q_heads * spec.head_dim, spec.kv_heads * spec.head_dim
+    layers = []
+    for i in range(spec.layers):
+        n = _hf_names(i)
+        qkv = bf16(spec.qkv_width, spec.hidden)
+        load_into(n["q"] + ".weight", qkv[:qw])
+        load_into(n["k"] + ".weight", qkv[qw:qw + kw])
+        load_into(n["v"] + ".weight", qkv[qw + kw:])
+        qkv_b = None
+        if n["q"] + ".bias" in where:
+            qkv_b = bf16(spec.qkv_width)
+            load_into(n["q"] + ".bias", qkv_b[:qw])
+            load_into(n["k"] + ".bias", qkv_b[qw:qw + kw])
+            load_into(n["v"] + ".bias", qkv_b[qw + kw:])
+        gate = load_into(n["gate"] + ".weight", bf16(spec.intermediate, spec.hidden))
+        up = load_into(n["up"] + ".weight", bf16(spec.intermediate, spec.hidden))
+        gu_b = None
+        if n["gate"] + ".bias" in where:
+            gb = load_into(n["gate"] + ".bias", bf16(spec.intermediate))
+            ub = load_into(n["up"] + ".bias", bf16(spec.intermediate))
+            gu_b = kernels.interleave_gate_up(gb, ub)
+        layers.append({
+            "input_norm": norm(n["input_norm"]),
+            "qkv_weight": qkv, "qkv_bias": qkv_b,
+            "o_weight": load_into(n["o"] + ".weight", bf16(spec.hidden, qw)),
+            "o_bias": optional_bias(n["o"] + ".bias", bf16(spec.hidden)),
+            "post_attention_norm": norm(n["post_attention_norm"]),
+            "gate_up_weight": kernels.interleave_gate_up(gate, up), "gate_up_bias": gu_b,
+            "down_weight": load_into(n["down"] + ".weight", bf16(spec.hidden, spec.intermediate)),
+            "down_bias": optional_bias(n["down"] + ".bias", bf16(spec.hidden)),
+        })
+        del gate, up
+    embed = load_into("model.embed_tokens.weight", bf16(spec.vocab, spec.hidden))
+    lm_head = None
+    if not spec.tie_word_embeddings:
+        lm_head = load_into("lm_head.weight", bf16(spec.vocab, spec.hidden))
+    weights = DecoderWeights(embed=embed, final_norm=norm("model.norm.weight"), layers=layers,
+                             lm_head=lm_head)
+    torch.cuda.current_stream(device).synchronize()
+    for f in files.values():
+        f.close()
+    return weights

@@ -384,3 +384,147 @@ def decoder_forward(ids, embed, layers, final_norm, lm_head, cos, sin, q_heads, 
         hidden = round_bf16(hidden + mlp)
     n = rms_norm(hidden, final_norm, eps, bf16=True)
     return matmul_bf16(n, embed if lm_head is None else lm_head)
+
+
+# ------------------------------------------------------------ safetensors
+# Restatement of packages/safetensors/root.zig:136-193 (header) and 197-228
+# (index) with Python's json module. Errors are returned as the reference's
+# error names.
+ST_DTYPES = [("BOOL", 8), ("U8", 8), ("I8", 8), ("U16", 16), ("I16", 16), ("U32", 32),
+             ("I32", 32), ("U64", 64), ("I64", 64), ("F4", 4), ("F6_E2M3", 6), ("F6_E3M2", 6),
+             ("F8_E5M2", 8), ("F8_E4M3", 8), ("F8_E8M0", 8), ("F8_E4M3FNUZ", 8),
+             ("F8_E5M2FNUZ", 8), ("F16", 16), ("BF16", 16), ("F32", 32), ("F64", 64),
+             ("C64", 64)]
+ST_MAX_HEADER = 100_000_000
+
+
+class StError(Exception):
+    pass
+
+
+def _st_json(text):
+    import json
+
+    def pairs(kv):
+        out = {}
+        for k, v in kv:
+            out[k] = v  # a repeated key keeps its first position, last value
+        return out
+
+    def bad_constant(_):
+        raise StError("SyntaxError")
+
+    try:
+        root = json.loads(text, object_pairs_hook=pairs, parse_constant=bad_constant)
+    except ValueError:
+        raise StError("SyntaxError")
+
+    def check(v):  # a lone surrogate escape is not a valid JSON string
+        for x in (list(v.keys()) + list(v.values()) if isinstance(v, dict) else
+                  v if isinstance(v, list) else [v]):
+            if isinstance(x, str):
+                try:
+                    x.encode("utf-8")
+                except UnicodeEncodeError:
+                    raise StError("SyntaxError")
+            elif isinstance(x, (dict, list)):
+                check(x)
+
+    check(root)
+    return root
+
+
+def _st_uint(v):
+    # std.json integers are i64; anything else (floats, bools, larger
+    # integers, negatives) is not a non-negative integer.
+    if isinstance(v, bool) or not isinstance(v, int) or v < 0 or v > 2**63 - 1:
+        raise StError("InvalidHeader")
+    return v
+
+
+def st_parse_header(data: bytes, file_size: int):
+    """Returns (header_len, data_len, [(name, dtype_index, shape, begin, end)])
+    in data-offset order, or raises StError(name)."""
+    if len(data) < 8:
+        raise StError("HeaderTooSmall")
+    hl = int.from_bytes(data[:8], "little")
+    if hl > ST_MAX_HEADER:
+        raise StError("HeaderTooLarge")
+    if len(data) < 8 + hl:
+        raise StError("InvalidHeaderLength")
+    try:
+        text = data[8:8 + hl].decode("utf-8")
+    except UnicodeDecodeError:
+        raise StError("InvalidUtf8")
+    root = _st_json(text)
+    if not isinstance(root, dict):
+        raise StError("InvalidHeader")
+    names = [n for n, _ in ST_DTYPES]
+    tensors = []
+    for name, value in root.items():
+        if name == "__metadata__":
+            if not isinstance(value, dict) or not all(isinstance(x, str) for x in value.values()):
+                raise StError("InvalidHeader")
+            continue
+        if not isinstance(value, dict):
+            raise StError("InvalidHeader")
+        dt = value.get("dtype")
+        if not isinstance(dt, str):
+            raise StError("InvalidHeader")
+        if dt not in names:
+            raise StError("UnknownDtype")
+        shape = value.get("shape")
+        if not isinstance(shape, list):
+            raise StError("InvalidHeader")
+        shape = [_st_uint(d) for d in shape]
+        offs = value.get("data_offsets")
+        if not isinstance(offs, list) or len(offs) != 2:
+            raise StError("InvalidHeader")
+        begin, end = _st_uint(offs[0]), _st_uint(offs[1])
+        tensors.append((name, names.index(dt), shape, begin, end))
+    tensors.sort(key=lambda t: (t[3], t[4]))
+    expected = 0
+    for name, dt, shape, begin, end in tensors:
+        if begin != expected or end < begin:
+            raise StError("InvalidOffsets")
+        expected = end
+        count = 1
+        for d in shape:
+            count *= d
+            if count >= 2**64:
+                raise StError("ShapeOverflow")
+        bits = count * ST_DTYPES[dt][1]
+        if bits >= 2**64:
+            raise StError("ShapeOverflow")
+        if bits % 8:
+            raise StError("MisalignedBits")
+        if end - begin != bits // 8:
+            raise StError("SizeMismatch")
+    if 8 + hl + expected != file_size:
+        raise StError("FileSizeMismatch")
+    return hl, expected, tensors
+
+
+def st_parse_index(text: str):
+    """Returns ([(tensor, shard)], total_size or None), or raises StError."""
+    root = _st_json(text)
+    if not isinstance(root, dict):
+        raise StError("InvalidIndex")
+    wm = root.get("weight_map")
+    if not isinstance(wm, dict):
+        raise StError("InvalidIndex")
+    entries = []
+    for tensor, shard in wm.items():
+        if not isinstance(shard, str):
+            raise StError("InvalidIndex")
+        if shard in ("", ".", "..") or any(c in shard for c in "/\\\0"):
+            raise StError("UnsafeShardName")
+        entries.append((tensor, shard))
+    total = None
+    if "metadata" in root:
+        md = root["metadata"]
+        if not isinstance(md, dict):
+            raise StError("InvalidIndex")
+        if "total_size" in md:
+            total = _st_uint(md["total_size"])
+    return entries, total

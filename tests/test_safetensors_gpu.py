@@ -1,0 +1,130 @@
+"""Device weight path: safetensors tensors uploaded to HBM as stored (bytes
+identical, across the pinned staging chunks) and a Llama-layout checkpoint
+(single file and sharded) loaded into the decoder's layout: the forward
+gives the same bits as with the same weights handed over directly."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from ncmorph_amd import safetensors as st
+from ncmorph_amd import synth
+
+from .decoder_f64 import random_model
+
+pytestmark = pytest.mark.gpu
+
+
+def test_upload_bytes_identical(ncm, cuda, tmp_path):
+    import torch
+
+    rng = np.random.default_rng(1)
+    big = rng.integers(0, 2**16, 150 * 2**20 // 2 + 7, dtype=np.uint16)  # > two 64 MB chunks
+    small = rng.standard_normal(33).astype(np.float32)
+    p = str(tmp_path / "w.safetensors")
+    st.write_file(p, {"big": ("BF16", (big.size,), big.tobytes()),
+                      "small": ("F32", (33,), small.tobytes()),
+                      "empty": ("BF16", (0, 4), b"")})
+    with st.SafetensorsFile(p) as f:
+        out = torch.empty(big.size, dtype=torch.int16, device=cuda)
+        f.upload("big", out)
+        o2 = torch.empty(33, dtype=torch.float32, device=cuda)
+        f.upload("small", o2)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy().view(np.uint16), big)
+        assert np.array_equal(o2.cpu().numpy(), small)
+        with pytest.raises(st.NcmError):  # wrong byte count
+            f.upload("small", torch.empty(32, dtype=torch.float32, device=cuda))
+        with pytest.raises(st.NcmError):
+            f.upload("missing", o2)
+        assert f.find("empty").shape == (0, 4)
+
+
+def _write_checkpoint(path, embed, layers, fnorm, hq, hkv, hd, shards=1, f32_keys=()):
+    tensors = {"model.embed_tokens.weight": embed}
+    qw, kw = hq * hd, hkv * hd
+    inter = layers[0]["gate_up_weight"].shape[0] // 2
+    for i, L in enumerate(layers):
+        p = f"model.layers.{i}."
+        tensors[p + "input_layernorm.weight"] = L["input_norm"]
+        tensors[p + "self_attn.q_proj.weight"] = L["qkv_weight"][:qw]
+        tensors[p + "self_attn.k_proj.weight"] = L["qkv_weight"][qw:qw + kw]
+        tensors[p + "self_attn.v_proj.weight"] = L["qkv_weight"][qw + kw:]
+        if L.get("qkv_bias") is not None:
+            tensors[p + "self_attn.q_proj.bias"] = L["qkv_bias"][:qw]
+            tensors[p + "self_attn.k_proj.bias"] = L["qkv_bias"][qw:qw + kw]
+            tensors[p + "self_attn.v_proj.bias"] = L["qkv_bias"][qw + kw:]
+        tensors[p + "self_attn.o_proj.weight"] = L["o_weight"]
+        tensors[p + "post_attention_layernorm.weight"] = L["post_attention_norm"]
+        tensors[p + "mlp.gate_proj.weight"] = L["gate_up_weight"][:inter]
+        tensors[p + "mlp.up_proj.weight"] = L["gate_up_weight"][inter:]
+        tensors[p + "mlp.down_proj.weight"] = L["down_weight"]
+        if L.get("o_bias") is not None:
+            tensors[p + "self_attn.o_proj.bias"] = L["o_bias"]
+        if L.get("gate_up_bias") is not None:
+            tensors[p + "mlp.gate_proj.bias"] = L["gate_up_bias"][:inter]
+            tensors[p + "mlp.up_proj.bias"] = L["gate_up_bias"][inter:]
+        if L.get("down_bias") is not None:
+            tensors[p + "mlp.down_proj.bias"] = L["down_bias"]
+    tensors["model.norm.weight"] = fnorm
+
+    def entry(name, a):
+        a = np.ascontiguousarray(a, np.float32)
+        if name in f32_keys:
+            return ("F32", a.shape, a.tobytes())
+        return ("BF16", a.shape, synth.bf16_bits(a).tobytes())
+
+    names = list(tensors)
+    if shards == 1:
+        st.write_file(os.path.join(path, "model.safetensors"),
+                      {n: entry(n, tensors[n]) for n in names}, metadata={"format": "pt"})
+        return
+    wm = {}
+    for s in range(shards):
+        part = names[s::shards]
+        fname = f"model-{s + 1:05d}-of-{shards:05d}.safetensors"
+        st.write_file(os.path.join(path, fname), {n: entry(n, tensors[n]) for n in part})
+        wm.update({n: fname for n in part})
+    with open(os.path.join(path, "model.safetensors.index.json"), "w") as f:
+        json.dump({"metadata": {"total_size": 0}, "weight_map": wm}, f)
+
+
+@pytest.mark.parametrize("shards,biases,f32", [(1, False, False), (3, True, True)])
+def test_checkpoint_loads_into_decoder(ncm, oracle, cuda, tmp_path, shards, biases, f32):
+    import torch
+    from ncmorph_amd import decoder, kernels
+
+    rng = np.random.default_rng(shards)
+    hidden, inter, vocab, hq, hkv, hd, nl = 256, 512, 300, 4, 2, 64, 2
+    embed, layers, fnorm = random_model(rng, oracle.round_bf16, hidden, inter, vocab, hq, hkv,
+                                        hd, nl, biases=biases)
+    f32_keys = ("model.layers.0.mlp.down_proj.weight", "model.norm.weight") if f32 else ()
+    _write_checkpoint(str(tmp_path), embed, layers, fnorm, hq, hkv, hd, shards, f32_keys)
+    spec = decoder.DecoderSpec(hidden=hidden, intermediate=inter, vocab=vocab, q_heads=hq,
+                               kv_heads=hkv, head_dim=hd, layers=nl)
+    loaded = decoder.load_safetensors(spec, str(tmp_path), cuda)
+
+    def dev16(a):
+        return torch.from_numpy(synth.bf16_bits(np.ascontiguousarray(a, np.float32))
+                                .view(np.int16).copy()).to(cuda).view(torch.bfloat16)
+
+    direct = []
+    for L in layers:
+        d = {k: (torch.from_numpy(v).to(cuda) if k.endswith("norm") else
+                 (None if v is None else dev16(v))) for k, v in L.items()}
+        d["gate_up_weight"] = dev16(kernels.interleave_gate_up(L["gate_up_weight"][:inter],
+                                                                L["gate_up_weight"][inter:]))
+        if L.get("gate_up_bias") is not None:
+            d["gate_up_bias"] = dev16(kernels.interleave_gate_up(L["gate_up_bias"][:inter],
+                                                                  L["gate_up_bias"][inter:]))
+        direct.append(d)
+    w = decoder.DecoderWeights(embed=dev16(embed), final_norm=torch.from_numpy(fnorm).to(cuda),
+                               layers=direct)
+    cos, sin = decoder.rope_tables(spec, 40)
+    cd, sd = torch.from_numpy(cos).to(cuda), torch.from_numpy(sin).to(cuda)
+    ids = rng.integers(0, vocab, (2, 40))
+    a = decoder.forward(spec, loaded, ids, cd, sd)
+    b = decoder.forward(spec, w, ids, cd, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
