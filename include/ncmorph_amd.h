@@ -227,6 +227,34 @@ int ncm_attention_bf16_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
                            int q_heads, int kv_heads, int head_dim, int64_t q_stride,
                            int64_t kv_stride, int64_t out_stride, int64_t window, int out_mode);
 
+/* The same attention under NCM's block-diagonal level mask
+ * (src/ncm_mask.zig:10-42) instead of the causal one: key k is allowed for
+ * query q when k is an unpadded prefix key (k < prefix_len) or lies in q's
+ * level block [seg_lo[q], seg_hi[q]) (prefix queries: an empty block).
+ * seg_lo, seg_hi: device int32 [seq_len] (positions within one sequence,
+ * the same for every sequence of the batch), from
+ * ncm_block_diagonal_segments; prefix_pad_bits: device uint64
+ * [ceil(prefix_len / 64)] (bit k % 64 of word k / 64 = prefix key k padded)
+ * or NULL. A query with no allowed key gets a zero context (root.zig:563-565).
+ * Other arguments and the tolerance as ncm_attention_bf16_dev. */
+int ncm_attention_bf16_seg_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
+                               const uint16_t* v, void* out, int64_t batch, int64_t seq_len,
+                               int q_heads, int kv_heads, int head_dim, int64_t q_stride,
+                               int64_t kv_stride, int64_t out_stride, int64_t prefix_len,
+                               const int32_t* seg_lo, const int32_t* seg_hi,
+                               const uint64_t* prefix_pad_bits, int out_mode);
+
+/* Host: the block-diagonal mask of block_diagonal_mask (src/ncm_mask.zig:
+ * 10-42) in the compact form the attention reads: per position the level
+ * block [seg_lo, seg_hi) (empty for the prefix) and the prefix pad flags
+ * packed into bits (pad_bits [ceil(prefix_len / 64)], may be NULL).
+ * NCM_E_LENGTH where the reference returns InvalidPrefixMask (pad_len not 0
+ * or prefix_len) or InvalidMaskSize (prefix + levels != seq_len). */
+int ncm_block_diagonal_segments(int64_t prefix_len, const int64_t* level_lengths,
+                                int64_t n_levels, const uint8_t* prefix_pad_mask,
+                                int64_t pad_len, int64_t seq_len, int32_t* seg_lo,
+                                int32_t* seg_hi, uint64_t* pad_bits);
+
 /* ---- bf16 decoder prefill forward (src/decoder.zig:62-228) ---- */
 
 /* Model shape (config.spec_t fields the forward reads). window: sliding

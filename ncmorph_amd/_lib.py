@@ -54,6 +54,9 @@ SIGNATURES = [
     ("ncm_rope_rotate_dev", i32, [vp, vp, i64, i64, i32, i32, i64, vp, vp]),
     ("ncm_attention_bf16_dev", i32, [vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, i64, i64, i64,
                                      i64, i32]),
+    ("ncm_attention_bf16_seg_dev", i32, [vp, vp, vp, vp, vp, i64, i64, i32, i32, i32, i64, i64,
+                                         i64, i64, vp, vp, vp, i32]),
+    ("ncm_block_diagonal_segments", i32, [i64, vp, i64, vp, i64, i64, vp, vp, vp]),
     ("ncm_decoder_forward_dev", i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]),
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
     ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),

@@ -415,6 +415,70 @@ int ncm_attention_bf16_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
     return NCM_OK;
 }
 
+int ncm_attention_bf16_seg_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
+                               const uint16_t* v, void* out, int64_t batch, int64_t seq_len,
+                               int q_heads, int kv_heads, int head_dim, int64_t q_stride,
+                               int64_t kv_stride, int64_t out_stride, int64_t prefix_len,
+                               const int32_t* seg_lo, const int32_t* seg_hi,
+                               const uint64_t* prefix_pad_bits, int out_mode) {
+    if (!ctx) return NCM_E_NULL;
+    if (batch < 0 || seq_len < 0 || q_heads <= 0 || kv_heads <= 0) return NCM_E_SHAPE;
+    if (prefix_len < 0 || prefix_len > seq_len) return NCM_E_SHAPE;
+    if (head_dim != 64 && head_dim != 128) return NCM_E_SHAPE;
+    if (q_heads % kv_heads) return NCM_E_SHAPE;
+    if (out_mode != NCM_OUT_BF16_F32 && out_mode != NCM_OUT_BF16) return NCM_E_ARG;
+    if (q_stride < (int64_t)q_heads * head_dim || kv_stride < (int64_t)kv_heads * head_dim ||
+        out_stride < (int64_t)q_heads * head_dim)
+        return NCM_E_SHAPE;
+    if (batch == 0 || seq_len == 0) return NCM_OK;
+    if (!q || !k || !v || !out || !seg_lo || !seg_hi) return NCM_E_NULL;
+    if (q_stride % 8 || kv_stride % 8) return NCM_E_ARG;
+    if ((uintptr_t)q % 16 || (uintptr_t)k % 16 || (uintptr_t)v % 16) return NCM_E_ARG;
+    if (batch > 65535 || q_heads > 65535 || seq_len > (int64_t(1) << 30)) return NCM_E_SHAPE;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_attention_bf16_seg(q, k, v, out, batch, seq_len, q_heads, kv_heads,
+                                                  head_dim, q_stride, kv_stride, out_stride,
+                                                  prefix_len, seg_lo, seg_hi, prefix_pad_bits,
+                                                  out_mode, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "attention (level mask) launch");
+    return NCM_OK;
+}
+
+int ncm_block_diagonal_segments(int64_t prefix_len, const int64_t* level_lengths,
+                                int64_t n_levels, const uint8_t* prefix_pad_mask,
+                                int64_t pad_len, int64_t seq_len, int32_t* seg_lo,
+                                int32_t* seg_hi, uint64_t* pad_bits) {
+    if (prefix_len < 0 || n_levels < 0 || seq_len < 0) return NCM_E_SHAPE;
+    if (n_levels > 0 && !level_lengths) return NCM_E_NULL;
+    // InvalidPrefixMask: a pad mask is empty or one flag per prefix key.
+    if (pad_len != 0 && pad_len != prefix_len) return NCM_E_LENGTH;
+    if (pad_len > 0 && !prefix_pad_mask) return NCM_E_NULL;
+    int64_t total = prefix_len;
+    for (int64_t l = 0; l < n_levels; ++l) {
+        if (level_lengths[l] < 0 || __builtin_add_overflow(total, level_lengths[l], &total))
+            return NCM_E_SHAPE;
+    }
+    if (total != seq_len) return NCM_E_LENGTH;  // InvalidMaskSize
+    if (seq_len > (int64_t(1) << 30)) return NCM_E_SHAPE;
+    if (seq_len > 0 && (!seg_lo || !seg_hi)) return NCM_E_NULL;
+    for (int64_t t = 0; t < prefix_len; ++t) seg_lo[t] = seg_hi[t] = 0;
+    int64_t off = prefix_len;
+    for (int64_t l = 0; l < n_levels; ++l) {
+        for (int64_t t = off; t < off + level_lengths[l]; ++t) {
+            seg_lo[t] = (int32_t)off;
+            seg_hi[t] = (int32_t)(off + level_lengths[l]);
+        }
+        off += level_lengths[l];
+    }
+    if (pad_bits) {
+        for (int64_t w = 0; w < (prefix_len + 63) / 64; ++w) pad_bits[w] = 0;
+        for (int64_t t = 0; t < pad_len; ++t)
+            if (prefix_pad_mask[t]) pad_bits[t / 64] |= 1ull << (t % 64);
+    }
+    return NCM_OK;
+}
+
 int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
                             const ncm_decoder_layer_t* layers, const uint16_t* embed,
                             const float* final_norm, const uint16_t* lm_head,

@@ -140,14 +140,40 @@ __device__ __forceinline__ f32x16_t score_tile(const char* kl, const u32x4_t (&q
     return a;
 }
 
+__device__ __forceinline__ int wave_min_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
+    return v;
+}
+__device__ __forceinline__ int wave_max_i(int v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
 }  // namespace
 
-template <int HD, int OUT_MODE, bool POW2 = (HD == 64)>
+// Prefix + level-block mask (MASK = 1): key k is allowed for query q when k
+// is a prefix key (k < prefix) that is not padded, or k lies in q's own
+// range [seg_lo[q], seg_hi[q]) (NCM's block-diagonal mask,
+// src/ncm_mask.zig:10-42: prefix queries have an empty range). Positions
+// are per sequence. pad: bit (k % 64) of word k / 64 set = prefix key k
+// padded; null = none.
+struct SegArgs {
+    int64_t prefix;
+    const int32_t* seg_lo;
+    const int32_t* seg_hi;
+    const uint64_t* pad;
+};
+
+template <int HD, int OUT_MODE, int MASK, bool POW2 = (HD == 64)>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 2 : 1, 4)))
 void attention_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, void* __restrict__ out, int64_t T, int group,
-    int64_t q_stride, int64_t kv_stride, int64_t out_stride, int64_t window, float scale) {
+    int64_t q_stride, int64_t kv_stride, int64_t out_stride, int64_t window, float scale,
+    SegArgs sa) {
+    __shared__ int seg_red[8];
     using L = AttnLds<HD>;
     __shared__ __attribute__((aligned(16))) char kl[L::K_BYTES];
     __shared__ __attribute__((aligned(16))) char vl[L::V_BYTES];
@@ -179,24 +205,85 @@ void attention_bf16_kernel(
             qf[s] = qq < T ? *(const u32x4_t*)(qrow + 16 * s) : u32x4_t{0u, 0u, 0u, 0u};
     }
 
-    // Key blocks of the workgroup: keys <= its last query; with a window,
-    // keys > (first query - window).
-    const int64_t q_last = (q0 + kBq < T ? q0 + kBq : T) - 1;
-    int64_t k_lo = window > 0 ? q0 - window + 1 : 0;
-    if (k_lo < 0) k_lo = 0;
-    const int64_t kb_begin = k_lo / kBk, kb_end = q_last / kBk + 1;
-    // This wave's queries (up to T) and the keys they can see.
-    const int64_t wq_last = (qw0 + 31 < T ? qw0 + 31 : T - 1);
-    int64_t wk_lo = window > 0 ? qw0 - window + 1 : 0;
-    if (wk_lo < 0) wk_lo = 0;
     const bool wave_live = qw0 < T;
-
-    // Masks in block-relative int32 offsets. A block is "full" for this wave
-    // when every key in it is allowed for all 32 of its queries (only
-    // blocks on the diagonal or the window's edge need the per-element test).
+    const int64_t wq_last = (qw0 + 31 < T ? qw0 + 31 : T - 1);
+    // The key blocks the workgroup walks: [kb_begin, kb_end) (causal), or
+    // the prefix blocks [0, kb_pre) and then the level blocks
+    // [kb_seg0, kb_end) (MASK 1); a block outside both is skipped.
+    int64_t kb_begin, kb_end, kb_pre = 0, kb_seg0 = 0;
+    // Causal: this wave's first visible key. MASK 1: this lane's range and
+    // the wave's extremes (w_lo / w_hi: union; w_maxlo / w_minhi: the range
+    // every query of the wave sees).
+    int64_t wk_lo = 0;
+    int seg_lo_q = 0, seg_hi_q = 0, w_lo = 0, w_hi = 0, w_maxlo = 0, w_minhi = 0;
+    if (MASK == 0) {
+        // Keys <= the workgroup's last query; with a window, keys > (first
+        // query - window).
+        const int64_t q_last = (q0 + kBq < T ? q0 + kBq : T) - 1;
+        int64_t k_lo = window > 0 ? q0 - window + 1 : 0;
+        if (k_lo < 0) k_lo = 0;
+        kb_begin = k_lo / kBk;
+        kb_end = q_last / kBk + 1;
+        wk_lo = window > 0 ? qw0 - window + 1 : 0;
+        if (wk_lo < 0) wk_lo = 0;
+    } else {
+        const int P = (int)sa.prefix;
+        if (qq < T) {
+            seg_lo_q = sa.seg_lo[qq] > P ? sa.seg_lo[qq] : P;
+            seg_hi_q = sa.seg_hi[qq] < T ? sa.seg_hi[qq] : (int)T;
+            if (seg_hi_q < seg_lo_q) seg_hi_q = seg_lo_q;
+        }
+        const bool live = qq < T;
+        const bool nonempty = live && seg_hi_q > seg_lo_q;
+        w_lo = wave_min_i(nonempty ? seg_lo_q : 0x7FFFFFFF);
+        w_hi = wave_max_i(nonempty ? seg_hi_q : 0);
+        w_maxlo = wave_max_i(live ? seg_lo_q : 0);
+        w_minhi = wave_min_i(live ? seg_hi_q : 0x7FFFFFFF);
+        __syncthreads();  // the previous part's readers are done with seg_red
+        if (lane == 0) { seg_red[2 * wave] = w_lo; seg_red[2 * wave + 1] = w_hi; }
+        __syncthreads();
+        int g_lo = 0x7FFFFFFF, g_hi = 0;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            g_lo = min(g_lo, seg_red[2 * w]);
+            g_hi = max(g_hi, seg_red[2 * w + 1]);
+        }
+        kb_pre = (P + kBk - 1) / kBk;
+        if (g_hi > g_lo) {
+            kb_seg0 = g_lo / kBk;
+            kb_end = (g_hi + kBk - 1) / kBk;
+            if (kb_end < kb_pre) kb_end = kb_pre;
+        } else {
+            kb_seg0 = kb_pre;
+            kb_end = kb_pre;
+        }
+        kb_begin = kb_pre > 0 ? 0 : kb_seg0;
+    }
+    auto next_kb = [&](int64_t kb) {
+        if (MASK == 0) return kb + 1;
+        ++kb;
+        return kb >= kb_pre && kb < kb_seg0 ? kb_seg0 : kb;
+    };
+    // Whether this wave has any visible key in the block at key0.
+    auto wave_sees = [&](int64_t key0) {
+        if (!wave_live) return false;
+        if (MASK == 0) return key0 <= wq_last && key0 + kBk > wk_lo;
+        return key0 < sa.prefix || (key0 + kBk > w_lo && key0 < w_hi);
+    };
+    // Padded-prefix bits of the block at key0 (MASK 1).
+    auto pad_bits = [&](int64_t key0) -> uint64_t {
+        return (MASK == 1 && sa.pad && key0 < sa.prefix) ? sa.pad[key0 / kBk] : 0ull;
+    };
+    // A block is "full" for this wave when every key in it is allowed for
+    // all 32 of its queries: only blocks on the diagonal or a window's or
+    // range's edge need the per-element test.
     auto block_full = [&](int64_t key0) {
-        return key0 + kBk - 1 <= qw0 && key0 + kBk <= T &&
-               (window <= 0 || key0 + window > qw0 + 31);
+        if (MASK == 0)
+            return key0 + kBk - 1 <= qw0 && key0 + kBk <= T &&
+                   (window <= 0 || key0 + window > qw0 + 31);
+        return (key0 + kBk <= sa.prefix && pad_bits(key0) == 0) ||
+               (key0 >= sa.prefix && key0 >= w_maxlo && key0 + kBk <= w_minhi &&
+                wq_last == qw0 + 31);
     };
     const int koff = 4 * hl;  // + 32 t + 8 (i / 4) + i % 4: the key of element i of tile t
     // bf16 RNE without the NaN canonicalisation of bf16_bits_rne: exact for
@@ -232,15 +319,29 @@ void attention_bf16_kernel(
     float m = -INFINITY, lsum = 0.0f;
     KRegs<HD> kr;
     load_k<HD>(kr, kbase, kv_stride, kb_begin * kBk, T);
-    for (int64_t kb = kb_begin; kb < kb_end; ++kb) {
+    for (int64_t kb = kb_begin; kb < kb_end; kb = next_kb(kb)) {
         const int64_t key0 = kb * kBk;
+        const int64_t kb_next = next_kb(kb);
         store_k<HD>(kl, kr);
         lds_barrier();
-        if (kb + 1 < kb_end) load_k<HD>(kr, kbase, kv_stride, key0 + kBk, T);
-        if (wave_live && key0 <= wq_last && key0 + kBk > wk_lo) {
+        if (kb_next < kb_end) load_k<HD>(kr, kbase, kv_stride, kb_next * kBk, T);
+        if (wave_sees(key0)) {
             const bool full = block_full(key0);
+            // Causal: key offset kr is allowed when kr <= rq, kr < rt (keys
+            // before T) and kr > rw (inside the window). MASK 1: kr < rp is a
+            // prefix key (allowed unless its pad bit is set), else allowed
+            // when rlo <= kr < rhi (offsets clamped to [-1, kBk]).
             const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
             const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
+            auto clampk = [](int64_t x) { return (int)(x < -1 ? -1 : (x > kBk ? kBk : x)); };
+            const int rp = MASK == 1 ? clampk(sa.prefix - key0) : 0;
+            const int rlo = MASK == 1 ? clampk(seg_lo_q - key0) : 0;
+            const int rhi = MASK == 1 ? clampk(seg_hi_q - key0) : 0;
+            const uint64_t pbits = pad_bits(key0);
+            auto ok = [&](int kk) {
+                if (MASK == 0) return kk <= rq && kk < rt && kk > rw;
+                return kk < rp ? ((pbits >> kk) & 1ull) == 0ull : (kk >= rlo && kk < rhi);
+            };
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 f32x16_t acc = score_tile<HD>(kl, qf, t, lane);
@@ -248,7 +349,7 @@ void attention_bf16_kernel(
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int k = kr_of(t, i);
-                        acc[i] = (k <= rq && k < rt && k > rw) ? acc[i] : -INFINITY;
+                        acc[i] = ok(k) ? acc[i] : -INFINITY;
                     }
                 float mb = -INFINITY;
 #pragma unroll
@@ -272,8 +373,12 @@ void attention_bf16_kernel(
         lds_barrier();
     }
     const float ltot = lsum + __shfl_xor(lsum, 32, 64);
-    const float inv_l = 1.0f / ltot;
-    const float nm = -m * kLog2e;  // m is a score: -m log2 e as in pass 1
+    // A query with no allowed key (a prefix query whose prefix is all
+    // padding) gets zero probabilities, hence a zero context, as the
+    // reference (root.zig:563-565).
+    const bool any_key = ltot > 0.0f;
+    const float inv_l = any_key ? 1.0f / ltot : 0.0f;
+    const float nm = any_key ? -m * kLog2e : 0.0f;  // m is a score: -m log2 e as in pass 1
 
     // ---- pass 2: bf16 probabilities and P V.
     constexpr int NT = HD / 32;
@@ -283,19 +388,33 @@ void attention_bf16_kernel(
     VRegs<HD> vr;
     load_k<HD>(kr, kbase, kv_stride, kb_begin * kBk, T);
     load_v<HD>(vr, vbase, kv_stride, kb_begin * kBk, T);
-    for (int64_t kb = kb_begin; kb < kb_end; ++kb) {
+    for (int64_t kb = kb_begin; kb < kb_end; kb = next_kb(kb)) {
         const int64_t key0 = kb * kBk;
+        const int64_t kb_next = next_kb(kb);
         store_k<HD>(kl, kr);
         store_v<HD>(vl, vr);
         lds_barrier();
-        if (kb + 1 < kb_end) {
-            load_k<HD>(kr, kbase, kv_stride, key0 + kBk, T);
-            load_v<HD>(vr, vbase, kv_stride, key0 + kBk, T);
+        if (kb_next < kb_end) {
+            load_k<HD>(kr, kbase, kv_stride, kb_next * kBk, T);
+            load_v<HD>(vr, vbase, kv_stride, kb_next * kBk, T);
         }
-        if (wave_live && key0 <= wq_last && key0 + kBk > wk_lo) {
+        if (wave_sees(key0)) {
             const bool full = block_full(key0);
+            // Causal: key offset kr is allowed when kr <= rq, kr < rt (keys
+            // before T) and kr > rw (inside the window). MASK 1: kr < rp is a
+            // prefix key (allowed unless its pad bit is set), else allowed
+            // when rlo <= kr < rhi (offsets clamped to [-1, kBk]).
             const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
             const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
+            auto clampk = [](int64_t x) { return (int)(x < -1 ? -1 : (x > kBk ? kBk : x)); };
+            const int rp = MASK == 1 ? clampk(sa.prefix - key0) : 0;
+            const int rlo = MASK == 1 ? clampk(seg_lo_q - key0) : 0;
+            const int rhi = MASK == 1 ? clampk(seg_hi_q - key0) : 0;
+            const uint64_t pbits = pad_bits(key0);
+            auto ok = [&](int kk) {
+                if (MASK == 0) return kk <= rq && kk < rt && kk > rw;
+                return kk < rp ? ((pbits >> kk) & 1ull) == 0ull : (kk >= rlo && kk < rhi);
+            };
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
                 f32x16_t acc = score_tile<HD>(kl, qf, t, lane);
@@ -303,7 +422,7 @@ void attention_bf16_kernel(
 #pragma unroll
                     for (int i = 0; i < 16; ++i) {
                         const int k = kr_of(t, i);
-                        acc[i] = (k <= rq && k < rt && k > rw) ? acc[i] : -INFINITY;
+                        acc[i] = ok(k) ? acc[i] : -INFINITY;
                     }
                 // p = round_bf16(e / sum): u + 0x7FFF + lsb carries the RNE
                 // result in the high half; v_perm packs two high halves.
@@ -357,22 +476,23 @@ void attention_bf16_kernel(
     }  // part
 }
 
-template <int HD>
+template <int HD, int MASK>
 static hipError_t launch_attn_hd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                  void* out, int64_t batch, int64_t T, int hq, int hkv,
                                  int64_t q_stride, int64_t kv_stride, int64_t out_stride,
-                                 int64_t window, int out_mode, hipStream_t stream) {
+                                 int64_t window, SegArgs sa, int out_mode, hipStream_t stream) {
     const int64_t nqb = (T + kBq - 1) / kBq;
     const dim3 grid((unsigned)((nqb + 1) / 2), (unsigned)hq, (unsigned)batch);
     const float scale = 1.0f / sqrtf((float)HD);
     const int group = hq / hkv;
     if (out_mode == NCM_OUT_BF16)
-        hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16>), grid, dim3(256), 0, stream,
-                           q, k, v, out, T, group, q_stride, kv_stride, out_stride, window, scale);
-    else
-        hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16_F32>), grid, dim3(256), 0,
+        hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16, MASK>), grid, dim3(256), 0,
                            stream, q, k, v, out, T, group, q_stride, kv_stride, out_stride, window,
-                           scale);
+                           scale, sa);
+    else
+        hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16_F32, MASK>), grid, dim3(256),
+                           0, stream, q, k, v, out, T, group, q_stride, kv_stride, out_stride,
+                           window, scale, sa);
     return hipGetLastError();
 }
 
@@ -383,13 +503,35 @@ hipError_t launch_attention_bf16(const uint16_t* q, const uint16_t* k, const uin
                                  hipStream_t stream) {
     // A window of seq_len or more admits every causal key.
     if (window >= seq_len) window = 0;
+    const SegArgs none{0, nullptr, nullptr, nullptr};
     switch (head_dim) {
         case 64:
-            return launch_attn_hd<64>(q, k, v, out, batch, seq_len, q_heads, kv_heads, q_stride,
-                                      kv_stride, out_stride, window, out_mode, stream);
+            return launch_attn_hd<64, 0>(q, k, v, out, batch, seq_len, q_heads, kv_heads, q_stride,
+                                         kv_stride, out_stride, window, none, out_mode, stream);
         case 128:
-            return launch_attn_hd<128>(q, k, v, out, batch, seq_len, q_heads, kv_heads, q_stride,
-                                       kv_stride, out_stride, window, out_mode, stream);
+            return launch_attn_hd<128, 0>(q, k, v, out, batch, seq_len, q_heads, kv_heads,
+                                          q_stride, kv_stride, out_stride, window, none, out_mode,
+                                          stream);
+        default:
+            return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_attention_bf16_seg(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                     void* out, int64_t batch, int64_t seq_len, int q_heads,
+                                     int kv_heads, int head_dim, int64_t q_stride,
+                                     int64_t kv_stride, int64_t out_stride, int64_t prefix,
+                                     const int32_t* seg_lo, const int32_t* seg_hi,
+                                     const uint64_t* pad, int out_mode, hipStream_t stream) {
+    const SegArgs sa{prefix, seg_lo, seg_hi, pad};
+    switch (head_dim) {
+        case 64:
+            return launch_attn_hd<64, 1>(q, k, v, out, batch, seq_len, q_heads, kv_heads, q_stride,
+                                         kv_stride, out_stride, 0, sa, out_mode, stream);
+        case 128:
+            return launch_attn_hd<128, 1>(q, k, v, out, batch, seq_len, q_heads, kv_heads,
+                                          q_stride, kv_stride, out_stride, 0, sa, out_mode,
+                                          stream);
         default:
             return hipErrorInvalidValue;
     }

@@ -56,6 +56,14 @@ hipError_t launch_attention_bf16(const uint16_t* q, const uint16_t* k, const uin
                                  int64_t out_stride, int64_t window, int out_mode,
                                  hipStream_t stream);
 
+// The same attention with the prefix + level-block mask (see attention.hip).
+hipError_t launch_attention_bf16_seg(const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                                     void* out, int64_t batch, int64_t seq_len, int q_heads,
+                                     int kv_heads, int head_dim, int64_t q_stride,
+                                     int64_t kv_stride, int64_t out_stride, int64_t prefix,
+                                     const int32_t* seg_lo, const int32_t* seg_hi,
+                                     const uint64_t* pad, int out_mode, hipStream_t stream);
+
 hipError_t launch_bf16_from_f32(const float* src, uint16_t* dst, int64_t n, int flush,
                                 hipStream_t stream);
 // Row-padded variant: src [rows, cols] -> dst [rows, ld] (ld >= cols),

@@ -330,3 +330,47 @@ def attention_bf16(q, k, v, batch: int, seq_len: int, q_heads: int, kv_heads: in
                                        kv_heads, head_dim, qs, ks, os_, window, mode),
           "attention_bf16")
     return out
+
+
+def block_diagonal_segments(prefix_len: int, level_lengths, prefix_pad_mask=None):
+    """Host: (seg_lo, seg_hi, pad_bits) numpy arrays of NCM's block-diagonal
+    mask (src/ncm_mask.zig:10-42) for ncm_attention_bf16_seg_dev."""
+    lv = np.ascontiguousarray(level_lengths, dtype=np.int64)
+    seq = int(prefix_len + lv.sum())
+    lo = np.zeros(seq, np.int32)
+    hi = np.zeros(seq, np.int32)
+    pad = None if prefix_pad_mask is None else np.ascontiguousarray(prefix_pad_mask, np.uint8)
+    bits = np.zeros(max(1, (prefix_len + 63) // 64), np.uint64)
+    check(lib().ncm_block_diagonal_segments(
+        prefix_len, lv.ctypes.data_as(C.c_void_p), lv.size,
+        None if pad is None else pad.ctypes.data_as(C.c_void_p), 0 if pad is None else pad.size,
+        seq, lo.ctypes.data_as(C.c_void_p), hi.ctypes.data_as(C.c_void_p),
+        bits.ctypes.data_as(C.c_void_p)), "block_diagonal_segments")
+    return lo, hi, bits
+
+
+def attention_bf16_seg(q, k, v, batch: int, seq_len: int, q_heads: int, kv_heads: int,
+                       head_dim: int, prefix_len: int, seg_lo, seg_hi, pad_bits=None,
+                       out_mode: str = "bf16_f32", out=None, ctx=None):
+    """bf16 attention under NCM's block-diagonal level mask; seg_lo / seg_hi
+    int32 and pad_bits uint64 device tensors (block_diagonal_segments)."""
+    import torch
+
+    qp, qs = _rows_ptr(q, "q")
+    kp, ks = _rows_ptr(k, "k")
+    vp_, vs = _rows_ptr(v, "v")
+    if ks != vs:
+        raise NcmError(-2, "attention_bf16_seg: k and v row strides differ")
+    mode = _OUT_MODES[out_mode]
+    if out is None:
+        dt = torch.bfloat16 if mode == NCM_OUT_BF16 else torch.float32
+        out = torch.empty((batch * seq_len, q_heads * head_dim), dtype=dt, device=q.device)
+    op, os_ = _rows_ptr(out, "out")
+    ctx = ctx or default_context(q.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_attention_bf16_seg_dev(ctx.handle, qp, kp, vp_, op, batch, seq_len, q_heads,
+                                           kv_heads, head_dim, qs, ks, os_, prefix_len,
+                                           _dev_ptr(seg_lo, "seg_lo"), _dev_ptr(seg_hi, "seg_hi"),
+                                           _dev_ptr(pad_bits, "pad_bits"), mode),
+          "attention_bf16_seg")
+    return out

@@ -793,3 +793,27 @@ void ncmo_rope_tables(const float* inv, size_t half, size_t positions, float* co
         }
     }
 }
+
+int ncmo_block_diagonal_mask(size_t prefix_length, const size_t* level_lengths, size_t levels,
+                             const uint8_t* prefix_pad_mask, size_t pad_len, uint8_t* output,
+                             size_t output_len) {
+    if (pad_len != 0 && pad_len != prefix_length) return -1; /* InvalidPrefixMask */
+    size_t target = 0;
+    for (size_t l = 0; l < levels; ++l) target += level_lengths[l];
+    const size_t seq = prefix_length + target;
+    if (output_len != seq * seq) return -2; /* InvalidMaskSize */
+    memset(output, 0, output_len);
+    for (size_t q = 0; q < prefix_length; ++q)
+        for (size_t k = 0; k < prefix_length; ++k)
+            output[q * seq + k] = !(pad_len && prefix_pad_mask[k]);
+    size_t off = prefix_length;
+    for (size_t l = 0; l < levels; ++l) {
+        for (size_t q = off; q < off + level_lengths[l]; ++q) {
+            for (size_t k = 0; k < prefix_length; ++k)
+                output[q * seq + k] = !(pad_len && prefix_pad_mask[k]);
+            for (size_t k = off; k < off + level_lengths[l]; ++k) output[q * seq + k] = 1;
+        }
+        off += level_lengths[l];
+    }
+    return 0;
+}

@@ -148,6 +148,12 @@ void ncmo_rope_llama3(size_t head_dim, float theta, float factor, float low_freq
                       float high_freq_factor, size_t original_max_positions, float* inv);
 void ncmo_rope_tables(const float* inv, size_t half, size_t positions, float* cosine,
                       float* sine);
+/* block_diagonal_mask (src/ncm_mask.zig:10-42): prefix queries see unpadded
+ * prefix keys; a level's queries see unpadded prefix keys and their own
+ * level. Returns -1 (InvalidPrefixMask), -2 (InvalidMaskSize) or 0. */
+int ncmo_block_diagonal_mask(size_t prefix_length, const size_t* level_lengths, size_t levels,
+                             const uint8_t* prefix_pad_mask, size_t pad_len, uint8_t* output,
+                             size_t output_len);
 void ncmo_attention_core(const float* queries, const float* keys, const float* values,
                          const uint8_t* mask, float* context, size_t tokens, size_t q_heads,
                          size_t kv_heads, size_t head_dim, int bf16);

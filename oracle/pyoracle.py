@@ -77,6 +77,7 @@ def lib():
         L.ncmo_silu_mul_bf16.argtypes = [f32p, f32p, f32p, sz]
         L.ncmo_rotate_head.argtypes = [f32p, f32p, f32p, sz, C.c_int]
         L.ncmo_causal_mask.argtypes = [sz, sz, sz, u8p]
+        L.ncmo_block_diagonal_mask.argtypes = [sz, vp, sz, vp, sz, u8p, sz]
         L.ncmo_rope_default_frequencies.argtypes = [sz, C.c_float, f32p]
         L.ncmo_rope_llama3.argtypes = [sz, C.c_float, C.c_float, C.c_float, C.c_float, sz, f32p]
         L.ncmo_rope_tables.argtypes = [f32p, sz, sz, f32p, f32p]
@@ -528,3 +529,19 @@ def st_parse_index(text: str):
         if "total_size" in md:
             total = _st_uint(md["total_size"])
     return entries, total
+
+
+
+def block_diagonal_mask(prefix_length: int, level_lengths, prefix_pad_mask=None):
+    """NCM's block-diagonal allow mask (src/ncm_mask.zig:10-42), uint8 [S, S];
+    raises ValueError("InvalidPrefixMask") for a pad mask of the wrong length."""
+    lv = np.ascontiguousarray(level_lengths, dtype=np.uintp)
+    pad = None if prefix_pad_mask is None else np.ascontiguousarray(prefix_pad_mask, np.uint8)
+    seq = prefix_length + int(lv.sum())
+    out = np.empty((seq, seq), np.uint8)
+    rc = lib().ncmo_block_diagonal_mask(prefix_length, lv.ctypes.data_as(C.c_void_p), lv.size,
+                                        None if pad is None else pad.ctypes.data_as(C.c_void_p),
+                                        0 if pad is None else pad.size, out, out.size)
+    if rc == -1:
+        raise ValueError("InvalidPrefixMask")
+    return out

@@ -168,3 +168,42 @@ def test_attention_rejects_bad_shapes(ncm, cuda):
     y = torch.zeros((8, 192), dtype=torch.bfloat16, device=cuda)
     with pytest.raises(NcmError):  # 3 query heads over 2 kv heads
         kernels.attention_bf16(y[:, :192], y[:, :128], y[:, :128], 1, 8, 3, 2, 64)
+
+
+@pytest.mark.parametrize("batch,prefix,levels,pad,hq,hkv,hd", [
+    (1, 2, [1, 2], [0, 1], 1, 1, 64),              # the reference's mask case
+    (2, 70, [64, 1, 100], "rand", 4, 2, 64),       # ragged blocks, padded prefix
+    (1, 0, [128, 128, 128], None, 2, 1, 128),      # no prefix, aligned levels
+    (1, 64, [8] * 8, "all", 2, 2, 64),             # all-padded prefix: zero contexts
+    (2, 130, [256, 33], None, 4, 1, 64),
+])
+def test_attention_level_mask_against_oracle(ncm, oracle, cuda, batch, prefix, levels, pad, hq,
+                                             hkv, hd):
+    import torch
+    from ncmorph_amd import kernels
+
+    if pad == "rand":
+        pad = (np.random.default_rng(prefix).random(prefix) < 0.3).astype(np.uint8)
+    elif pad == "all":
+        pad = np.ones(prefix, np.uint8)
+    seq = prefix + sum(levels)
+    rng = np.random.default_rng(seq + hd)
+    rb = oracle.round_bf16
+    q = rb(rng.standard_normal((batch * seq, hq * hd)).astype(np.float32) * 1.5)
+    k = rb(rng.standard_normal((batch * seq, hkv * hd)).astype(np.float32) * 1.5)
+    v = rb((rng.standard_normal((batch * seq, hkv * hd))
+            + np.repeat(np.arange(hkv), hd)).astype(np.float32))
+    lo, hi, bits = kernels.block_diagonal_segments(prefix, levels, pad)
+    dl, dh = torch.from_numpy(lo).to(cuda), torch.from_numpy(hi).to(cuda)
+    db = torch.from_numpy(bits.view(np.int64)).to(cuda) if pad is not None else None
+    out = kernels.attention_bf16_seg(_bf16_dev(q, cuda), _bf16_dev(k, cuda), _bf16_dev(v, cuda),
+                                     batch, seq, hq, hkv, hd, prefix, dl, dh, db)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    mask = oracle.block_diagonal_mask(prefix, levels, pad)
+    for b in range(batch):
+        rows = slice(b * seq, (b + 1) * seq)
+        ref = oracle.attention_core(q[rows], k[rows], v[rows], mask, hq, hkv, hd)
+        _check(got[rows], ref, v[rows])
+    if pad is not None and np.all(pad):
+        assert np.all(got.reshape(batch, seq, -1)[:, :prefix] == 0)

@@ -184,3 +184,46 @@ def test_attention_bf16_against_f64(oracle):
     # bf16 scores (|s| <~ 4: a step is <= 2^-6 absolute), bf16 probabilities
     # and a bf16 context: a few percent of max |v| at most.
     assert np.max(np.abs(got - want)) <= 0.05 * np.max(np.abs(v))
+
+
+def test_block_diagonal_mask_reference_case(oracle):
+    # src/ncm_mask.zig:46-64
+    m = oracle.block_diagonal_mask(2, [1, 2], [0, 1]).astype(bool)
+    assert m[0, 0] and not m[0, 1] and not m[0, 2]
+    assert m[2, 0] and not m[2, 1] and m[2, 2] and not m[2, 3]
+    assert m[3, 3] and m[3, 4] and m[4, 3]
+    with pytest.raises(ValueError):
+        oracle.block_diagonal_mask(2, [1], [0])
+
+
+@pytest.mark.parametrize("prefix,levels,pad", [(0, [5], None), (3, [1, 2], [0, 1, 0]),
+                                               (70, [64, 1, 100], "rand"), (5, [], None),
+                                               (130, [8, 8, 8, 8, 8, 8, 8, 8], "rand")])
+def test_block_diagonal_segments_expand_to_the_mask(ncm, oracle, prefix, levels, pad):
+    from ncmorph_amd import kernels
+
+    if pad == "rand":
+        pad = (np.random.default_rng(prefix).random(prefix) < 0.3).astype(np.uint8)
+    lo, hi, bits = kernels.block_diagonal_segments(prefix, levels, pad)
+    seq = lo.size
+    q, k = np.meshgrid(np.arange(seq), np.arange(seq), indexing="ij")
+    padded = np.array([(int(bits[i // 64]) >> (i % 64)) & 1 for i in range(prefix)], bool)
+    prefix_ok = (k < prefix) & ~padded[np.minimum(k, max(prefix - 1, 0))] if prefix else k < 0
+    mine = prefix_ok | ((k >= lo[q]) & (k < hi[q]))
+    want = oracle.block_diagonal_mask(prefix, levels, pad).astype(bool)
+    assert np.array_equal(mine, want)
+
+
+def test_block_diagonal_segments_errors(ncm):
+    import ctypes as C
+
+    L = ncm.lib()
+    lv = np.array([2, 3], np.int64)
+    lo = np.zeros(8, np.int32)
+    hi = np.zeros(8, np.int32)
+    pad = np.zeros(2, np.uint8)
+    p = lambda a: C.c_void_p(a.ctypes.data)
+    # pad mask of the wrong length (InvalidPrefixMask), wrong total (InvalidMaskSize)
+    assert L.ncm_block_diagonal_segments(3, p(lv), 2, p(pad), 2, 8, p(lo), p(hi), None) == -3
+    assert L.ncm_block_diagonal_segments(3, p(lv), 2, None, 0, 7, p(lo), p(hi), None) == -3
+    assert L.ncm_block_diagonal_segments(3, p(lv), 2, None, 0, 8, p(lo), p(hi), None) == 0
