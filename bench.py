@@ -233,6 +233,47 @@ def run_decoder(torch, reps=10, warmup=3):
 
 
 PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
+NCM_PREFIX, NCM_LEVELS = 64, [32, 64, 128, 256, 512, 1024, 2048, 4096]
+
+
+def run_ncm_attention(torch, reps=10):
+    """Attention of the NCM level-parallel step at the Llama-3-8B head shape
+    (32 query / 8 key-value heads of 128): a 64-token prefix and 8 levels of
+    one 4096-position sequence (4096 / 2^(7 - l) positions at level l), under
+    the block-diagonal level mask. Flops: 4 hd per allowed (query, key) pair
+    and query head (QK^T and PV)."""
+    from ncmorph_amd import kernels
+
+    dev = torch.device("cuda", 0)
+    hq, hkv, hd = 32, 8, 128
+    lo, hi, bits = kernels.block_diagonal_segments(NCM_PREFIX, NCM_LEVELS)
+    seq = lo.size
+    g = torch.Generator(device=dev).manual_seed(15)
+    qkv = torch.randn(seq, (hq + 2 * hkv) * hd, device=dev, generator=g).to(torch.bfloat16)
+    q, k, v = qkv[:, :hq * hd], qkv[:, hq * hd:(hq + hkv) * hd], qkv[:, (hq + hkv) * hd:]
+    dl, dh = torch.from_numpy(lo).to(dev), torch.from_numpy(hi).to(dev)
+    out = torch.empty(seq, hq * hd, dtype=torch.bfloat16, device=dev)
+
+    def run():
+        kernels.attention_bf16_seg(q, k, v, 1, seq, hq, hkv, hd, NCM_PREFIX, dl, dh, None,
+                                   out_mode="bf16", out=out)
+
+    for _ in range(3):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / reps
+    pairs = NCM_PREFIX * NCM_PREFIX + sum(n * (NCM_PREFIX + n) for n in NCM_LEVELS)
+    flops = 4.0 * hd * hq * pairs
+    tf = flops / sec / 1e12
+    return {"positions": seq, "us": round(sec * 1e6, 1), "flops": flops,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4)}}
 
 
 def run_weight_upload(torch, mib=512):
@@ -435,6 +476,7 @@ def main():
     if args.only in ("decoder", "all"):
         dec = run_decoder(torch)
         dec["weight_upload"] = run_weight_upload(torch)
+        dec["ncm_level_attention"] = run_ncm_attention(torch)
         if not args.no_cpu:
             dec["cpu_baseline"] = cpu_decoder_baseline()
         res["decoder_prefill"] = dec

@@ -167,7 +167,7 @@ struct SegArgs {
 };
 
 template <int HD, int OUT_MODE, int MASK, bool POW2 = (HD == 64)>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(HD == 64 ? 2 : 1, 4)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((HD == 64 || MASK == 1) ? 2 : 1, 4)))
 void attention_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, void* __restrict__ out, int64_t T, int group,
@@ -186,10 +186,12 @@ void attention_bf16_kernel(
     // keys) and then block x (the fewest), so every workgroup walks about
     // the same number of key blocks (the middle block of an odd count is
     // taken once).
+    // Level mask: one query block per workgroup, the last (longest level)
+    // blocks first.
     const int nqb = (int)((T + kBq - 1) / kBq);
     for (int part = 0; part < 2; ++part) {
     const int qbi = part == 0 ? nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    if (part == 1 && qbi == nqb - 1 - (int)blockIdx.x) break;
+    if (part == 1 && (MASK == 1 || qbi == nqb - 1 - (int)blockIdx.x)) break;
     const int64_t q0 = (int64_t)qbi * kBq;
     const int64_t qw0 = q0 + 32 * wave;
     const int64_t qq = qw0 + c;  // the query of this lane's score column
@@ -482,7 +484,7 @@ static hipError_t launch_attn_hd(const uint16_t* q, const uint16_t* k, const uin
                                  int64_t q_stride, int64_t kv_stride, int64_t out_stride,
                                  int64_t window, SegArgs sa, int out_mode, hipStream_t stream) {
     const int64_t nqb = (T + kBq - 1) / kBq;
-    const dim3 grid((unsigned)((nqb + 1) / 2), (unsigned)hq, (unsigned)batch);
+    const dim3 grid((unsigned)(MASK == 0 ? (nqb + 1) / 2 : nqb), (unsigned)hq, (unsigned)batch);
     const float scale = 1.0f / sqrtf((float)HD);
     const int group = hq / hkv;
     if (out_mode == NCM_OUT_BF16)
