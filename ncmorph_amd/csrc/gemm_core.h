@@ -46,6 +46,11 @@ namespace ncm {
 //      one shared pipeline, NST / 2 - 1 tile pairs ahead; at the end group 1
 //      hands its accumulators to group 0 through LDS and group 0 holds
 //      acc(group 0) + acc(group 1).
+//   8  (DMA) SCHED 5's stage rotation and barrier, with each tile's loads
+//      spread over its first DSPREAD k-steps and, inside a k-step, the
+//      loads and the next k-step's fragment reads placed one by one between
+//      the MFMAs (scheduling-group barriers): the matrix core keeps working
+//      while they issue instead of waiting for a block of them.
 // DMA: global -> LDS directly (buffer_load ... lds), no staging registers
 // and no ds_write instructions; this path waits for its own loads (vmcnt)
 // explicitly at each barrier. Without DMA, one K tile is staged through
@@ -53,7 +58,7 @@ namespace ncm {
 // NST: LDS stages of the DMA path; K tiles up to NST - 1 ahead are in flight.
 // F32: fp32 operands (else bf16). KG: K groups (SCHED 7).
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int OCC_, int SCHED_, bool DMA_,
-          int NST_ = 2, bool F32_ = false, int KG_ = 1>
+          int NST_ = 2, bool F32_ = false, int KG_ = 1, int BS_ = -1, int DSP_ = -1>
 struct GemmShape {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_;
     static constexpr int OCC = OCC_, SCHED = SCHED_, NST = NST_, KG = KG_;
@@ -67,6 +72,10 @@ struct GemmShape {
     static constexpr int NWG = WGM * WGN;  // wavefronts per K group
     static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int MB = WM / 32, NB = WN / 32;
+    // SCHED 5: MFMAs of the last k-step issued before the K-tile barrier.
+    static constexpr int BSPLIT = BS_ < 0 ? MB * NB / 2 : BS_;
+    // SCHED 8: k-steps over which a tile's direct-to-LDS loads are spread.
+    static constexpr int DSPREAD = DSP_ < 0 ? (BK * ESZ / 32) - 1 : DSP_;
     static constexpr int CH = RB / 16;
     static constexpr int KSTEPS = CH / 2;
     static constexpr int RPP = NT / CH;
@@ -86,7 +95,8 @@ struct GemmShape {
     static_assert(RB == 64 || RB == 128 || RB == 256, "a K tile row is 64, 128 or 256 bytes");
     static_assert(NT % CH == 0 && BM % RPP == 0 && BN % RPP == 0, "loader shape");
     static_assert(RPP % (CH << SWZ_SHIFT) == 0, "swizzle must not depend on the pass");
-    static_assert(SCHED == 0 || SCHED == 4 || SCHED == 5 || SCHED == 6 || SCHED == 7,
+    static_assert(SCHED == 0 || SCHED == 4 || SCHED == 5 || SCHED == 6 || SCHED == 7 ||
+                      SCHED == 8,
                   "schedule");
     static_assert((KG == 2) == (SCHED == 7), "K groups go with SCHED 7");
     static_assert(SCHED != 7 || (NST % 2 == 0 && NST >= 4), "SCHED 7 stages come in pairs");
@@ -95,7 +105,9 @@ struct GemmShape {
     static_assert(!DMA || (BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0), "DMA loader shape");
     static_assert(NST == 2 || SCHED >= 5, "more than two stages: SCHED 5, 6 or 7 only");
     static_assert(SCHED != 6 || (NST >= 3 && NW % 2 == 0), "ping-pong layout");
-    static_assert(SCHED != 5 || KSTEPS % 2 == 0, "SCHED 5 splits the last k-step pair");
+    static_assert((SCHED != 5 && SCHED != 8) || KSTEPS % 2 == 0,
+                  "SCHED 5 and 8 split the last k-step pair");
+    static_assert(SCHED != 8 || KSTEPS >= 2, "SCHED 8 spreads the loads over the first k-steps");
     static_assert(NST >= 2 && (NST - 2) * (A_DMA + B_DMA) <= 63, "vmcnt range");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget of a gfx950 CU");
 };
@@ -151,7 +163,7 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
                                               int64_t K, char* lds, GemmAcc<S>& acc) {
     const int tid = threadIdx.x;
     const int lane = tid & 63;
-    const int wave = tid >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wl = wave % S::NWG;  // wavefront inside its K group
     const int wm = wl % S::WGM;
     const int wn = wl / S::WGM;
@@ -259,11 +271,13 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
     // wave; past K the loads are out of range and fill zeros.
     const int drow0 = wave * S::RPI + lane / S::CH;
     const int dslot = lane % S::CH;
-    auto dma = [&](int stage, int64_t k0) {
+    // Loads lo .. hi - 1 of the A_DMA + B_DMA of one tile.
+    auto dma_range = [&](int stage, int64_t k0, int lo, int hi) {
         char* sbase = lds + stage * S::LDS_STAGE;
         const uint32_t kb = (uint32_t)(k0 * S::ESZ);
 #pragma unroll
         for (int p = 0; p < S::A_DMA + S::B_DMA; ++p) {
+            if (p < lo || p >= hi) continue;
             const bool is_a = p < S::A_DMA;
             const int pp = is_a ? p : p - S::A_DMA;
             const int row = pp * S::NW * S::RPI + drow0;
@@ -276,6 +290,7 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
                 valid ? off : kOobOffset, 0, 0, 0);
         }
     };
+    auto dma = [&](int stage, int64_t k0) { dma_range(stage, k0, 0, S::A_DMA + S::B_DMA); };
     // At a barrier a wave keeps its last NST - 2 tiles of loads in flight.
     constexpr int VM = (S::NST - 2) * (S::A_DMA + S::B_DMA);
 
@@ -380,7 +395,7 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
         // Tile kt + NST - 1 goes to the stage tile kt - 1 used; the barrier
         // in the middle of tile kt's last k-step sees tile kt + 1 landed
         // and every wave done reading tile kt.
-        constexpr int HALF = NMF / 2;
+        constexpr int HALF = S::BSPLIT;
 #pragma unroll
         for (int st = 0; st + 1 < S::NST; ++st) dma(st, (int64_t)st * S::BK);
         wait_barrier<VM>();
@@ -405,6 +420,58 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
                     if (kt + 1 < KT) fload(fs ^ 1, lds + nxt * S::LDS_STAGE, 0);
                     __builtin_amdgcn_sched_barrier(0);
                     mfma_range(fs, HALF, NMF);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            cur = nxt;
+        }
+    } else if constexpr (S::SCHED == 8) {
+        // SCHED 5's stage rotation and barrier, with the tile's loads spread
+        // over its first k-steps: k-step kk < KSTEPS - 1 issues one MFMA,
+        // then one fragment read of k-step kk + 1 and one direct-to-LDS load,
+        // and so on, so the matrix core keeps working while they issue.
+        constexpr int HALF = S::BSPLIT;
+        constexpr int ND = S::A_DMA + S::B_DMA;
+        constexpr int NFR = S::MB + S::NB;
+        constexpr int DPK = (ND + S::DSPREAD - 1) / S::DSPREAD;
+        static_assert(S::DSPREAD >= 1 && S::DSPREAD < S::KSTEPS, "SCHED 8 load spread");
+#pragma unroll
+        for (int st = 0; st + 1 < S::NST; ++st) dma(st, (int64_t)st * S::BK);
+        wait_barrier<VM>();
+        fload(0, lds, 0);
+        int cur = 0;
+        for (int kt = 0; kt < KT; ++kt) {
+            const char* base = lds + cur * S::LDS_STAGE;
+            const int nxt = cur + 1 == S::NST ? 0 : cur + 1;
+            const int dst = cur == 0 ? S::NST - 1 : cur - 1;
+            const int64_t k_ld = (int64_t)(kt + S::NST - 1) * S::BK;
+#pragma unroll
+            for (int kk = 0; kk < S::KSTEPS; ++kk) {
+                const int fs = kk & 1;
+                if (kk + 1 < S::KSTEPS) {
+                    const int d_lo = kk * DPK < ND ? kk * DPK : ND;
+                    const int d_hi = (kk + 1) * DPK < ND ? (kk + 1) * DPK : ND;
+                    fload(fs ^ 1, base, kk + 1);
+                    dma_range(dst, k_ld, d_lo, d_hi);
+                    mfma_range(fs, 0, NMF);
+#pragma unroll
+                    for (int i = 0; i < NMF; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        if (i < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                        if (i < d_hi - d_lo) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                } else {
+                    mfma_range(fs, 0, HALF);
+                    __builtin_amdgcn_sched_barrier(0);
+                    wait_barrier<VM>();
+                    if (kt + 1 < KT) fload(fs ^ 1, lds + nxt * S::LDS_STAGE, 0);
+                    mfma_range(fs, HALF, NMF);
+#pragma unroll
+                    for (int i = HALF; i < NMF; ++i) {
+                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                        if (i - HALF < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                    }
                     __builtin_amdgcn_sched_barrier(0);
                 }
             }

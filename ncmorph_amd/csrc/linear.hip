@@ -181,31 +181,38 @@ static hipError_t launch_linear_s(const uint16_t* x, const uint16_t* w, const ui
 
 // Tile configurations of the bf16 linear (index = NCM_LINEAR_TILE):
 //  0: 256x256x64, 8 waves (64x128 each, 2 per SIMD), direct-to-LDS loads,
-//     barrier in the middle of the last k-step (SCHED 5), 2 LDS stages
-//  1: 128x128x64, 4 waves (64x64), DMA, SCHED 5, 4 LDS stages
+//     2 LDS stages; SCHED 8: loads and fragment reads interleaved between
+//     the MFMAs of the first two k-steps, barrier in the middle of the last
+//     k-step
+//  1: 128x128x64, 4 waves (64x64), DMA, SCHED 8, 4 LDS stages
 //  2: 128x128x64, 4 waves, DMA, fences (SCHED 4), 2 stages: two workgroups
 //     per CU
 //  3: 256x256x32, 8 waves, DMA, ping-pong (SCHED 6), 4 LDS stages
 //  4: 256x256x64, 4 waves (128x128, 1 per SIMD), DMA, SCHED 5
-//  5: 256x128x64, 8 waves (64x64), DMA, SCHED 5, 3 LDS stages
+//  5: 256x128x64, 8 waves (64x64), DMA, SCHED 8, 3 LDS stages
 //  6: 256x256x64, 8 waves, register-staged loads, fences
 //  7: 128x128x64, 4 waves, register-staged loads, fences
 //  8: 128x128x32, two K groups of 4 waves (SCHED 7: 8 waves, two per SIMD,
 //     alternate K tiles from 8 LDS stages, summed through LDS at the end)
 //  9: as 8 with 128x128x64 tiles and 4 LDS stages
 // 10: 128x128x128 (256-byte rows), 4 waves, DMA, SCHED 5, 2 stages
-using Lin0 = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
-using Lin1 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
+// 11, 12, 13: as 0, 1 and 5 with SCHED 5 (all loads of a tile issued
+//     together at its start, fragment reads of a k-step as one group)
+using Lin0 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
+using Lin1 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
 using Lin2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
 using Lin3 = GemmShape<256, 256, 32, 4, 2, 2, 6, true, 4>;
 using Lin4 = GemmShape<256, 256, 64, 2, 2, 1, 5, true>;
-using Lin5 = GemmShape<256, 128, 64, 4, 2, 2, 5, true, 3>;
+using Lin5 = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3>;
 using Lin6 = GemmShape<256, 256, 64, 4, 2, 2, 4, false>;
 using Lin7 = GemmShape<128, 128, 64, 2, 2, 2, 4, false>;
 using Lin8 = GemmShape<128, 128, 32, 2, 2, 2, 7, true, 8, false, 2>;
 using Lin9 = GemmShape<128, 128, 64, 2, 2, 2, 7, true, 4, false, 2>;
 using Lin10 = GemmShape<128, 128, 128, 2, 2, 2, 5, true, 2>;
-constexpr int kLinConfigs = 11;
+using Lin11 = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
+using Lin12 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
+using Lin13 = GemmShape<256, 128, 64, 4, 2, 2, 5, true, 3>;
+constexpr int kLinConfigs = 14;
 
 // fp32 linear: 128x128x32 (128-byte rows), 4 waves, DMA, SCHED 5, two
 // stages (64 KB: two workgroups per CU). The fp32 MFMA has 1/16 of the bf16
@@ -218,14 +225,13 @@ int linear_tile_config(int64_t M, int64_t N, int64_t K, int forced) {
     auto tiles = [&](int64_t bm, int64_t bn) { return ((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     // 256x256 with 8 waves when it fills at least three quarters of the
     // CUs; 128x128 with four LDS stages when that gives at most one tile per
-    // CU (latency-bound: deeper prefetch pays); for long K, 256x128 with
-    // three stages when its tiles fill the CUs about once or twice; else
-    // 128x128 with two stages (two workgroups per CU). All with
-    // direct-to-LDS loads. (Measured on the decoder's and the benchmark's
-    // shapes.)
+    // CU (latency-bound: deeper prefetch pays); 256x128 with three stages
+    // when its tiles fill the CUs about once or twice; else 128x128 with two
+    // stages (two workgroups per CU). All with direct-to-LDS loads.
+    // (Measured on the decoder's and the benchmark's shapes.)
     if (tiles(256, 256) * 4 >= cus * 3) return 0;
     if (tiles(128, 128) <= cus) return 1;
-    if (K >= 4096 && tiles(256, 128) * 4 >= cus * 3 && tiles(256, 128) <= 2 * cus) return 5;
+    if (tiles(256, 128) * 4 >= cus * 3 && tiles(256, 128) <= 2 * cus) return 5;
     return 2;
 }
 
@@ -249,7 +255,10 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
         case 7: return launch_linear_s<Lin7>(x, w, bias, y, M, K, N, out_mode, stream);
         case 8: return launch_linear_s<Lin8>(x, w, bias, y, M, K, N, out_mode, stream);
         case 9: return launch_linear_s<Lin9>(x, w, bias, y, M, K, N, out_mode, stream);
-        default: return launch_linear_s<Lin10>(x, w, bias, y, M, K, N, out_mode, stream);
+        case 10: return launch_linear_s<Lin10>(x, w, bias, y, M, K, N, out_mode, stream);
+        case 11: return launch_linear_s<Lin11>(x, w, bias, y, M, K, N, out_mode, stream);
+        case 12: return launch_linear_s<Lin12>(x, w, bias, y, M, K, N, out_mode, stream);
+        default: return launch_linear_s<Lin13>(x, w, bias, y, M, K, N, out_mode, stream);
     }
 }
 

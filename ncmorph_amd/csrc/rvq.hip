@@ -731,9 +731,9 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
 //              latency-bound small grids): at most one workgroup per CU;
 //   DistSmall2 128 x 128, 2 stages (64 KB: two workgroups per CU) between.
 // DistSmall and DistSmall2 share the candidate layout.
-using DistBig = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
-using DistSmall = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
-using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 2>;
+using DistBig = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
+using DistSmall = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
+using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 2>;
 constexpr int64_t kCus = 256;
 
 static int nch_for(int64_t d) {
