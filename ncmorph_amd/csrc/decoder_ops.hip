@@ -49,7 +49,17 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
     };
     int64_t g = 0;
     while (g + step <= groups) {
-        for (int64_t s = 0; s < step; ++s) a0 = a0 + sq((g + s) * 4 + r);
+        if (step == 16) {
+            // The common case (up to 2^20 elements): the 16 loads of a run
+            // issue together, then the chain adds them in order.
+            float t[16];
+#pragma unroll
+            for (int s = 0; s < 16; ++s) t[s] = sq((g + s) * 4 + r);
+#pragma unroll
+            for (int s = 0; s < 16; ++s) a0 = a0 + t[s];
+        } else {
+            for (int64_t s = 0; s < step; ++s) a0 = a0 + sq((g + s) * 4 + r);
+        }
         g += step;
         a1 = a1 + a0;
         a0 = 0.0f;
@@ -94,11 +104,38 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
             ((float*)y)[row * n + i] = __uint_as_float(bits << 16);
     };
     if ((n & 3) == 0) {
+        // Four elements per lane and step: one 8-byte (bf16) or 16-byte
+        // (bf16 values as fp32) store when y is aligned for it.
+        const bool yvec = ((uintptr_t)y & (OUT_MODE == NCM_OUT_BF16 ? 7 : 15)) == 0;
         for (int64_t i = 4 * lane; i < n; i += 256) {
             const f32x4_t v = *(const f32x4_t*)(xr + i);
             const f32x4_t wv = *(const f32x4_t*)(weight + i);
+            uint32_t bits[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) out1(i + e, v[e], wv[e]);
+            for (int e = 0; e < 4; ++e) {
+                const float normalized = __uint_as_float(bf16_bits_rne(v[e] * inv) << 16);
+                bits[e] = bf16_bits_rne(normalized *
+                                        __uint_as_float(bf16_bits_rne(wv[e]) << 16));
+            }
+            if (!yvec) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    if (OUT_MODE == NCM_OUT_BF16)
+                        ((uint16_t*)y)[row * n + i + e] = (uint16_t)bits[e];
+                    else
+                        ((float*)y)[row * n + i + e] = __uint_as_float(bits[e] << 16);
+                }
+            } else if (OUT_MODE == NCM_OUT_BF16) {
+                u32x2_t o;
+                o[0] = bits[0] | (bits[1] << 16);
+                o[1] = bits[2] | (bits[3] << 16);
+                *(u32x2_t*)((uint16_t*)y + row * n + i) = o;
+            } else {
+                f32x4_t o;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) o[e] = __uint_as_float(bits[e] << 16);
+                *(f32x4_t*)((float*)y + row * n + i) = o;
+            }
         }
     } else {
         for (int64_t i = lane; i < n; i += 64) out1(i, xr[i], weight[i]);

@@ -236,23 +236,37 @@ __global__ void rvq_pyramid_kernel(const float* __restrict__ src, int64_t rows, 
 // ------------------------------------------------- per-encode set-up kernel
 
 // cmax[l] = sqrt(max_k csq[l, k]) (rounded up); zeroes the flag counters.
-__global__ void rvq_setup_kernel(const float* __restrict__ csq, int64_t v, float* cmax,
-                                 int32_t* flag_count, int levels) {
+// One 1024-thread block per level; each thread issues its (up to) four loads
+// of a pass together, so the block waits for one memory round trip per
+// 4096 codes.
+constexpr int kSetupThreads = 1024;
+__global__ __launch_bounds__(kSetupThreads) void rvq_setup_kernel(const float* __restrict__ csq,
+                                                                 int64_t v, float* cmax,
+                                                                 int32_t* flag_count) {
     const int l = blockIdx.x;
+    const float* row = csq + (int64_t)l * v;
     float m = 0.0f;
-    for (int64_t k = threadIdx.x; k < v; k += blockDim.x) m = fmaxf(m, csq[l * v + k]);
-    __shared__ float red[256];
-    red[threadIdx.x] = m;
-    __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) red[threadIdx.x] = fmaxf(red[threadIdx.x], red[threadIdx.x + s]);
-        __syncthreads();
+    for (int64_t k0 = threadIdx.x; k0 < v; k0 += 4 * kSetupThreads) {
+        float t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t k = k0 + (int64_t)j * kSetupThreads;
+            t[j] = k < v ? row[k] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m = fmaxf(m, t[j]);
     }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    __shared__ float red[kSetupThreads / 64];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
     if (threadIdx.x == 0) {
-        cmax[l] = sqrtf(red[0]) * 1.00001f;
+        float r = red[0];
+        for (int w = 1; w < kSetupThreads / 64; ++w) r = fmaxf(r, red[w]);
+        cmax[l] = sqrtf(r) * 1.00001f;
         flag_count[l] = 0;
     }
-    (void)levels;
 }
 
 // ------------------------------------------------------ level-0 prep kernel
@@ -724,14 +738,18 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
 // ------------------------------------------------------------ host side
 
 // Distance GEMM tiles (codes x rows), all loading global -> LDS directly
-// with two wavefronts per SIMD:
+// with two wavefronts per SIMD (SCHED 8 main loop):
 //   DistBig    256 x 256, 8 wavefronts, 2 LDS stages: when it gives at least
 //              one workgroup per CU;
+//   DistMid    256 x 128, 8 wavefronts, 3 stages: when its tiles fill the CUs
+//              at least once;
 //   DistSmall  128 x 128, 4 wavefronts, 4 stages (deeper prefetch for the
 //              latency-bound small grids): at most one workgroup per CU;
 //   DistSmall2 128 x 128, 2 stages (64 KB: two workgroups per CU) between.
-// DistSmall and DistSmall2 share the candidate layout.
+// DistBig and DistMid share one candidate layout (256 codes per tile, 4
+// wavefronts along the codes), DistSmall and DistSmall2 another.
 using DistBig = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
+using DistMid = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3>;
 using DistSmall = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
 using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 2>;
 constexpr int64_t kCus = 256;
@@ -795,7 +813,7 @@ static CandGeom cand_geom_t(int64_t n_rows, int64_t v) {
     return cg;
 }
 
-enum DistKind { kDistBig, kDistSmall, kDistSmall2 };
+enum DistKind { kDistBig, kDistMid, kDistSmall, kDistSmall2 };
 
 static int64_t dist_grid(const CandGeom& cg, int64_t n_rows, int64_t bn) {
     return (n_rows + bn - 1) / bn * cg.nranges;
@@ -803,14 +821,18 @@ static int64_t dist_grid(const CandGeom& cg, int64_t n_rows, int64_t bn) {
 
 static DistKind dist_kind(int64_t n_rows, int64_t v) {
     if (dist_grid(cand_geom_t<DistBig>(n_rows, v), n_rows, DistBig::BN) >= kCus) return kDistBig;
+    if (dist_grid(cand_geom_t<DistMid>(n_rows, v), n_rows, DistMid::BN) >= kCus) return kDistMid;
     if (dist_grid(cand_geom_t<DistSmall>(n_rows, v), n_rows, DistSmall::BN) <= kCus)
         return kDistSmall;
     return kDistSmall2;
 }
 
 static CandGeom cand_geom(int64_t n_rows, int64_t v) {
-    return dist_kind(n_rows, v) == kDistBig ? cand_geom_t<DistBig>(n_rows, v)
-                                            : cand_geom_t<DistSmall>(n_rows, v);
+    switch (dist_kind(n_rows, v)) {
+        case kDistBig: return cand_geom_t<DistBig>(n_rows, v);
+        case kDistMid: return cand_geom_t<DistMid>(n_rows, v);
+        default: return cand_geom_t<DistSmall>(n_rows, v);
+    }
 }
 
 template <class S>
@@ -882,8 +904,8 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
     // D_{l+1} (coarse reconstruction) is written by level l into dbuf[(l+1)&1].
     float* dbuf[2] = {(float*)(W + o_d0), (float*)(W + o_d1)};
 
-    hipLaunchKernelGGL(rvq_setup_kernel, dim3((unsigned)levels), dim3(256), 0, st, csq, v, cmax,
-                       fcount, (int)levels);
+    hipLaunchKernelGGL(rvq_setup_kernel, dim3((unsigned)levels), dim3(kSetupThreads), 0, st, csq,
+                       v, cmax, fcount);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return NCM_E_HIP;
 
@@ -935,6 +957,7 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         da.cg = cg;
         switch (dist_kind(n, v)) {
             case kDistBig: e = launch_dist<DistBig>(da, st); break;
+            case kDistMid: e = launch_dist<DistMid>(da, st); break;
             case kDistSmall: e = launch_dist<DistSmall>(da, st); break;
             default: e = launch_dist<DistSmall2>(da, st); break;
         }

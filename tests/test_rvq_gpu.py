@@ -69,6 +69,8 @@ def test_small_config_golden(ncm, oracle, cuda):
     dict(b=3, t=64, d=320, v=300, strides=(16, 16, 4, 1), seed=22),
     dict(b=1, t=32, d=64, v=7, strides=(8, 2, 1), seed=23),
     dict(b=2, t=128, d=2048, v=1000, strides=(32, 8, 1), seed=24),
+    # 1024 rows on 128 x 128 tiles, then 2048 rows on 256 x 128 tiles
+    dict(b=1, t=2048, d=64, v=4096, strides=(2, 1), seed=25),
 ])
 def test_multiscale_matches_oracle(ncm, oracle, cuda, case):
     L = len(case["strides"])
