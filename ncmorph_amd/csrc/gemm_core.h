@@ -190,6 +190,15 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
         for (int nb = 0; nb < S::NB; ++nb)
             bfr[fs][nb] = *(const u32x4_t*)(base + b_frag0 + nb * 32 * S::RB + cofs);
     };
+    // Fragment j of k-step kk: A block j (j < MB) or B block j - MB.
+    auto fload_one = [&](int fs, const char* base, int kk, int j) {
+        const uint32_t cofs = (uint32_t)((((kk * 2 + khalf) ^ swz)) * 16);
+        if (j < S::MB)
+            af[fs][j] = *(const u32x4_t*)(base + a_frag0 + j * 32 * S::RB + cofs);
+        else
+            bfr[fs][j - S::MB] =
+                *(const u32x4_t*)(base + b_frag0 + (j - S::MB) * 32 * S::RB + cofs);
+    };
     // MFMAs lo .. hi - 1 of one k-step, in (mb, nb) row-major order.
     auto mfma_range = [&](int fs, int lo, int hi) {
 #pragma unroll
@@ -451,8 +460,15 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
                 if (kk + 1 < S::KSTEPS) {
                     const int d_lo = kk * DPK < ND ? kk * DPK : ND;
                     const int d_hi = (kk + 1) * DPK < ND ? (kk + 1) * DPK : ND;
-                    fload(fs ^ 1, base, kk + 1);
-                    dma_range(dst, k_ld, d_lo, d_hi);
+                    // Program order alternates fragment reads and loads
+                    // (the loads write LDS, so the scheduler keeps the two
+                    // kinds in program order); the MFMAs go between them.
+                    constexpr int NJ = NFR > DPK ? NFR : DPK;
+#pragma unroll
+                    for (int j = 0; j < NJ; ++j) {
+                        if (j < NFR) fload_one(fs ^ 1, base, kk + 1, j);
+                        if (j < d_hi - d_lo) dma_range(dst, k_ld, d_lo + j, d_lo + j + 1);
+                    }
                     mfma_range(fs, 0, NMF);
 #pragma unroll
                     for (int i = 0; i < NMF; ++i) {
@@ -465,7 +481,9 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
                     mfma_range(fs, 0, HALF);
                     __builtin_amdgcn_sched_barrier(0);
                     wait_barrier<VM>();
-                    if (kt + 1 < KT) fload(fs ^ 1, lds + nxt * S::LDS_STAGE, 0);
+                    // Unconditional (no branch to split the schedule): after
+                    // the last tile this reads a stage that is never used.
+                    fload(fs ^ 1, lds + nxt * S::LDS_STAGE, 0);
                     mfma_range(fs, HALF, NMF);
 #pragma unroll
                     for (int i = HALF; i < NMF; ++i) {
