@@ -175,15 +175,20 @@ def test_linear_zero_k_and_empty(ncm, cuda):
     assert kernels.linear_bf16(x, w).shape == (0, 3)
 
 
-def test_linear_ragged_long_k_bias_modes_repeatable(ncm, cuda):
+@pytest.mark.parametrize("m,k,n", [
+    (200, 1096, 300),     # 128 x 128 tiles, four LDS stages
+    (2148, 1096, 5400),   # 256 x 256 tiles (198 of them)
+    (2148, 1096, 2800),   # 256 x 128 tiles (198 of them)
+])
+def test_linear_ragged_long_k_bias_modes_repeatable(ncm, cuda, m, k, n):
     """Ragged M and N, K not a multiple of the 64-wide K tile (partial last
     tile), bias, every output mode against the D53 bound and each other, and
-    identical bits over repeated launches."""
+    identical bits over repeated launches; one shape per tile configuration
+    the automatic choice uses."""
     import torch
     from ncmorph_amd import kernels
 
-    rng = np.random.default_rng(77)
-    m, k, n = 200, 1096, 300
+    rng = np.random.default_rng(77 + m)
     xb = synth.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
     wb = synth.bf16_bits((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
     bb = synth.bf16_bits(rng.standard_normal(n).astype(np.float32))

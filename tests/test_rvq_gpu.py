@@ -71,6 +71,8 @@ def test_small_config_golden(ncm, oracle, cuda):
     dict(b=2, t=128, d=2048, v=1000, strides=(32, 8, 1), seed=24),
     # 1024 rows on 128 x 128 tiles, then 2048 rows on 256 x 128 tiles
     dict(b=1, t=2048, d=64, v=4096, strides=(2, 1), seed=25),
+    # 8192 rows at the finest level, few codes (four code ranges per tile row)
+    dict(b=2, t=4096, d=64, v=512, strides=(16, 4, 1), seed=26),
 ])
 def test_multiscale_matches_oracle(ncm, oracle, cuda, case):
     L = len(case["strides"])
