@@ -276,6 +276,47 @@ def run_ncm_attention(torch, reps=10):
                          "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4)}}
 
 
+def run_ncm_tied_head(torch, reps=5):
+    """Codebook-tied code heads of the NCM level-parallel step at the 8B shape
+    (PROJECT.md:222): for each of the 8 levels (the level lengths of
+    run_ncm_attention), logits [n_l, 8192] = (2 z E_l^T - ||E_l||^2) *
+    exp(log_inv_T) / mean ||E_l||^2 with z bf16 [n_l, 4096] and the level's
+    bf16 codebook E_l [8192, 4096] ~N(0, 1/4096). Flops: 2 V d per row."""
+    from ncmorph_amd import kernels, vq
+
+    dev = torch.device("cuda", 0)
+    v, d = 8192, 4096
+    g = torch.Generator(device=dev).manual_seed(17)
+    rows = sum(NCM_LEVELS)
+    z = torch.randn(rows, d, device=dev, generator=g).to(torch.bfloat16)
+    cb = (torch.randn(len(NCM_LEVELS), v, d, device=dev, generator=g) / d ** 0.5).to(torch.bfloat16)
+    csq = vq.prepare(cb)
+    out = torch.empty(rows, v, dtype=torch.float32, device=dev)
+
+    def run():
+        off = 0
+        for lvl, n in enumerate(NCM_LEVELS):
+            kernels.tied_head_logits(z[off:off + n], cb[lvl], csq[lvl], 0.0, out=out[off:off + n])
+            off += n
+
+    for _ in range(2):
+        run()
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / reps
+    flops = 2.0 * v * d * rows
+    tf = flops / sec / 1e12
+    return {"rows": rows, "codes": v, "d": d, "levels": len(NCM_LEVELS),
+            "us": round(sec * 1e6, 1), "flops": flops,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": BF16_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4)}}
+
+
 def run_weight_upload(torch, mib=512):
     """Device weight path: one bf16 tensor of `mib` MiB in a safetensors file
     (written first, so it is in the page cache) copied to HBM as stored
@@ -477,6 +518,7 @@ def main():
         dec = run_decoder(torch)
         dec["weight_upload"] = run_weight_upload(torch)
         dec["ncm_level_attention"] = run_ncm_attention(torch)
+        dec["ncm_tied_head"] = run_ncm_tied_head(torch)
         if not args.no_cpu:
             dec["cpu_baseline"] = cpu_decoder_baseline()
         res["decoder_prefill"] = dec

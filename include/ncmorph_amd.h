@@ -255,6 +255,20 @@ int ncm_block_diagonal_segments(int64_t prefix_len, const int64_t* level_lengths
                                 int64_t pad_len, int64_t seq_len, int32_t* seg_lo,
                                 int32_t* seg_hi, uint64_t* pad_bits);
 
+/* Codebook-tied code head of the NCM generator (described at PROJECT.md:222,
+ * upstream _TiedCodebookHead; the reference has no code for it yet):
+ *   logits[r, k] = (2 z_r . E_k - csq[k]) * scale (+ bias[k]),
+ *   scale = expf(log_inv_t) / d_scale, d_scale = mean_k csq[k]
+ * with z: bf16 [rows, d] (the head's projection of the hidden state), E: the
+ * level's bf16 codebook [v, d], csq: fp32 [v] = ||E_k||^2 (ncm_rvq_prepare),
+ * bias: fp32 [v] or NULL, logits: fp32 [rows, v]. The bf16 MFMA of the RVQ
+ * distance with the affine map in its epilogue; d_scale is summed in f64 on
+ * the device. argmax_k logits[r] is the nearest code to z_r. d % 8 == 0,
+ * z and E 16-byte aligned, v >= 1. Device pointers. */
+int ncm_tied_head_logits(ncm_ctx_t* ctx, const uint16_t* z, const uint16_t* codebook,
+                         const float* csq, const float* bias, float log_inv_t, float* logits,
+                         int64_t rows, int64_t d, int64_t v);
+
 /* ---- bf16 decoder prefill forward (src/decoder.zig:62-228) ---- */
 
 /* Model shape (config.spec_t fields the forward reads). window: sliding

@@ -295,6 +295,26 @@ int ncm_linear_bf16_rope64(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
     return NCM_OK;
 }
 
+int ncm_tied_head_logits(ncm_ctx_t* ctx, const uint16_t* z, const uint16_t* codebook,
+                         const float* csq, const float* bias, float log_inv_t, float* logits,
+                         int64_t rows, int64_t d, int64_t v) {
+    if (!ctx) return NCM_E_NULL;
+    if (v < 1) return NCM_E_SHAPE;  // d_scale is a mean over the codes
+    int rc = check_linear_args(z, codebook, logits, rows, d, v);
+    if (rc) return rc;
+    if (!csq) return NCM_E_NULL;
+    if (rows == 0) return NCM_OK;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, 256, &ws);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_tied_head(z, codebook, csq, bias, log_inv_t, (float*)ws, logits,
+                                         rows, d, v, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "tied head launch");
+    return NCM_OK;
+}
+
 int ncm_linear_f32(ncm_ctx_t* ctx, const float* x, const float* w, float* y, int64_t m,
                    int64_t k, int64_t n) {
     if (!ctx) return NCM_E_NULL;

@@ -374,3 +374,25 @@ def attention_bf16_seg(q, k, v, batch: int, seq_len: int, q_heads: int, kv_heads
                                            _dev_ptr(pad_bits, "pad_bits"), mode),
           "attention_bf16_seg")
     return out
+
+
+def tied_head_logits(z, codebook, csq, log_inv_t: float = 0.0, bias=None, out=None, ctx=None):
+    """Codebook-tied NCM code head (PROJECT.md:222): logits = (2 z E^T - csq)
+    * exp(log_inv_t) / mean(csq) (+ bias). z: torch.bfloat16 [rows, d] on the
+    GPU, codebook: torch.bfloat16 [v, d], csq: float32 [v] (vq.prepare), bias:
+    float32 [v] or None; returns float32 [rows, v]."""
+    import torch
+
+    rows, d = z.shape
+    v, d2 = codebook.shape
+    if d != d2 or tuple(csq.shape) != (v,):
+        raise NcmError(-2, "tied_head_logits")
+    if out is None:
+        out = torch.empty((rows, v), dtype=torch.float32, device=z.device)
+    ctx = ctx or default_context(z.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_tied_head_logits(ctx.handle, _dev_ptr(z, "z"), _dev_ptr(codebook, "codebook"),
+                                     _dev_ptr(csq, "csq"), _dev_ptr(bias, "bias"),
+                                     float(log_inv_t), _dev_ptr(out, "out"), rows, d, v),
+          "tied_head_logits")
+    return out

@@ -545,3 +545,22 @@ def block_diagonal_mask(prefix_length: int, level_lengths, prefix_pad_mask=None)
     if rc == -1:
         raise ValueError("InvalidPrefixMask")
     return out
+
+
+def tied_head_logits_f64(z, codebook, log_inv_t=0.0, bias=None):
+    """The NCM codebook-tied code head as the reference describes it
+    (PROJECT.md:222, upstream _TiedCodebookHead; no reference code exists):
+    E_sq = sum E^2 per code, d_scale = mean(E_sq), logits = (2 z E^T - E_sq)
+    / d_scale * exp(log_inv_T) (+ bias), evaluated in f64 on the values given
+    (bf16 operands widened to float). Returns (logits, sum of |2 z_i E_ki|
+    per entry) for error bounds."""
+    z64 = np.asarray(z, np.float64)
+    e64 = np.asarray(codebook, np.float64)
+    esq = np.sum(e64 * e64, axis=1)
+    scale = np.exp(np.float64(log_inv_t)) / esq.mean()
+    s = z64 @ e64.T
+    logits = (2.0 * s - esq[None, :]) * scale
+    if bias is not None:
+        logits = logits + np.asarray(bias, np.float64)[None, :]
+    mag = 2.0 * (np.abs(z64) @ np.abs(e64).T)
+    return logits, mag
