@@ -269,6 +269,18 @@ int ncm_tied_head_logits(ncm_ctx_t* ctx, const uint16_t* z, const uint16_t* code
                          const float* csq, const float* bias, float log_inv_t, float* logits,
                          int64_t rows, int64_t d, int64_t v);
 
+/* Every level's tied head of the level-parallel step in one launch: z holds
+ * the levels' rows one level after another (level_rows[l] rows of level l,
+ * host array), codebooks: bf16 [n_levels, v, d], csq: fp32 [n_levels, v],
+ * bias: fp32 [n_levels, v] or NULL, log_inv_t: host float [n_levels] (one
+ * learned scalar per level's head), logits: fp32 [sum rows, v]. Level l's
+ * rows get level l's codebook, norms, bias and scale; each as
+ * ncm_tied_head_logits. 1 <= n_levels <= 32. */
+int ncm_tied_head_logits_levels(ncm_ctx_t* ctx, const uint16_t* z, const uint16_t* codebooks,
+                                const float* csq, const float* bias, const float* log_inv_t,
+                                const int64_t* level_rows, int64_t n_levels, int64_t d,
+                                int64_t v, float* logits);
+
 /* ---- bf16 decoder prefill forward (src/decoder.zig:62-228) ---- */
 
 /* Model shape (config.spec_t fields the forward reads). window: sliding

@@ -58,6 +58,7 @@ SIGNATURES = [
                                          i64, i64, vp, vp, vp, i32]),
     ("ncm_block_diagonal_segments", i32, [i64, vp, i64, vp, i64, i64, vp, vp, vp]),
     ("ncm_tied_head_logits", i32, [vp, vp, vp, vp, vp, C.c_float, vp, i64, i64, i64]),
+    ("ncm_tied_head_logits_levels", i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, vp]),
     ("ncm_decoder_forward_dev", i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]),
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
     ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),

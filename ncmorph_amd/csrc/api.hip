@@ -295,12 +295,20 @@ int ncm_linear_bf16_rope64(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
     return NCM_OK;
 }
 
-int ncm_tied_head_logits(ncm_ctx_t* ctx, const uint16_t* z, const uint16_t* codebook,
-                         const float* csq, const float* bias, float log_inv_t, float* logits,
-                         int64_t rows, int64_t d, int64_t v) {
+int ncm_tied_head_logits_levels(ncm_ctx_t* ctx, const uint16_t* z, const uint16_t* codebooks,
+                                const float* csq, const float* bias, const float* log_inv_t,
+                                const int64_t* level_rows, int64_t n_levels, int64_t d,
+                                int64_t v, float* logits) {
     if (!ctx) return NCM_E_NULL;
-    if (v < 1) return NCM_E_SHAPE;  // d_scale is a mean over the codes
-    int rc = check_linear_args(z, codebook, logits, rows, d, v);
+    if (n_levels < 1 || n_levels > 32 || v < 1) return NCM_E_SHAPE;
+    if (!log_inv_t || !level_rows) return NCM_E_NULL;
+    int64_t rows = 0;
+    for (int64_t l = 0; l < n_levels; ++l) {
+        if (level_rows[l] < 0) return NCM_E_SHAPE;
+        rows += level_rows[l];
+        if (rows > (int64_t(1) << 31)) return NCM_E_SHAPE;
+    }
+    int rc = check_linear_args(z, codebooks, logits, rows, d, v);
     if (rc) return rc;
     if (!csq) return NCM_E_NULL;
     if (rows == 0) return NCM_OK;
@@ -309,10 +317,19 @@ int ncm_tied_head_logits(ncm_ctx_t* ctx, const uint16_t* z, const uint16_t* code
     void* ws = nullptr;
     rc = ncm_ctx_workspace(ctx, 256, &ws);
     if (rc) return rc;
-    hipError_t e = ncm::launch_tied_head(z, codebook, csq, bias, log_inv_t, (float*)ws, logits,
-                                         rows, d, v, ctx->stream);
+    hipError_t e = ncm::launch_tied_head(z, codebooks, csq, bias, log_inv_t, level_rows,
+                                         (int)n_levels, (float*)ws, logits, d, v, ctx->stream);
+    if (e == hipErrorInvalidConfiguration) return NCM_E_SHAPE;
     if (e != hipSuccess) return fail_hip(e, "tied head launch");
     return NCM_OK;
+}
+
+int ncm_tied_head_logits(ncm_ctx_t* ctx, const uint16_t* z, const uint16_t* codebook,
+                         const float* csq, const float* bias, float log_inv_t, float* logits,
+                         int64_t rows, int64_t d, int64_t v) {
+    if (rows < 0) return NCM_E_SHAPE;
+    return ncm_tied_head_logits_levels(ctx, z, codebook, csq, bias, &log_inv_t, &rows, 1, d, v,
+                                       logits);
 }
 
 int ncm_linear_f32(ncm_ctx_t* ctx, const float* x, const float* w, float* y, int64_t m,

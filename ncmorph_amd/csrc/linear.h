@@ -45,11 +45,14 @@ hipError_t launch_silu_mul(const float* gate, const float* up, void* y, int64_t 
                            hipStream_t stream);
 
 // RoPE rotate-half (bf16 mode) in place on bf16 bits; see decoder_ops.hip.
-// Codebook-tied head logits: y = (2 z E^T - csq) * expf(log_inv_t) / mean(csq)
-// (+ bias); scale: one float of device scratch.
+// Codebook-tied head logits of `levels` levels in one launch: level l's rows
+// (rows[l] of them, after those of the levels before it) against codebook l:
+// y = (2 z E_l^T - csq_l) * expf(log_inv_t[l]) / mean(csq_l) (+ bias_l);
+// scale: `levels` floats of device scratch. log_inv_t and rows: host arrays.
 hipError_t launch_tied_head(const uint16_t* z, const uint16_t* cb, const float* csq,
-                            const float* bias, float log_inv_t, float* scale, float* y,
-                            int64_t M, int64_t K, int64_t N, hipStream_t st);
+                            const float* bias, const float* log_inv_t, const int64_t* rows,
+                            int levels, float* scale, float* y, int64_t d, int64_t v,
+                            hipStream_t st);
 hipError_t launch_rope_rotate(uint16_t* x, int64_t rows, int64_t row_stride, int heads, int hd,
                               int64_t seq_len, const float* cosine, const float* sine,
                               hipStream_t stream);

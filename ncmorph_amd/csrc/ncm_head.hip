@@ -10,19 +10,43 @@
 // E_sq from ncm_rvq_prepare, and the affine map fused into the epilogue.
 // fp32 operation order of the epilogue (tolerance-based parity, like the
 // linear): t = 2 S - E_sq[k]; logit = t * scale (+ bias[k]), with
-// scale = expf(log_inv_T) / d_scale computed once per call and d_scale the
-// f64 sum of E_sq rounded to fp32 after the division by V.
+// scale = expf(log_inv_T) / d_scale computed once per level and call and
+// d_scale the f64 sum of E_sq rounded to fp32 after the division by V. The
+// level-parallel step evaluates every level's head at once (each level's
+// positions against its own codebook), so one launch covers all levels.
 #include "gemm_core.h"
 #include "linear.h"
 
 namespace ncm {
 
-// scale[0] = expf(log_inv_T) / (float)(sum_k csq[k] / v), one block.
-__global__ __launch_bounds__(256) void tied_head_scale_kernel(const float* __restrict__ csq,
-                                                              int64_t v, float log_inv_t,
-                                                              float* __restrict__ scale) {
+constexpr int kHeadMaxLevels = 32;
+
+// One launch covers every level: level l owns rows [row0[l], row0[l] +
+// rows[l]) of z and of the logits, codebook l, E_sq row l, bias row l and
+// output tiles [tile0[l], tile0[l + 1]).
+struct HeadArgs {
+    const uint16_t* z;
+    const uint16_t* cb;    // [levels, v, d]
+    const float* csq;      // [levels, v]
+    const float* bias;     // [levels, v] or null
+    const float* scale;    // [levels], device
+    float* y;              // [sum rows, v]
+    int64_t v, d;
+    int levels;
+    int tiles_n;
+    int64_t row0[kHeadMaxLevels];
+    int64_t rows[kHeadMaxLevels];
+    int tile0[kHeadMaxLevels + 1];
+    float log_inv_t[kHeadMaxLevels];
+};
+
+// scale[l] = expf(log_inv_t[l]) / (float)(sum_k csq[l, k] / v), one block
+// per level.
+__global__ __launch_bounds__(256) void tied_head_scale_kernel(HeadArgs a, float* scale) {
+    const int l = blockIdx.x;
+    const float* c = a.csq + (int64_t)l * a.v;
     double s = 0.0;
-    for (int64_t k = threadIdx.x; k < v; k += 256) s += (double)csq[k];
+    for (int64_t k = threadIdx.x; k < a.v; k += 256) s += (double)c[k];
     __shared__ double red[256];
     red[threadIdx.x] = s;
     __syncthreads();
@@ -31,34 +55,41 @@ __global__ __launch_bounds__(256) void tied_head_scale_kernel(const float* __res
         __syncthreads();
     }
     if (threadIdx.x == 0) {
-        const float d_scale = (float)(red[0] / (double)v);
-        scale[0] = expf(log_inv_t) / d_scale;
+        const float d_scale = (float)(red[0] / (double)a.v);
+        scale[l] = expf(a.log_inv_t[l]) / d_scale;
     }
 }
 
 template <class S, bool HAS_BIAS>
 __global__ __launch_bounds__(S::NT)
-__attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void tied_head_kernel(
-    const uint16_t* __restrict__ z, const uint16_t* __restrict__ cb, const float* __restrict__ csq,
-    const float* __restrict__ bias, const float* __restrict__ scale_p, float* __restrict__ y,
-    int64_t M, int64_t K, int64_t N, int tiles_n, int group_m) {
+__attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void tied_head_kernel(HeadArgs a) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
-    // XCD-aware grouped tile order, as in the linear.
     const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int per_group = group_m * tiles_n;
-    const int g = logical / per_group;
+    int l = 0;
+    while (l + 1 < a.levels && logical >= a.tile0[l + 1]) ++l;
+    // Inside the level: grouped tile order (bands of up to 4 row tiles).
+    const int64_t M = a.rows[l], N = a.v, K = a.d;
+    const int local = logical - a.tile0[l];
     const int tiles_m = (int)((M + S::BM - 1) / S::BM);
+    const int group_m = tiles_m < 4 ? tiles_m : 4;
+    const int per_group = group_m * a.tiles_n;
+    const int g = local / per_group;
     const int gm = min(group_m, tiles_m - g * group_m);
-    const int in_g = logical % per_group;
+    const int in_g = local % per_group;
     const int64_t m0 = (int64_t)(g * group_m + in_g % gm) * S::BM;
     const int64_t n0 = (int64_t)(in_g / gm) * S::BN;
+    const uint16_t* z = a.z + a.row0[l] * K;
+    const uint16_t* cb = a.cb + (int64_t)l * N * K;
+    const float* csq = a.csq + (int64_t)l * N;
+    const float* bias = HAS_BIAS ? a.bias + (int64_t)l * N : nullptr;
+    float* y = a.y + a.row0[l] * N;
 
     GemmAcc<S> acc;
     acc.zero();
     gemm_mainloop<S>(z + m0 * K, K, operand_bytes(M, m0, K), cb + n0 * K, K,
                      operand_bytes(N, n0, K), K, lds, acc);
 
-    const float scale = scale_p[0];
+    const float scale = a.scale[l];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int wm = wave % S::WGM;
@@ -117,50 +148,61 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void tied_head_kernel(
     }
 }
 
-template <class S, bool HAS_BIAS>
-static hipError_t launch_head_t(const uint16_t* z, const uint16_t* cb, const float* csq,
-                                const float* bias, const float* scale, float* y, int64_t M,
-                                int64_t K, int64_t N, hipStream_t st) {
-    auto kern = tied_head_kernel<S, HAS_BIAS>;
-    static bool attr_set = false;
-    if (!attr_set) {
+template <class S>
+static hipError_t launch_head_t(HeadArgs& a, hipStream_t st) {
+    int64_t t = 0;
+    const int64_t tn = (a.v + S::BN - 1) / S::BN;
+    for (int l = 0; l < a.levels; ++l) {
+        a.tile0[l] = (int)t;
+        t += (a.rows[l] + S::BM - 1) / S::BM * tn;
+        if (t > 0x7fffffff) return hipErrorInvalidConfiguration;
+    }
+    a.tiles_n = (int)tn;
+    a.tile0[a.levels] = (int)t;
+    if (t == 0) return hipSuccess;
+    auto kern = a.bias ? tied_head_kernel<S, true> : tied_head_kernel<S, false>;
+    static bool attr_set[2] = {false, false};
+    if (!attr_set[a.bias ? 1 : 0]) {
         hipError_t e = hipFuncSetAttribute((const void*)kern,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            S::LDS_BYTES);
         if (e != hipSuccess) return e;
-        attr_set = true;
+        attr_set[a.bias ? 1 : 0] = true;
     }
-    const int tiles_m = (int)((M + S::BM - 1) / S::BM);
-    const int tiles_n = (int)((N + S::BN - 1) / S::BN);
-    const int group_m = tiles_m < 4 ? tiles_m : 4;
-    hipLaunchKernelGGL(kern, dim3(tiles_m * tiles_n), dim3(S::NT), S::LDS_BYTES, st, z, cb, csq,
-                       bias, scale, y, M, K, N, tiles_n, group_m);
+    hipLaunchKernelGGL(kern, dim3((unsigned)t), dim3(S::NT), S::LDS_BYTES, st, a);
     return hipGetLastError();
 }
 
 hipError_t launch_tied_head(const uint16_t* z, const uint16_t* cb, const float* csq,
-                            const float* bias, float log_inv_t, float* scale, float* y,
-                            int64_t M, int64_t K, int64_t N, hipStream_t st) {
-    hipLaunchKernelGGL(tied_head_scale_kernel, dim3(1), dim3(256), 0, st, csq, N, log_inv_t,
-                       scale);
+                            const float* bias, const float* log_inv_t, const int64_t* rows,
+                            int levels, float* scale, float* y, int64_t d, int64_t v,
+                            hipStream_t st) {
+    if (levels < 1 || levels > kHeadMaxLevels) return hipErrorInvalidValue;
+    HeadArgs a{};
+    a.z = z; a.cb = cb; a.csq = csq; a.bias = bias; a.scale = scale; a.y = y;
+    a.v = v; a.d = d; a.levels = levels;
+    int64_t r = 0, tiles_big = 0, tiles_small = 0;
+    for (int l = 0; l < levels; ++l) {
+        a.row0[l] = r;
+        a.rows[l] = rows[l];
+        a.log_inv_t[l] = log_inv_t[l];
+        r += rows[l];
+        tiles_big += ((rows[l] + 255) / 256) * ((v + 255) / 256);
+        tiles_small += ((rows[l] + 127) / 128) * ((v + 127) / 128);
+    }
+    hipLaunchKernelGGL(tied_head_scale_kernel, dim3(levels), dim3(256), 0, st, a, scale);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    // The linear's tile shapes and automatic choice.
+    // The linear's tiles: 256 x 256 when the levels together fill three
+    // quarters of the CUs with them, else 128 x 128 with four LDS stages (at
+    // most about one tile per CU) or two (two workgroups per CU).
     using H0 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
     using H1 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
     using H2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
-    using H5 = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3>;
-    const bool hb = bias != nullptr;
-#define NCM_HEAD(SH) \
-    (hb ? launch_head_t<SH, true>(z, cb, csq, bias, scale, y, M, K, N, st) \
-        : launch_head_t<SH, false>(z, cb, csq, bias, scale, y, M, K, N, st))
-    switch (linear_tile_config(M, N, K, -1)) {
-        case 0: return NCM_HEAD(H0);
-        case 1: return NCM_HEAD(H1);
-        case 5: return NCM_HEAD(H5);
-        default: return NCM_HEAD(H2);
-    }
-#undef NCM_HEAD
+    const int64_t cus = 256;
+    if (tiles_big * 4 >= cus * 3) return launch_head_t<H0>(a, st);
+    if (tiles_small <= cus) return launch_head_t<H1>(a, st);
+    return launch_head_t<H2>(a, st);
 }
 
 }  // namespace ncm

@@ -396,3 +396,28 @@ def tied_head_logits(z, codebook, csq, log_inv_t: float = 0.0, bias=None, out=No
                                      float(log_inv_t), _dev_ptr(out, "out"), rows, d, v),
           "tied_head_logits")
     return out
+
+
+def tied_head_logits_levels(z, codebooks, csq, level_rows, log_inv_t=None, bias=None, out=None,
+                            ctx=None):
+    """Every level's tied head in one launch: z torch.bfloat16 [sum rows, d]
+    (level blocks in order, level_rows[l] rows each), codebooks bfloat16
+    [levels, v, d], csq float32 [levels, v], log_inv_t: one float per level
+    (default 0), bias float32 [levels, v] or None; float32 [sum rows, v]."""
+    import torch
+
+    L, v, d = codebooks.shape
+    rows = np.ascontiguousarray(level_rows, dtype=np.int64)
+    lit = np.ascontiguousarray(np.zeros(L) if log_inv_t is None else log_inv_t, dtype=np.float32)
+    if (rows.size != L or lit.size != L or tuple(z.shape) != (int(rows.sum()), d)
+            or tuple(csq.shape) != (L, v)):
+        raise NcmError(-2, "tied_head_logits_levels")
+    if out is None:
+        out = torch.empty((int(rows.sum()), v), dtype=torch.float32, device=z.device)
+    ctx = ctx or default_context(z.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_tied_head_logits_levels(
+        ctx.handle, _dev_ptr(z, "z"), _dev_ptr(codebooks, "codebooks"), _dev_ptr(csq, "csq"),
+        _dev_ptr(bias, "bias"), lit.ctypes.data_as(C.c_void_p), rows.ctypes.data_as(C.c_void_p),
+        L, d, v, _dev_ptr(out, "out")), "tied_head_logits_levels")
+    return out

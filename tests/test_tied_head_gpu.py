@@ -75,3 +75,40 @@ def test_tied_head_rejects_bad_arguments(ncm, cuda):
     c = torch.ones(6, device=cuda)
     with pytest.raises(NcmError):
         kernels.tied_head_logits(z, e, c)
+
+
+def test_tied_head_levels_one_launch(ncm, oracle, cuda):
+    """Several levels in one launch (ragged row counts, an empty level, a
+    scale and a bias per level): each level block against the oracle with the
+    level's own codebook, norms, bias and scale."""
+    import torch
+    from ncmorph_amd import kernels, vq
+
+    rng = np.random.default_rng(123)
+    d, v = 256, 1000
+    level_rows = [40, 0, 300, 129]
+    lit = [0.0, 1.0, -0.5, 0.25]
+    L = len(level_rows)
+    zb = synth.bf16_bits(rng.standard_normal((sum(level_rows), d)).astype(np.float32))
+    eb = synth.bf16_bits((rng.standard_normal((L, v, d)) / np.sqrt(d)).astype(np.float32))
+    bf = rng.standard_normal((L, v)).astype(np.float32)
+    zd, ed = _bf16_dev(zb, cuda), _bf16_dev(eb, cuda)
+    csq = vq.prepare(ed)
+    got = kernels.tied_head_logits_levels(zd, ed, csq, level_rows, lit,
+                                          bias=torch.from_numpy(bf).to(cuda))
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    off = 0
+    for l, n in enumerate(level_rows):
+        if n:
+            z = synth.bf16_to_f32(zb[off:off + n])
+            E = synth.bf16_to_f32(eb[l])
+            ref, mag = oracle.tied_head_logits_f64(z, E, lit[l], bf[l])
+            esq = np.sum(E.astype(np.float64) ** 2, axis=1)
+            scale = np.exp(lit[l]) / esq.mean()
+            t = np.abs(ref - bf[l]) / scale
+            bound = (scale * ((d + 4) * 2.0**-24 * mag + d * 2.0**-24 * esq[None, :]
+                              + 2.0**-22 * t) + 2.0**-21 * (np.abs(ref) + np.abs(bf[l])) + 1e-30)
+            err = np.abs(got[off:off + n].astype(np.float64) - ref)
+            assert np.all(err <= bound), (l, float(np.max(err / bound)))
+        off += n
