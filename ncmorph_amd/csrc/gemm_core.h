@@ -21,6 +21,8 @@
 //   D (both): lane l, element i holds D[8 (i / 4) + 4 (l / 32) + i % 4][l % 32].
 #pragma once
 
+#include <type_traits>
+
 #include "common.h"
 
 namespace ncm {
@@ -281,7 +283,12 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
     const int drow0 = wave * S::RPI + lane / S::CH;
     const int dslot = lane % S::CH;
     // Loads lo .. hi - 1 of the A_DMA + B_DMA of one tile.
-    auto dma_range = [&](int stage, int64_t k0, int lo, int hi) {
+    // Loads lo .. hi - 1 of one tile. CHECK: K-chunks at or past K load as
+    // zero (the K tail). Without CHECK (K a multiple of BK) a tile at or past
+    // K reads whatever follows the rows or zeros past the operand's end; such
+    // tiles are prefetches that are never read.
+    auto dma_range_t = [&](int stage, int64_t k0, int lo, int hi, auto check) {
+        constexpr bool CHECK = decltype(check)::value;
         char* sbase = lds + stage * S::LDS_STAGE;
         const uint32_t kb = (uint32_t)(k0 * S::ESZ);
 #pragma unroll
@@ -291,13 +298,17 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
             const int pp = is_a ? p : p - S::A_DMA;
             const int row = pp * S::NW * S::RPI + drow0;
             const int ch = dslot ^ ((row >> S::SWZ_SHIFT) & (S::CH - 1));
-            const bool valid = (k0 + ch * S::EPC) < K;
             const uint32_t off = (uint32_t)(row * (is_a ? lda : ldb) * S::ESZ + ch * 16) + kb;
             char* dst = sbase + (is_a ? 0 : S::LDS_A) + (pp * S::NW + wave) * 1024;
+            uint32_t o = off;
+            if (CHECK) o = (k0 + ch * S::EPC) < K ? off : kOobOffset;
             __builtin_amdgcn_raw_ptr_buffer_load_lds(
-                is_a ? rsa : rsb, (__attribute__((address_space(3))) void*)dst, 16,
-                valid ? off : kOobOffset, 0, 0, 0);
+                is_a ? rsa : rsb, (__attribute__((address_space(3))) void*)dst, 16, o, 0, 0, 0);
         }
+    };
+    using Checked = std::integral_constant<bool, true>;
+    auto dma_range = [&](int stage, int64_t k0, int lo, int hi) {
+        dma_range_t(stage, k0, lo, hi, Checked{});
     };
     auto dma = [&](int stage, int64_t k0) { dma_range(stage, k0, 0, S::A_DMA + S::B_DMA); };
     // At a barrier a wave keeps its last NST - 2 tiles of loads in flight.
@@ -435,66 +446,75 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
             cur = nxt;
         }
     } else if constexpr (S::SCHED == 8) {
-        // SCHED 5's stage rotation and barrier, with the tile's loads spread
-        // over its first k-steps: k-step kk < KSTEPS - 1 issues one MFMA,
-        // then one fragment read of k-step kk + 1 and one direct-to-LDS load,
-        // and so on, so the matrix core keeps working while they issue.
-        constexpr int HALF = S::BSPLIT;
-        constexpr int ND = S::A_DMA + S::B_DMA;
-        constexpr int NFR = S::MB + S::NB;
-        constexpr int DPK = (ND + S::DSPREAD - 1) / S::DSPREAD;
-        static_assert(S::DSPREAD >= 1 && S::DSPREAD < S::KSTEPS, "SCHED 8 load spread");
+        // One copy of the loop for a K that is a multiple of BK (no per-load
+        // tail check) and one with the check.
+        auto sched8 = [&](auto check) {
+            // SCHED 5's stage rotation and barrier, with the tile's loads spread
+            // over its first k-steps: k-step kk < KSTEPS - 1 issues one MFMA,
+            // then one fragment read of k-step kk + 1 and one direct-to-LDS load,
+            // and so on, so the matrix core keeps working while they issue.
+            constexpr int HALF = S::BSPLIT;
+            constexpr int ND = S::A_DMA + S::B_DMA;
+            constexpr int NFR = S::MB + S::NB;
+            constexpr int DPK = (ND + S::DSPREAD - 1) / S::DSPREAD;
+            static_assert(S::DSPREAD >= 1 && S::DSPREAD < S::KSTEPS, "SCHED 8 load spread");
 #pragma unroll
-        for (int st = 0; st + 1 < S::NST; ++st) dma(st, (int64_t)st * S::BK);
-        wait_barrier<VM>();
-        fload(0, lds, 0);
-        int cur = 0;
-        for (int kt = 0; kt < KT; ++kt) {
-            const char* base = lds + cur * S::LDS_STAGE;
-            const int nxt = cur + 1 == S::NST ? 0 : cur + 1;
-            const int dst = cur == 0 ? S::NST - 1 : cur - 1;
-            const int64_t k_ld = (int64_t)(kt + S::NST - 1) * S::BK;
+            for (int st = 0; st + 1 < S::NST; ++st)
+                dma_range_t(st, (int64_t)st * S::BK, 0, ND, check);
+            wait_barrier<VM>();
+            fload(0, lds, 0);
+            int cur = 0;
+            for (int kt = 0; kt < KT; ++kt) {
+                const char* base = lds + cur * S::LDS_STAGE;
+                const int nxt = cur + 1 == S::NST ? 0 : cur + 1;
+                const int dst = cur == 0 ? S::NST - 1 : cur - 1;
+                const int64_t k_ld = (int64_t)(kt + S::NST - 1) * S::BK;
 #pragma unroll
-            for (int kk = 0; kk < S::KSTEPS; ++kk) {
-                const int fs = kk & 1;
-                if (kk + 1 < S::KSTEPS) {
-                    const int d_lo = kk * DPK < ND ? kk * DPK : ND;
-                    const int d_hi = (kk + 1) * DPK < ND ? (kk + 1) * DPK : ND;
-                    // Program order alternates fragment reads and loads
-                    // (the loads write LDS, so the scheduler keeps the two
-                    // kinds in program order); the MFMAs go between them.
-                    constexpr int NJ = NFR > DPK ? NFR : DPK;
+                for (int kk = 0; kk < S::KSTEPS; ++kk) {
+                    const int fs = kk & 1;
+                    if (kk + 1 < S::KSTEPS) {
+                        const int d_lo = kk * DPK < ND ? kk * DPK : ND;
+                        const int d_hi = (kk + 1) * DPK < ND ? (kk + 1) * DPK : ND;
+                        // Program order alternates fragment reads and loads
+                        // (the loads write LDS, so the scheduler keeps the two
+                        // kinds in program order); the MFMAs go between them.
+                        constexpr int NJ = NFR > DPK ? NFR : DPK;
 #pragma unroll
-                    for (int j = 0; j < NJ; ++j) {
-                        if (j < NFR) fload_one(fs ^ 1, base, kk + 1, j);
-                        if (j < d_hi - d_lo) dma_range(dst, k_ld, d_lo + j, d_lo + j + 1);
+                        for (int j = 0; j < NJ; ++j) {
+                            if (j < NFR) fload_one(fs ^ 1, base, kk + 1, j);
+                            if (j < d_hi - d_lo) dma_range_t(dst, k_ld, d_lo + j, d_lo + j + 1, check);
+                        }
+                        mfma_range(fs, 0, NMF);
+#pragma unroll
+                        for (int i = 0; i < NMF; ++i) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            if (i < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                            if (i < d_hi - d_lo) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+                    } else {
+                        mfma_range(fs, 0, HALF);
+                        __builtin_amdgcn_sched_barrier(0);
+                        wait_barrier<VM>();
+                        // Unconditional (no branch to split the schedule): after
+                        // the last tile this reads a stage that is never used.
+                        fload(fs ^ 1, lds + nxt * S::LDS_STAGE, 0);
+                        mfma_range(fs, HALF, NMF);
+#pragma unroll
+                        for (int i = HALF; i < NMF; ++i) {
+                            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                            if (i - HALF < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
                     }
-                    mfma_range(fs, 0, NMF);
-#pragma unroll
-                    for (int i = 0; i < NMF; ++i) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                        if (i < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                        if (i < d_hi - d_lo) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
-                } else {
-                    mfma_range(fs, 0, HALF);
-                    __builtin_amdgcn_sched_barrier(0);
-                    wait_barrier<VM>();
-                    // Unconditional (no branch to split the schedule): after
-                    // the last tile this reads a stage that is never used.
-                    fload(fs ^ 1, lds + nxt * S::LDS_STAGE, 0);
-                    mfma_range(fs, HALF, NMF);
-#pragma unroll
-                    for (int i = HALF; i < NMF; ++i) {
-                        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-                        if (i - HALF < NFR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-                    }
-                    __builtin_amdgcn_sched_barrier(0);
                 }
+                cur = nxt;
             }
-            cur = nxt;
-        }
+        };
+        if (K % S::BK == 0)
+            sched8(std::integral_constant<bool, false>{});
+        else
+            sched8(Checked{});
     } else {
         // Two stages, barrier after each tile.
         dma(0, 0);
