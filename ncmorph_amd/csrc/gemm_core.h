@@ -449,10 +449,11 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
         // One copy of the loop for a K that is a multiple of BK (no per-load
         // tail check) and one with the check.
         auto sched8 = [&](auto check) {
-            // SCHED 5's stage rotation and barrier, with the tile's loads spread
-            // over its first k-steps: k-step kk < KSTEPS - 1 issues one MFMA,
-            // then one fragment read of k-step kk + 1 and one direct-to-LDS load,
-            // and so on, so the matrix core keeps working while they issue.
+            // SCHED 5's stage rotation and barrier; the loads of tile
+            // kt + NST - 1 (into the stage tile kt - 1 used) are spread over
+            // the first DSPREAD k-steps of tile kt, and inside a k-step each
+            // MFMA is followed by one fragment read of the next k-step and one
+            // load, so the matrix core keeps working while they issue.
             constexpr int HALF = S::BSPLIT;
             constexpr int ND = S::A_DMA + S::B_DMA;
             constexpr int NFR = S::MB + S::NB;
@@ -482,7 +483,8 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
 #pragma unroll
                         for (int j = 0; j < NJ; ++j) {
                             if (j < NFR) fload_one(fs ^ 1, base, kk + 1, j);
-                            if (j < d_hi - d_lo) dma_range_t(dst, k_ld, d_lo + j, d_lo + j + 1, check);
+                            if (j < d_hi - d_lo)
+                                dma_range_t(dst, k_ld, d_lo + j, d_lo + j + 1, check);
                         }
                         mfma_range(fs, 0, NMF);
 #pragma unroll
