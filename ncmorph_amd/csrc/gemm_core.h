@@ -59,8 +59,12 @@ namespace ncm {
 // registers while the previous one feeds the MFMAs.
 // NST: LDS stages of the DMA path; K tiles up to NST - 1 ahead are in flight.
 // F32: fp32 operands (else bf16). KG: K groups (SCHED 7).
+// MF16: (bf16, SCHED 8) v_mfma_f32_16x16x32_bf16 on 16-row fragments
+// instead of v_mfma_f32_32x32x16_bf16; the main loop converts the
+// accumulators to the 32x32x16 layout at its end, so epilogues are the same.
 template <int BM_, int BN_, int BK_, int WGM_, int WGN_, int OCC_, int SCHED_, bool DMA_,
-          int NST_ = 2, bool F32_ = false, int KG_ = 1, int BS_ = -1, int DSP_ = -1>
+          int NST_ = 2, bool F32_ = false, int KG_ = 1, int BS_ = -1, int DSP_ = -1,
+          bool MF16_ = false>
 struct GemmShape {
     static constexpr int BM = BM_, BN = BN_, BK = BK_, WGM = WGM_, WGN = WGN_;
     static constexpr int OCC = OCC_, SCHED = SCHED_, NST = NST_, KG = KG_;
@@ -74,12 +78,17 @@ struct GemmShape {
     static constexpr int NWG = WGM * WGN;  // wavefronts per K group
     static constexpr int WM = BM / WGM, WN = BN / WGN;
     static constexpr int MB = WM / 32, NB = WN / 32;
-    // SCHED 5: MFMAs of the last k-step issued before the K-tile barrier.
-    static constexpr int BSPLIT = BS_ < 0 ? MB * NB / 2 : BS_;
-    // SCHED 8: k-steps over which a tile's direct-to-LDS loads are spread.
-    static constexpr int DSPREAD = DSP_ < 0 ? (BK * ESZ / 32) - 1 : DSP_;
+    static constexpr bool MF16 = MF16_;
+    // Fragments (A, B) and MFMAs of one k-step; a k-step is 16 (32x32x16) or
+    // 32 (16x16x32) elements of K.
+    static constexpr int FM = MF16 ? 2 * MB : MB, FN = MF16 ? 2 * NB : NB;
+    static constexpr int NMFS = FM * FN;
+    // SCHED 5 and 8: MFMAs of the last k-step issued before the K-tile barrier.
+    static constexpr int BSPLIT = BS_ < 0 ? NMFS / 2 : BS_;
     static constexpr int CH = RB / 16;
-    static constexpr int KSTEPS = CH / 2;
+    static constexpr int KSTEPS = MF16 ? CH / 4 : CH / 2;
+    // SCHED 8: k-steps over which a tile's direct-to-LDS loads are spread.
+    static constexpr int DSPREAD = DSP_ < 0 ? KSTEPS - 1 : DSP_;
     static constexpr int RPP = NT / CH;
     static constexpr int A_PASS = BM / RPP;
     static constexpr int B_PASS = BN / RPP;
@@ -103,6 +112,7 @@ struct GemmShape {
     static_assert((KG == 2) == (SCHED == 7), "K groups go with SCHED 7");
     static_assert(SCHED != 7 || (NST % 2 == 0 && NST >= 4), "SCHED 7 stages come in pairs");
     static_assert(DMA || SCHED <= 4, "SCHED 5, 6 and 7 need direct-to-LDS loads");
+    static_assert(!MF16 || (SCHED == 8 && !F32 && CH % 4 == 0), "16x16x32: bf16, SCHED 8");
     static_assert(!DMA || SCHED >= 4, "direct-to-LDS loads need fragment double buffering");
     static_assert(!DMA || (BM % (NW * RPI) == 0 && BN % (NW * RPI) == 0), "DMA loader shape");
     static_assert(NST == 2 || SCHED >= 5, "more than two stages: SCHED 5, 6 or 7 only");
@@ -173,42 +183,62 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
     const __amdgpu_buffer_rsrc_t rsa = make_rsrc(A, a_bytes);
     const __amdgpu_buffer_rsrc_t rsb = make_rsrc(B, b_bytes);
 
-    // Fragment rows are wave_base + lane % 32 with wave_base a multiple of 32,
-    // so their swizzle term is ((lane % 32) >> SWZ_SHIFT) % CH.
-    const int frow = lane & 31;
-    const int khalf = lane >> 5;
+    // Fragment rows are wave_base + lane % FR (FR = 32, or 16 for 16x16x32)
+    // with wave_base a multiple of FR, so their swizzle term is
+    // ((lane % FR) >> SWZ_SHIFT) % CH; a k-step reads CPK chunks of each row,
+    // lane / FR picking the chunk.
+    constexpr int FR = S::MF16 ? 16 : 32;
+    constexpr int CPK = S::MF16 ? 4 : 2;
+    const int frow = lane & (FR - 1);
+    const int khalf = lane / FR;
     const int swz = (frow >> S::SWZ_SHIFT) & (S::CH - 1);
     const uint32_t a_frag0 = (uint32_t)((wm * S::WM + frow) * S::RB);
     const uint32_t b_frag0 = (uint32_t)(S::LDS_A + (wn * S::WN + frow) * S::RB);
 
     constexpr int NFS = S::FDB ? 2 : 1;
-    u32x4_t af[NFS][S::MB], bfr[NFS][S::NB];
+    u32x4_t af[NFS][S::FM], bfr[NFS][S::FN];
     auto fload = [&](int fs, const char* base, int kk) {
-        const uint32_t cofs = (uint32_t)((((kk * 2 + khalf) ^ swz)) * 16);
+        const uint32_t cofs = (uint32_t)((((kk * CPK + khalf) ^ swz)) * 16);
 #pragma unroll
-        for (int mb = 0; mb < S::MB; ++mb)
-            af[fs][mb] = *(const u32x4_t*)(base + a_frag0 + mb * 32 * S::RB + cofs);
+        for (int mb = 0; mb < S::FM; ++mb)
+            af[fs][mb] = *(const u32x4_t*)(base + a_frag0 + mb * FR * S::RB + cofs);
 #pragma unroll
-        for (int nb = 0; nb < S::NB; ++nb)
-            bfr[fs][nb] = *(const u32x4_t*)(base + b_frag0 + nb * 32 * S::RB + cofs);
+        for (int nb = 0; nb < S::FN; ++nb)
+            bfr[fs][nb] = *(const u32x4_t*)(base + b_frag0 + nb * FR * S::RB + cofs);
     };
-    // Fragment j of k-step kk: A block j (j < MB) or B block j - MB.
+    // Fragment j of k-step kk: A block j (j < FM) or B block j - FM.
     auto fload_one = [&](int fs, const char* base, int kk, int j) {
-        const uint32_t cofs = (uint32_t)((((kk * 2 + khalf) ^ swz)) * 16);
-        if (j < S::MB)
-            af[fs][j] = *(const u32x4_t*)(base + a_frag0 + j * 32 * S::RB + cofs);
+        const uint32_t cofs = (uint32_t)((((kk * CPK + khalf) ^ swz)) * 16);
+        if (j < S::FM)
+            af[fs][j] = *(const u32x4_t*)(base + a_frag0 + j * FR * S::RB + cofs);
         else
-            bfr[fs][j - S::MB] =
-                *(const u32x4_t*)(base + b_frag0 + (j - S::MB) * 32 * S::RB + cofs);
+            bfr[fs][j - S::FM] =
+                *(const u32x4_t*)(base + b_frag0 + (j - S::FM) * FR * S::RB + cofs);
     };
-    // MFMAs lo .. hi - 1 of one k-step, in (mb, nb) row-major order.
+    // MFMAs lo .. hi - 1 of one k-step, in (A block, B block) row-major order.
+    // 16x16x32: 16-row blocks (2 mb + sa, 2 nb + sb) accumulate into elements
+    // 4 (2 sa + sb) .. + 3 of the 32x32 block (mb, nb) until the end of the
+    // main loop converts them.
     auto mfma_range = [&](int fs, int lo, int hi) {
 #pragma unroll
-        for (int i = 0; i < S::MB * S::NB; ++i)
-            if (i >= lo && i < hi)
-                mfma_kstep<S>(acc.v[i / S::NB][i % S::NB], af[fs][i / S::NB], bfr[fs][i % S::NB]);
+        for (int i = 0; i < S::NMFS; ++i) {
+            if (i < lo || i >= hi) continue;
+            const int ia = i / S::FN, ib = i % S::FN;
+            if constexpr (S::MF16) {
+                f32x16_t& c = acc.v[ia >> 1][ib >> 1];
+                const int e0 = 4 * (2 * (ia & 1) + (ib & 1));
+                f32x4_t d;
+                d[0] = c[e0]; d[1] = c[e0 + 1]; d[2] = c[e0 + 2]; d[3] = c[e0 + 3];
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                    __builtin_bit_cast(bf16x8_t, af[fs][ia]),
+                    __builtin_bit_cast(bf16x8_t, bfr[fs][ib]), d, 0, 0, 0);
+                c[e0] = d[0]; c[e0 + 1] = d[1]; c[e0 + 2] = d[2]; c[e0 + 3] = d[3];
+            } else {
+                mfma_kstep<S>(acc.v[ia][ib], af[fs][ia], bfr[fs][ib]);
+            }
+        }
     };
-    constexpr int NMF = S::MB * S::NB;
+    constexpr int NMF = S::NMFS;
     // All k-steps of one LDS stage (SCHED 0 and 4).
     auto compute = [&](int stage) {
         const char* base = lds + stage * S::LDS_STAGE;
@@ -456,7 +486,7 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
             // load, so the matrix core keeps working while they issue.
             constexpr int HALF = S::BSPLIT;
             constexpr int ND = S::A_DMA + S::B_DMA;
-            constexpr int NFR = S::MB + S::NB;
+            constexpr int NFR = S::FM + S::FN;
             constexpr int DPK = (ND + S::DSPREAD - 1) / S::DSPREAD;
             static_assert(S::DSPREAD >= 1 && S::DSPREAD < S::KSTEPS, "SCHED 8 load spread");
 #pragma unroll
@@ -517,6 +547,31 @@ __device__ __forceinline__ void gemm_mainloop(const void* A, int64_t lda, uint32
             sched8(std::integral_constant<bool, false>{});
         else
             sched8(Checked{});
+        if constexpr (S::MF16) {
+            // 16x16x32 -> 32x32x16 accumulator layout. In a 32x32 block, the
+            // 16x16 result D_(sa,sb)[4 (l / 16) + j][l % 16] sits in lane l,
+            // element 4 (2 sa + sb) + j; the 32x32x16 layout wants
+            // D[8 (i / 4) + 4 (t / 32) + i % 4][t % 32] in lane t, element i.
+            // For each pair (elements 8 h + j, 8 h + 4 + j), a permlane16 swap
+            // then a permlane32 swap move every value to its lane group, in
+            // place.
+#pragma unroll
+            for (int mb = 0; mb < S::MB; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < S::NB; ++nb)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            f32x16_t& c = acc.v[mb][nb];
+                            auto r = __builtin_amdgcn_permlane16_swap(
+                                __float_as_uint(c[8 * h + j]), __float_as_uint(c[8 * h + 4 + j]),
+                                false, false);
+                            auto q = __builtin_amdgcn_permlane32_swap(r[0], r[1], false, false);
+                            c[8 * h + j] = __uint_as_float(q[0]);
+                            c[8 * h + 4 + j] = __uint_as_float(q[1]);
+                        }
+        }
     } else {
         // Two stages, barrier after each tile.
         dma(0, 0);

@@ -198,12 +198,12 @@ static hipError_t launch_linear_s(const uint16_t* x, const uint16_t* w, const ui
 // 10: 128x128x128 (256-byte rows), 4 waves, DMA, SCHED 5, 2 stages
 // 11, 12, 13: as 0, 1 and 5 with SCHED 5 (all loads of a tile issued
 //     together at its start, fragment reads of a k-step as one group)
-using Lin0 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
+using Lin0 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, -1, true>;
 using Lin1 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
 using Lin2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
 using Lin3 = GemmShape<256, 256, 32, 4, 2, 2, 6, true, 4>;
 using Lin4 = GemmShape<256, 256, 64, 2, 2, 1, 5, true>;
-using Lin5 = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3>;
+using Lin5 = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3, false, 1, -1, -1, true>;
 using Lin6 = GemmShape<256, 256, 64, 4, 2, 2, 4, false>;
 using Lin7 = GemmShape<128, 128, 64, 2, 2, 2, 4, false>;
 using Lin8 = GemmShape<128, 128, 32, 2, 2, 2, 7, true, 8, false, 2>;
@@ -212,7 +212,9 @@ using Lin10 = GemmShape<128, 128, 128, 2, 2, 2, 5, true, 2>;
 using Lin11 = GemmShape<256, 256, 64, 4, 2, 2, 5, true>;
 using Lin12 = GemmShape<128, 128, 64, 2, 2, 2, 5, true, 4>;
 using Lin13 = GemmShape<256, 128, 64, 4, 2, 2, 5, true, 3>;
-constexpr int kLinConfigs = 14;
+using Lin14 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
+using Lin15 = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3>;
+constexpr int kLinConfigs = 16;
 
 // fp32 linear: 128x128x32 (128-byte rows), 4 waves, DMA, SCHED 5, two
 // stages (64 KB: two workgroups per CU). The fp32 MFMA has 1/16 of the bf16
@@ -258,7 +260,9 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
         case 10: return launch_linear_s<Lin10>(x, w, bias, y, M, K, N, out_mode, stream);
         case 11: return launch_linear_s<Lin11>(x, w, bias, y, M, K, N, out_mode, stream);
         case 12: return launch_linear_s<Lin12>(x, w, bias, y, M, K, N, out_mode, stream);
-        default: return launch_linear_s<Lin13>(x, w, bias, y, M, K, N, out_mode, stream);
+        case 13: return launch_linear_s<Lin13>(x, w, bias, y, M, K, N, out_mode, stream);
+        case 14: return launch_linear_s<Lin14>(x, w, bias, y, M, K, N, out_mode, stream);
+        default: return launch_linear_s<Lin15>(x, w, bias, y, M, K, N, out_mode, stream);
     }
 }
 

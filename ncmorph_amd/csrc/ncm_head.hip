@@ -196,7 +196,7 @@ hipError_t launch_tied_head(const uint16_t* z, const uint16_t* cb, const float* 
     // The linear's tiles: 256 x 256 when the levels together fill three
     // quarters of the CUs with them, else 128 x 128 with four LDS stages (at
     // most about one tile per CU) or two (two workgroups per CU).
-    using H0 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
+    using H0 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, -1, true>;
     using H1 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
     using H2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
     const int64_t cus = 256;

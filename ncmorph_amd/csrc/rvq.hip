@@ -749,7 +749,7 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
 // DistBig and DistMid share one candidate layout (256 codes per tile, 4
 // wavefronts along the codes), DistSmall and DistSmall2 another.
 using DistBig = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
-using DistMid = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3>;
+using DistMid = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3, false, 1, -1, -1, true>;
 using DistSmall = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
 using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 2>;
 constexpr int64_t kCus = 256;
