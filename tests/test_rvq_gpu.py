@@ -73,6 +73,10 @@ def test_small_config_golden(ncm, oracle, cuda):
     dict(b=1, t=2048, d=64, v=4096, strides=(2, 1), seed=25),
     # 8192 rows at the finest level, few codes (four code ranges per tile row)
     dict(b=2, t=4096, d=64, v=512, strides=(16, 4, 1), seed=26),
+    # 5000 codes: more code tiles than ranges, so workgroups loop over two
+    # tiles (the last one ragged), on 128 x 128 tiles (1024 rows) and on
+    # 256 x 256 tiles (4096 rows)
+    dict(b=1, t=4096, d=64, v=5000, strides=(4, 1), seed=27),
 ])
 def test_multiscale_matches_oracle(ncm, oracle, cuda, case):
     L = len(case["strides"])
