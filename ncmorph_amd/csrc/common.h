@@ -77,20 +77,28 @@ __device__ __forceinline__ void lds_barrier() {
 // Applied to an MFMA D fragment (lane = column, element = row), it leaves
 // each lane with four consecutive columns of one row.
 __device__ __forceinline__ float dpp_quad_xor1(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0xB1, 0xF, 0xF, true));
 }
 __device__ __forceinline__ float dpp_quad_xor2(float v) {
-    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, false));
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x4E, 0xF, 0xF, true));
 }
+// Written as selects only (no conditional assignments), which compile to
+// v_cndmask and DPP moves without branches.
 __device__ __forceinline__ void quad_transpose4(float (&v)[4], int q) {
     const bool odd = (q & 1) != 0;
-    float r0 = dpp_quad_xor1(odd ? v[0] : v[1]);
-    float r1 = dpp_quad_xor1(odd ? v[2] : v[3]);
-    if (odd) { v[0] = r0; v[2] = r1; } else { v[1] = r0; v[3] = r1; }
+    const float r0 = dpp_quad_xor1(odd ? v[0] : v[1]);
+    const float r1 = dpp_quad_xor1(odd ? v[2] : v[3]);
+    const float a0 = odd ? r0 : v[0];
+    const float a1 = odd ? v[1] : r0;
+    const float a2 = odd ? r1 : v[2];
+    const float a3 = odd ? v[3] : r1;
     const bool hi = (q & 2) != 0;
-    r0 = dpp_quad_xor2(hi ? v[0] : v[2]);
-    r1 = dpp_quad_xor2(hi ? v[1] : v[3]);
-    if (hi) { v[0] = r0; v[1] = r1; } else { v[2] = r0; v[3] = r1; }
+    const float u0 = dpp_quad_xor2(hi ? a0 : a2);
+    const float u1 = dpp_quad_xor2(hi ? a1 : a3);
+    v[0] = hi ? u0 : a0;
+    v[1] = hi ? u1 : a1;
+    v[2] = hi ? a2 : u0;
+    v[3] = hi ? a3 : u1;
 }
 
 // Wavefront butterfly reductions in VALU (no LDS round trip): permlane32 /

@@ -229,3 +229,39 @@ def test_linear_decoder_caller_shapes(ncm, oracle, cuda, m, n, k):
     for r in (0, m - 1):
         _, s = oracle.matmul_bf16_u16_rows(xb[r:r + 1], wb, 0, 1)
         assert np.all(np.abs(y[r] - s[0]) <= ATOL + RTOL * np.abs(s[0]))
+
+
+@pytest.mark.parametrize("m,n,k", [
+    (4096, 8192, 8),      # 256 x 256 tiles, 512 of them (two rounds), one K tile
+    (4096, 8192, 200),    # the same with a partial last K tile
+    (2560, 3584, 64),     # 256 x 128 tiles (280): one K tile, fewer than the stages
+    (2560, 3584, 136),    # 256 x 128 with three K tiles, the last partial
+    (2560, 3584, 1024),
+])
+def test_linear_multi_round_grids(ncm, cuda, m, n, k):
+    """Grids with more tiles than the CUs hold at once, short and partial K:
+    rows from every row tile against the D53 bound; the bf16 modes and the
+    residual-fused form against the fp32 output."""
+    import torch
+    from ncmorph_amd import kernels
+
+    rng = np.random.default_rng(m + n + k)
+    xb = synth.bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    wb = synth.bf16_bits((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+    bb = synth.bf16_bits(rng.standard_normal(n).astype(np.float32))
+    x, w, b = _to_dev(xb, cuda), _to_dev(wb, cuda), _to_dev(bb, cuda)
+    y = kernels.linear_bf16(x, w, bias=b)
+    ybf = kernels.linear_bf16(x, w, bias=b, out_mode="bf16_f32")
+    res = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(cuda)
+    yres = kernels.linear_bf16_residual(x, w, res, bias=b, out_mode="f32")
+    torch.cuda.synchronize()
+    y = y.cpu().numpy()
+    rows = np.arange(0, m, 37)
+    x64 = synth.bf16_to_f32(xb[rows]).astype(np.float64)
+    w64 = synth.bf16_to_f32(wb).astype(np.float64)
+    b64 = synth.bf16_to_f32(bb).astype(np.float64)
+    ref = x64 @ w64.T + b64
+    asum = np.abs(x64) @ np.abs(w64).T + np.abs(b64)
+    assert np.all(np.abs(y[rows] - ref) <= (k + 2) * 2.0**-24 * asum)
+    assert np.array_equal(ybf.cpu().numpy(), synth.bf16_to_f32(synth.bf16_bits(y)))
+    assert np.array_equal(yres.cpu().numpy(), res.cpu().numpy() + y)
