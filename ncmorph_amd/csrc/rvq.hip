@@ -362,7 +362,10 @@ __device__ __forceinline__ void dist_epilogue(const GemmAcc<S>& acc, const DistA
     }
 }
 
-template <class S>
+// ONE: each workgroup has one code tile (ntv == 1), so the per-row state
+// (offsets, top-4 keys) is created after the main loop and holds no registers
+// during it.
+template <class S, bool ONE>
 __global__ __launch_bounds__(S::NT)
 __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void rvq_dist_kernel(DistArgs a) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
@@ -377,40 +380,66 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void rvq_dist_kernel(DistAr
     const int half = lane >> 5;
     const uint32_t imask = (1u << a.cg.ib) - 1u;
 
-    float rowc[S::NB];
+    auto load_rowc = [&](float (&rowc)[S::NB]) {
 #pragma unroll
-    for (int nb = 0; nb < S::NB; ++nb) {
-        const int64_t r = row0 + wn * S::WN + nb * 32 + (lane & 31);
-        rowc[nb] = r < a.n_rows ? a.rowc[r] : 0.0f;
-    }
-    uint32_t top[S::NB][4];
+        for (int nb = 0; nb < S::NB; ++nb) {
+            const int64_t r = row0 + wn * S::WN + nb * 32 + (lane & 31);
+            rowc[nb] = r < a.n_rows ? a.rowc[r] : 0.0f;
+        }
+    };
+    auto init_top = [&](uint32_t (&top)[S::NB][4]) {
 #pragma unroll
-    for (int nb = 0; nb < S::NB; ++nb)
+        for (int nb = 0; nb < S::NB; ++nb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) top[nb][j] = 0xFFFFFFFFu;
+            for (int j = 0; j < 4; ++j) top[nb][j] = 0xFFFFFFFFu;
+    };
+    auto store_top = [&](const uint32_t (&top)[S::NB][4]) {
+        const int chunk = (range * S::WGM + wm) * 2 + half;
+#pragma unroll
+        for (int nb = 0; nb < S::NB; ++nb) {
+            const int64_t r = row0 + wn * S::WN + nb * 32 + (lane & 31);
+            if (r < a.n_rows) {
+                u32x4_t o;
+                o[0] = top[nb][0]; o[1] = top[nb][1]; o[2] = top[nb][2]; o[3] = top[nb][3];
+                *(u32x4_t*)(a.cand + (r * a.cg.nchunk + chunk) * 4) = o;
+            }
+        }
+    };
 
     const uint32_t b_bytes = operand_bytes(a.n_rows, row0, a.d);
-    for (int tile = 0; tile < a.cg.ntv; ++tile) {
-        const int64_t code0 = ((int64_t)range * a.cg.ntv + tile) * S::BM;
-        if (code0 >= a.v) break;
+    if constexpr (ONE) {
+        const int64_t code0 = (int64_t)range * S::BM;
         GemmAcc<S> acc;
         acc.zero();
         gemm_mainloop<S>(a.cb + code0 * a.d, a.d, operand_bytes(a.v, code0, a.d),
                          a.ubuf + row0 * a.d, a.d, b_bytes, a.d, lds, acc);
+        float rowc[S::NB];
+        load_rowc(rowc);
+        uint32_t top[S::NB][4];
+        init_top(top);
         if (code0 + S::BM <= a.v)
-            dist_epilogue<S, true>(acc, a, code0, tile, wm, half, rowc, imask, top);
+            dist_epilogue<S, true>(acc, a, code0, 0, wm, half, rowc, imask, top);
         else
-            dist_epilogue<S, false>(acc, a, code0, tile, wm, half, rowc, imask, top);
-    }
-    const int chunk = (range * S::WGM + wm) * 2 + half;
-#pragma unroll
-    for (int nb = 0; nb < S::NB; ++nb) {
-        const int64_t r = row0 + wn * S::WN + nb * 32 + (lane & 31);
-        if (r < a.n_rows) {
-            u32x4_t o;
-            o[0] = top[nb][0]; o[1] = top[nb][1]; o[2] = top[nb][2]; o[3] = top[nb][3];
-            *(u32x4_t*)(a.cand + (r * a.cg.nchunk + chunk) * 4) = o;
+            dist_epilogue<S, false>(acc, a, code0, 0, wm, half, rowc, imask, top);
+        store_top(top);
+    } else {
+        float rowc[S::NB];
+        load_rowc(rowc);
+        uint32_t top[S::NB][4];
+        init_top(top);
+        for (int tile = 0; tile < a.cg.ntv; ++tile) {
+            const int64_t code0 = ((int64_t)range * a.cg.ntv + tile) * S::BM;
+            if (code0 >= a.v) break;
+            GemmAcc<S> acc;
+            acc.zero();
+            gemm_mainloop<S>(a.cb + code0 * a.d, a.d, operand_bytes(a.v, code0, a.d),
+                             a.ubuf + row0 * a.d, a.d, b_bytes, a.d, lds, acc);
+            if (code0 + S::BM <= a.v)
+                dist_epilogue<S, true>(acc, a, code0, tile, wm, half, rowc, imask, top);
+            else
+                dist_epilogue<S, false>(acc, a, code0, tile, wm, half, rowc, imask, top);
         }
+        store_top(top);
     }
 }
 
@@ -749,6 +778,9 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
 // DistBig and DistMid share one candidate layout (256 codes per tile, 4
 // wavefronts along the codes), DistSmall and DistSmall2 another.
 using DistBig = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, 2>;
+// DistBig on 16x16x32 MFMAs (its fragments take 48 more VGPRs: only with one
+// code tile per workgroup, when no per-row state lives through the main loop).
+using DistBig16 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, -1, true>;
 using DistMid = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3, false, 1, -1, -1, true>;
 using DistSmall = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
 using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 2>;
@@ -835,20 +867,26 @@ static CandGeom cand_geom(int64_t n_rows, int64_t v) {
     }
 }
 
-template <class S>
-static hipError_t launch_dist(const DistArgs& da, hipStream_t st) {
+template <class S, bool ONE>
+static hipError_t launch_dist_t(const DistArgs& da, hipStream_t st) {
+    auto kern = rvq_dist_kernel<S, ONE>;
     static bool attr_set = false;
     if (!attr_set) {
-        hipError_t e = hipFuncSetAttribute((const void*)rvq_dist_kernel<S>,
+        hipError_t e = hipFuncSetAttribute((const void*)kern,
                                            hipFuncAttributeMaxDynamicSharedMemorySize,
                                            S::LDS_BYTES);
         if (e != hipSuccess) return e;
         attr_set = true;
     }
     const int64_t rt = (da.n_rows + S::BN - 1) / S::BN;
-    hipLaunchKernelGGL(rvq_dist_kernel<S>, dim3((unsigned)(rt * da.cg.nranges)), dim3(S::NT),
-                       S::LDS_BYTES, st, da);
+    hipLaunchKernelGGL(kern, dim3((unsigned)(rt * da.cg.nranges)), dim3(S::NT), S::LDS_BYTES,
+                       st, da);
     return hipGetLastError();
+}
+
+template <class S>
+static hipError_t launch_dist(const DistArgs& da, hipStream_t st) {
+    return da.cg.ntv == 1 ? launch_dist_t<S, true>(da, st) : launch_dist_t<S, false>(da, st);
 }
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
@@ -956,7 +994,10 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         da.n_rows = n; da.v = v; da.d = d;
         da.cg = cg;
         switch (dist_kind(n, v)) {
-            case kDistBig: e = launch_dist<DistBig>(da, st); break;
+            case kDistBig:
+                e = da.cg.ntv == 1 ? launch_dist_t<DistBig16, true>(da, st)
+                                   : launch_dist_t<DistBig, false>(da, st);
+                break;
             case kDistMid: e = launch_dist<DistMid>(da, st); break;
             case kDistSmall: e = launch_dist<DistSmall>(da, st); break;
             default: e = launch_dist<DistSmall2>(da, st); break;
