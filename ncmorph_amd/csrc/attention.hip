@@ -297,6 +297,24 @@ void attention_bf16_kernel(
         return __uint_as_float((u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u);
     };
     auto score = [&](float acc) { return rnd(rnd(acc) * scale); };
+    // The scores of a whole tile, two per v_cvt_pk_bf16_f32 (the same bits
+    // as rnd / score for every non-NaN value).
+    auto round_pairs = [](f32x16_t& v) {
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+            const uint32_t p = bf16x2_rne(v[i], v[i + 1]);
+            v[i] = __uint_as_float(p << 16);
+            v[i + 1] = __uint_as_float(p & 0xFFFF0000u);
+        }
+    };
+    auto to_scores = [&](f32x16_t& v) {
+        round_pairs(v);
+        if (!POW2) {
+#pragma unroll
+            for (int i = 0; i < 16; ++i) v[i] = v[i] * scale;
+            round_pairs(v);
+        }
+    };
     // exp(s - m) as exp2(s log2 e - m log2 e): v_exp_f32 on one FMA.
     constexpr float kLog2e = 1.4426950408889634f;
     // The exp2 argument of a raw sum: fma(score, log2 e, -m log2 e). When the
@@ -307,9 +325,9 @@ void attention_bf16_kernel(
     // The one exception, a product below 2^-126, moves the FMA's addend by
     // less than 2^-130 and cannot change exp2 of the sum.
     const float sl = POW2 ? scale * kLog2e : kLog2e;
-    auto expo = [&](float acc, float nm_) {
-        return fmaf(POW2 ? rnd(acc) : score(acc), sl, nm_);
-    };
+    // s: a tile value after to_scores (for POW2 the rounded sum; the scale
+    // sits in sl).
+    auto expo = [&](float s, float nm_) { return fmaf(s, sl, nm_); };
     // Per-element mask inside a block: key offset kr (element i of tile t) is
     // allowed for query offset rq when kr <= rq, kr < rt (keys before T) and
     // kr > rw (inside the window).
@@ -363,6 +381,7 @@ void attention_bf16_kernel(
                     const float nm = -mn * kLog2e;
                     const float alpha =
                         m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(m, kLog2e, nm));
+                    to_scores(acc);
                     float part = 0.0f;
 #pragma unroll
                     for (int i = 0; i < 16; ++i)
@@ -426,22 +445,18 @@ void attention_bf16_kernel(
                         const int k = kr_of(t, i);
                         acc[i] = ok(k) ? acc[i] : -INFINITY;
                     }
-                // p = round_bf16(e / sum): u + 0x7FFF + lsb carries the RNE
-                // result in the high half; v_perm packs two high halves.
-                uint32_t pr[16];
+                // p = round_bf16(e / sum), packed two per register.
+                to_scores(acc);
+                float pf[16];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float e = __builtin_amdgcn_exp2f(expo(acc[i], nm));
-                    const uint32_t u = __float_as_uint(e * inv_l);
-                    pr[i] = u + 0x7FFFu + ((u >> 16) & 1u);
-                }
+                for (int i = 0; i < 16; ++i)
+                    pf[i] = __builtin_amdgcn_exp2f(expo(acc[i], nm)) * inv_l;
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     u32x4_t pa;
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        pa[e] = __builtin_amdgcn_perm(pr[8 * j + 2 * e + 1], pr[8 * j + 2 * e],
-                                                      0x07060302u);
+                        pa[e] = bf16x2_rne(pf[8 * j + 2 * e], pf[8 * j + 2 * e + 1]);
                     const int kofs = (32 * t + 16 * j + 4 * hl) * 2;
 #pragma unroll
                     for (int n = 0; n < NT; ++n) {

@@ -14,6 +14,8 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
@@ -23,6 +25,14 @@ __device__ __forceinline__ uint32_t bf16_bits_rne(float v) {
     uint32_t x = __float_as_uint(v);
     if ((x & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
     return (x + 0x7FFFu + ((x >> 16) & 1u)) >> 16;
+}
+
+// Round-to-nearest-even of two floats to bf16 in one v_cvt_pk_bf16_f32, a
+// in the low half: the bits of bf16_bits_rne for every non-NaN input (a NaN
+// becomes some quiet NaN instead of 0x7FC0).
+__device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
+    const f32x2_t v = {a, b};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // Exponent bits zero -> signed zero (packages/kernels/root.zig:144-148).
