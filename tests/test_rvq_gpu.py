@@ -75,8 +75,14 @@ def test_small_config_golden(ncm, oracle, cuda):
     dict(b=2, t=4096, d=64, v=512, strides=(16, 4, 1), seed=26),
     # 5000 codes: more code tiles than ranges, so workgroups loop over two
     # tiles (the last one ragged), on 128 x 128 tiles (1024 rows) and on
-    # 256 x 256 tiles (4096 rows)
+    # 256 x 128 tiles (4096 rows)
     dict(b=1, t=4096, d=64, v=5000, strides=(4, 1), seed=27),
+    # 256 x 256 tiles (8192 rows) with two code tiles per workgroup
+    # (32x32x16 MFMAs, per-row state kept across the tiles)
+    dict(b=2, t=4096, d=64, v=5000, strides=(1,), seed=28),
+    # 256 x 256 tiles with one code tile per workgroup (16x16x32 MFMAs), the
+    # last code tile ragged (4000 = 15 * 256 + 160)
+    dict(b=2, t=4096, d=64, v=4000, strides=(2, 1), seed=29),
 ])
 def test_multiscale_matches_oracle(ncm, oracle, cuda, case):
     L = len(case["strides"])
