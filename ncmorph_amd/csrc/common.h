@@ -35,6 +35,15 @@ __device__ __forceinline__ uint32_t bf16x2_rne(float a, float b) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
+// bf16_bits_rne of a (low half) and b (high half), bit for bit, NaN -> 0x7FC0
+// included: one v_cvt_pk_bf16_f32 and the NaN rule.
+__device__ __forceinline__ uint32_t bf16x2_bits_rne(float a, float b) {
+    uint32_t p = bf16x2_rne(a, b);
+    p = a != a ? (p & 0xFFFF0000u) | 0x7FC0u : p;
+    p = b != b ? (p & 0x0000FFFFu) | 0x7FC00000u : p;
+    return p;
+}
+
 // Exponent bits zero -> signed zero (packages/kernels/root.zig:144-148).
 __device__ __forceinline__ float flush_subnormal(float v) {
     uint32_t b = __float_as_uint(v);

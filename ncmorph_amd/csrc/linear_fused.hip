@@ -36,10 +36,22 @@ __device__ __forceinline__ uint32_t proj_bits(float acc, float bias) {
     return bf16_bits_rne(flush_subnormal(acc + bias));
 }
 
-__device__ __forceinline__ uint32_t swiglu_bits(uint32_t gb, uint32_t ub) {
-    const float g = __uint_as_float(gb << 16);
-    const float a = rb(g / (1.0f + expf(-g)));
-    return bf16_bits_rne(a * __uint_as_float(ub << 16));
+// round(silu_bf16(gate) * up) of two elements from their accumulators
+// (root.zig:265-270, decoder.zig:210-211): the gate and up projections' bits
+// (as proj_bits), a = round(g / (1 + expf(-g))), round(a * up); the
+// roundings two values per v_cvt_pk_bf16_f32, bit for bit the same as
+// bf16_bits_rne (the unfused SiLU x up kernel's arithmetic).
+__device__ __forceinline__ void swiglu_bits2(float ga0, float ua0, float ga1, float ua1,
+                                             float bg, float bu, uint32_t& o0, uint32_t& o1) {
+    const uint32_t p0 = bf16x2_bits_rne(flush_subnormal(ga0 + bg), flush_subnormal(ua0 + bu));
+    const uint32_t p1 = bf16x2_bits_rne(flush_subnormal(ga1 + bg), flush_subnormal(ua1 + bu));
+    const float g0 = __uint_as_float(p0 << 16), u0 = __uint_as_float(p0 & 0xFFFF0000u);
+    const float g1 = __uint_as_float(p1 << 16), u1 = __uint_as_float(p1 & 0xFFFF0000u);
+    const uint32_t a = bf16x2_bits_rne(g0 / (1.0f + expf(-g0)), g1 / (1.0f + expf(-g1)));
+    const uint32_t r = bf16x2_bits_rne(__uint_as_float(a << 16) * u0,
+                                       __uint_as_float(a & 0xFFFF0000u) * u1);
+    o0 = r & 0xFFFFu;
+    o1 = r >> 16;
 }
 
 }  // namespace
@@ -103,6 +115,29 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_pair_kernel(
 #pragma unroll
             for (int blk = 0; blk < 4; ++blk) {
                 const int64_t m = m0 + wm * S::WM + mb * 32 + 8 * blk + hrow;
+                if (EPI == kEpiSwiGLU) {
+                    // Elementwise first (gate and up of a column sit in the
+                    // same lane and element), then one transpose of the
+                    // results.
+                    float r[4];
+#pragma unroll
+                    for (int j = 0; j < 4; j += 2) {
+                        uint32_t o0, o1;
+                        swiglu_bits2(acc.v[mb][2 * p][4 * blk + j], acc.v[mb][2 * p + 1][4 * blk + j],
+                                     acc.v[mb][2 * p][4 * blk + j + 1],
+                                     acc.v[mb][2 * p + 1][4 * blk + j + 1], ba, bb, o0, o1);
+                        r[j] = __uint_as_float(o0);
+                        r[j + 1] = __uint_as_float(o1);
+                    }
+                    quad_transpose4(r, q);
+                    if (m < M) {
+                        u32x2_t o;
+                        o[0] = __float_as_uint(r[0]) | (__float_as_uint(r[1]) << 16);
+                        o[1] = __float_as_uint(r[2]) | (__float_as_uint(r[3]) << 16);
+                        __builtin_nontemporal_store(o, (u32x2_t*)(y + m * ld + ca));
+                    }
+                    continue;
+                }
                 float va[4], vb[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -117,10 +152,7 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_pair_kernel(
                     ra[j] = __float_as_uint(va[j]);
                     rbits[j] = __float_as_uint(vb[j]);
                 }
-                if (EPI == kEpiSwiGLU) {
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) ra[j] = swiglu_bits(ra[j], rbits[j]);
-                } else if (rotate) {
+                if (rotate) {
                     const int64_t t = (m < M ? m : 0) % pa.seq_len;
                     const f32x4_t cf = *(const f32x4_t*)(pa.cosine + t * 64 + c4);
                     const f32x4_t cs = *(const f32x4_t*)(pa.cosine + t * 64 + 32 + c4);
