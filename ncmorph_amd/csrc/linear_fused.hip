@@ -29,25 +29,24 @@ struct PairArgs {
     int64_t rot_cols;  // columns [0, rot_cols) are rotated
 };
 
-__device__ __forceinline__ float rb(float v) { return __uint_as_float(bf16_bits_rne(v) << 16); }
-
-// The projection's output value of one accumulator: bf16(flush(acc + bias)).
-__device__ __forceinline__ uint32_t proj_bits(float acc, float bias) {
-    return bf16_bits_rne(flush_subnormal(acc + bias));
-}
+// rb(v): v rounded to a bf16 value (RNE, NaN -> 0x7FC0), as an fp32. The
+// projections' output value of one accumulator: bf16(flush(acc + bias)).
+// Both are computed two values at a time with bf16x2_bits_rne below.
 
 // round(silu_bf16(gate) * up) of two elements from their accumulators
 // (root.zig:265-270, decoder.zig:210-211): the gate and up projections' bits
-// (as proj_bits), a = round(g / (1 + expf(-g))), round(a * up); the
+// (bf16(flush(acc + bias))), a = rb(g / (1 + expf(-g))), round(a * up); the
 // roundings two values per v_cvt_pk_bf16_f32, bit for bit the same as
 // bf16_bits_rne (the unfused SiLU x up kernel's arithmetic).
 __device__ __forceinline__ void swiglu_bits2(float ga0, float ua0, float ga1, float ua1,
                                              float bg, float bu, uint32_t& o0, uint32_t& o1) {
-    const uint32_t p0 = bf16x2_bits_rne(flush_subnormal(ga0 + bg), flush_subnormal(ua0 + bu));
-    const uint32_t p1 = bf16x2_bits_rne(flush_subnormal(ga1 + bg), flush_subnormal(ua1 + bu));
+    // Intermediate roundings without the NaN rule: a NaN stays a NaN through
+    // the products and the quotient, and the final rounding maps it to 0x7FC0.
+    const uint32_t p0 = bf16x2_rne(flush_subnormal(ga0 + bg), flush_subnormal(ua0 + bu));
+    const uint32_t p1 = bf16x2_rne(flush_subnormal(ga1 + bg), flush_subnormal(ua1 + bu));
     const float g0 = __uint_as_float(p0 << 16), u0 = __uint_as_float(p0 & 0xFFFF0000u);
     const float g1 = __uint_as_float(p1 << 16), u1 = __uint_as_float(p1 & 0xFFFF0000u);
-    const uint32_t a = bf16x2_bits_rne(g0 / (1.0f + expf(-g0)), g1 / (1.0f + expf(-g1)));
+    const uint32_t a = bf16x2_rne(g0 / (1.0f + expf(-g0)), g1 / (1.0f + expf(-g1)));
     const uint32_t r = bf16x2_bits_rne(__uint_as_float(a << 16) * u0,
                                        __uint_as_float(a & 0xFFFF0000u) * u1);
     o0 = r & 0xFFFFu;
@@ -138,11 +137,16 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_pair_kernel(
                     }
                     continue;
                 }
+                // The two tiles' projection bits, bf16(flush(acc + bias)), one
+                // v_cvt_pk_bf16_f32 per pair.
                 float va[4], vb[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    va[j] = __uint_as_float(proj_bits(acc.v[mb][2 * p][4 * blk + j], ba));
-                    vb[j] = __uint_as_float(proj_bits(acc.v[mb][2 * p + 1][4 * blk + j], bb));
+                    const uint32_t pr =
+                        bf16x2_bits_rne(flush_subnormal(acc.v[mb][2 * p][4 * blk + j] + ba),
+                                        flush_subnormal(acc.v[mb][2 * p + 1][4 * blk + j] + bb));
+                    va[j] = __uint_as_float(pr & 0xFFFFu);
+                    vb[j] = __uint_as_float(pr >> 16);
                 }
                 quad_transpose4(va, q);
                 quad_transpose4(vb, q);
@@ -158,16 +162,38 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_pair_kernel(
                     const f32x4_t cs = *(const f32x4_t*)(pa.cosine + t * 64 + 32 + c4);
                     const f32x4_t sf = *(const f32x4_t*)(pa.sine + t * 64 + c4);
                     const f32x4_t ss = *(const f32x4_t*)(pa.sine + t * 64 + 32 + c4);
+                    // Per column: left = rb(first rb(cos)), right =
+                    // rb(-second rb(sin)), right2 = rb(first rb(sin2)),
+                    // left2 = rb(second rb(cos2)), then round(left + right)
+                    // and round(left2 + right2); each rounding done for two
+                    // columns at once (bf16x2_bits_rne, the bits of rb).
+                    auto lo = [](uint32_t pr) { return __uint_as_float(pr << 16); };
+                    auto hi = [](uint32_t pr) { return __uint_as_float(pr & 0xFFFF0000u); };
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const float first = __uint_as_float(ra[j] << 16);
-                        const float second = __uint_as_float(rbits[j] << 16);
-                        const float left = rb(first * rb(cf[j]));
-                        const float right = rb(-second * rb(sf[j]));
-                        const float right2 = rb(first * rb(ss[j]));
-                        const float left2 = rb(second * rb(cs[j]));
-                        ra[j] = bf16_bits_rne(left + right);
-                        rbits[j] = bf16_bits_rne(left2 + right2);
+                    for (int j = 0; j < 4; j += 2) {
+                        const float f0 = __uint_as_float(ra[j] << 16);
+                        const float f1 = __uint_as_float(ra[j + 1] << 16);
+                        const float s0 = __uint_as_float(rbits[j] << 16);
+                        const float s1 = __uint_as_float(rbits[j + 1] << 16);
+                        // Intermediates without the NaN rule (a NaN stays a
+                        // NaN through products and sums; the final rounding
+                        // maps it to 0x7FC0).
+                        const uint32_t tc = bf16x2_rne(cf[j], cf[j + 1]);
+                        const uint32_t ts = bf16x2_rne(sf[j], sf[j + 1]);
+                        const uint32_t ts2 = bf16x2_rne(ss[j], ss[j + 1]);
+                        const uint32_t tc2 = bf16x2_rne(cs[j], cs[j + 1]);
+                        const uint32_t left = bf16x2_rne(f0 * lo(tc), f1 * hi(tc));
+                        const uint32_t right = bf16x2_rne(-s0 * lo(ts), -s1 * hi(ts));
+                        const uint32_t right2 = bf16x2_rne(f0 * lo(ts2), f1 * hi(ts2));
+                        const uint32_t left2 = bf16x2_rne(s0 * lo(tc2), s1 * hi(tc2));
+                        const uint32_t o1 = bf16x2_bits_rne(lo(left) + lo(right),
+                                                            hi(left) + hi(right));
+                        const uint32_t o2 = bf16x2_bits_rne(lo(left2) + lo(right2),
+                                                            hi(left2) + hi(right2));
+                        ra[j] = o1 & 0xFFFFu;
+                        ra[j + 1] = o1 >> 16;
+                        rbits[j] = o2 & 0xFFFFu;
+                        rbits[j + 1] = o2 >> 16;
                     }
                 }
                 if (m < M) {
