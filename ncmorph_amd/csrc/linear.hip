@@ -88,20 +88,33 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void linear_kernel(const vo
                             for (int j = 0; j < 4; ++j) o[j] = rv[j] + o[j];
                         __builtin_nontemporal_store(o, (f32x4_t*)((float*)y + m * N + ncol));
                     } else {
-                        uint32_t b[4];
+                        // bf16(flush(v)) (then bf16(residual + that)) for two
+                        // columns per v_cvt_pk_bf16_f32; the NaN rule on the
+                        // stored rounding only (a NaN stays a NaN through the
+                        // residual add).
+                        uint32_t pr[2];
 #pragma unroll
-                        for (int j = 0; j < 4; ++j) {
-                            b[j] = bf16_bits_rne(flush_subnormal(v[j]));
-                            if (HAS_RES) b[j] = bf16_bits_rne(rv[j] + __uint_as_float(b[j] << 16));
+                        for (int h = 0; h < 2; ++h) {
+                            const float f0 = flush_subnormal(v[2 * h]);
+                            const float f1 = flush_subnormal(v[2 * h + 1]);
+                            if (HAS_RES) {
+                                const uint32_t t = bf16x2_rne(f0, f1);
+                                pr[h] = bf16x2_bits_rne(rv[2 * h] + __uint_as_float(t << 16),
+                                                        rv[2 * h + 1] +
+                                                            __uint_as_float(t & 0xFFFF0000u));
+                            } else {
+                                pr[h] = bf16x2_bits_rne(f0, f1);
+                            }
                         }
                         if (OUT_MODE == NCM_OUT_BF16_F32) {
                             u32x4_t o;
-                            o[0] = b[0] << 16; o[1] = b[1] << 16; o[2] = b[2] << 16; o[3] = b[3] << 16;
+                            o[0] = pr[0] << 16; o[1] = pr[0] & 0xFFFF0000u;
+                            o[2] = pr[1] << 16; o[3] = pr[1] & 0xFFFF0000u;
                             __builtin_nontemporal_store(o, (u32x4_t*)((float*)y + m * N + ncol));
                         } else {
                             u32x2_t o;
-                            o[0] = b[0] | (b[1] << 16);
-                            o[1] = b[2] | (b[3] << 16);
+                            o[0] = pr[0];
+                            o[1] = pr[1];
                             __builtin_nontemporal_store(o, (u32x2_t*)((uint16_t*)y + m * N + ncol));
                         }
                     }
