@@ -265,3 +265,49 @@ def test_linear_multi_round_grids(ncm, cuda, m, n, k):
     assert np.all(np.abs(y[rows] - ref) <= (k + 2) * 2.0**-24 * asum)
     assert np.array_equal(ybf.cpu().numpy(), synth.bf16_to_f32(synth.bf16_bits(y)))
     assert np.array_equal(yres.cpu().numpy(), res.cpu().numpy() + y)
+
+
+def _flush_f32(a):
+    """Subnormal fp32 values to signed zero (packages/kernels/root.zig:144-148)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).copy()
+    sub = (u & np.uint32(0x7F800000)) == 0
+    u[sub] &= np.uint32(0x80000000)
+    return u.view(np.float32)
+
+
+def test_linear_bf16_modes_special_values(ncm, cuda):
+    """The bf16 output modes on sums that are NaN, infinite, overflowing or
+    subnormal: every output equals the reference's rounding of the fp32 sum
+    (flush, RNE, NaN -> 0x7FC0), with and without the residual add, on a
+    whole-tile shape (the paired-rounding epilogue) and a ragged one."""
+    import torch
+    from ncmorph_amd import kernels
+
+    for m, n, k in [(512, 512, 256), (300, 200, 72)]:
+        rng = np.random.default_rng(m + k)
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        x[1, 5] = np.nan
+        x[2, 7] = np.inf
+        x[3, :] = np.float32(3e38)            # sums overflow to +-inf
+        x[4, :] = np.float32(1.2e-38)         # products and sums subnormal
+        x[5, 0] = -np.inf
+        xb = synth.bf16_bits(x)
+        wb = synth.bf16_bits((rng.standard_normal((n, k)) * 0.05).astype(np.float32))
+        xd, wd = _to_dev(xb, cuda), _to_dev(wb, cuda)
+        y32 = kernels.linear_bf16(xd, wd)
+        ybf = kernels.linear_bf16(xd, wd, out_mode="bf16")
+        yb32 = kernels.linear_bf16(xd, wd, out_mode="bf16_f32")
+        res = rng.standard_normal((m, n)).astype(np.float32)
+        res[6, :3] = [np.nan, np.inf, -np.inf]
+        resd = torch.from_numpy(res).to(cuda)
+        yres = kernels.linear_bf16_residual(xd, wd, resd, out_mode="bf16_f32")
+        torch.cuda.synchronize()
+        y = y32.cpu().numpy()
+        want = synth.bf16_bits(_flush_f32(y))
+        assert np.isnan(y[1]).any() and np.isinf(y[3]).any()
+        assert np.array_equal(ybf.cpu().numpy().view(np.uint16), want)
+        bits = lambda a: np.ascontiguousarray(a, np.float32).view(np.uint32)
+        assert np.array_equal(bits(yb32.cpu().numpy()), bits(synth.bf16_to_f32(want)))
+        with np.errstate(invalid="ignore"):
+            want_res = synth.bf16_bits(res + synth.bf16_to_f32(want))
+        assert np.array_equal(bits(yres.cpu().numpy()), bits(synth.bf16_to_f32(want_res)))
