@@ -110,12 +110,18 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
         for (int64_t i = 4 * lane; i < n; i += 256) {
             const f32x4_t v = *(const f32x4_t*)(xr + i);
             const f32x4_t wv = *(const f32x4_t*)(weight + i);
+            // The same roundings two elements per v_cvt_pk_bf16_f32; the NaN
+            // rule on the stored one (a NaN stays a NaN through the product).
             uint32_t bits[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float normalized = __uint_as_float(bf16_bits_rne(v[e] * inv) << 16);
-                bits[e] = bf16_bits_rne(normalized *
-                                        __uint_as_float(bf16_bits_rne(wv[e]) << 16));
+            for (int e = 0; e < 4; e += 2) {
+                const uint32_t nb = bf16x2_rne(v[e] * inv, v[e + 1] * inv);
+                const uint32_t wb = bf16x2_rne(wv[e], wv[e + 1]);
+                const uint32_t r = bf16x2_bits_rne(
+                    __uint_as_float(nb << 16) * __uint_as_float(wb << 16),
+                    __uint_as_float(nb & 0xFFFF0000u) * __uint_as_float(wb & 0xFFFF0000u));
+                bits[e] = r & 0xFFFFu;
+                bits[e + 1] = r >> 16;
             }
             if (!yvec) {
 #pragma unroll
@@ -161,8 +167,17 @@ __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__
         const f32x4_t g = *(const f32x4_t*)(gate + i0);
         f32x4_t u = {1.0f, 1.0f, 1.0f, 1.0f};
         if (up) u = *(const f32x4_t*)(up + i0);
+        // act() two elements at a time: the roundings per v_cvt_pk_bf16_f32,
+        // the NaN rule on the stored one (a NaN stays a NaN through a * u).
 #pragma unroll
-        for (int e = 0; e < 4; ++e) b[e] = act(g[e], u[e]);
+        for (int e = 0; e < 4; e += 2) {
+            const uint32_t a = bf16x2_rne(g[e] / (1.0f + expf(-g[e])),
+                                          g[e + 1] / (1.0f + expf(-g[e + 1])));
+            const uint32_t r = bf16x2_bits_rne(__uint_as_float(a << 16) * u[e],
+                                               __uint_as_float(a & 0xFFFF0000u) * u[e + 1]);
+            b[e] = r & 0xFFFFu;
+            b[e + 1] = r >> 16;
+        }
         if (OUT_MODE == NCM_OUT_BF16 && ((uintptr_t)y & 7) == 0) {
             u32x2_t o;
             o[0] = b[0] | (b[1] << 16);
