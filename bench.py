@@ -35,11 +35,11 @@ LINEAR_M = 2048
 LINEAR_NK = [(2048, 2048), (8192, 2048), (2048, 8192)]
 # HBM-side bytes measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (each in its
 # own run, fetch scaled by the factor a plain copy shows): the linear figure is
-# the mean over the step's three launches (453.5 MB per step), the RVQ figure
+# the mean over the step's three launches (466.0 MB per step), the RVQ figure
 # one whole encode; the summaries and commands are in
 # profiles/linear_bf16_1b_shapes.md and profiles/rvq_encode_b16_t2048_d2048_l8_v4096.md.
-LINEAR_TRAFFIC_BYTES_PER_LAUNCH = 151.2e6
-RVQ_TRAFFIC_BYTES_PER_ENCODE = 6607e6
+LINEAR_TRAFFIC_BYTES_PER_LAUNCH = 155.3e6
+RVQ_TRAFFIC_BYTES_PER_ENCODE = 6663e6
 
 
 def _events(torch):
