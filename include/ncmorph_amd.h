@@ -37,8 +37,10 @@ enum {
     NCM_E_NOMEM = -5,     /* device or host allocation failed */
     NCM_E_DEVICE = -6,    /* no usable gfx950 device */
     NCM_E_ARG = -7,       /* an argument value is out of range */
-    NCM_E_FORMAT = -8     /* malformed file or header; ncm_last_error() names
+    NCM_E_FORMAT = -8,    /* malformed file or header; ncm_last_error() names
                              the reference's error (e.g. "InvalidOffsets") */
+    NCM_E_SCRATCH = -9    /* the call needs more than the fixed scratch of an
+                             allocation-free entry point holds */
 };
 
 /* Linear output modes. */
@@ -362,6 +364,21 @@ int ncm_rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t
                    int64_t levels, const int32_t* strides, const uint16_t* codebooks,
                    const float* csq, int64_t v, int32_t* codes, float* recon, float* gap,
                    const int32_t* force_codes, int64_t* n_flagged);
+
+/* Allocation-free variant of ncm_rvq_encode. No counterpart in the
+ * reference: it exists for callers that cannot allocate device memory (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, results and stream ordering as ncm_rvq_encode without
+ * n_flagged. Its workspace is a fixed device array of NCM_RVQ_SCRATCH_BYTES
+ * per GPU, held until the process ends; a shape that needs more returns
+ * NCM_E_SCRATCH (ncm_last_error() gives both sizes) before any device work.
+ * It calls no hipMalloc / hipFree. Calls on one GPU share that array: calls
+ * that overlap on one GPU (other streams or host threads) race. */
+#define NCM_RVQ_SCRATCH_BYTES (64u << 20)
+int ncm_rvq_encode_noalloc(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d,
+                           int64_t levels, const int32_t* strides, const uint16_t* codebooks,
+                           const float* csq, int64_t v, int32_t* codes, float* recon,
+                           float* gap, const int32_t* force_codes);
 
 /* recon[b, t, :] = sum over levels (in order) of codebooks[l][codes_l]. */
 int ncm_rvq_decode(ncm_ctx_t* ctx, const int32_t* codes, int64_t b, int64_t t, int64_t d,

@@ -21,6 +21,8 @@ NCM_E_NOMEM = -5
 NCM_E_DEVICE = -6
 NCM_E_ARG = -7
 NCM_E_FORMAT = -8
+NCM_E_SCRATCH = -9
+NCM_RVQ_SCRATCH_BYTES = 64 << 20
 
 NCM_OUT_F32 = 0
 NCM_OUT_BF16_F32 = 1
@@ -62,6 +64,8 @@ SIGNATURES = [
     ("ncm_decoder_forward_dev", i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]),
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
     ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
+    ("ncm_rvq_encode_noalloc", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp,
+                                     vp]),
     ("ncm_rvq_decode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, i64, vp]),
     ("ncm_st_parse", i32, [vp, sz, C.c_uint64, C.POINTER(vp)]),
     ("ncm_st_open", i32, [C.c_char_p, C.POINTER(vp)]),
@@ -95,7 +99,8 @@ class NcmError(RuntimeError):
             detail = _lib.ncm_last_error().decode()
         msg = f"{where}: {text} ({status})"
         self.detail = detail if status == NCM_E_FORMAT else ""
-        if detail and status in (NCM_E_HIP, NCM_E_NOMEM, NCM_E_DEVICE, NCM_E_FORMAT):
+        if detail and status in (NCM_E_HIP, NCM_E_NOMEM, NCM_E_DEVICE, NCM_E_FORMAT,
+                                 NCM_E_SCRATCH):
             msg += f" [{detail}]"
         super().__init__(msg)
 

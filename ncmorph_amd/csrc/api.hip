@@ -79,6 +79,8 @@ int ncm_ctx_workspace(ncm_ctx_t* ctx, size_t bytes, void** out) {
 
 hipStream_t ncm_ctx_stream(ncm_ctx_t* ctx) { return ctx->stream; }
 
+int ncm_ctx_device(ncm_ctx_t* ctx) { return ctx->device; }
+
 void ncm_set_error_detail(const std::string& what) { g_last_error = what; }
 
 int ncm_upload_host_bytes(ncm_ctx_t* ctx, const void* src, void* dst, size_t n) {
@@ -147,6 +149,7 @@ const char* ncm_status_string(int status) {
         case NCM_E_DEVICE: return "no usable gfx950 device";
         case NCM_E_ARG: return "argument out of range";
         case NCM_E_FORMAT: return "malformed file or header";
+        case NCM_E_SCRATCH: return "shape exceeds the fixed scratch buffer";
         default: return "unknown status";
     }
 }
@@ -175,6 +178,13 @@ int ncm_init(int device, ncm_ctx_t** out) {
         return fail_hip(e, "ncm_init");
     }
     ctx->stream = ctx->own_stream;
+    // The allocation-free entry points need this device's scratch address.
+    const int rc = ncm::noalloc_setup(device);
+    if (rc) {
+        (void)hipStreamDestroy(ctx->own_stream);
+        delete ctx;
+        return rc;
+    }
     *out = ctx;
     return NCM_OK;
 }

@@ -8,8 +8,13 @@
 
 int ncm_ctx_workspace(ncm_ctx_t* ctx, size_t bytes, void** out);
 hipStream_t ncm_ctx_stream(ncm_ctx_t* ctx);
+int ncm_ctx_device(ncm_ctx_t* ctx);
 
 namespace ncm {
+
+// Looks up this device's address of the allocation-free encode's scratch
+// array (once per device; the device must be current).
+int noalloc_setup(int device);
 
 constexpr int kMaxLevels = 32;
 constexpr int kMaxPyr = 24;  // pyramid strides 2^1 .. 2^23
@@ -41,5 +46,14 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
                const int32_t* strides, const uint16_t* codebooks, const float* csq, int64_t v,
                int32_t* codes, float* recon, float* gap, const int32_t* force_codes,
                int64_t* n_flagged);
+// Device bytes of the workspace one encode of this shape uses.
+int rvq_workspace_bytes(int64_t b, int64_t t, int64_t d, int64_t levels, const int32_t* strides,
+                        int64_t v, size_t* bytes);
+// The encode on a caller-provided workspace (256-byte aligned, at least
+// rvq_workspace_bytes long): allocates nothing.
+int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int64_t b,
+                  int64_t t, int64_t d, int64_t levels, const int32_t* strides,
+                  const uint16_t* codebooks, const float* csq, int64_t v, int32_t* codes,
+                  float* recon, float* gap, const int32_t* force_codes, int64_t* n_flagged);
 
 }  // namespace ncm

@@ -891,20 +891,22 @@ static hipError_t launch_dist(const DistArgs& da, hipStream_t st) {
 
 static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
-int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
-               const int32_t* strides, const uint16_t* codebooks, const float* csq, int64_t v,
-               int32_t* codes, float* recon, float* gap, const int32_t* force_codes,
-               int64_t* n_flagged) {
-    hipStream_t st = ncm_ctx_stream(ctx);
-    RvqGeom g{};
+// Workspace layout of one encode (byte offsets from a 256-byte aligned base).
+struct RvqLayout {
+    size_t pyr, u, d0, d1, rc0, rc1, cand, cmax, fc, total;
+};
+
+// Fills the geometry and the workspace layout; NCM_E_SHAPE if the strides
+// need more pyramid levels than the geometry holds.
+static int rvq_layout(int64_t b, int64_t t, int64_t d, int64_t levels, const int32_t* strides,
+                      int64_t v, RvqGeom& g, RvqLayout& lay) {
+    g = RvqGeom{};
     g.b = b; g.t = t; g.d = d; g.v = v;
     g.L = make_level_table(t, levels, strides);
     const int64_t smax = strides[0];
     int jmax = 0;
     while ((int64_t(1) << jmax) < smax) ++jmax;
     if (jmax >= kMaxPyr) return NCM_E_SHAPE;
-
-    // Workspace layout.
     size_t off = 0;
     auto carve = [&](size_t bytes) { size_t o = off; off = align256(off + bytes); return o; };
     int64_t pyr_floats = 0;
@@ -918,29 +920,66 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
         max_rows = std::max(max_rows, n);
         max_cand = std::max(max_cand, n * (int64_t)cand_geom(n, v).nchunk * 4);
     }
-    const size_t o_pyr = carve((size_t)pyr_floats * 4);
-    const size_t o_u = carve((size_t)max_rows * d * 2);
+    lay.pyr = carve((size_t)pyr_floats * 4);
+    lay.u = carve((size_t)max_rows * d * 2);
     // Level l (l + 1 < levels) writes D_{l+1} to dbuf[(l + 1) & 1]: dbuf[1]
     // from level 0 on (two or more levels), dbuf[0] from level 1 on.
-    const size_t o_d0 = carve(levels > 2 ? (size_t)max_rows * d * 4 : 0);
-    const size_t o_d1 = carve(levels > 1 ? (size_t)max_rows * d * 4 : 0);
-    const size_t o_rc0 = carve((size_t)max_rows * 4);
-    const size_t o_rc1 = carve((size_t)max_rows * 4);
-    const size_t o_cand = carve((size_t)max_cand * 4);
-    const size_t o_cmax = carve((size_t)levels * 4);
-    const size_t o_fc = carve((size_t)levels * 4);
-    void* ws = nullptr;
-    int rc = ncm_ctx_workspace(ctx, off, &ws);
+    lay.d0 = carve(levels > 2 ? (size_t)max_rows * d * 4 : 0);
+    lay.d1 = carve(levels > 1 ? (size_t)max_rows * d * 4 : 0);
+    lay.rc0 = carve((size_t)max_rows * 4);
+    lay.rc1 = carve((size_t)max_rows * 4);
+    lay.cand = carve((size_t)max_cand * 4);
+    lay.cmax = carve((size_t)levels * 4);
+    lay.fc = carve((size_t)levels * 4);
+    lay.total = off;
+    return NCM_OK;
+}
+
+int rvq_workspace_bytes(int64_t b, int64_t t, int64_t d, int64_t levels, const int32_t* strides,
+                        int64_t v, size_t* bytes) {
+    RvqGeom g;
+    RvqLayout lay;
+    const int rc = rvq_layout(b, t, d, levels, strides, v, g, lay);
     if (rc) return rc;
+    *bytes = lay.total;
+    return NCM_OK;
+}
+
+int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
+               const int32_t* strides, const uint16_t* codebooks, const float* csq, int64_t v,
+               int32_t* codes, float* recon, float* gap, const int32_t* force_codes,
+               int64_t* n_flagged) {
+    size_t bytes = 0;
+    int rc = rvq_workspace_bytes(b, t, d, levels, strides, v, &bytes);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, bytes, &ws);
+    if (rc) return rc;
+    return rvq_encode_ws(ncm_ctx_stream(ctx), ws, bytes, x, b, t, d, levels, strides, codebooks,
+                         csq, v, codes, recon, gap, force_codes, n_flagged);
+}
+
+int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int64_t b,
+                  int64_t t, int64_t d, int64_t levels, const int32_t* strides,
+                  const uint16_t* codebooks, const float* csq, int64_t v, int32_t* codes,
+                  float* recon, float* gap, const int32_t* force_codes, int64_t* n_flagged) {
+    RvqGeom g;
+    RvqLayout lay;
+    int rc = rvq_layout(b, t, d, levels, strides, v, g, lay);
+    if (rc) return rc;
+    if (ws_bytes < lay.total || ((uintptr_t)ws & 255)) return NCM_E_ARG;
+    const int64_t smax = strides[0];
+    int jmax = 0;
+    while ((int64_t(1) << jmax) < smax) ++jmax;
     char* W = (char*)ws;
-    float* pyr = (float*)(W + o_pyr);
-    uint16_t* ubuf = (uint16_t*)(W + o_u);
-    float* rowc[2] = {(float*)(W + o_rc0), (float*)(W + o_rc1)};
-    uint32_t* cand = (uint32_t*)(W + o_cand);
-    float* cmax = (float*)(W + o_cmax);
-    int32_t* fcount = (int32_t*)(W + o_fc);
+    float* pyr = (float*)(W + lay.pyr);
+    uint16_t* ubuf = (uint16_t*)(W + lay.u);
+    float* rowc[2] = {(float*)(W + lay.rc0), (float*)(W + lay.rc1)};
+    uint32_t* cand = (uint32_t*)(W + lay.cand);
+    float* cmax = (float*)(W + lay.cmax);
+    int32_t* fcount = (int32_t*)(W + lay.fc);
     // D_{l+1} (coarse reconstruction) is written by level l into dbuf[(l+1)&1].
-    float* dbuf[2] = {(float*)(W + o_d0), (float*)(W + o_d1)};
+    float* dbuf[2] = {(float*)(W + lay.d0), (float*)(W + lay.d1)};
 
     hipLaunchKernelGGL(rvq_setup_kernel, dim3((unsigned)levels), dim3(kSetupThreads), 0, st, csq,
                        v, cmax, fcount);

@@ -1,0 +1,110 @@
+"""The allocation-free RVQ encode (ncm_rvq_encode_noalloc) against the
+allocating one (ncm_rvq_encode), through the C ABI: identical codes,
+reconstruction and gaps on two calls in a row, the second on a smaller
+input, and a clear error for a shape beyond the fixed scratch."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _p(t):
+    return None if t is None else C.c_void_p(t.data_ptr())
+
+
+def _encode(lib, name, ctx, xd, cbd, csq, strides, force=None):
+    import torch
+
+    b, t, d = xd.shape
+    levels, v, _ = cbd.shape
+    total = sum(t // s for s in strides)
+    codes = torch.full((b, total), -7, dtype=torch.int32, device=xd.device)
+    recon = torch.full((b, t, d), float("nan"), dtype=torch.float32, device=xd.device)
+    gap = torch.full((b, total), -1.0, dtype=torch.float32, device=xd.device)
+    s = np.ascontiguousarray(strides, dtype=np.int32)
+    args = [ctx.handle, _p(xd), b, t, d, levels, C.c_void_p(s.ctypes.data), _p(cbd), _p(csq), v,
+            _p(codes), _p(recon), _p(gap), _p(force)]
+    if name == "ncm_rvq_encode":
+        args.append(None)
+    rc = getattr(lib, name)(*args)
+    torch.cuda.synchronize()
+    return rc, codes.cpu().numpy(), recon.cpu().numpy(), gap.cpu().numpy()
+
+
+def _inputs(torch, dev, seed, b, t, d, levels, v):
+    from ncmorph_amd import synth, vq
+
+    x, cb = synth.rvq_inputs(seed, b, t, d, levels, v)
+    xd = torch.from_numpy(x).to(dev)
+    cbd = torch.from_numpy(cb.view(np.int16)).to(dev).view(torch.bfloat16)
+    return x, cb, xd, cbd, vq.prepare(cbd)
+
+
+@pytest.mark.parametrize("first,second", [
+    # (seed, b, t, d, strides, v)
+    ((3, 2, 256, 512, (16, 4, 2, 1), 1000), (4, 1, 64, 256, (8, 1), 300)),
+    ((0, 1, 128, 256, (1, 1, 1, 1), 512), (5, 1, 32, 128, (2, 1), 64)),
+])
+def test_noalloc_matches_allocating_encode(cuda, ncm, oracle, first, second):
+    import torch
+    from ncmorph_amd import _lib
+    from ncmorph_amd.context import default_context
+
+    lib = _lib.lib()
+    ctx = default_context(0)
+    ctx.bind_stream()
+    for case in (first, second):
+        seed, b, t, d, strides, v = case
+        print(f"noalloc case seed={seed} b={b} t={t} d={d} strides={strides} v={v}", flush=True)
+        x, cb, xd, cbd, csq = _inputs(torch, cuda, seed, b, t, d, len(strides), v)
+        rc0, c0, r0, g0 = _encode(lib, "ncm_rvq_encode", ctx, xd, cbd, csq, strides)
+        rc1, c1, r1, g1 = _encode(lib, "ncm_rvq_encode_noalloc", ctx, xd, cbd, csq, strides)
+        assert rc0 == 0 and rc1 == 0, (rc0, rc1)
+        assert np.array_equal(c0, c1)
+        assert np.array_equal(r0.view(np.uint32), r1.view(np.uint32))
+        assert np.array_equal(g0.view(np.uint32), g1.view(np.uint32))
+        ref = oracle.rvq_encode(x, cb, strides)
+        assert np.array_equal(c1, ref["codes"])
+        assert np.array_equal(r1, ref["recon"])
+
+
+def test_noalloc_teacher_forcing_matches(cuda, ncm):
+    import torch
+    from ncmorph_amd import _lib
+    from ncmorph_amd.context import default_context
+
+    lib = _lib.lib()
+    ctx = default_context(0)
+    ctx.bind_stream()
+    strides = (8, 2, 1)
+    x, cb, xd, cbd, csq = _inputs(torch, cuda, 9, 2, 64, 256, 3, 200)
+    total = sum(64 // s for s in strides)
+    force = torch.from_numpy(
+        np.random.default_rng(2).integers(0, 200, (2, total)).astype(np.int32)).to(cuda)
+    rc0, c0, r0, g0 = _encode(lib, "ncm_rvq_encode", ctx, xd, cbd, csq, strides, force)
+    rc1, c1, r1, g1 = _encode(lib, "ncm_rvq_encode_noalloc", ctx, xd, cbd, csq, strides, force)
+    assert rc0 == 0 and rc1 == 0
+    assert np.array_equal(c0, c1)
+    assert np.array_equal(r0.view(np.uint32), r1.view(np.uint32))
+
+
+def test_noalloc_rejects_shape_beyond_scratch(cuda, ncm):
+    import torch
+    from ncmorph_amd import _lib
+    from ncmorph_amd.context import default_context
+
+    lib = _lib.lib()
+    ctx = default_context(0)
+    ctx.bind_stream()
+    # 64 x 4096 positions of width 1024 need far more than the 64 MiB scratch;
+    # the call must fail before touching any pointer, so tiny buffers suffice.
+    b, t, d, v = 64, 4096, 1024, 16
+    strides = np.ascontiguousarray([1], dtype=np.int32)
+    tiny = torch.zeros(64, dtype=torch.float32, device=cuda)
+    rc = lib.ncm_rvq_encode_noalloc(ctx.handle, _p(tiny), b, t, d, 1,
+                                    C.c_void_p(strides.ctypes.data), _p(tiny), _p(tiny), v,
+                                    _p(tiny), None, None, None)
+    assert rc == _lib.NCM_E_SCRATCH
+    assert b"scratch" in lib.ncm_last_error()
