@@ -86,22 +86,31 @@ SIGNATURES = [
 
 _lib = None
 
+# Status texts for errors raised before the library is loaded.
+_STATUS_TEXT = {NCM_E_NULL: "null pointer argument", NCM_E_SHAPE: "invalid or unsupported shape",
+                NCM_E_ARG: "argument out of range"}
+
 
 class NcmError(RuntimeError):
     """A nonzero status from the C ABI."""
 
-    def __init__(self, status: int, where: str):
+    def __init__(self, status: int, where: str, detail: str | None = None):
+        """detail: the reason, for an error raised by a wrapper's own
+        argument checks (the library's last-error text otherwise)."""
         self.status = status
-        text = "library not loaded"
-        detail = ""
+        text = _STATUS_TEXT.get(status, "unknown status")
+        lib_detail = ""
         if _lib is not None:
             text = _lib.ncm_status_string(status).decode()
-            detail = _lib.ncm_last_error().decode()
+            if detail is None:
+                lib_detail = _lib.ncm_last_error().decode()
         msg = f"{where}: {text} ({status})"
-        self.detail = detail if status == NCM_E_FORMAT else ""
-        if detail and status in (NCM_E_HIP, NCM_E_NOMEM, NCM_E_DEVICE, NCM_E_FORMAT,
-                                 NCM_E_SCRATCH):
-            msg += f" [{detail}]"
+        self.detail = lib_detail if status == NCM_E_FORMAT else (detail or "")
+        if detail:
+            msg += f": {detail}"
+        elif lib_detail and status in (NCM_E_HIP, NCM_E_NOMEM, NCM_E_DEVICE, NCM_E_FORMAT,
+                                       NCM_E_SCRATCH):
+            msg += f" [{lib_detail}]"
         super().__init__(msg)
 
 

@@ -17,6 +17,7 @@ from dataclasses import dataclass, field
 
 import numpy as np
 
+from . import _check as _ck
 from ._lib import check, lib
 from .context import default_context
 
@@ -189,13 +190,19 @@ def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine,
         raise ValueError("token_ids must be [batch, seq]")
     batch, seq = ids.shape
     dev = weights.embed.device
+    W = "decoder_forward"
+    a = _ck.Args(W)
+    a.dev(cosine, "cosine", _ck.F32, (seq, spec.head_dim))
+    a.dev(sine, "sine", _ck.F32, (seq, spec.head_dim))
     if logits is None:
         logits = torch.empty((batch * seq, spec.vocab), dtype=torch.float32, device=dev)
+    a.dev(logits, "logits", _ck.F32, (batch * seq, spec.vocab))
     shape = _Shape(spec.hidden, spec.intermediate, spec.vocab, spec.q_heads, spec.kv_heads,
                    spec.head_dim, spec.layers, spec.window, spec.rms_eps)
     arr = (_Layer * max(1, spec.layers))()
     for i, layer in enumerate(weights.layers):
         arr[i] = _Layer(*[_ptr(layer.get(n)) for n in _LAYER_FIELDS])
+    a.done()
     ctx = ctx or default_context(dev.index or 0)
     ctx.bind_stream()
     check(lib().ncm_decoder_forward_dev(ctx.handle, C.byref(shape), arr, _ptr(weights.embed),

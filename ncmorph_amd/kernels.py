@@ -16,6 +16,7 @@ import ctypes as C
 
 import numpy as np
 
+from . import _check as _ck
 from ._lib import NCM_OUT_BF16, NCM_OUT_BF16_F32, NCM_OUT_F32, NcmError, check, lib
 from .context import default_context
 
@@ -92,32 +93,54 @@ def round_bf16(value):
 
 
 # ------------------------------------------------------------ device path
-def _dev_ptr(t, name):
-    if t is None:
-        return None
-    if not t.is_cuda or not t.is_contiguous():
-        raise ValueError(f"{name} must be a contiguous GPU tensor")
-    return C.c_void_p(t.data_ptr())
+# Every tensor argument, caller-supplied outputs included, is checked for
+# dtype, exact shape and device before the call (ncmorph_amd._check): the C
+# ABI cannot see allocation sizes.
+def _ctx_for(t, ctx):
+    ctx = ctx or default_context(t.device.index or 0)
+    ctx.bind_stream()
+    return ctx
+
+
+def _out_dtypes(mode):
+    return _ck.BF16 if mode == NCM_OUT_BF16 else _ck.F32
+
+
+def _new_out(torch, mode, shape, device, bf16_dtype=None):
+    """A new output: float32, or for the bf16 mode bf16_dtype (default
+    torch.bfloat16)."""
+    dt = (bf16_dtype or torch.bfloat16) if mode == NCM_OUT_BF16 else torch.float32
+    return torch.empty(shape, dtype=dt, device=device)
+
+
+def _mode(out_mode, where):
+    if out_mode not in _OUT_MODES:
+        raise NcmError(-7, where, f"out_mode must be one of {sorted(_OUT_MODES)}")
+    return _OUT_MODES[out_mode]
 
 
 def linear_bf16(x, w, bias=None, out=None, out_mode: str = "f32", ctx=None):
     """y = x @ w.T with bf16 operands (torch.bfloat16 tensors [m, k] and
-    [n, k]), fp32 accumulation, on torch's current stream."""
+    [n, k]), optional bf16 bias [n], fp32 accumulation, on torch's current
+    stream; out [m, n] float32 ("f32", "bf16_f32") or 16-bit bf16 patterns
+    ("bf16": int16 when allocated here; a bfloat16 out is accepted too)."""
     import torch
 
-    m, k = x.shape
-    n, k2 = w.shape
-    if k != k2:
-        raise NcmError(-2, "linear_bf16")
-    mode = _OUT_MODES[out_mode]
+    W = "linear_bf16"
+    a = _ck.Args(W)
+    m, k = _ck.dims(x, "x", W, 2)
+    n, _ = _ck.dims(w, "w", W, 2)
+    mode = _mode(out_mode, W)
+    dv = x.device
+    px = a.dev(x, "x", _ck.BF16, (m, k))
+    pw = a.dev(w, "w", _ck.BF16, (n, k))
+    pb = a.dev(bias, "bias", _ck.BF16, (n,), optional=True)
     if out is None:
-        dt = torch.int16 if mode == NCM_OUT_BF16 else torch.float32
-        out = torch.empty((m, n), dtype=dt, device=x.device)
-    ctx = ctx or default_context(x.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_linear_bf16(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
-                                _dev_ptr(bias, "bias"), _dev_ptr(out, "out"), m, k, n, mode),
-          "linear_bf16")
+        out = _new_out(torch, mode, (m, n), dv, torch.int16)
+    po = a.dev(out, "out", _out_dtypes(mode), (m, n))
+    a.done()
+    ctx = _ctx_for(x, ctx)
+    check(lib().ncm_linear_bf16(ctx.handle, px, pw, pb, po, m, k, n, mode), W)
     return out
 
 
@@ -128,40 +151,48 @@ def linear_bf16_residual(x, w, residual, bias=None, out=None, out_mode: str = "b
     [m, n]; out may be residual itself for the "f32" and "bf16_f32" modes."""
     import torch
 
-    m, k = x.shape
-    n, k2 = w.shape
-    if k != k2 or tuple(residual.shape) != (m, n) or residual.dtype != torch.float32:
-        raise NcmError(-2, "linear_bf16_residual")
-    mode = _OUT_MODES[out_mode]
+    W = "linear_bf16_residual"
+    a = _ck.Args(W)
+    m, k = _ck.dims(x, "x", W, 2)
+    n, _ = _ck.dims(w, "w", W, 2)
+    mode = _mode(out_mode, W)
+    dv = x.device
+    px = a.dev(x, "x", _ck.BF16, (m, k))
+    pw = a.dev(w, "w", _ck.BF16, (n, k))
+    pr = a.dev(residual, "residual", _ck.F32, (m, n))
+    pb = a.dev(bias, "bias", _ck.BF16, (n,), optional=True)
     if out is None:
-        dt = torch.int16 if mode == NCM_OUT_BF16 else torch.float32
-        out = torch.empty((m, n), dtype=dt, device=x.device)
-    ctx = ctx or default_context(x.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_linear_bf16_residual(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
-                                         _dev_ptr(bias, "bias"), _dev_ptr(residual, "residual"),
-                                         _dev_ptr(out, "out"), m, k, n, mode),
-          "linear_bf16_residual")
+        out = _new_out(torch, mode, (m, n), dv, torch.int16)
+    po = a.dev(out, "out", _out_dtypes(mode), (m, n))
+    a.done()
+    ctx = _ctx_for(x, ctx)
+    check(lib().ncm_linear_bf16_residual(ctx.handle, px, pw, pb, pr, po, m, k, n, mode), W)
     return out
 
 
 def linear_bf16_swiglu(x, w, bias=None, out=None, ctx=None):
     """round(silu_bf16(gate) * up) of the gate/up projection in one pass: w
     torch.bfloat16 [2 I, k] with gate and up rows interleaved in groups of
-    32 (see interleave_gate_up); returns torch.bfloat16 [m, I]."""
+    32 (see interleave_gate_up), bias bf16 [2 I] or None; returns
+    torch.bfloat16 [m, I]."""
     import torch
 
-    m, k = x.shape
-    n2, k2 = w.shape
-    if k != k2:
-        raise NcmError(-2, "linear_bf16_swiglu")
+    W = "linear_bf16_swiglu"
+    a = _ck.Args(W)
+    m, k = _ck.dims(x, "x", W, 2)
+    n2, _ = _ck.dims(w, "w", W, 2)
+    if n2 % 64:
+        raise NcmError(-2, W, "w must have a multiple of 64 rows")
+    dv = x.device
+    px = a.dev(x, "x", _ck.BF16, (m, k))
+    pw = a.dev(w, "w", _ck.BF16, (n2, k))
+    pb = a.dev(bias, "bias", _ck.BF16, (n2,), optional=True)
     if out is None:
-        out = torch.empty((m, n2 // 2), dtype=torch.bfloat16, device=x.device)
-    ctx = ctx or default_context(x.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_linear_bf16_swiglu(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
-                                       _dev_ptr(bias, "bias"), _dev_ptr(out, "out"), m, k, n2),
-          "linear_bf16_swiglu")
+        out = torch.empty((m, n2 // 2), dtype=torch.bfloat16, device=dv)
+    po = a.dev(out, "out", _ck.BF16, (m, n2 // 2))
+    a.done()
+    ctx = _ctx_for(x, ctx)
+    check(lib().ncm_linear_bf16_swiglu(ctx.handle, px, pw, pb, po, m, k, n2), W)
     return out
 
 
@@ -187,22 +218,28 @@ def interleave_gate_up(gate, up):
 def linear_bf16_rope64(x, w, rot_cols: int, seq_len: int, cosine, sine, bias=None, out=None,
                        ctx=None):
     """bf16 projection with the RoPE of its 64-wide heads in columns
-    [0, rot_cols) fused (table row = row % seq_len); torch.bfloat16 out."""
+    [0, rot_cols) fused (table row = row % seq_len; cosine, sine float32
+    [seq_len, 64]); torch.bfloat16 out [m, n]."""
     import torch
 
-    m, k = x.shape
-    n, k2 = w.shape
-    if k != k2:
-        raise NcmError(-2, "linear_bf16_rope64")
+    W = "linear_bf16_rope64"
+    a = _ck.Args(W)
+    m, k = _ck.dims(x, "x", W, 2)
+    n, _ = _ck.dims(w, "w", W, 2)
+    dv = x.device
+    px = a.dev(x, "x", _ck.BF16, (m, k))
+    pw = a.dev(w, "w", _ck.BF16, (n, k))
+    pb = a.dev(bias, "bias", _ck.BF16, (n,), optional=True)
+    rot = int(rot_cols) > 0
+    pc = a.dev(cosine, "cosine", _ck.F32, (seq_len, 64), optional=not rot)
+    ps = a.dev(sine, "sine", _ck.F32, (seq_len, 64), optional=not rot)
     if out is None:
-        out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
-    ctx = ctx or default_context(x.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_linear_bf16_rope64(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"),
-                                       _dev_ptr(bias, "bias"), _dev_ptr(out, "out"), m, k, n,
-                                       rot_cols, seq_len, _dev_ptr(cosine, "cosine"),
-                                       _dev_ptr(sine, "sine")),
-          "linear_bf16_rope64")
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=dv)
+    po = a.dev(out, "out", _ck.BF16, (m, n))
+    a.done()
+    ctx = _ctx_for(x, ctx)
+    check(lib().ncm_linear_bf16_rope64(ctx.handle, px, pw, pb, po, m, k, n, rot_cols, seq_len,
+                                       pc, ps), W)
     return out
 
 
@@ -211,16 +248,19 @@ def linear_f32(x, w, out=None, ctx=None):
     the fp32 MFMA, on torch's current stream."""
     import torch
 
-    m, k = x.shape
-    n, k2 = w.shape
-    if k != k2:
-        raise NcmError(-2, "linear_f32")
+    W = "linear_f32"
+    a = _ck.Args(W)
+    m, k = _ck.dims(x, "x", W, 2)
+    n, _ = _ck.dims(w, "w", W, 2)
+    dv = x.device
+    px = a.dev(x, "x", _ck.F32, (m, k))
+    pw = a.dev(w, "w", _ck.F32, (n, k))
     if out is None:
-        out = torch.empty((m, n), dtype=torch.float32, device=x.device)
-    ctx = ctx or default_context(x.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_linear_f32(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(w, "w"), _dev_ptr(out, "out"),
-                               m, k, n), "linear_f32")
+        out = torch.empty((m, n), dtype=torch.float32, device=dv)
+    po = a.dev(out, "out", _ck.F32, (m, n))
+    a.done()
+    ctx = _ctx_for(x, ctx)
+    check(lib().ncm_linear_f32(ctx.handle, px, pw, po, m, k, n), W)
     return out
 
 
@@ -228,11 +268,14 @@ def bf16_from_f32(src, flush: bool = False, ctx=None):
     """Device f32 -> bf16 (RNE, NaN -> 0x7FC0), returned as torch.bfloat16."""
     import torch
 
+    W = "bf16_from_f32"
+    a = _ck.Args(W)
+    ps = a.dev(src, "src", _ck.F32)
     out = torch.empty(src.shape, dtype=torch.bfloat16, device=src.device)
-    ctx = ctx or default_context(src.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_bf16_from_f32_dev(ctx.handle, _dev_ptr(src, "src"), _dev_ptr(out, "out"),
-                                      src.numel(), 1 if flush else 0), "bf16_from_f32")
+    a.done()
+    ctx = _ctx_for(src, ctx)
+    check(lib().ncm_bf16_from_f32_dev(ctx.handle, ps, C.c_void_p(out.data_ptr()), src.numel(),
+                                      1 if flush else 0), W)
     return out
 
 
@@ -240,11 +283,13 @@ def bf16_widen(src, ctx=None):
     """Device bf16 -> f32 (exact)."""
     import torch
 
+    W = "bf16_widen"
+    a = _ck.Args(W)
+    ps = a.dev(src, "src", _ck.BF16)
     out = torch.empty(src.shape, dtype=torch.float32, device=src.device)
-    ctx = ctx or default_context(src.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_bf16_widen_dev(ctx.handle, _dev_ptr(src, "src"), _dev_ptr(out, "out"),
-                                   src.numel()), "bf16_widen")
+    a.done()
+    ctx = _ctx_for(src, ctx)
+    check(lib().ncm_bf16_widen_dev(ctx.handle, ps, C.c_void_p(out.data_ptr()), src.numel()), W)
     return out
 
 
@@ -254,41 +299,48 @@ def rms_norm_rows(x, weight, epsilon: float, out_mode: str = "bf16_f32", out=Non
     (float32 holding bf16 values) or "bf16" (torch.bfloat16)."""
     import torch
 
-    rows, width = x.shape
-    mode = _OUT_MODES[out_mode]
+    W = "rms_norm_rows"
+    a = _ck.Args(W)
+    rows_, width = _ck.dims(x, "x", W, 2)
+    mode = _mode(out_mode, W)
+    if mode == NCM_OUT_F32:
+        raise NcmError(-7, W, 'out_mode must be "bf16_f32" or "bf16"')
+    dv = x.device
+    px = a.dev(x, "x", _ck.F32, (rows_, width))
+    pw = a.dev(weight, "weight", _ck.F32, (width,))
     if out is None:
-        dt = torch.bfloat16 if mode == NCM_OUT_BF16 else torch.float32
-        out = torch.empty((rows, width), dtype=dt, device=x.device)
-    ctx = ctx or default_context(x.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_rms_norm_rows_dev(ctx.handle, _dev_ptr(x, "x"), _dev_ptr(weight, "weight"),
-                                      _dev_ptr(out, "out"), rows, width, float(epsilon), mode),
-          "rms_norm_rows")
+        out = _new_out(torch, mode, (rows_, width), dv)
+    po = a.dev(out, "out", _out_dtypes(mode), (rows_, width))
+    a.done()
+    ctx = _ctx_for(x, ctx)
+    check(lib().ncm_rms_norm_rows_dev(ctx.handle, px, pw, po, rows_, width, float(epsilon), mode),
+          W)
     return out
 
 
 def silu_mul(gate, up=None, out_mode: str = "bf16_f32", out=None, ctx=None):
     """round_bf16(silu_bf16(gate) * up) elementwise (up None: silu_bf16) on
-    torch's current stream."""
+    torch's current stream; gate, up float32 of one shape."""
     import torch
 
-    mode = _OUT_MODES[out_mode]
+    W = "silu_mul"
+    a = _ck.Args(W)
+    mode = _mode(out_mode, W)
+    if mode == NCM_OUT_F32:
+        raise NcmError(-7, W, 'out_mode must be "bf16_f32" or "bf16"')
+    if gate is None:
+        raise NcmError(-1, W, "gate is required")
+    dv = gate.device
+    shape = tuple(gate.shape)
+    pg = a.dev(gate, "gate", _ck.F32, shape)
+    pu = a.dev(up, "up", _ck.F32, shape, optional=True)
     if out is None:
-        dt = torch.bfloat16 if mode == NCM_OUT_BF16 else torch.float32
-        out = torch.empty(gate.shape, dtype=dt, device=gate.device)
-    ctx = ctx or default_context(gate.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_silu_mul_dev(ctx.handle, _dev_ptr(gate, "gate"), _dev_ptr(up, "up"),
-                                 _dev_ptr(out, "out"), gate.numel(), mode), "silu_mul")
+        out = _new_out(torch, mode, shape, dv)
+    po = a.dev(out, "out", _out_dtypes(mode), shape)
+    a.done()
+    ctx = _ctx_for(gate, ctx)
+    check(lib().ncm_silu_mul_dev(ctx.handle, pg, pu, po, gate.numel(), mode), W)
     return out
-
-
-def _rows_ptr(t, name):
-    """Pointer and row stride of a 2-D GPU tensor whose rows are contiguous
-    (a column slice of a wider buffer is allowed)."""
-    if not t.is_cuda or t.dim() != 2 or t.stride(1) != 1:
-        raise ValueError(f"{name} must be a 2-D GPU tensor with contiguous rows")
-    return C.c_void_p(t.data_ptr()), t.stride(0)
 
 
 def rope_rotate(x, heads: int, head_dim: int, seq_len: int, cosine, sine, ctx=None):
@@ -296,13 +348,35 @@ def rope_rotate(x, heads: int, head_dim: int, seq_len: int, cosine, sine, ctx=No
     every row of x (torch.bfloat16 [rows, >= heads * head_dim], rows may be
     strided); row r uses table row r % seq_len of cosine/sine (float32
     [seq_len, head_dim])."""
-    ptr, stride = _rows_ptr(x, "x")
-    ctx = ctx or default_context(x.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_rope_rotate_dev(ctx.handle, ptr, x.shape[0], stride, heads, head_dim, seq_len,
-                                    _dev_ptr(cosine, "cosine"), _dev_ptr(sine, "sine")),
-          "rope_rotate")
+    W = "rope_rotate"
+    a = _ck.Args(W)
+    n_rows, _ = _ck.dims(x, "x", W, 2)
+    dv = x.device
+    ptr, stride = a.rows(x, "x", _ck.BF16, n_rows, heads * head_dim)
+    pc = a.dev(cosine, "cosine", _ck.F32, (seq_len, head_dim))
+    ps = a.dev(sine, "sine", _ck.F32, (seq_len, head_dim))
+    a.done()
+    ctx = _ctx_for(x, ctx)
+    check(lib().ncm_rope_rotate_dev(ctx.handle, ptr, n_rows, stride, heads, head_dim, seq_len,
+                                    pc, ps), W)
     return x
+
+
+def _attention_operands(a, q, k, v, out, batch, seq_len, q_heads, kv_heads, head_dim, mode):
+    import torch
+
+    W = a.where
+    n = batch * seq_len
+    dv = q.device if q is not None else None
+    qp, qs = a.rows(q, "q", _ck.BF16, n, q_heads * head_dim)
+    kp, ks = a.rows(k, "k", _ck.BF16, n, kv_heads * head_dim)
+    vp_, vs = a.rows(v, "v", _ck.BF16, n, kv_heads * head_dim)
+    if ks != vs:
+        raise NcmError(-2, W, "k and v row strides differ")
+    if out is None:
+        out = _new_out(torch, mode, (n, q_heads * head_dim), dv)
+    op, os_ = a.rows(out, "out", _out_dtypes(mode), n, q_heads * head_dim)
+    return out, qp, qs, kp, ks, vp_, op, os_
 
 
 def attention_bf16(q, k, v, batch: int, seq_len: int, q_heads: int, kv_heads: int,
@@ -312,23 +386,15 @@ def attention_bf16(q, k, v, batch: int, seq_len: int, q_heads: int, kv_heads: in
     [batch * seq_len, >= q_heads * head_dim], k and v [batch * seq_len,
     >= kv_heads * head_dim], torch.bfloat16 with contiguous rows (column
     slices of one q|k|v buffer are allowed)."""
-    import torch
-
-    qp, qs = _rows_ptr(q, "q")
-    kp, ks = _rows_ptr(k, "k")
-    vp_, vs = _rows_ptr(v, "v")
-    if ks != vs:
-        raise NcmError(-2, "attention_bf16: k and v row strides differ")
-    mode = _OUT_MODES[out_mode]
-    if out is None:
-        dt = torch.bfloat16 if mode == NCM_OUT_BF16 else torch.float32
-        out = torch.empty((batch * seq_len, q_heads * head_dim), dtype=dt, device=q.device)
-    op, os_ = _rows_ptr(out, "out")
-    ctx = ctx or default_context(q.device.index or 0)
-    ctx.bind_stream()
+    W = "attention_bf16"
+    a = _ck.Args(W)
+    mode = _mode(out_mode, W)
+    out, qp, qs, kp, ks, vp_, op, os_ = _attention_operands(
+        a, q, k, v, out, batch, seq_len, q_heads, kv_heads, head_dim, mode)
+    a.done()
+    ctx = _ctx_for(q, ctx)
     check(lib().ncm_attention_bf16_dev(ctx.handle, qp, kp, vp_, op, batch, seq_len, q_heads,
-                                       kv_heads, head_dim, qs, ks, os_, window, mode),
-          "attention_bf16")
+                                       kv_heads, head_dim, qs, ks, os_, window, mode), W)
     return out
 
 
@@ -353,26 +419,23 @@ def attention_bf16_seg(q, k, v, batch: int, seq_len: int, q_heads: int, kv_heads
                        head_dim: int, prefix_len: int, seg_lo, seg_hi, pad_bits=None,
                        out_mode: str = "bf16_f32", out=None, ctx=None):
     """bf16 attention under NCM's block-diagonal level mask; seg_lo / seg_hi
-    int32 and pad_bits uint64 device tensors (block_diagonal_segments)."""
-    import torch
-
-    qp, qs = _rows_ptr(q, "q")
-    kp, ks = _rows_ptr(k, "k")
-    vp_, vs = _rows_ptr(v, "v")
-    if ks != vs:
-        raise NcmError(-2, "attention_bf16_seg: k and v row strides differ")
-    mode = _OUT_MODES[out_mode]
-    if out is None:
-        dt = torch.bfloat16 if mode == NCM_OUT_BF16 else torch.float32
-        out = torch.empty((batch * seq_len, q_heads * head_dim), dtype=dt, device=q.device)
-    op, os_ = _rows_ptr(out, "out")
-    ctx = ctx or default_context(q.device.index or 0)
-    ctx.bind_stream()
+    int32 [seq_len] and pad_bits uint64 [ceil(prefix_len / 64)] device
+    tensors (block_diagonal_segments)."""
+    W = "attention_bf16_seg"
+    a = _ck.Args(W)
+    mode = _mode(out_mode, W)
+    out, qp, qs, kp, ks, vp_, op, os_ = _attention_operands(
+        a, q, k, v, out, batch, seq_len, q_heads, kv_heads, head_dim, mode)
+    dv = q.device
+    pl = a.dev(seg_lo, "seg_lo", _ck.I32, (seq_len,))
+    ph = a.dev(seg_hi, "seg_hi", _ck.I32, (seq_len,))
+    pp = a.dev(pad_bits, "pad_bits", _ck.U64, (max(1, (prefix_len + 63) // 64),),
+                 optional=True)
+    a.done()
+    ctx = _ctx_for(q, ctx)
     check(lib().ncm_attention_bf16_seg_dev(ctx.handle, qp, kp, vp_, op, batch, seq_len, q_heads,
-                                           kv_heads, head_dim, qs, ks, os_, prefix_len,
-                                           _dev_ptr(seg_lo, "seg_lo"), _dev_ptr(seg_hi, "seg_hi"),
-                                           _dev_ptr(pad_bits, "pad_bits"), mode),
-          "attention_bf16_seg")
+                                           kv_heads, head_dim, qs, ks, os_, prefix_len, pl, ph,
+                                           pp, mode), W)
     return out
 
 
@@ -383,18 +446,22 @@ def tied_head_logits(z, codebook, csq, log_inv_t: float = 0.0, bias=None, out=No
     float32 [v] or None; returns float32 [rows, v]."""
     import torch
 
-    rows, d = z.shape
-    v, d2 = codebook.shape
-    if d != d2 or tuple(csq.shape) != (v,):
-        raise NcmError(-2, "tied_head_logits")
+    W = "tied_head_logits"
+    a = _ck.Args(W)
+    rows_, d = _ck.dims(z, "z", W, 2)
+    v, _ = _ck.dims(codebook, "codebook", W, 2)
+    dv = z.device
+    pz = a.dev(z, "z", _ck.BF16, (rows_, d))
+    pe = a.dev(codebook, "codebook", _ck.BF16, (v, d))
+    pc = a.dev(csq, "csq", _ck.F32, (v,))
+    pb = a.dev(bias, "bias", _ck.F32, (v,), optional=True)
     if out is None:
-        out = torch.empty((rows, v), dtype=torch.float32, device=z.device)
-    ctx = ctx or default_context(z.device.index or 0)
-    ctx.bind_stream()
-    check(lib().ncm_tied_head_logits(ctx.handle, _dev_ptr(z, "z"), _dev_ptr(codebook, "codebook"),
-                                     _dev_ptr(csq, "csq"), _dev_ptr(bias, "bias"),
-                                     float(log_inv_t), _dev_ptr(out, "out"), rows, d, v),
-          "tied_head_logits")
+        out = torch.empty((rows_, v), dtype=torch.float32, device=dv)
+    po = a.dev(out, "out", _ck.F32, (rows_, v))
+    a.done()
+    ctx = _ctx_for(z, ctx)
+    check(lib().ncm_tied_head_logits(ctx.handle, pz, pe, pc, pb, float(log_inv_t), po, rows_, d,
+                                     v), W)
     return out
 
 
@@ -406,18 +473,25 @@ def tied_head_logits_levels(z, codebooks, csq, level_rows, log_inv_t=None, bias=
     (default 0), bias float32 [levels, v] or None; float32 [sum rows, v]."""
     import torch
 
-    L, v, d = codebooks.shape
+    W = "tied_head_logits_levels"
+    a = _ck.Args(W)
+    L, v, d = _ck.dims(codebooks, "codebooks", W, 3)
     rows = np.ascontiguousarray(level_rows, dtype=np.int64)
     lit = np.ascontiguousarray(np.zeros(L) if log_inv_t is None else log_inv_t, dtype=np.float32)
-    if (rows.size != L or lit.size != L or tuple(z.shape) != (int(rows.sum()), d)
-            or tuple(csq.shape) != (L, v)):
-        raise NcmError(-2, "tied_head_logits_levels")
+    if rows.size != L or lit.size != L:
+        raise NcmError(-2, W, "level_rows and log_inv_t need one entry per level")
+    total = int(rows.sum())
+    dv = codebooks.device
+    pz = a.dev(z, "z", _ck.BF16, (total, d))
+    pe = a.dev(codebooks, "codebooks", _ck.BF16, (L, v, d))
+    pc = a.dev(csq, "csq", _ck.F32, (L, v))
+    pb = a.dev(bias, "bias", _ck.F32, (L, v), optional=True)
     if out is None:
-        out = torch.empty((int(rows.sum()), v), dtype=torch.float32, device=z.device)
-    ctx = ctx or default_context(z.device.index or 0)
-    ctx.bind_stream()
+        out = torch.empty((total, v), dtype=torch.float32, device=dv)
+    po = a.dev(out, "out", _ck.F32, (total, v))
+    a.done()
+    ctx = _ctx_for(codebooks, ctx)
     check(lib().ncm_tied_head_logits_levels(
-        ctx.handle, _dev_ptr(z, "z"), _dev_ptr(codebooks, "codebooks"), _dev_ptr(csq, "csq"),
-        _dev_ptr(bias, "bias"), lit.ctypes.data_as(C.c_void_p), rows.ctypes.data_as(C.c_void_p),
-        L, d, v, _dev_ptr(out, "out")), "tied_head_logits_levels")
+        ctx.handle, pz, pe, pc, pb, lit.ctypes.data_as(C.c_void_p),
+        rows.ctypes.data_as(C.c_void_p), L, d, v, po), W)
     return out
