@@ -40,6 +40,17 @@ LINEAR_NK = [(2048, 2048), (8192, 2048), (2048, 8192)]
 # profiles/linear_bf16_1b_shapes.md and profiles/rvq_encode_b16_t2048_d2048_l8_v4096.md.
 LINEAR_TRAFFIC_BYTES_PER_LAUNCH = 155.3e6
 RVQ_TRAFFIC_BYTES_PER_ENCODE = 6663e6
+NEAR_TIE_REL = 1e-5  # relative top-2 distance gap under which a code is a near-tie
+
+
+def cpu_threads():
+    """Host threads for the N-core CPU baselines: the cores this process may
+    use, capped at 16 (the GPU box's share of the host)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return max(1, min(16, n))
 
 
 def _events(torch):
@@ -128,13 +139,19 @@ def run_rvq(torch, reps, warmup):
     e1.record()
     torch.cuda.synchronize()
     t = e0.elapsed_time(e1) * 1e-3 / reps
+    # Untimed: one encode with the per-code relative top-2 gap, for the
+    # near-tie count (gap < 1e-5: the rows where any fp32 order could pick
+    # another code).
+    g = vq.encode(xd, cbd, c["strides"], csq=csq, want_recon=False, want_gap=True)["gap"]
+    torch.cuda.synchronize()
+    near = int((g < NEAR_TIE_REL).sum())
     rows = sum(c["b"] * c["t"] // s for s in c["strides"])
     flops = 2.0 * c["v"] * c["d"] * rows
     # x read once, codebooks read once, codes and reconstruction written once.
     bytes_alg = (c["b"] * c["t"] * c["d"] * 4 + c["levels"] * c["v"] * c["d"] * 2 +
                  rows * 4 + c["b"] * c["t"] * c["d"] * 4)
     return {"encode_s": t, "tokens": c["b"] * c["t"], "flops": flops, "bytes": bytes_alg,
-            "n_flagged": n_flagged}
+            "n_flagged": n_flagged, "near_ties": near, "codes": rows}
 
 
 def run_decoder_ops(torch, reps=20):
@@ -407,6 +424,53 @@ def cpu_linear_baseline():
                       "(pair-FMA, FTZ, K-blocks), 1 thread, extrapolated to M=2048"}
 
 
+def cpu_linear_baseline_ncores():
+    """The same oracle on a 384-row slice of each shape, rows split over
+    cpu_threads() host threads (rows are independent, so the outputs are the
+    1-thread ones), extrapolated linearly in M."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from ncmorph_amd import synth
+    from oracle import pyoracle
+
+    nt = cpu_threads()
+    rows = 24 * nt
+    t_total = 0.0
+    for (n, k) in LINEAR_NK:
+        xb = synth.normal_bf16(synth.LINEAR_SEED_X + k, (rows, k))
+        wb = synth.normal_bf16(synth.LINEAR_SEED_W + n * 7 + k, (n, k), std=0.02)
+        step = rows // nt
+        t0 = time.perf_counter()
+        with ThreadPoolExecutor(nt) as ex:
+            list(ex.map(lambda i: pyoracle.matmul_bf16_u16_rows(xb, wb, i * step, (i + 1) * step),
+                        range(nt)))
+        t_total += (time.perf_counter() - t0) * (LINEAR_M / rows)
+    flops = sum(2.0 * LINEAR_M * n * k for (n, k) in LINEAR_NK)
+    return {"value": flops / t_total / 1e12, "unit": "TFLOP/s", "cores": nt, "kind": "port",
+            "sample": f"first {rows} rows of x for each of the 3 shapes, oracle matmul_bf16 "
+                      f"rows split over {nt} threads, extrapolated to M=2048"}
+
+
+def cpu_rvq_baseline_ncores():
+    """Oracle encode of one whole sequence (2048 positions, all 8 levels)
+    with each level's rows split over cpu_threads() host threads."""
+    from ncmorph_amd import synth
+    from oracle import pyoracle
+
+    c = synth.RVQ_LARGE
+    nt = cpu_threads()
+    x, cb = synth.rvq_inputs(c["seed"], c["b"], c["t"], c["d"], c["levels"], c["v"])
+    xs = np.ascontiguousarray(x[:1])
+    del x
+    csq = pyoracle.rvq_csq(cb)
+    t0 = time.perf_counter()
+    pyoracle.rvq_encode(xs, cb, c["strides"], csq=csq, want_gap=False, threads=nt)
+    dt = time.perf_counter() - t0
+    return {"value": c["t"] / dt, "unit": "tokens/s", "cores": nt, "kind": "port",
+            "sample": f"sequence 0 (2048 positions), all 8 levels, 4096 codes/level, d=2048, "
+                      f"oracle exhaustive search, each level's rows over {nt} threads"}
+
+
 def cpu_rvq_baseline():
     """Oracle encode (exhaustive fp32 search, 1 thread) of the first 256
     positions of sequence 0, all 8 levels."""
@@ -484,6 +548,7 @@ def main():
         res["linear_max_abs_err_vs_fp32"] = lin["max_abs_err_vs_fp32"]
         if not args.no_cpu:
             res["cpu_baseline"] = cpu_linear_baseline()
+            res["cpu_baseline_ncores"] = cpu_linear_baseline_ncores()
     if args.only in ("linear", "all"):
         res["decoder_ops"] = run_decoder_ops(torch)
     if args.only in ("rvq", "all"):
@@ -502,9 +567,12 @@ def main():
                             "traffic": RVQ_TRAFFIC_BYTES_PER_ENCODE,
                             "hbm_gbs_algorithmic": round(gbs, 1),
                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
-               "flagged_rows": rv["n_flagged"]}
+               "flagged_rows": rv["n_flagged"],
+               "near_ties": {"count": rv["near_ties"], "codes": rv["codes"],
+                             "rel_gap_below": NEAR_TIE_REL}}
         if not args.no_cpu:
             rvq["cpu_baseline"] = cpu_rvq_baseline()
+            rvq["cpu_baseline_ncores"] = cpu_rvq_baseline_ncores()
         res["rvq_encode"] = rvq
         if "value" not in res:
             res.update({"value": rvq["value"], "unit": "tokens/s",

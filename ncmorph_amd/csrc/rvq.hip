@@ -445,9 +445,13 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void rvq_dist_kernel(DistAr
 
 // --------------------------------------------------------- rescore kernel
 
-// Candidate keys per row are read 64 per lane slot: at most 512 per row.
+// Candidate keys per row are read 64 per lane slot: KS slots hold up to
+// 16 KS chunks of four keys (KS = 8 for the default tiles, 16 for the small
+// levels' 64 x 64 tiles, whose rows have twice as many chunks).
 constexpr int kKeySlots = 8;
 constexpr int kMaxChunks = kKeySlots * 64 / 4;
+constexpr int kKeySlotsWide = 16;
+constexpr int kMaxChunksWide = kKeySlotsWide * 64 / 4;
 
 // Per-level arguments of the rescore kernel.
 struct RowArgs {
@@ -490,13 +494,46 @@ struct Best {
     int32_t code;
 };
 
-__device__ __forceinline__ void best_update(Best& b, float dist, int32_t code) {
+// Returns true when `code` becomes the best (wave-uniform: every lane holds
+// the same distance bits).
+__device__ __forceinline__ bool best_update(Best& b, float dist, int32_t code) {
     if (dist < b.best || (dist == b.best && code < b.code)) {
         b.second = b.best;
         b.best = dist;
         b.code = code;
-    } else if (dist < b.second) {
-        b.second = dist;
+        return true;
+    }
+    if (dist < b.second) b.second = dist;
+    return false;
+}
+
+// The bf16 elements of one code row that a lane owns (lane j: elements
+// 256 m + 4 j .. + 3), as loaded for a dot product.
+template <int NCH>
+struct CodeRow {
+    u32x2_t p[NCH];
+};
+
+template <int NCH>
+__device__ __forceinline__ void load_code_row(const uint16_t* c, int64_t d, int lane,
+                                              CodeRow<NCH>& r) {
+#pragma unroll
+    for (int m = 0; m < NCH; ++m)
+        if (lane_chunk_valid(d, m, lane)) r.p[m] = *(const u32x2_t*)(c + m * 256 + 4 * lane);
+}
+
+// acc += widen(code row) elementwise (fp32 adds, one per element).
+template <int NCH>
+__device__ __forceinline__ void add_code_row(const CodeRow<NCH>& r, int64_t d, int lane,
+                                             RowVec<NCH>& acc) {
+#pragma unroll
+    for (int m = 0; m < NCH; ++m) {
+        if (lane_chunk_valid(d, m, lane)) {
+            acc.v[m][0] = acc.v[m][0] + bf16_lo_to_f32(r.p[m][0]);
+            acc.v[m][1] = acc.v[m][1] + bf16_hi_to_f32(r.p[m][0]);
+            acc.v[m][2] = acc.v[m][2] + bf16_lo_to_f32(r.p[m][1]);
+            acc.v[m][3] = acc.v[m][3] + bf16_hi_to_f32(r.p[m][1]);
+        }
     }
 }
 
@@ -514,13 +551,10 @@ constexpr int kDotBatch = 2;
 template <int NCH>
 __device__ __forceinline__ void dotn_fixed(const RowVec<NCH>& u,
                                            const uint16_t* const (&c)[kDotBatch], int64_t d,
-                                           int lane, float (&out)[kDotBatch]) {
-    u32x2_t p[kDotBatch][NCH];
+                                           int lane, float (&out)[kDotBatch],
+                                           CodeRow<NCH> (&rows)[kDotBatch]) {
 #pragma unroll
-    for (int j = 0; j < kDotBatch; ++j)
-#pragma unroll
-        for (int m = 0; m < NCH; ++m)
-            if (lane_chunk_valid(d, m, lane)) p[j][m] = *(const u32x2_t*)(c[j] + m * 256 + 4 * lane);
+    for (int j = 0; j < kDotBatch; ++j) load_code_row<NCH>(c[j], d, lane, rows[j]);
     float acc[kDotBatch];
 #pragma unroll
     for (int j = 0; j < kDotBatch; ++j) acc[j] = 0.0f;
@@ -529,10 +563,10 @@ __device__ __forceinline__ void dotn_fixed(const RowVec<NCH>& u,
         if (lane_chunk_valid(d, m, lane)) {
 #pragma unroll
             for (int j = 0; j < kDotBatch; ++j) {
-                acc[j] = __builtin_fmaf(u.v[m][0], bf16_lo_to_f32(p[j][m][0]), acc[j]);
-                acc[j] = __builtin_fmaf(u.v[m][1], bf16_hi_to_f32(p[j][m][0]), acc[j]);
-                acc[j] = __builtin_fmaf(u.v[m][2], bf16_lo_to_f32(p[j][m][1]), acc[j]);
-                acc[j] = __builtin_fmaf(u.v[m][3], bf16_hi_to_f32(p[j][m][1]), acc[j]);
+                acc[j] = __builtin_fmaf(u.v[m][0], bf16_lo_to_f32(rows[j].p[m][0]), acc[j]);
+                acc[j] = __builtin_fmaf(u.v[m][1], bf16_hi_to_f32(rows[j].p[m][0]), acc[j]);
+                acc[j] = __builtin_fmaf(u.v[m][2], bf16_lo_to_f32(rows[j].p[m][1]), acc[j]);
+                acc[j] = __builtin_fmaf(u.v[m][3], bf16_hi_to_f32(rows[j].p[m][1]), acc[j]);
             }
         }
     }
@@ -540,11 +574,13 @@ __device__ __forceinline__ void dotn_fixed(const RowVec<NCH>& u,
     for (int j = 0; j < kDotBatch; ++j) out[j] = wave_sum(acc[j]);
 }
 
-// Exact distances of `n` codes listed in `list` (wave-uniform), folded into b.
+// Exact distances of `n` codes listed in `list` (wave-uniform), folded into
+// b; best_row keeps the elements of b's code once it was scored here.
 template <int NCH>
 __device__ __forceinline__ void score_list(const RowVec<NCH>& u, const uint16_t* cbl,
                                            const float* csql, const int32_t* list, int n,
-                                           int64_t d, int lane, Best& b) {
+                                           int64_t d, int lane, Best& b,
+                                           CodeRow<NCH>& best_row) {
     for (int i = 0; i < n; i += kDotBatch) {
         int32_t k[kDotBatch];
         const uint16_t* c[kDotBatch];
@@ -554,10 +590,12 @@ __device__ __forceinline__ void score_list(const RowVec<NCH>& u, const uint16_t*
             c[j] = cbl + (int64_t)k[j] * d;
         }
         float dots[kDotBatch];
-        dotn_fixed<NCH>(u, c, d, lane, dots);
+        CodeRow<NCH> rows[kDotBatch];
+        dotn_fixed<NCH>(u, c, d, lane, dots, rows);
 #pragma unroll
         for (int j = 0; j < kDotBatch; ++j)
-            if (i + j < n) best_update(b, __builtin_fmaf(-2.0f, dots[j], csql[k[j]]), k[j]);
+            if (i + j < n && best_update(b, __builtin_fmaf(-2.0f, dots[j], csql[k[j]]), k[j]))
+                best_row = rows[j];
     }
 }
 
@@ -573,11 +611,10 @@ __device__ __forceinline__ void load_coarse(const RowArgs& a, int64_t row, int l
     }
 }
 
-// u = P_l - D_l for one row.
+// u = P_l - D_l for one row (D_l left in D).
 template <int NCH>
 __device__ __forceinline__ void load_residual(const RowArgs& a, int64_t row, int lane,
-                                              RowVec<NCH>& u) {
-    RowVec<NCH> D;
+                                              RowVec<NCH>& u, RowVec<NCH>& D) {
     load_coarse<NCH>(a, row, lane, D);
     load_f32_row<NCH>(pooled_row_ptr(a.g, a.x, a.pyr, a.level, row), a.g.d, lane, u);
 #pragma unroll
@@ -588,9 +625,12 @@ __device__ __forceinline__ void load_residual(const RowArgs& a, int64_t row, int
 
 // Code and gap of a finished row; D_{l+1} and the next level's bf16 rows, or
 // the reconstruction at the last level.
-template <int NCH>
+// best_row holds the elements of b.code when have_row is true. KEEP_D: D_l
+// is still in D (else it is loaded again).
+template <int NCH, bool KEEP_D>
 __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const Best& b,
-                                          double unorm2, int lane) {
+                                          const CodeRow<NCH>& best_row, bool have_row,
+                                          double unorm2, int lane, RowVec<NCH>& D) {
     const RvqGeom& g = a.g;
     const int l = a.level;
     const int64_t d = g.d;
@@ -606,9 +646,14 @@ __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const 
     if (last && !a.recon) return;
     int32_t k = a.force_codes ? a.force_codes[ci] : b.code;
     k = k < 0 ? 0 : (k >= g.v ? (int32_t)(g.v - 1) : k);
-    RowVec<NCH> D;
-    load_coarse<NCH>(a, row, lane, D);
-    add_bf16_row<NCH>(a.cb + ((int64_t)l * g.v + k) * d, d, lane, D);  // D_{l+1}
+    if (!KEEP_D) load_coarse<NCH>(a, row, lane, D);
+    if (have_row && k == b.code) {
+        add_code_row<NCH>(best_row, d, lane, D);  // D_{l+1}
+    } else {
+        CodeRow<NCH> r;
+        load_code_row<NCH>(a.cb + ((int64_t)l * g.v + k) * d, d, lane, r);
+        add_code_row<NCH>(r, d, lane, D);
+    }
     if (last) {
         // recon[bb, tp * s .. tp * s + s - 1] = D_L
         for (int64_t r = 0; r < s; ++r) {
@@ -647,10 +692,14 @@ __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const 
     }
 }
 
-template <int NCH>
+// KEEP_D: D_l stays in registers from the residual to the finish (one memory
+// round trip less, more registers: the small levels, whose few rows leave
+// occupancy to spare).
+template <int NCH, int KS, bool KEEP_D>
 __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
+    constexpr int kKeySlots = KS;
     __shared__ int32_t cand_list[4][kKeySlots * 64];
-    __shared__ int32_t inc_list[4][kMaxChunks];
+    __shared__ int32_t inc_list[4][kKeySlots * 16];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -659,8 +708,8 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     const int l = a.level;
     const int64_t d = g.d;
 
-    RowVec<NCH> u;
-    load_residual<NCH>(a, row, lane, u);
+    RowVec<NCH> u, D;
+    load_residual<NCH>(a, row, lane, u, D);
     const int nk = a.cg.nchunk * 4;
     const uint32_t* ck = a.cand + row * (int64_t)nk;
     uint32_t key[kKeySlots];
@@ -732,7 +781,17 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     const uint16_t* cbl = a.cb + (int64_t)l * g.v * d;
     const float* csql = a.csq + (int64_t)l * g.v;
     Best b{INFINITY, INFINITY, 0x7FFFFFFF};
-    score_list<NCH>(u, cbl, csql, list, nsel, d, lane, b);
+    CodeRow<NCH> best_row;
+    bool have_row = false;
+    if (nsel == 1 && ninc == 0) {
+        // One code under the threshold: it is the exact argmin and no other
+        // code lies within the near-tie window, so no exact distance is
+        // needed (the gap is +inf, as for any single rescored candidate).
+        b.code = list[0];
+    } else {
+        score_list<NCH>(u, cbl, csql, list, nsel, d, lane, b, best_row);
+        have_row = nsel > 0;
+    }
     if (ninc > 0) {
         if (lane == 0) atomicAdd(a.flag_count, 1);
         // Every code of each incomplete chunk, listed in LDS then rescored.
@@ -757,11 +816,12 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
                     n += __popcll(m);
                 }
                 wave_lds_sync();
-                score_list<NCH>(u, cbl, csql, list, n, d, lane, b);
+                score_list<NCH>(u, cbl, csql, list, n, d, lane, b, best_row);
+                have_row = true;
             }
         }
     }
-    finish_row<NCH>(a, row, b, st.unorm2, lane);
+    finish_row<NCH, KEEP_D>(a, row, b, best_row, have_row, st.unorm2, lane, D);
 }
 
 // ------------------------------------------------------------ host side
@@ -784,7 +844,14 @@ using DistBig16 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, -1,
 using DistMid = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3, false, 1, -1, -1, true>;
 using DistSmall = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
 using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 2>;
+// DistTiny    64 x 64, 4 wavefronts (32 x 32 each), 4 stages (64 KB: two
+//             workgroups per CU): the small levels, whose 128 x 128 grids
+//             leave most CUs idle; one code tile per workgroup, 16 candidate
+//             key slots per row.
+using DistTiny = GemmShape<64, 64, 64, 2, 2, 2, 8, true, 4>;
 constexpr int64_t kCus = 256;
+// Levels with at most this many rows rescore with KEEP_D.
+constexpr int64_t kSmallLevelRows = 4096;
 
 static int nch_for(int64_t d) {
     const int64_t n = (d + 255) / 256;
@@ -801,8 +868,14 @@ static hipError_t launch_row_kernels(const PrepArgs* pa, const RowArgs* ra, int6
     const dim3 grid((unsigned)((rows + 3) / 4));
     if (pa)
         hipLaunchKernelGGL(rvq_prep_kernel<NCH>, grid, dim3(256), 0, st, *pa);
+    else if (ra->cg.nchunk > kMaxChunks)
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlotsWide, true>), grid, dim3(256), 0, st,
+                           *ra);
+    else if (rows <= kSmallLevelRows)
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, true>), grid, dim3(256), 0, st, *ra);
     else
-        hipLaunchKernelGGL(rvq_rescore_kernel<NCH>, grid, dim3(256), 0, st, *ra);
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, false>), grid, dim3(256), 0, st,
+                           *ra);
     return hipGetLastError();
 }
 
@@ -819,7 +892,7 @@ static hipError_t launch_rows(int nch, const PrepArgs* pa, const RowArgs* ra, in
 }
 
 template <class S>
-static CandGeom cand_geom_t(int64_t n_rows, int64_t v) {
+static CandGeom cand_geom_t(int64_t n_rows, int64_t v, int max_chunks = kMaxChunks) {
     CandGeom cg{};
     cg.bm = S::BM;
     cg.wm_codes = S::WM;
@@ -827,7 +900,7 @@ static CandGeom cand_geom_t(int64_t n_rows, int64_t v) {
     cg.wgm = S::WGM;
     const int64_t tiles_v = (v + S::BM - 1) / S::BM;
     const int64_t rt = (n_rows + S::BN - 1) / S::BN;
-    const int64_t max_ranges = kMaxChunks / (S::WGM * 2);
+    const int64_t max_ranges = max_chunks / (S::WGM * 2);
     int64_t nr = std::min<int64_t>(max_ranges, tiles_v);
     // Large levels: fewer, longer ranges (less candidate traffic).
     while (nr > 8 && rt * nr > 2048) nr /= 2;
@@ -845,7 +918,7 @@ static CandGeom cand_geom_t(int64_t n_rows, int64_t v) {
     return cg;
 }
 
-enum DistKind { kDistBig, kDistMid, kDistSmall, kDistSmall2 };
+enum DistKind { kDistBig, kDistMid, kDistSmall, kDistSmall2, kDistTiny };
 
 static int64_t dist_grid(const CandGeom& cg, int64_t n_rows, int64_t bn) {
     return (n_rows + bn - 1) / bn * cg.nranges;
@@ -854,8 +927,11 @@ static int64_t dist_grid(const CandGeom& cg, int64_t n_rows, int64_t bn) {
 static DistKind dist_kind(int64_t n_rows, int64_t v) {
     if (dist_grid(cand_geom_t<DistBig>(n_rows, v), n_rows, DistBig::BN) >= kCus) return kDistBig;
     if (dist_grid(cand_geom_t<DistMid>(n_rows, v), n_rows, DistMid::BN) >= kCus) return kDistMid;
-    if (dist_grid(cand_geom_t<DistSmall>(n_rows, v), n_rows, DistSmall::BN) <= kCus)
-        return kDistSmall;
+    const int64_t small = dist_grid(cand_geom_t<DistSmall>(n_rows, v), n_rows, DistSmall::BN);
+    if (small <= kCus / 2 &&
+        cand_geom_t<DistTiny>(n_rows, v, kMaxChunksWide).ntv == 1)
+        return kDistTiny;
+    if (small <= kCus) return kDistSmall;
     return kDistSmall2;
 }
 
@@ -863,6 +939,7 @@ static CandGeom cand_geom(int64_t n_rows, int64_t v) {
     switch (dist_kind(n_rows, v)) {
         case kDistBig: return cand_geom_t<DistBig>(n_rows, v);
         case kDistMid: return cand_geom_t<DistMid>(n_rows, v);
+        case kDistTiny: return cand_geom_t<DistTiny>(n_rows, v, kMaxChunksWide);
         default: return cand_geom_t<DistSmall>(n_rows, v);
     }
 }
@@ -1039,6 +1116,7 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
                 break;
             case kDistMid: e = launch_dist<DistMid>(da, st); break;
             case kDistSmall: e = launch_dist<DistSmall>(da, st); break;
+            case kDistTiny: e = launch_dist_t<DistTiny, true>(da, st); break;
             default: e = launch_dist<DistSmall2>(da, st); break;
         }
         if (e != hipSuccess) return NCM_E_HIP;

@@ -83,6 +83,12 @@ def test_small_config_golden(ncm, oracle, cuda):
     # 256 x 256 tiles with one code tile per workgroup (16x16x32 MFMAs), the
     # last code tile ragged (4000 = 15 * 256 + 160)
     dict(b=2, t=4096, d=64, v=4000, strides=(2, 1), seed=29),
+    # 256 x 256 tiles, one code tile per workgroup, three rounds of the CUs
+    # (768 tiles)
+    dict(b=3, t=4096, d=128, v=4096, strides=(4, 1), seed=30),
+    # 756 tiles (not a multiple of the 8 XCDs, so the tile order is not
+    # remapped), ragged last row tile, 12 code tiles with the last one ragged
+    dict(b=1, t=16000, d=64, v=3000, strides=(1,), seed=36),
 ])
 def test_multiscale_matches_oracle(ncm, oracle, cuda, case):
     L = len(case["strides"])
@@ -162,6 +168,7 @@ def test_large_config_properties(ncm, oracle, cuda):
     rec = vq.decode(r["codes"], cbd, c["strides"], c["t"])
     torch.cuda.synchronize()
     codes = r["codes"].cpu().numpy()
+    gap = r["gap"].cpu().numpy()
     assert codes.shape == (16, 4080)
     assert codes.min() >= 0 and codes.max() < c["v"]
     assert torch.equal(rec, r["recon"])
@@ -172,8 +179,17 @@ def test_large_config_properties(ncm, oracle, cuda):
     for l, s in enumerate(c["strides"]):
         n = 16 * (c["t"] // s)
         rows = np.unique(rng.integers(0, n, size=24)).astype(np.int64)
-        got, _ = oracle.rvq_level_rows(x, cb, c["strides"], csq, codes, l, rows)
+        got, ogap = oracle.rvq_level_rows(x, cb, c["strides"], csq, codes, l, rows)
         per_b = c["t"] // s
         gpu = codes[rows // per_b, off + rows % per_b]
         assert np.array_equal(got, gpu), (l, np.sum(got != gpu))
+        # Near-ties (relative top-2 gap < 1e-5) are reported: the GPU's gap
+        # classifies every sampled row as the oracle's full search does, and
+        # equals it where it is small.
+        g = gap[rows // per_b, off + rows % per_b]
+        assert np.array_equal(g < 1e-5, ogap < 1e-5), (l, g, ogap)
+        small = ogap < 1e-4
+        assert np.allclose(g[small], ogap[small], rtol=1e-3, atol=1e-9), (l, g[small], ogap[small])
+        assert np.all(ogap[~np.isfinite(g)] >= 1e-5)
         off += per_b
+    print("near-ties (gap < 1e-5):", int((gap < 1e-5).sum()), "of", gap.size)
