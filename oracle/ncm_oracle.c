@@ -655,6 +655,17 @@ void ncmo_silu_bf16(const float* x, float* out, size_t n) {
     }
 }
 
+/* kernels.silu (packages/kernels/root.zig:255-261): value * (1 / (1 +
+ * exp(-value))), f32 mode. libm expf stands in for Zig's std.math.exp (not
+ * bit-pinned; see the decoder ops). */
+void ncmo_silu(const float* x, float* out, size_t n) {
+    for (size_t i = 0; i < n; ++i) {
+        const float v = x[i];
+        const float sigmoid = 1.0f / (1.0f + expf(-v));
+        out[i] = v * sigmoid;
+    }
+}
+
 void ncmo_silu_mul_bf16(const float* gate, const float* up, float* out, size_t n) {
     for (size_t i = 0; i < n; ++i) {
         const float v = gate[i];
@@ -815,5 +826,54 @@ int ncmo_block_diagonal_mask(size_t prefix_length, const size_t* level_lengths, 
         }
         off += level_lengths[l];
     }
+    return 0;
+}
+
+/* ------------------------------------------------------------------ */
+/* NCM body helpers (src/ncm_position.zig, src/ncm_model.zig)          */
+/* ------------------------------------------------------------------ */
+
+/* fill_level_positions (src/ncm_position.zig:11-22): the prefix takes
+ * 0 .. P-1 and every level restarts at 0. -1 = InvalidPositionBuffer. */
+int ncmo_fill_level_positions(size_t prefix_length, const size_t* level_lengths, size_t levels,
+                              int64_t* positions, size_t positions_len) {
+    size_t total = prefix_length;
+    for (size_t l = 0; l < levels; ++l) total += level_lengths[l];
+    if (positions_len != total) return -1;
+    for (size_t p = 0; p < prefix_length; ++p) positions[p] = (int64_t)p;
+    size_t off = prefix_length;
+    for (size_t l = 0; l < levels; ++l) {
+        for (size_t p = 0; p < level_lengths[l]; ++p) positions[off + p] = (int64_t)p;
+        off += level_lengths[l];
+    }
+    return 0;
+}
+
+/* apply_post_upsample_conv (src/ncm_model.zig:296-326) on one level chunk
+ * [rows, width], in place: value = bias[o], then for every input channel and
+ * kernel tap in that order value += weight[o][i][k] * input[p + k - 1][i]
+ * (taps outside the chunk skipped; separate multiply and add), and
+ * output = input + value. weight: [width][width][3]. -1 on a bad size. */
+int ncmo_post_upsample_conv(float* input, const float* weight, const float* bias, size_t rows,
+                            size_t width) {
+    if (rows == 0 || width == 0) return 0;
+    float* out = (float*)malloc(rows * width * sizeof(float));
+    if (!out) return -2;
+    for (size_t p = 0; p < rows; ++p) {
+        for (size_t o = 0; o < width; ++o) {
+            float value = bias[o];
+            for (size_t i = 0; i < width; ++i) {
+                for (size_t k = 0; k < 3; ++k) {
+                    const long ip = (long)p + (long)k - 1;
+                    if (ip < 0 || ip >= (long)rows) continue;
+                    const float prod = weight[o * width * 3 + i * 3 + k] * input[(size_t)ip * width + i];
+                    value = value + prod;
+                }
+            }
+            out[p * width + o] = input[p * width + o] + value;
+        }
+    }
+    memcpy(input, out, rows * width * sizeof(float));
+    free(out);
     return 0;
 }

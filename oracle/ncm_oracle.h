@@ -158,6 +158,13 @@ void ncmo_attention_core(const float* queries, const float* keys, const float* v
                          const uint8_t* mask, float* context, size_t tokens, size_t q_heads,
                          size_t kv_heads, size_t head_dim, int bf16);
 
+/* NCM body helpers. */
+void ncmo_silu(const float* x, float* out, size_t n);
+int ncmo_fill_level_positions(size_t prefix_length, const size_t* level_lengths, size_t levels,
+                              int64_t* positions, size_t positions_len);
+int ncmo_post_upsample_conv(float* input, const float* weight, const float* bias, size_t rows,
+                            size_t width);
+
 #ifdef __cplusplus
 }
 #endif

@@ -82,6 +82,9 @@ def lib():
         L.ncmo_rope_llama3.argtypes = [sz, C.c_float, C.c_float, C.c_float, C.c_float, sz, f32p]
         L.ncmo_rope_tables.argtypes = [f32p, sz, sz, f32p, f32p]
         L.ncmo_attention_core.argtypes = [f32p, f32p, f32p, u8p, f32p, sz, sz, sz, sz, C.c_int]
+        L.ncmo_silu.argtypes = [f32p, f32p, sz]
+        L.ncmo_fill_level_positions.argtypes = [sz, vp, sz, i64p, sz]
+        L.ncmo_post_upsample_conv.argtypes = [f32p, f32p, f32p, sz, sz]
         _lib = L
     return _lib
 
@@ -385,6 +388,209 @@ def decoder_forward(ids, embed, layers, final_norm, lm_head, cos, sin, q_heads, 
         hidden = round_bf16(hidden + mlp)
     n = rms_norm(hidden, final_norm, eps, bf16=True)
     return matmul_bf16(n, embed if lm_head is None else lm_head)
+
+
+# ------------------------------------------------------------ NCM body
+def silu(x) -> np.ndarray:
+    """kernels.silu, f32 mode (root.zig:255-261)."""
+    a = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(a)
+    lib().ncmo_silu(a.ravel(), out.ravel(), a.size)
+    return out
+
+
+def fill_level_positions(prefix_length: int, level_lengths) -> np.ndarray:
+    """src/ncm_position.zig:11-22: prefix 0 .. P-1, each level from 0."""
+    lv = np.ascontiguousarray(level_lengths, dtype=np.uintp)
+    out = np.empty(prefix_length + int(lv.sum()), np.int64)
+    rc = lib().ncmo_fill_level_positions(prefix_length, lv.ctypes.data_as(C.c_void_p), lv.size,
+                                         out, out.size)
+    if rc:
+        raise ValueError("InvalidPositionBuffer")
+    return out
+
+
+def tables_at_positions(inv, positions):
+    """src/ncm_position.zig:73-118: rope_tables over 0 .. max(positions), then
+    the rows at `positions`."""
+    pos = np.asarray(positions, np.int64)
+    cos, sin = rope_tables(inv, int(pos.max()) + 1 if pos.size else 0)
+    return np.ascontiguousarray(cos[pos]), np.ascontiguousarray(sin[pos])
+
+
+def post_upsample_conv(x, weight, bias) -> np.ndarray:
+    """apply_post_upsample_conv (src/ncm_model.zig:296-326) of one level chunk
+    x [rows, width] with weight [width, width, 3] and bias [width]."""
+    a = np.array(x, np.float32, copy=True, order="C")
+    w = np.ascontiguousarray(weight, np.float32)
+    b = np.ascontiguousarray(bias, np.float32)
+    rows, width = a.shape
+    if w.size != width * width * 3 or b.size != width:
+        raise ValueError("InvalidNcmTensorSize")
+    rc = lib().ncmo_post_upsample_conv(a.ravel(), w.ravel(), b.ravel(), rows, width)
+    if rc:
+        raise ValueError("InvalidNcmTensorSize")
+    return a
+
+
+def block_causal_mask(prefix_length: int, level_lengths, prefix_pad_mask=None):
+    """Block-causal level mask (no reference code: the reference builds only
+    block_diagonal_mask, decision D8): prefix queries see the unpadded prefix
+    keys, and a level-l query sees the unpadded prefix keys and every key of
+    levels 0 .. l. uint8 [S, S]."""
+    lv = [int(n) for n in level_lengths]
+    seq = prefix_length + sum(lv)
+    pad = np.zeros(prefix_length, bool) if prefix_pad_mask is None else \
+        np.asarray(prefix_pad_mask, bool)
+    if pad.size != prefix_length:
+        raise ValueError("InvalidPrefixMask")
+    out = np.zeros((seq, seq), np.uint8)
+    out[:, :prefix_length] = ~pad[None, :]
+    off = prefix_length
+    for n in lv:
+        out[off:off + n, prefix_length:off + n] = 1
+        off += n
+    return out
+
+
+def rms_norm_rows_with_bias(x, weight, bias, epsilon: float, bf16: bool) -> np.ndarray:
+    """src/ncm_norm.zig:22-49: rms_norm of every row, then + bias. bf16 mode:
+    rms_norm_bf16, and the bias add rounded to bf16 as every other tensor op
+    of the bf16 forward (src/decoder.zig:279-282)."""
+    y = rms_norm(x, weight, epsilon, bf16=bf16)
+    if bias is not None:
+        y = y + np.asarray(bias, np.float32)[None, :]
+        if bf16:
+            y = round_bf16(y)
+    return y
+
+
+def ncm_forward(cfg, weights, prefix_ids, prefix_pad_mask, target_inputs, bf16: bool = False,
+                mask: str = "block_diagonal", trace: bool = False):
+    """forward_with_trace of the NCM level-parallel body (src/ncm_model.zig:
+    89-250). bf16=False restates the reference exactly (f32 matmul,
+    attention, RMSNorm and SiLU); bf16=True is the same body in the bf16
+    mode of the source decoder (src/decoder.zig:62-228 with bf16_compute):
+    every projection is matmul_bf16(_bias), norms are rms_norm_bf16, SiLU is
+    silu_bf16 with a rounded product, attention is attention_bf16, and every
+    add (level embedding, norm bias, residual) is rounded to bf16.
+    mask: "block_diagonal" (the reference, src/ncm_mask.zig:10-42) or
+    "block_causal". Returns the final-normalized hidden states [S, hidden]
+    (and the states after the input stage and each layer when trace)."""
+    H = cfg["hidden_size"]
+    vq = cfg["vq_width"]
+    hq, hkv, hd = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
+    inter = cfg["intermediate_size"]
+    eps = cfg["rms_norm_epsilon"]
+    levels = [int(n) for n in cfg["level_lengths"]]
+    P = cfg["prefix_length"]
+    ids = [int(i) for i in prefix_ids]
+    pad = [] if prefix_pad_mask is None else list(prefix_pad_mask)
+    if len(ids) != P:
+        raise ValueError("InvalidPrefixLength")
+    if len(pad) not in (0, P):
+        raise ValueError("InvalidPrefixMask")
+    if not levels:
+        raise ValueError("InvalidNcmMode")
+    if min(H, vq, hd, inter) == 0 or hd % 2 or hq == 0 or hkv == 0 or hq % hkv:
+        raise ValueError("InvalidNcmDimensions")
+    T = sum(levels)
+    S = P + T
+    tgt = np.asarray(target_inputs, np.float32).reshape(-1)
+    if tgt.size != T * vq:
+        raise ValueError("InvalidNcmTensorSize")
+    table = np.asarray(weights["prefix_token_embedding"], np.float32).reshape(-1, vq)
+    l0q = weights.get("l0_queries")
+    if cfg.get("query_level0", False):
+        if l0q is None or np.asarray(l0q).size != levels[0] * vq:
+            raise ValueError("InvalidNcmTensorSize")
+    convs = weights.get("post_upsample_convs") or []
+    if convs and len(convs) != len(levels):
+        raise ValueError("InvalidNcmTensorSize")
+    layers = weights["layers"]
+    if not layers:
+        raise ValueError("InvalidNcmTensorSize")
+
+    rb = round_bf16 if bf16 else (lambda a: np.asarray(a, np.float32))
+
+    def project(x, w, b):
+        if bf16:
+            return matmul_bf16(x, w, b)
+        y = matmul_reference(x, w)
+        return y if b is None else (y + np.asarray(b, np.float32)[None, :]).astype(np.float32)
+
+    projected = np.empty((S, vq), np.float32)
+    for i, t in enumerate(ids):
+        if t >= table.shape[0] or t < 0:
+            raise ValueError("PrefixTokenOutOfRange")
+        projected[i] = table[t]
+    projected[P:] = tgt.reshape(T, vq)
+    if cfg.get("query_level0", False):
+        projected[P:P + levels[0]] = np.asarray(l0q, np.float32).reshape(levels[0], vq)
+    off = P
+    for n, conv in zip(levels, convs):
+        projected[off:off + n] = post_upsample_conv(projected[off:off + n], conv["weight"],
+                                                    conv["bias"])
+        off += n
+    hidden = project(projected, weights["input_projection"], weights["input_projection_bias"])
+    if cfg.get("use_level_encoding", True):
+        emb = np.asarray(weights["level_embedding"], np.float32).reshape(len(levels), H)
+        off = P
+        for l, n in enumerate(levels):
+            hidden[off:off + n] = rb(hidden[off:off + n] + emb[l][None, :])
+            off += n
+    states = [hidden.copy()] if trace else None
+
+    positions = fill_level_positions(P, levels)
+    if cfg.get("rope", "default") == "llama3":
+        inv = rope_llama3(hd, cfg["rope_theta"], cfg.get("rope_factor", 1.0),
+                          cfg.get("rope_low_freq_factor", 1.0),
+                          cfg.get("rope_high_freq_factor", 4.0),
+                          cfg.get("rope_original_max_position_embeddings", 8192))
+    else:
+        inv = rope_default_frequencies(hd, cfg["rope_theta"])
+    cos, sin = tables_at_positions(inv, positions)
+    if cfg.get("source_causal", False):
+        m = causal_mask(S, cfg.get("sliding_window") or 0)
+    elif mask == "block_causal":
+        m = block_causal_mask(P, levels, pad if pad else None)
+    else:
+        m = block_diagonal_mask(P, levels, pad if pad else None)
+
+    qw, kvw = hq * hd, hkv * hd
+    for layer in layers:
+        n = rms_norm_rows_with_bias(hidden, layer["ln_1_weight"], layer.get("ln_1_bias"), eps,
+                                    bf16)
+        wq, bq = np.asarray(layer["fused_qkv_weight"], np.float32), layer.get("fused_qkv_bias")
+        sl = lambda lo, hi: (wq[lo:hi], None if bq is None else np.asarray(bq)[lo:hi])
+        q = project(n, *sl(0, qw))
+        k = project(n, *sl(qw, qw + kvw))
+        v = project(n, *sl(qw + kvw, qw + 2 * kvw))
+        if layer.get("query_norm_weight") is not None:
+            q = rms_norm(q.reshape(S * hq, hd), layer["query_norm_weight"], eps,
+                         bf16=bf16).reshape(S, qw)
+            k = rms_norm(k.reshape(S * hkv, hd), layer["key_norm_weight"], eps,
+                         bf16=bf16).reshape(S, kvw)
+        q = rotate_heads(q, cos, sin, hq, hd, bf16=bf16)
+        k = rotate_heads(k, cos, sin, hkv, hd, bf16=bf16)
+        ctx = attention_core(q, k, v, m, hq, hkv, hd, bf16=bf16)
+        attn = project(ctx, layer["output_weight"], layer.get("output_bias"))
+        hidden = rb(hidden + attn)
+        n = rms_norm_rows_with_bias(hidden, layer["ln_2_weight"], layer.get("ln_2_bias"), eps,
+                                    bf16)
+        gate = project(n, layer["gate_weight"], layer.get("gate_bias"))
+        up = project(n, layer["up_weight"], layer.get("up_bias"))
+        act = silu_mul_bf16(gate, up) if bf16 else (silu(gate) * up).astype(np.float32)
+        mlp = project(act, layer["down_weight"], layer.get("down_bias"))
+        hidden = rb(hidden + mlp)
+        if trace:
+            states.append(hidden.copy())
+    out = rms_norm_rows_with_bias(hidden, weights["final_norm_weight"],
+                                  weights.get("final_norm_bias"), eps, bf16)
+    if trace:
+        states[-1] = out
+        return out, states
+    return out
 
 
 # ------------------------------------------------------------ safetensors
