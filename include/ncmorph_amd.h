@@ -318,6 +318,14 @@ typedef struct ncm_decoder_layer {
     const uint16_t* gate_up_bias;      /* [2 intermediate] or NULL, interleaved */
     const uint16_t* down_weight;       /* [hidden, intermediate] */
     const uint16_t* down_bias;         /* [hidden] or NULL */
+    /* QK-norm scales (Qwen3, root.zig:501-530): rms_norm_bf16 of every q and
+     * k head before the rotation; both NULL or both float [head_dim]. */
+    const float* q_norm;
+    const float* k_norm;
+    /* Norm biases (rms_norm_rows_with_bias, src/ncm_norm.zig:22-49): float
+     * [hidden] added (and rounded to bf16) after the norm, or NULL. */
+    const float* input_norm_bias;
+    const float* post_attention_norm_bias;
 } ncm_decoder_layer_t;
 
 /* Bf16 prefill forward of `batch` sequences of seq_len tokens each (the
@@ -330,14 +338,91 @@ typedef struct ncm_decoder_layer {
  * [seq_len, head_dim] RoPE tables (rope_tables layout, root.zig:328-348,
  * built on the host with the system libm as the reference does). logits:
  * float [batch * seq_len, vocab] (bf16 values, token-major). Intermediates
- * live in the context's workspace. No QK norm (Llama / Mistral / Qwen2
- * layouts). Linear outputs, scores and P V are summed in MFMA order, so
- * logits agree with the reference within bf16 tolerance, not bit for bit. */
+ * live in the context's workspace. A layer with q_norm / k_norm applies the
+ * QK-norm (Qwen3 layouts). Linear outputs, scores and P V are summed in MFMA
+ * order, so logits agree with the reference within bf16 tolerance, not bit
+ * for bit. */
 int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
                             const ncm_decoder_layer_t* layers, const uint16_t* embed,
                             const float* final_norm, const uint16_t* lm_head,
                             const float* cosine, const float* sine, const int64_t* token_ids,
                             int64_t batch, int64_t seq_len, float* logits);
+
+/* ---- NCM level-parallel body (src/ncm_model.zig) ---- */
+
+#define NCM_MAX_LEVELS 32
+
+/* Attention pattern of the NCM body. */
+enum {
+    NCM_MASK_BLOCK_DIAGONAL = 0, /* the reference's block_diagonal_mask
+                                    (src/ncm_mask.zig:10-42, decision D8):
+                                    prefix keys (unpadded) and the own level */
+    NCM_MASK_BLOCK_CAUSAL = 1,   /* unpadded prefix keys and every level up to
+                                    and including the query's own */
+    NCM_MASK_CAUSAL = 2          /* config.source_causal: causal over the
+                                    sequence, optional sliding window */
+};
+
+/* config_t (src/ncm_model.zig:15-35) without the RoPE fields (the tables
+ * come precomputed) and with the mask choice. */
+typedef struct ncm_ncm_shape {
+    int64_t hidden;         /* hidden_size, % 8 == 0 */
+    int64_t vq_width;       /* vq_width, % 8 == 0 */
+    int64_t intermediate;   /* intermediate_size, % 32 == 0 */
+    int32_t q_heads;        /* num_attention_heads */
+    int32_t kv_heads;       /* num_key_value_heads */
+    int32_t head_dim;       /* 64 or 128 */
+    int32_t layers;         /* >= 1 */
+    int64_t prefix_length;
+    int64_t prefix_vocab;   /* rows of prefix_token_embedding */
+    int32_t n_levels;       /* 1 .. NCM_MAX_LEVELS */
+    int32_t mask_mode;      /* NCM_MASK_* */
+    int32_t query_level0;   /* nonzero: l0_queries replace level 0's inputs */
+    int32_t use_level_encoding; /* nonzero: add level_embedding */
+    int64_t window;         /* sliding window of NCM_MASK_CAUSAL, 0 = none */
+    float rms_eps;          /* rms_norm_epsilon */
+    int32_t reserved;       /* 0 */
+    int64_t level_lengths[NCM_MAX_LEVELS];
+} ncm_ncm_shape_t;
+
+/* weights_t (src/ncm_model.zig:61-72) on the device, bf16 bits unless
+ * stated. conv_weight / conv_bias: HOST arrays [n_levels] of device float
+ * pointers ([vq_width, vq_width, 3] in the reference's [out][in][tap] order,
+ * and [vq_width]) for post_upsample_convs, or both NULL for none. */
+typedef struct ncm_ncm_weights {
+    const uint16_t* prefix_token_embedding; /* [prefix_vocab, vq_width] */
+    const uint16_t* input_projection;       /* [hidden, vq_width] */
+    const uint16_t* input_projection_bias;  /* [hidden] */
+    const uint16_t* level_embedding;        /* [n_levels, hidden] */
+    const uint16_t* l0_queries;             /* [level_lengths[0], vq_width] or NULL */
+    const float* final_norm;                /* [hidden] */
+    const float* final_norm_bias;           /* [hidden] or NULL */
+    const float* const* conv_weight;
+    const float* const* conv_bias;
+} ncm_ncm_weights_t;
+
+/* The NCM body forward (forward_with_trace without the trace,
+ * src/ncm_model.zig:89-250) for one prefix and one target sequence, in the
+ * bf16 mode of the source decoder: bf16 projections with fp32 accumulation
+ * (operands rounded and flushed as matmul_bf16 does), rms_norm_bf16,
+ * silu_bf16, bf16 attention, every add rounded to bf16; the convolutions
+ * run in fp32. prefix_ids: HOST int64 [prefix_length], each < prefix_vocab
+ * (else NCM_E_ARG, PrefixTokenOutOfRange). prefix_pad_mask: HOST uint8
+ * [pad_len], pad_len 0 or prefix_length (else NCM_E_LENGTH,
+ * InvalidPrefixMask). target_inputs: float [sum level_lengths, vq_width].
+ * layers: HOST array [layers] (ncm_decoder_layer_t: fused q|k|v rows, gate
+ * and up rows interleaved in groups of 32, optional QK-norm and norm biases
+ * as ln_1_bias / ln_2_bias). cosine, sine: float [S, head_dim], S =
+ * prefix_length + sum level_lengths, the RoPE tables gathered at the
+ * positions of fill_level_positions (src/ncm_position.zig:11-118).
+ * output: float [S, hidden] (bf16 values), the final-normalized hidden
+ * states in [prefix | levels] order. Intermediates live in the context's
+ * workspace. */
+int ncm_ncm_forward_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
+                        const ncm_decoder_layer_t* layers, const ncm_ncm_weights_t* weights,
+                        const int64_t* prefix_ids, const uint8_t* prefix_pad_mask,
+                        int64_t pad_len, const float* target_inputs, const float* cosine,
+                        const float* sine, float* output);
 
 /* ---- multiscale residual vector quantization ---- */
 

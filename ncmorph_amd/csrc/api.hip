@@ -14,6 +14,7 @@
 #include "../../include/ncmorph_amd.h"
 #include "decoder.h"
 #include "linear.h"
+#include "ncm_body.h"
 #include "rvq.h"
 #include "status.h"
 
@@ -526,6 +527,24 @@ int ncm_block_diagonal_segments(int64_t prefix_len, const int64_t* level_lengths
     return NCM_OK;
 }
 
+namespace {
+// Every layer's required weights present and 16-byte aligned; QK-norm scales
+// come in pairs (attention_impl asserts, root.zig:464).
+int check_layers(const ncm_decoder_layer_t* layers, int n) {
+    for (int l = 0; l < n; ++l) {
+        const ncm_decoder_layer_t& L = layers[l];
+        if (!L.input_norm || !L.qkv_weight || !L.o_weight || !L.post_attention_norm ||
+            !L.gate_up_weight || !L.down_weight)
+            return NCM_E_NULL;
+        if (!L.q_norm != !L.k_norm) return NCM_E_NULL;
+        if ((uintptr_t)L.qkv_weight % 16 || (uintptr_t)L.o_weight % 16 ||
+            (uintptr_t)L.gate_up_weight % 16 || (uintptr_t)L.down_weight % 16)
+            return NCM_E_ARG;
+    }
+    return NCM_OK;
+}
+}  // namespace
+
 int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
                             const ncm_decoder_layer_t* layers, const uint16_t* embed,
                             const float* final_norm, const uint16_t* lm_head,
@@ -547,18 +566,11 @@ int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
     if (!embed || !final_norm || !cosine || !sine || !token_ids || !logits) return NCM_E_NULL;
     if (s.layers > 0 && !layers) return NCM_E_NULL;
     if ((uintptr_t)embed % 16 || (lm_head && (uintptr_t)lm_head % 16)) return NCM_E_ARG;
-    for (int l = 0; l < s.layers; ++l) {
-        const ncm_decoder_layer_t& L = layers[l];
-        if (!L.input_norm || !L.qkv_weight || !L.o_weight || !L.post_attention_norm ||
-            !L.gate_up_weight || !L.down_weight)
-            return NCM_E_NULL;
-        if ((uintptr_t)L.qkv_weight % 16 || (uintptr_t)L.o_weight % 16 ||
-            (uintptr_t)L.gate_up_weight % 16 || (uintptr_t)L.down_weight % 16)
-            return NCM_E_ARG;
-    }
+    int rc = check_layers(layers, s.layers);
+    if (rc) return rc;
     for (int64_t i = 0; i < batch * seq_len; ++i)
         if (token_ids[i] < 0 || token_ids[i] >= s.vocab) return NCM_E_ARG;  // TokenIdOutOfRange
-    int rc = ctx_bind(ctx);
+    rc = ctx_bind(ctx);
     if (rc) return rc;
     void* ws = nullptr;
     rc = ncm_ctx_workspace(ctx, ncm::decoder_workspace_bytes(s, batch, seq_len), &ws);
@@ -566,6 +578,68 @@ int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
     hipError_t e = ncm::decoder_forward(s, layers, embed, final_norm, lm_head, cosine, sine,
                                         token_ids, batch, seq_len, logits, ws, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "decoder forward");
+    return NCM_OK;
+}
+
+// The checks of forward_with_trace (src/ncm_model.zig:99-123) in its order,
+// then the device path's own limits.
+int ncm_ncm_forward_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
+                        const ncm_decoder_layer_t* layers, const ncm_ncm_weights_t* weights,
+                        const int64_t* prefix_ids, const uint8_t* prefix_pad_mask,
+                        int64_t pad_len, const float* target_inputs, const float* cosine,
+                        const float* sine, float* output) {
+    if (!ctx || !shape || !weights) return NCM_E_NULL;
+    const ncm_ncm_shape_t& s = *shape;
+    if (s.prefix_length < 0 || s.n_levels < 0 || s.n_levels > NCM_MAX_LEVELS) return NCM_E_SHAPE;
+    if (pad_len != 0 && pad_len != s.prefix_length) return NCM_E_LENGTH;  // InvalidPrefixMask
+    if (s.n_levels == 0) return NCM_E_ARG;                                // InvalidNcmMode
+    if (s.hidden <= 0 || s.vq_width <= 0 || s.head_dim <= 0 || s.intermediate <= 0 ||
+        s.q_heads <= 0 || s.kv_heads <= 0 || s.head_dim % 2 || s.q_heads % s.kv_heads)
+        return NCM_E_SHAPE;  // InvalidNcmDimensions
+    if (s.layers <= 0) return NCM_E_LENGTH;  // weights.layers.len == 0: InvalidNcmTensorSize
+    if (s.mask_mode < NCM_MASK_BLOCK_DIAGONAL || s.mask_mode > NCM_MASK_CAUSAL || s.window < 0)
+        return NCM_E_ARG;
+    int64_t S = s.prefix_length;
+    for (int l = 0; l < s.n_levels; ++l) {
+        if (s.level_lengths[l] < 0 || __builtin_add_overflow(S, s.level_lengths[l], &S))
+            return NCM_E_SHAPE;
+    }
+    // Device limits: the attention kernel's head widths, 16-byte rows.
+    if (s.head_dim != 64 && s.head_dim != 128) return NCM_E_SHAPE;
+    if (s.hidden % 8 || s.vq_width % 8 || s.intermediate % 32) return NCM_E_SHAPE;
+    if (S > (int64_t(1) << 30) || s.hidden > (int64_t(1) << 21) ||
+        s.vq_width > (int64_t(1) << 19) || s.intermediate > (int64_t(1) << 20) ||
+        (int64_t)s.q_heads * s.head_dim > (int64_t(1) << 21))
+        return NCM_E_SHAPE;
+    if (S == s.prefix_length) return NCM_E_ARG;  // no target position
+    const bool convs = weights->conv_weight || weights->conv_bias;
+    if (!weights->prefix_token_embedding && s.prefix_length > 0) return NCM_E_NULL;
+    if (!weights->input_projection || !weights->input_projection_bias || !weights->final_norm)
+        return NCM_E_NULL;
+    if (s.use_level_encoding && !weights->level_embedding) return NCM_E_NULL;
+    if (s.query_level0 && !weights->l0_queries && s.level_lengths[0] > 0) return NCM_E_NULL;
+    if (convs) {
+        if (!weights->conv_weight || !weights->conv_bias) return NCM_E_NULL;
+        for (int l = 0; l < s.n_levels; ++l)
+            if (!weights->conv_weight[l] || !weights->conv_bias[l]) return NCM_E_NULL;
+    }
+    if (!target_inputs || !cosine || !sine || !output || !layers) return NCM_E_NULL;
+    if (pad_len > 0 && !prefix_pad_mask) return NCM_E_NULL;
+    if (s.prefix_length > 0 && !prefix_ids) return NCM_E_NULL;
+    if ((uintptr_t)weights->input_projection % 16) return NCM_E_ARG;
+    int rc = check_layers(layers, s.layers);
+    if (rc) return rc;
+    for (int64_t i = 0; i < s.prefix_length; ++i)
+        if (prefix_ids[i] < 0 || prefix_ids[i] >= s.prefix_vocab)
+            return NCM_E_ARG;  // PrefixTokenOutOfRange
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::ncm_workspace_bytes(s, convs), &ws);
+    if (rc) return rc;
+    hipError_t e = ncm::ncm_forward(s, layers, *weights, prefix_ids, prefix_pad_mask, pad_len,
+                                    target_inputs, cosine, sine, output, ws, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "ncm forward");
     return NCM_OK;
 }
 

@@ -10,6 +10,31 @@ namespace ncm {
 
 size_t decoder_workspace_bytes(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq);
 
+// The layer stack of the bf16 forward over `batch` sequences of `seq` rows:
+// hidden [batch * seq, hidden] fp32 (bf16 values) is updated in place.
+// Attention: causal with shape->window, or, when seg_lo is set, the prefix +
+// level-block mask of ncm_attention_bf16_seg_dev. cosine / sine: [seq,
+// head_dim], table row = row % seq. Scratch: normed [rows, hidden], qkv
+// [rows, (q_heads + 2 kv_heads) head_dim], ctx [rows, q_heads head_dim], act
+// [rows, intermediate], all bf16 bits.
+struct LayerStack {
+    const ncm_decoder_shape_t* shape;
+    const ncm_decoder_layer_t* layers;  // host array [shape->layers]
+    int64_t batch, seq;
+    const float* cosine;
+    const float* sine;
+    int64_t prefix;
+    const int32_t* seg_lo;
+    const int32_t* seg_hi;
+    const uint64_t* pad;
+    float* hidden;
+    uint16_t* normed;
+    uint16_t* qkv;
+    uint16_t* ctx;
+    uint16_t* act;
+};
+hipError_t run_layers(const LayerStack& a, hipStream_t st);
+
 // All pointers device memory except `layers` (host array) and `host_ids`.
 hipError_t decoder_forward(const ncm_decoder_shape_t& s, const ncm_decoder_layer_t* layers,
                            const uint16_t* embed, const float* final_norm,

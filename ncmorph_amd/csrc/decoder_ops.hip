@@ -18,22 +18,12 @@ namespace ncm {
 // (n % 4 == 0, n <= kRmsStageMax), and both passes read it from there.
 constexpr int64_t kRmsStageMax = 8192;
 
-template <int OUT_MODE, bool STAGE>
-__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restrict__ x,
-                                                            const float* __restrict__ weight,
-                                                            void* __restrict__ y, int64_t rows,
-                                                            int64_t n, float epsilon) {
-    extern __shared__ __attribute__((aligned(16))) float stage[];
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
-    const float* xr = x + row * n;
-    if (STAGE) {
-        float* sr = stage + (threadIdx.x >> 6) * n;
-        for (int64_t i = 4 * lane; i < n; i += 256) *(f32x4_t*)(sr + i) = *(const f32x4_t*)(xr + i);
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // this wave's row is in LDS
-        xr = sr;
-    }
+// The pinned sum of squares of one row (root.zig:152-227) by one
+// wavefront: lane c < 32 runs chain (r = c / 8, l = c % 8) with its four
+// levels in registers, and the merges that cross chains run in the
+// reference's order on values gathered by shuffles. Every lane returns the
+// same bits. xr: the row in global memory or LDS.
+__device__ __forceinline__ float rms_sum_squares(const float* xr, int64_t n, int lane) {
     const bool chain = lane < 32;
     const int r = (lane >> 3) & 3, l = lane & 7;
 
@@ -91,6 +81,26 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) sum = sum + __shfl(vs, k, 64);
+    return sum;
+}
+
+template <int OUT_MODE, bool STAGE>
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ weight,
+                                                            void* __restrict__ y, int64_t rows,
+                                                            int64_t n, float epsilon) {
+    extern __shared__ __attribute__((aligned(16))) float stage[];
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + row * n;
+    if (STAGE) {
+        float* sr = stage + (threadIdx.x >> 6) * n;
+        for (int64_t i = 4 * lane; i < n; i += 256) *(f32x4_t*)(sr + i) = *(const f32x4_t*)(xr + i);
+        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // this wave's row is in LDS
+        xr = sr;
+    }
+    const float sum = rms_sum_squares(xr, n, lane);
     const float mean = sum / (float)n;
     const float inv = 1.0f / sqrtf(mean + epsilon);
 
@@ -247,6 +257,74 @@ hipError_t launch_rope_rotate(uint16_t* x, int64_t rows, int64_t row_stride, int
     const int64_t n = rows * heads * (hd / 2);
     hipLaunchKernelGGL(rope_rotate_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                        x, rows, row_stride, heads, hd, seq_len, cosine, sine);
+    return hipGetLastError();
+}
+
+// QK-norm of the bf16 attention (root.zig:501-530): rms_norm_bf16 of every
+// head_dim-wide head of the q (or k) columns, in place on bf16 bits, before
+// the rotation. One wavefront per (row, head); the head is widened into LDS
+// and reduced with the pinned cascade, as rms_norm_bf16 does for a vector of
+// head_dim values.
+__global__ __launch_bounds__(256) void qk_norm_kernel(uint16_t* __restrict__ x, int64_t rows,
+                                                      int64_t row_stride, int heads, int hd,
+                                                      const float* __restrict__ weight,
+                                                      float epsilon) {
+    __shared__ float stage[4][256];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t item = (int64_t)blockIdx.x * 4 + wave;
+    if (item >= rows * heads) return;
+    const int64_t r = item / heads;
+    const int h = (int)(item % heads);
+    uint16_t* e = x + r * row_stride + (int64_t)h * hd;
+    float* sr = stage[wave];
+    for (int i = lane; i < hd; i += 64) sr[i] = __uint_as_float((uint32_t)e[i] << 16);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    const float sum = rms_sum_squares(sr, hd, lane);
+    const float mean = sum / (float)hd;
+    const float inv = 1.0f / sqrtf(mean + epsilon);
+    for (int i = lane; i < hd; i += 64) {
+        const float normalized = __uint_as_float(bf16_bits_rne(sr[i] * inv) << 16);
+        e[i] = (uint16_t)bf16_bits_rne(normalized *
+                                       __uint_as_float(bf16_bits_rne(weight[i]) << 16));
+    }
+}
+
+hipError_t launch_qk_norm(uint16_t* x, int64_t rows, int64_t row_stride, int heads, int hd,
+                          const float* weight, float epsilon, hipStream_t stream) {
+    if (hd > 256) return hipErrorInvalidValue;
+    const int64_t items = rows * heads;
+    hipLaunchKernelGGL(qk_norm_kernel, dim3((unsigned)((items + 3) / 4)), dim3(256), 0, stream, x,
+                       rows, row_stride, heads, hd, weight, epsilon);
+    return hipGetLastError();
+}
+
+// y = round_bf16(y + bias[column]) in place over [rows, n]: the bias of
+// rms_norm_rows_with_bias (src/ncm_norm.zig:22-49) in bf16 mode, on bf16 bits
+// (BITS) or on floats holding bf16 values.
+template <bool BITS>
+__global__ __launch_bounds__(256) void bias_round_kernel(void* __restrict__ y,
+                                                         const float* __restrict__ bias,
+                                                         int64_t rows, int64_t n) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= rows * n) return;
+    const float b = bias[i % n];
+    if (BITS) {
+        uint16_t* p = (uint16_t*)y + i;
+        *p = (uint16_t)bf16_bits_rne(__uint_as_float((uint32_t)*p << 16) + b);
+    } else {
+        float* p = (float*)y + i;
+        *p = __uint_as_float(bf16_bits_rne(*p + b) << 16);
+    }
+}
+
+hipError_t launch_bias_round(void* y, const float* bias, int64_t rows, int64_t n, bool bits,
+                             hipStream_t stream) {
+    const int64_t total = rows * n;
+    const dim3 grid((unsigned)((total + 255) / 256));
+    if (bits)
+        hipLaunchKernelGGL(bias_round_kernel<true>, grid, dim3(256), 0, stream, y, bias, rows, n);
+    else
+        hipLaunchKernelGGL(bias_round_kernel<false>, grid, dim3(256), 0, stream, y, bias, rows, n);
     return hipGetLastError();
 }
 

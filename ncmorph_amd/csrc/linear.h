@@ -40,6 +40,13 @@ hipError_t launch_linear_f32(const float* x, const float* w, float* y, int64_t M
 // NCM_OUT_BF16_F32 (f32 holding bf16 values) or NCM_OUT_BF16 (bits).
 hipError_t launch_rms_norm_rows(const float* x, const float* weight, void* y, int64_t rows,
                                 int64_t n, float epsilon, int out_mode, hipStream_t stream);
+// QK-norm (rms_norm_bf16 per head, in place on bf16 bits; hd <= 256).
+hipError_t launch_qk_norm(uint16_t* x, int64_t rows, int64_t row_stride, int heads, int hd,
+                          const float* weight, float epsilon, hipStream_t stream);
+// y = round_bf16(y + bias[column]) in place over [rows, n] (bits: bf16 bits,
+// else floats holding bf16 values).
+hipError_t launch_bias_round(void* y, const float* bias, int64_t rows, int64_t n, bool bits,
+                             hipStream_t stream);
 // y = round_bf16(silu_bf16(gate) * up) (up NULL: silu_bf16(gate) alone).
 hipError_t launch_silu_mul(const float* gate, const float* up, void* y, int64_t n, int out_mode,
                            hipStream_t stream);

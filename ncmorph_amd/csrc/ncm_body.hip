@@ -1,0 +1,264 @@
+// The NCM level-parallel body (forward_with_trace, src/ncm_model.zig:89-250)
+// in the bf16 mode of the source decoder, on one GPU:
+//   rows     = [prefix_token_embedding[ids] | target_inputs], level 0's rows
+//              replaced by l0_queries when query_level0        (fp32)
+//   rows    += Conv1d(rows) per level, when convolutions are given
+//              (apply_post_upsample_conv, :296-326; fp32 on the fp32 MFMA)
+//   h        = round(bf16(rows) W_in^T + bias)     (matmul_bf16_bias, flushed operands)
+//   h[level] = round(h + level_embedding[level])   (use_level_encoding)
+//   h        = the decoder's bf16 layer stack (run_layers) with the block-
+//              diagonal (reference) or block-causal level mask, or the causal
+//              one (source_causal), RoPE at positions restarting per level
+//   out      = rms_norm_bf16(h, final_norm) (+ bias, rounded)
+// The reference runs this body in f32 (kernels.matmul, f32 attention); the
+// bf16 rules are those decoder.zig applies with bf16_compute.
+#include <hip/hip_runtime.h>
+
+#include <vector>
+
+#include "common.h"
+#include "decoder.h"
+#include "linear.h"
+#include "ncm_body.h"
+
+namespace ncm {
+
+// out[r] (fp32, width vq): the prefix table row of ids[r] (r < P), a
+// learned level-0 query (P <= r < P + l0_rows), else target row r - P.
+__global__ __launch_bounds__(256) void ncm_input_rows_kernel(
+    const int64_t* __restrict__ ids, const uint16_t* __restrict__ table,
+    const uint16_t* __restrict__ l0, const float* __restrict__ target, float* __restrict__ out,
+    int64_t P, int64_t l0_rows, int64_t S, int64_t vq) {
+    for (int64_t r = blockIdx.y; r < S; r += gridDim.y) {
+        float* dst = out + r * vq;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < vq;
+             i += (int64_t)gridDim.x * 256) {
+            float v;
+            if (r < P)
+                v = __uint_as_float((uint32_t)table[ids[r] * vq + i] << 16);
+            else if (r - P < l0_rows)
+                v = __uint_as_float((uint32_t)l0[(r - P) * vq + i] << 16);
+            else
+                v = target[(r - P) * vq + i];
+            dst[i] = v;
+        }
+    }
+}
+
+// col[p, 3 i + k] = x[p + k - 1, i] (zero outside the level's rows): the
+// 3-tap Conv1d as a product with the reference's [out][in][3] weights.
+__global__ __launch_bounds__(256) void conv_im2col_kernel(const float* __restrict__ x,
+                                                          float* __restrict__ col, int64_t rows,
+                                                          int64_t width) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * width * 3) return;
+    const int64_t p = idx / (3 * width);
+    const int64_t j = idx % (3 * width);
+    const int64_t i = j / 3, k = j % 3;
+    const int64_t src = p + k - 1;
+    col[idx] = (src >= 0 && src < rows) ? x[src * width + i] : 0.0f;
+}
+
+// x = x + (y + bias): the residual of the post-upsample convolution.
+__global__ __launch_bounds__(256) void conv_finish_kernel(float* __restrict__ x,
+                                                          const float* __restrict__ y,
+                                                          const float* __restrict__ bias,
+                                                          int64_t rows, int64_t width) {
+    const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (idx >= rows * width) return;
+    x[idx] = x[idx] + (y[idx] + bias[idx % width]);
+}
+
+struct LevelTableArgs {
+    int64_t begin[kMaxNcmLevels + 1];  // row where each level starts; begin[n] = S
+    int32_t n;
+};
+
+// h[r] = round_bf16(h[r] + level_embedding[level of r]) for target rows.
+__global__ __launch_bounds__(256) void level_embed_kernel(float* __restrict__ h,
+                                                          const uint16_t* __restrict__ emb,
+                                                          LevelTableArgs lt, int64_t H) {
+    for (int64_t r = lt.begin[0] + blockIdx.y; r < lt.begin[lt.n]; r += gridDim.y) {
+        int l = 0;
+        while (l + 1 < lt.n && r >= lt.begin[l + 1]) ++l;
+        float* row = h + r * H;
+        const uint16_t* e = emb + (int64_t)l * H;
+        for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < H;
+             i += (int64_t)gridDim.x * 256)
+            row[i] = __uint_as_float(
+                bf16_bits_rne(row[i] + __uint_as_float((uint32_t)e[i] << 16)) << 16);
+    }
+}
+
+namespace {
+
+constexpr size_t kAlign = 256;
+size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
+
+struct NcmPlan {
+    int64_t S, T, max_level;
+    size_t o_rows, o_rows16, o_col, o_convy, o_hidden, o_normed, o_qkv, o_ctx, o_act, o_ids,
+        o_seg_lo, o_seg_hi, o_pad, total;
+};
+
+NcmPlan ncm_plan(const ncm_ncm_shape_t& s, bool convs) {
+    NcmPlan p{};
+    p.T = 0;
+    p.max_level = 0;
+    for (int l = 0; l < s.n_levels; ++l) {
+        p.T += s.level_lengths[l];
+        if (s.level_lengths[l] > p.max_level) p.max_level = s.level_lengths[l];
+    }
+    p.S = s.prefix_length + p.T;
+    const int64_t qkv_w = (int64_t)(s.q_heads + 2 * s.kv_heads) * s.head_dim;
+    const int64_t q_w = (int64_t)s.q_heads * s.head_dim;
+    size_t off = 0;
+    auto carve = [&](size_t bytes) { const size_t o = off; off += up(bytes); return o; };
+    p.o_rows = carve((size_t)p.S * s.vq_width * 4);
+    p.o_rows16 = carve((size_t)p.S * s.vq_width * 2);
+    p.o_col = carve(convs ? (size_t)p.max_level * 3 * s.vq_width * 4 : 0);
+    p.o_convy = carve(convs ? (size_t)p.max_level * s.vq_width * 4 : 0);
+    p.o_hidden = carve((size_t)p.S * s.hidden * 4);
+    p.o_normed = carve((size_t)p.S * s.hidden * 2);
+    p.o_qkv = carve((size_t)p.S * qkv_w * 2);
+    p.o_ctx = carve((size_t)p.S * q_w * 2);
+    p.o_act = carve((size_t)p.S * s.intermediate * 2);
+    p.o_ids = carve((size_t)(s.prefix_length > 0 ? s.prefix_length : 1) * 8);
+    p.o_seg_lo = carve((size_t)p.S * 4);
+    p.o_seg_hi = carve((size_t)p.S * 4);
+    p.o_pad = carve((size_t)((s.prefix_length + 63) / 64 + 1) * 8);
+    p.total = off;
+    return p;
+}
+
+#define NCM_TRY(call)                                  \
+    do {                                               \
+        hipError_t e_ = (call);                        \
+        if (e_ != hipSuccess) return e_;               \
+    } while (0)
+
+}  // namespace
+
+size_t ncm_workspace_bytes(const ncm_ncm_shape_t& s, bool convs) {
+    return ncm_plan(s, convs).total;
+}
+
+hipError_t ncm_forward(const ncm_ncm_shape_t& s, const ncm_decoder_layer_t* layers,
+                       const ncm_ncm_weights_t& w, const int64_t* host_ids,
+                       const uint8_t* host_pad, int64_t pad_len, const float* target,
+                       const float* cosine, const float* sine, float* output, void* ws,
+                       hipStream_t st) {
+    const bool convs = w.conv_weight != nullptr;
+    const NcmPlan p = ncm_plan(s, convs);
+    char* base = (char*)ws;
+    float* rows = (float*)(base + p.o_rows);
+    uint16_t* rows16 = (uint16_t*)(base + p.o_rows16);
+    int64_t* ids = (int64_t*)(base + p.o_ids);
+    int32_t* seg_lo = (int32_t*)(base + p.o_seg_lo);
+    int32_t* seg_hi = (int32_t*)(base + p.o_seg_hi);
+    uint64_t* pad = (uint64_t*)(base + p.o_pad);
+    const int64_t P = s.prefix_length, S = p.S, vq = s.vq_width, H = s.hidden;
+
+    // Host-built inputs: prefix ids, the level mask's per-position key range
+    // (block-diagonal: the own level; block-causal: every level up to the
+    // own one) and the prefix pad bits. Pageable copies: the host vectors
+    // may go once the calls return.
+    std::vector<int32_t> lo((size_t)S, 0), hi((size_t)S, 0);
+    LevelTableArgs lt{};
+    lt.n = s.n_levels;
+    {
+        int64_t off = P;
+        for (int l = 0; l < s.n_levels; ++l) {
+            lt.begin[l] = off;
+            for (int64_t t = off; t < off + s.level_lengths[l]; ++t) {
+                lo[(size_t)t] = (int32_t)(s.mask_mode == NCM_MASK_BLOCK_CAUSAL ? P : off);
+                hi[(size_t)t] = (int32_t)(off + s.level_lengths[l]);
+            }
+            off += s.level_lengths[l];
+        }
+        lt.begin[s.n_levels] = off;
+    }
+    std::vector<uint64_t> bits((size_t)((P + 63) / 64 + 1), 0ull);
+    for (int64_t t = 0; t < pad_len; ++t)
+        if (host_pad[t]) bits[(size_t)(t / 64)] |= 1ull << (t % 64);
+    if (P > 0) NCM_TRY(hipMemcpyAsync(ids, host_ids, (size_t)P * 8, hipMemcpyHostToDevice, st));
+    const bool levels_mask = s.mask_mode != NCM_MASK_CAUSAL;
+    if (levels_mask) {
+        NCM_TRY(hipMemcpyAsync(seg_lo, lo.data(), (size_t)S * 4, hipMemcpyHostToDevice, st));
+        NCM_TRY(hipMemcpyAsync(seg_hi, hi.data(), (size_t)S * 4, hipMemcpyHostToDevice, st));
+        NCM_TRY(hipMemcpyAsync(pad, bits.data(), bits.size() * 8, hipMemcpyHostToDevice, st));
+    }
+
+    // Input rows (fp32), then the per-level convolutions in place.
+    {
+        const unsigned gx = (unsigned)((vq + 255) / 256 < 16 ? (vq + 255) / 256 : 16);
+        const int64_t l0_rows = s.query_level0 ? s.level_lengths[0] : 0;
+        const unsigned gy = (unsigned)(S < 65535 ? S : 65535);
+        hipLaunchKernelGGL(ncm_input_rows_kernel, dim3(gx, gy), dim3(256), 0, st, ids,
+                           w.prefix_token_embedding, w.l0_queries, target, rows, P, l0_rows, S,
+                           vq);
+        NCM_TRY(hipGetLastError());
+    }
+    if (convs) {
+        float* col = (float*)(base + p.o_col);
+        float* cy = (float*)(base + p.o_convy);
+        for (int l = 0; l < s.n_levels; ++l) {
+            const int64_t n = s.level_lengths[l];
+            if (n == 0) continue;
+            float* x = rows + lt.begin[l] * vq;
+            hipLaunchKernelGGL(conv_im2col_kernel, dim3((unsigned)((n * vq * 3 + 255) / 256)),
+                               dim3(256), 0, st, x, col, n, vq);
+            NCM_TRY(hipGetLastError());
+            NCM_TRY(launch_linear_f32(col, w.conv_weight[l], cy, n, 3 * vq, vq, st));
+            hipLaunchKernelGGL(conv_finish_kernel, dim3((unsigned)((n * vq + 255) / 256)),
+                               dim3(256), 0, st, x, cy, w.conv_bias[l], n, vq);
+            NCM_TRY(hipGetLastError());
+        }
+    }
+    // bf16 operands as matmul_bf16 forms them (RNE, subnormals flushed).
+    NCM_TRY(launch_bf16_from_f32(rows, rows16, S * vq, 1, st));
+
+    LayerStack a{};
+    ncm_decoder_shape_t ds{};
+    ds.hidden = H;
+    ds.intermediate = s.intermediate;
+    ds.vocab = 1;
+    ds.q_heads = s.q_heads;
+    ds.kv_heads = s.kv_heads;
+    ds.head_dim = s.head_dim;
+    ds.layers = s.layers;
+    ds.window = s.mask_mode == NCM_MASK_CAUSAL ? s.window : 0;
+    ds.rms_eps = s.rms_eps;
+    a.shape = &ds;
+    a.layers = layers;
+    a.batch = 1;
+    a.seq = S;
+    a.cosine = cosine;
+    a.sine = sine;
+    a.prefix = P;
+    a.seg_lo = levels_mask ? seg_lo : nullptr;
+    a.seg_hi = levels_mask ? seg_hi : nullptr;
+    a.pad = levels_mask && pad_len > 0 ? pad : nullptr;
+    a.hidden = (float*)(base + p.o_hidden);
+    a.normed = (uint16_t*)(base + p.o_normed);
+    a.qkv = (uint16_t*)(base + p.o_qkv);
+    a.ctx = (uint16_t*)(base + p.o_ctx);
+    a.act = (uint16_t*)(base + p.o_act);
+
+    NCM_TRY(launch_linear(rows16, w.input_projection, w.input_projection_bias, a.hidden, S, vq, H,
+                          NCM_OUT_BF16_F32, -1, st));
+    if (s.use_level_encoding && p.T > 0) {
+        const unsigned gx = (unsigned)((H + 255) / 256 < 16 ? (H + 255) / 256 : 16);
+        const unsigned gy = (unsigned)(p.T < 65535 ? p.T : 65535);
+        hipLaunchKernelGGL(level_embed_kernel, dim3(gx, gy), dim3(256), 0, st, a.hidden,
+                           w.level_embedding, lt, H);
+        NCM_TRY(hipGetLastError());
+    }
+    NCM_TRY(run_layers(a, st));
+    NCM_TRY(launch_rms_norm_rows(a.hidden, w.final_norm, output, S, H, s.rms_eps,
+                                 NCM_OUT_BF16_F32, st));
+    if (w.final_norm_bias) NCM_TRY(launch_bias_round(output, w.final_norm_bias, S, H, false, st));
+    return hipSuccess;
+}
+
+}  // namespace ncm

@@ -18,7 +18,7 @@ from dataclasses import dataclass, field
 import numpy as np
 
 from . import _check as _ck
-from ._lib import check, lib
+from ._lib import NcmError, check, lib
 from .context import default_context
 
 
@@ -58,11 +58,37 @@ class _Shape(C.Structure):
 
 _LAYER_FIELDS = ("input_norm", "qkv_weight", "qkv_bias", "o_weight", "o_bias",
                  "post_attention_norm", "gate_up_weight", "gate_up_bias", "down_weight",
-                 "down_bias")
+                 "down_bias", "q_norm", "k_norm", "input_norm_bias",
+                 "post_attention_norm_bias")
 
 
 class _Layer(C.Structure):
     _fields_ = [(n, C.c_void_p) for n in _LAYER_FIELDS]
+
+
+def check_layer(a, L, spec, prefix=""):
+    """Name one layer's tensors on the argument checker `a` (dtype and exact
+    shape from spec: hidden, intermediate, q_heads, kv_heads, head_dim)."""
+    H, I, hd = spec.hidden, spec.intermediate, spec.head_dim
+    qkv, qw = (spec.q_heads + 2 * spec.kv_heads) * hd, spec.q_heads * hd
+    n = lambda f: prefix + f
+    a.dev(L.get("input_norm"), n("input_norm"), _ck.F32, (H,))
+    a.dev(L.get("qkv_weight"), n("qkv_weight"), _ck.BF16, (qkv, H))
+    a.dev(L.get("qkv_bias"), n("qkv_bias"), _ck.BF16, (qkv,), optional=True)
+    a.dev(L.get("o_weight"), n("o_weight"), _ck.BF16, (H, qw))
+    a.dev(L.get("o_bias"), n("o_bias"), _ck.BF16, (H,), optional=True)
+    a.dev(L.get("post_attention_norm"), n("post_attention_norm"), _ck.F32, (H,))
+    a.dev(L.get("gate_up_weight"), n("gate_up_weight"), _ck.BF16, (2 * I, H))
+    a.dev(L.get("gate_up_bias"), n("gate_up_bias"), _ck.BF16, (2 * I,), optional=True)
+    a.dev(L.get("down_weight"), n("down_weight"), _ck.BF16, (H, I))
+    a.dev(L.get("down_bias"), n("down_bias"), _ck.BF16, (H,), optional=True)
+    if (L.get("q_norm") is None) != (L.get("k_norm") is None):
+        raise NcmError(-1, a.where, n("q_norm and k_norm come together"))
+    a.dev(L.get("q_norm"), n("q_norm"), _ck.F32, (hd,), optional=True)
+    a.dev(L.get("k_norm"), n("k_norm"), _ck.F32, (hd,), optional=True)
+    a.dev(L.get("input_norm_bias"), n("input_norm_bias"), _ck.F32, (H,), optional=True)
+    a.dev(L.get("post_attention_norm_bias"), n("post_attention_norm_bias"), _ck.F32, (H,),
+          optional=True)
 
 
 @dataclass
@@ -197,6 +223,13 @@ def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine,
     if logits is None:
         logits = torch.empty((batch * seq, spec.vocab), dtype=torch.float32, device=dev)
     a.dev(logits, "logits", _ck.F32, (batch * seq, spec.vocab))
+    a.dev(weights.embed, "embed", _ck.BF16, (spec.vocab, spec.hidden))
+    a.dev(weights.lm_head, "lm_head", _ck.BF16, (spec.vocab, spec.hidden), optional=True)
+    a.dev(weights.final_norm, "final_norm", _ck.F32, (spec.hidden,))
+    if len(weights.layers) != spec.layers:
+        raise NcmError(-3, W, "one weight dict per layer")
+    for i, layer in enumerate(weights.layers):
+        check_layer(a, layer, spec, f"layers[{i}].")
     shape = _Shape(spec.hidden, spec.intermediate, spec.vocab, spec.q_heads, spec.kv_heads,
                    spec.head_dim, spec.layers, spec.window, spec.rms_eps)
     arr = (_Layer * max(1, spec.layers))()

@@ -1,0 +1,203 @@
+"""GPU NCM level-parallel body (ncm_ncm_forward_dev) against the oracle's
+bf16-mode composition (oracle.ncm_forward, pinned by the reference's
+invariant test and an f64 forward), and the reference's invariants on the
+device, at small shapes and at the Llama-3-8B shape with 8 levels of a
+4096-position sequence.
+
+Bar: the final-normalized states agree with the oracle within 3% of their
+largest magnitude (max) and 0.3% (mean): the GPU sums projections, scores
+and P V in MFMA order, so intermediate bf16 roundings differ from the
+oracle's now and then and the differences travel through the layers. The
+reference's invariants hold bit for bit on the device."""
+import numpy as np
+import pytest
+
+from .ncm_f64 import random_ncm
+
+pytestmark = pytest.mark.gpu
+
+
+def _spec(ncm, levels, P, hidden, vq, hq, hkv, hd, inter, layers, mask, vocab, window=0,
+          query_level0=True):
+    return ncm.NcmSpec(hidden=hidden, vq_width=vq, intermediate=inter, q_heads=hq,
+                       kv_heads=hkv, head_dim=hd, layers=layers, level_lengths=tuple(levels),
+                       prefix_length=P, prefix_vocab=vocab, query_level0=query_level0,
+                       mask=mask, window=window, rope_theta=10000.0, rope_llama3=None)
+
+
+def _oracle_cfg(spec):
+    return dict(hidden_size=spec.hidden, vq_width=spec.vq_width,
+                num_attention_heads=spec.q_heads, num_key_value_heads=spec.kv_heads,
+                head_dim=spec.head_dim, intermediate_size=spec.intermediate,
+                rms_norm_epsilon=spec.rms_eps, level_lengths=list(spec.level_lengths),
+                prefix_length=spec.prefix_length, query_level0=spec.query_level0,
+                rope="default", rope_theta=spec.rope_theta,
+                source_causal=spec.mask == "causal", sliding_window=spec.window or None)
+
+
+def _run(ncm, torch, cuda, spec, dw, ids, tgt, pad=None):
+    cos, sin = ncm.rope_tables(spec)
+    out = ncm.forward(spec, dw, ids, torch.from_numpy(tgt).to(cuda),
+                      torch.from_numpy(cos).to(cuda), torch.from_numpy(sin).to(cuda),
+                      prefix_pad_mask=pad)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+CASES = [
+    # (mask, head_dim, extras, window, query_level0, pad)
+    ("block_diagonal", 64, {}, 0, True, True),
+    ("block_causal", 64, dict(biases=True), 0, True, True),
+    ("block_diagonal", 128, dict(qk_norm=True), 0, False, False),
+    ("block_causal", 128, dict(convs=True, qk_norm=True, biases=True), 0, True, True),
+    ("causal", 64, {}, 0, True, False),
+    ("causal", 128, dict(biases=True), 24, True, False),
+]
+
+
+@pytest.mark.parametrize("mask,hd,extras,window,ql0,use_pad", CASES)
+def test_ncm_body_matches_oracle(cuda, ncm, oracle, mask, hd, extras, window, ql0, use_pad):
+    import torch
+    from ncmorph_amd import ncm as N
+
+    print(f"ncm case mask={mask} hd={hd} extras={extras} window={window}", flush=True)
+    rng = np.random.default_rng(hd + len(extras) + window)
+    levels, P = [8, 16, 32, 64], 12
+    hidden, vq, hq, hkv, inter, nl, vocab = 256, 128, 4, 2, 512, 2, 50
+    spec = _spec(N, levels, P, hidden, vq, hq, hkv, hd, inter, nl, mask, vocab, window, ql0)
+    w = random_ncm(rng, oracle.round_bf16, hidden, vq, inter, hq, hkv, hd, nl, levels, P, vocab,
+                   query_level0=ql0, **extras)
+    ids = rng.integers(0, vocab, P)
+    pad = (rng.random(P) < 0.3) if use_pad else None
+    tgt = oracle.round_bf16(rng.standard_normal((sum(levels), vq)).astype(np.float32))
+    dw = N.device_weights(spec, w, cuda)
+    got = _run(N, torch, cuda, spec, dw, ids, tgt, pad)
+    ref = oracle.ncm_forward(_oracle_cfg(spec), w, ids, pad, tgt, bf16=True,
+                             mask="block_diagonal" if mask == "causal" else mask)
+    scale = np.max(np.abs(ref))
+    err = np.abs(got - ref)
+    assert np.all(np.isfinite(got))
+    assert err.max() <= 0.03 * scale, err.max() / scale
+    assert err.mean() <= 0.003 * scale, err.mean() / scale
+    print("max / mean error relative to max|ref|:", err.max() / scale, err.mean() / scale)
+
+
+def test_ncm_body_reference_invariants(cuda, ncm, oracle):
+    """src/ncm_model.zig:332-429 on the device: level-0 inputs do not reach
+    the output when query_level0 (bit for bit), the queries, the level
+    embeddings and the prefix table do; a padded prefix stays finite. With
+    the block-diagonal mask a change of one level's inputs leaves every other
+    position bit-identical; with the block-causal mask, every earlier one."""
+    import torch
+    from ncmorph_amd import ncm as N
+
+    rng = np.random.default_rng(7)
+    levels, P = [4, 8, 16, 32], 6
+    hidden, vq, hd, inter, vocab = 256, 128, 64, 512, 20
+    for mask in ("block_diagonal", "block_causal"):
+        spec = _spec(N, levels, P, hidden, vq, 4, 2, hd, inter, 2, mask, vocab)
+        w = random_ncm(rng, oracle.round_bf16, hidden, vq, inter, 4, 2, hd, 2, levels, P, vocab)
+        dw = N.device_weights(spec, w, cuda)
+        ids = rng.integers(0, vocab, P)
+        tgt = oracle.round_bf16(rng.standard_normal((sum(levels), vq)).astype(np.float32))
+        out = _run(N, torch, cuda, spec, dw, ids, tgt)
+        t2 = tgt.copy()
+        t2[:levels[0]] += 5.0                       # level 0 is replaced by the queries
+        assert np.array_equal(out, _run(N, torch, cuda, spec, dw, ids, t2))
+        begin = np.cumsum([P] + levels)
+        t3 = tgt.copy()
+        t3[begin[2] - P:begin[3] - P] *= -1        # level 2's inputs
+        o3 = _run(N, torch, cuda, spec, dw, ids, t3)
+        changed = np.any(o3 != out, axis=1)
+        assert changed[begin[2]:begin[3]].all()
+        assert not changed[:begin[2]].any()
+        if mask == "block_diagonal":
+            assert not changed[begin[3]:].any()
+        else:
+            assert changed[begin[3]:].all()
+        w2 = dict(w, l0_queries=w["l0_queries"] + np.float32(0.5))
+        assert not np.array_equal(out, _run(N, torch, cuda, spec, N.device_weights(spec, w2, cuda),
+                                            ids, tgt))
+        w3 = dict(w, level_embedding=w["level_embedding"] + np.float32(0.25))
+        assert not np.array_equal(out, _run(N, torch, cuda, spec, N.device_weights(spec, w3, cuda),
+                                            ids, tgt))
+        ids2 = ids.copy()
+        ids2[0] = (ids2[0] + 1) % vocab
+        assert not np.array_equal(out, _run(N, torch, cuda, spec, dw, ids2, tgt))
+        assert np.all(np.isfinite(_run(N, torch, cuda, spec, dw, ids, tgt, np.ones(P, bool))))
+
+
+def test_ncm_code_heads_match_oracle(cuda, ncm, oracle):
+    """Per-level z projection of the body's output and the tied heads: z
+    agrees with the oracle's matmul_bf16 within one bf16 step (summation
+    order), and every logit is within the tied head's fp32 bound (see
+    test_tied_head_gpu.py) of the f64 head formula on that z, with each
+    level's rows, codebook and log_inv_T."""
+    import torch
+    from ncmorph_amd import kernels, ncm as N, vq
+
+    rng = np.random.default_rng(3)
+    levels, P, hidden, d, V = [4, 8, 16], 3, 256, 128, 300
+    spec = _spec(N, levels, P, hidden, 128, 4, 2, 64, 512, 1, "block_diagonal", 10)
+    h = oracle.round_bf16(rng.standard_normal((spec.seq_len, hidden)).astype(np.float32))
+    zw = oracle.round_bf16((rng.standard_normal((3, d, hidden)) * 0.05).astype(np.float32))
+    cb = oracle.round_bf16((rng.standard_normal((3, V, d)) / np.sqrt(d)).astype(np.float32))
+    to_bf = lambda a: torch.from_numpy((a.view(np.uint32) >> 16).astype(np.uint16).view(
+        np.int16)).to(cuda).view(torch.bfloat16)
+    cbd, zwd = to_bf(cb), to_bf(zw)
+    hd_ = torch.from_numpy(h).to(cuda)
+    csq = vq.prepare(cbd)
+    lit = np.asarray([0.0, 0.3, -0.2], np.float32)
+    got = N.code_head_logits(spec, hd_, zwd, cbd, csq, log_inv_t=lit).cpu().numpy()
+    h16 = kernels.bf16_from_f32(hd_[P:])
+    off = 0
+    for l, n in enumerate(levels):
+        zg = kernels.linear_bf16(h16[off:off + n], zwd[l], out_mode="bf16_f32").cpu().numpy()
+        zo = oracle.matmul_bf16(h[P + off:P + off + n], zw[l])
+        ulp = np.abs(zo).view(np.uint32) & 0x7F800000
+        step = (ulp.astype(np.uint32) >> 23).astype(np.int32)
+        assert np.all(np.abs(zg - zo) <= np.ldexp(1.0, step - 127 - 7) + 1e-30)
+        ref, mag = oracle.tied_head_logits_f64(zg, cb[l], log_inv_t=float(lit[l]))
+        esq = np.sum(cb[l].astype(np.float64) ** 2, axis=1)
+        scale = np.exp(float(lit[l])) / esq.mean()
+        t = np.abs(ref) / scale
+        bound = (scale * ((d + 4) * 2.0**-24 * mag + d * 2.0**-24 * esq[None, :] + 2.0**-22 * t)
+                 + 2.0**-21 * np.abs(ref) + 1e-30)
+        err = np.abs(got[off:off + n].astype(np.float64) - ref)
+        assert np.all(err <= bound), (l, float(np.max(err / bound)))
+        off += n
+
+
+def test_ncm_body_8b_shape_properties(cuda, ncm):
+    """The Llama-3-8B-shaped body (32 layers, hidden 4096, 32/8 heads of 128,
+    FFN 14336) over a 64-token prefix and the 8 levels of a 4096-position
+    sequence (8160 target positions), block-causal mask: finite output,
+    identical bits on a second run, level-0 inputs without effect (learned
+    queries), and a change of the last level's inputs confined to its rows."""
+    import torch
+    from ncmorph_amd import ncm as N
+
+    spec = N.LLAMA_3_8B_NCM
+    dw = N.random_weights(spec, cuda, seed=5)
+    g = torch.Generator(device=cuda).manual_seed(6)
+    T = sum(spec.level_lengths)
+    tgt = torch.randn(T, spec.vq_width, generator=g, device=cuda)
+    ids = np.random.default_rng(6).integers(0, spec.prefix_vocab, spec.prefix_length)
+    cos, sin = N.rope_tables(spec)
+    cd, sd = torch.from_numpy(cos).to(cuda), torch.from_numpy(sin).to(cuda)
+    out = N.forward(spec, dw, ids, tgt, cd, sd)
+    again = N.forward(spec, dw, ids, tgt, cd, sd)
+    torch.cuda.synchronize()
+    assert out.shape == (spec.seq_len, spec.hidden)
+    assert bool(torch.isfinite(out).all())
+    assert torch.equal(out, again)
+    t2 = tgt.clone()
+    t2[:spec.level_lengths[0]] += 3.0
+    assert torch.equal(out, N.forward(spec, dw, ids, t2, cd, sd))
+    last = spec.seq_len - spec.level_lengths[-1]
+    t3 = tgt.clone()
+    t3[last - spec.prefix_length:] *= -1
+    o3 = N.forward(spec, dw, ids, t3, cd, sd)
+    torch.cuda.synchronize()
+    changed = (o3 != out).any(dim=1).cpu().numpy()
+    assert not changed[:last].any() and changed[last:].all()

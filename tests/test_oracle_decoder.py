@@ -64,7 +64,8 @@ def test_decoder_struct_layout(ncm):
     # int64 x 3, int32 x 4, int64, float (+4 padding); ten pointers.
     assert C.sizeof(decoder._Shape) == 56
     assert decoder._Shape.window.offset == 40 and decoder._Shape.rms_eps.offset == 48
-    assert C.sizeof(decoder._Layer) == 80
+    # ten weight pointers, then q_norm, k_norm and the two norm biases
+    assert C.sizeof(decoder._Layer) == 112
 
 
 def test_decoder_entry_rejects_before_device_use(ncm):
