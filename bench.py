@@ -249,6 +249,97 @@ def run_decoder(torch, reps=10, warmup=3):
                          "flops_linear": lin, "flops_attention_causal": att}}
 
 
+def ncm_step_flops(spec, d, v):
+    """Algorithmic FLOPs of one NCM level-parallel step: 2 per multiply-add
+    of the input projection and every layer projection over all S
+    positions, 4 head_dim per allowed (query, key) pair and query head for
+    QK^T and P V, and per target position the level's z projection (hidden
+    -> d) and tied head (d -> v codes)."""
+    S = spec.seq_len
+    T = sum(spec.level_lengths)
+    qw, kvw = spec.q_heads * spec.head_dim, spec.kv_heads * spec.head_dim
+    per_layer = spec.hidden * (qw + 2 * kvw) + qw * spec.hidden + 3 * spec.hidden * spec.intermediate
+    linear = 2.0 * S * (spec.vq_width * spec.hidden + spec.layers * per_layer)
+    P = spec.prefix_length
+    pairs = P * P
+    seen = 0
+    for n in spec.level_lengths:
+        own = seen + n if spec.mask == "block_causal" else n
+        pairs += n * (P + own)
+        seen += n
+    attention = spec.layers * spec.q_heads * 4.0 * spec.head_dim * pairs
+    heads = 2.0 * T * (spec.hidden * d + d * v)
+    return linear, attention, heads
+
+
+def run_ncm_step(torch, reps=5, warmup=2):
+    """The NCM level-parallel step at the Llama-3-8B shape: the bf16 body
+    (32 layers, hidden 4096, 32 / 8 heads of 128, FFN 14336, input
+    projection from vq width 4096) over a 64-token prefix and the 8 levels
+    of one 4096-position sequence (32 ... 4096 positions, 8160 in all),
+    then the level's z projection (4096 -> 4096) and codebook-tied head
+    (8192 codes) at every target position. Random-init weights ~N(0, 0.02),
+    code heads' projections ~N(0, 0.02), codebooks ~N(0, 1/4096)."""
+    import dataclasses
+
+    from ncmorph_amd import ncm, vq
+
+    dev = torch.device("cuda", 0)
+    d, v = 4096, 8192
+    out = {}
+    base = ncm.LLAMA_3_8B_NCM
+    w = ncm.random_weights(base, dev, seed=21)
+    g = torch.Generator(device=dev).manual_seed(22)
+    L = len(base.level_lengths)
+    zw = (torch.randn(L, d, base.hidden, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    cb = (torch.randn(L, v, d, generator=g, device=dev) / d ** 0.5).to(torch.bfloat16)
+    csq = vq.prepare(cb)
+    T = sum(base.level_lengths)
+    tgt = torch.randn(T, base.vq_width, generator=g, device=dev)
+    ids = np.random.default_rng(23).integers(0, base.prefix_vocab, base.prefix_length)
+    cos, sin = ncm.rope_tables(base)
+    cd, sd = torch.from_numpy(cos).to(dev), torch.from_numpy(sin).to(dev)
+    hidden = torch.empty((base.seq_len, base.hidden), dtype=torch.float32, device=dev)
+    for mask in ("block_causal", "block_diagonal"):
+        spec = dataclasses.replace(base, mask=mask)
+
+        def step():
+            ncm.forward(spec, w, ids, tgt, cd, sd, out=hidden)
+            return ncm.code_head_logits(spec, hidden, zw, cb, csq)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(reps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        sec = e0.elapsed_time(e1) * 1e-3 / reps
+        lin, att, heads = ncm_step_flops(spec, d, v)
+        tf = (lin + att + heads) / sec / 1e12
+        out[mask] = {"ms_per_step": round(sec * 1e3, 3),
+                     "positions_per_s": round(spec.seq_len / sec, 1),
+                     "flops": {"linear": lin, "attention": att, "code_heads": heads},
+                     "roofline": {"bound": "mfma", "achieved": round(tf, 2),
+                                  "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                  "frac": round(tf / BF16_PEAK_TFLOPS, 4)}}
+    del w, zw, cb
+    res = out["block_causal"]
+    res.update({"metric": "NCM level-parallel step positions/s", "value":
+                res["positions_per_s"], "unit": "positions/s",
+                "config": {"workload": "random-init Llama-3-8B-shaped bf16 NCM body + tied code "
+                                       "heads, one 4096-position sequence",
+                           "layers": base.layers, "hidden": base.hidden,
+                           "heads": [base.q_heads, base.kv_heads], "head_dim": base.head_dim,
+                           "intermediate": base.intermediate, "prefix": base.prefix_length,
+                           "levels": list(base.level_lengths), "codebook": v, "d": d,
+                           "mask": "block_causal"},
+                "block_diagonal": out["block_diagonal"]})
+    return res
+
+
 PCIE_PEAK_GBS = 64.0  # PCIe 5.0 x16, one direction
 NCM_PREFIX, NCM_LEVELS = 64, [32, 64, 128, 256, 512, 1024, 2048, 4096]
 
@@ -496,7 +587,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--only", choices=["linear", "rvq", "decoder", "all", "copy"], default="all",
+    ap.add_argument("--only", choices=["linear", "rvq", "decoder", "ncm", "all", "copy"],
+                    default="all",
                     help="copy: a plain 256 MiB device copy, the reference point for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
@@ -580,11 +672,14 @@ def main():
                         "roofline": rvq["roofline"]})
             if "cpu_baseline" in rvq:
                 res["cpu_baseline"] = rvq["cpu_baseline"]
+    if args.only == "ncm":
+        res["ncm_level_step"] = run_ncm_step(torch)
     if args.only in ("decoder", "all"):
         dec = run_decoder(torch)
         dec["weight_upload"] = run_weight_upload(torch)
         dec["ncm_level_attention"] = run_ncm_attention(torch)
         dec["ncm_tied_head"] = run_ncm_tied_head(torch)
+        res["ncm_level_step"] = run_ncm_step(torch)
         if not args.no_cpu:
             dec["cpu_baseline"] = cpu_decoder_baseline()
         res["decoder_prefill"] = dec
