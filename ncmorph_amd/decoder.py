@@ -252,48 +252,178 @@ def _hf_names(i: int) -> dict:
     return {"input_norm": p + "input_layernorm.weight",
             "q": p + "self_attn.q_proj", "k": p + "self_attn.k_proj", "v": p + "self_attn.v_proj",
             "o": p + "self_attn.o_proj", "post_attention_norm": p + "post_attention_layernorm.weight",
-            "gate": p + "mlp.gate_proj", "up": p + "mlp.up_proj", "down": p + "mlp.down_proj"}
+            "gate": p + "mlp.gate_proj", "up": p + "mlp.up_proj", "down": p + "mlp.down_proj",
+            "q_norm": p + "self_attn.q_norm.weight", "k_norm": p + "self_attn.k_norm.weight"}
 
 
-def load_safetensors(spec: DecoderSpec, path: str, device) -> DecoderWeights:
+class CheckpointError(ValueError):
+    """A checkpoint the loader refuses, with the reference's rejection kind
+    (src/loader.zig:41-49, 225-276): InvalidConfig, InvalidManifest or
+    UnsupportedPickleWeights before any tensor data is read, and
+    TiedHeadMismatch (a stored lm_head.weight that differs from tied
+    embeddings) after. `problems` holds (feature, message) pairs."""
+
+    def __init__(self, kind: str, problems: list):
+        self.kind = kind
+        self.problems = problems
+        shown = "; ".join(f"{f}: {m}" for f, m in problems[:5])
+        more = f" (+{len(problems) - 5} more)" if len(problems) > 5 else ""
+        super().__init__(f"{kind}: {shown}{more}")
+
+
+# Weight files in a pickle format that the loader names instead of reading
+# (src/loader.zig:204-223).
+_PICKLE_WEIGHTS = ("pytorch_model.bin", "pytorch_model.bin.index.json", "model.bin",
+                   "model.bin.index.json", "pytorch_model.pt")
+
+
+def load_checkpoint(path: str, device, read_count: list | None = None):
+    """(ConfigSpec, DecoderSpec, DecoderWeights) of a Transformers checkpoint
+    directory: config.json, then model.safetensors or a sharded
+    model.safetensors.index.json (load_checkpoint_report_impl,
+    src/loader.zig:95-202). config.json is parsed with the reference's rules
+    (hf_config.parse_config) and every shard header is checked against the
+    spec's tensor manifest and the index before the first tensor data read;
+    any problem raises CheckpointError. read_count: a one-element list that
+    counts tensor data reads."""
+    import os
+
+    from . import hf_config
+
+    try:
+        text = open(os.path.join(path, "config.json"), "rb").read()
+        cfg, problems = hf_config.parse_config(text)
+    except hf_config.ConfigError:
+        raise CheckpointError("InvalidConfig", [(
+            "config.json", "invalid JSON; provide a valid supported decoder configuration")])
+    if cfg is None:
+        raise CheckpointError("InvalidConfig", problems)
+    spec = cfg.decoder_spec()
+    return cfg, spec, _load(spec, cfg, path, device, read_count)
+
+
+def _manifest_spec(spec: DecoderSpec, present) -> "hf_config.ConfigSpec":
+    """The manifest of a DecoderSpec given without config.json: the optional
+    tensors (biases, QK-norm) are those that layer 0 of the checkpoint holds."""
+    from . import hf_config
+
+    names = {t.name for t in present}
+    has = lambda suffix: f"model.layers.0.{suffix}" in names  # noqa: E731
+    return hf_config.ConfigSpec(
+        family="", vocab_size=spec.vocab, hidden_size=spec.hidden,
+        intermediate_size=spec.intermediate, num_hidden_layers=spec.layers,
+        num_attention_heads=spec.q_heads, num_key_value_heads=spec.kv_heads,
+        head_dim=spec.head_dim, rms_norm_eps=spec.rms_eps, rope_theta=spec.rope_theta,
+        rope_scaling=None, qkv_bias=has("self_attn.q_proj.bias"),
+        o_bias=has("self_attn.o_proj.bias"), mlp_bias=has("mlp.gate_proj.bias"),
+        qk_norm=has("self_attn.q_norm.weight"), tie_word_embeddings=spec.tie_word_embeddings,
+        sliding_window=None)
+
+
+def load_safetensors(spec: DecoderSpec, path: str, device,
+                     read_count: list | None = None) -> DecoderWeights:
     """Device weights of a Llama-layout checkpoint (Transformers names:
     model.embed_tokens, model.layers.N.{input_layernorm, self_attn.{q,k,v,o}_proj,
-    post_attention_layernorm, mlp.{gate,up,down}_proj}, model.norm, lm_head),
-    from one .safetensors file or a directory with model.safetensors or a
-    sharded model.safetensors.index.json (the loader's manifest-first order,
-    src/loader.zig:95-202). BF16 tensors are copied to HBM as stored
-    (ncm_st_upload); F32 projection weights are rounded to bf16 on the device
-    (RNE, the operand rounding of matmul_bf16); norm scales are widened to
-    f32. q|k|v rows are concatenated and gate/up rows interleaved in place."""
+    self_attn.{q,k}_norm, post_attention_layernorm, mlp.{gate,up,down}_proj},
+    model.norm, lm_head) for a spec given without config.json, from one
+    .safetensors file or a directory with model.safetensors or a sharded
+    model.safetensors.index.json. The manifest is checked before any data
+    read as in load_checkpoint, with the optional tensors that layer 0
+    holds."""
+    return _load(spec, None, path, device, read_count)
+
+
+def _load(spec: DecoderSpec, cfg, path: str, device, read_count):
+    """Manifest first, then the reads (src/loader.zig:95-202, 225-276).
+
+    Every shard header is parsed, then checked against the manifest of
+    `cfg` (hf_config.check) and the index (hf_config.check_index); any
+    problem raises CheckpointError("InvalidManifest") before the first
+    tensor read. BF16 tensors are copied to HBM as stored (ncm_st_upload);
+    F32 and F16 projection weights are widened to f32 on the device and
+    rounded to bf16 (RNE, the operand rounding of matmul_bf16); norm scales
+    are widened to f32. q|k|v rows are concatenated and gate/up rows
+    interleaved in place. Rotary inv_freq buffers are not read. A stored
+    lm_head with tied embeddings must decode to the same f32 values
+    (TiedHeadMismatch, src/loader.zig:259-267)."""
     import os
 
     import torch
 
-    from . import kernels
+    from . import hf_config, kernels
     from .safetensors import SafetensorsFile, parse_index
 
-    files, where = {}, {}
+    entries, shard_names, base = None, [], path
     if os.path.isdir(path):
         idx = os.path.join(path, "model.safetensors.index.json")
         if os.path.exists(idx):
-            entries, _ = parse_index(open(idx).read())
-            for tensor, shard in entries:
-                where[tensor] = os.path.join(path, shard)
+            try:
+                entries, _ = parse_index(open(idx).read())
+            except NcmError as e:
+                raise CheckpointError("InvalidManifest", [(
+                    "model.safetensors.index.json",
+                    f"invalid safetensors index: {e.detail or e}")]) from None
+            for _, shard in entries:
+                if shard not in shard_names:
+                    shard_names.append(shard)
         else:
-            path = os.path.join(path, "model.safetensors")
-    if not where:
-        f = SafetensorsFile(path)
-        files[path] = f
-        for t in f.tensors():
-            where[t.name] = path
+            shard_names = ["model.safetensors"]
+    else:
+        base, name = os.path.split(path)
+        shard_names = [name]
+
+    files, shards, present, where = {}, {}, [], {}
+    try:
+        for shard in shard_names:
+            p = os.path.join(base, shard)
+            if not os.path.exists(p):
+                if entries is None:
+                    for cand in _PICKLE_WEIGHTS:
+                        if os.path.exists(os.path.join(base, cand)):
+                            raise CheckpointError("UnsupportedPickleWeights", [(
+                                cand, "pickle-based weights are not supported; convert the "
+                                "checkpoint to safetensors, then retry")])
+                raise FileNotFoundError(p)
+            files[shard] = SafetensorsFile(p)
+            tensors = files[shard].tensors()
+            shards[shard] = [t.name for t in tensors]
+            present += tensors
+            for t in tensors:
+                where.setdefault(t.name, shard)
+        mspec = cfg if cfg is not None else _manifest_spec(spec, present)
+        problems, _notes = hf_config.check(mspec, present)
+        if entries is not None:
+            problems += hf_config.check_index(entries, shards)
+        if problems:
+            raise CheckpointError("InvalidManifest", problems)
+        weights = _read_weights(spec, mspec, files, where, device, read_count, torch, kernels)
+        torch.cuda.current_stream(device).synchronize()
+        return weights
+    finally:
+        for f in files.values():
+            f.close()
+
+
+def _read_weights(spec, mspec, files, where, device, read_count, torch, kernels):
+    """The tensor reads of a checkpoint whose manifest passed."""
 
     def handle(name):
-        if name not in where:
-            raise KeyError(f"checkpoint has no tensor {name}")
-        p = where[name]
-        if p not in files:
-            files[p] = SafetensorsFile(p)
-        return files[p], files[p].find(name)
+        f = files[where[name]]
+        return f, f.find(name)
+
+    def raw(name, info, f):
+        """Tensor `name` as a flat f32 (F32, F16) or bf16 (BF16) device tensor."""
+        n = 1
+        for d in info.shape:
+            n *= d
+        if read_count is not None:
+            read_count[0] += 1
+        if info.dtype == "BF16":
+            return f.upload(name, torch.empty(n, dtype=torch.int16, device=device)).view(
+                torch.bfloat16)
+        if info.dtype == "F16":
+            return f.upload(name, torch.empty(n, dtype=torch.float16, device=device)).float()
+        return f.upload(name, torch.empty(n, dtype=torch.float32, device=device))
 
     def load_into(name, out):
         """Tensor `name` into the bf16 device tensor `out` (same element count)."""
@@ -304,25 +434,23 @@ def load_safetensors(spec: DecoderSpec, path: str, device) -> DecoderWeights:
         if n != out.numel():
             raise ValueError(f"{name}: {info.shape} does not fit {tuple(out.shape)}")
         if info.dtype == "BF16":
+            if read_count is not None:
+                read_count[0] += 1
             f.upload(name, out)
-        elif info.dtype == "F32":
-            tmp = torch.empty(n, dtype=torch.float32, device=device)
-            f.upload(name, tmp)
-            out.view(-1).copy_(kernels.bf16_from_f32(tmp).view(-1))
         else:
-            raise ValueError(f"{name}: dtype {info.dtype} is not BF16 or F32")
+            out.view(-1).copy_(kernels.bf16_from_f32(raw(name, info, f)).view(-1))
         return out
+
+    def as_f32(name):
+        f, info = handle(name)
+        v = raw(name, info, f)
+        return v.float() if v.dtype == torch.bfloat16 else v
 
     def bf16(*shape):
         return torch.empty(*shape, dtype=torch.bfloat16, device=device)
 
     def norm(name):
-        f, info = handle(name)
-        if info.dtype == "F32":
-            out = torch.empty(spec.hidden, dtype=torch.float32, device=device)
-            f.upload(name, out)
-            return out
-        return load_into(name, bf16(spec.hidden)).float()
+        return as_f32(name)
 
     def optional_bias(name, out):
         return load_into(name, out) if name in where else None
@@ -357,15 +485,21 @@ def load_safetensors(spec: DecoderSpec, path: str, device) -> DecoderWeights:
             "gate_up_weight": kernels.interleave_gate_up(gate, up), "gate_up_bias": gu_b,
             "down_weight": load_into(n["down"] + ".weight", bf16(spec.hidden, spec.intermediate)),
             "down_bias": optional_bias(n["down"] + ".bias", bf16(spec.hidden)),
+            "q_norm": norm(n["q_norm"]) if mspec.qk_norm else None,
+            "k_norm": norm(n["k_norm"]) if mspec.qk_norm else None,
         })
         del gate, up
     embed = load_into("model.embed_tokens.weight", bf16(spec.vocab, spec.hidden))
     lm_head = None
     if not spec.tie_word_embeddings:
         lm_head = load_into("lm_head.weight", bf16(spec.vocab, spec.hidden))
-    weights = DecoderWeights(embed=embed, final_norm=norm("model.norm.weight"), layers=layers,
-                             lm_head=lm_head)
-    torch.cuda.current_stream(device).synchronize()
-    for f in files.values():
-        f.close()
-    return weights
+    elif "lm_head.weight" in where:
+        # The reference compares the decoded f32 values bit for bit.
+        same = torch.equal(as_f32("lm_head.weight").view(torch.int32),
+                           as_f32("model.embed_tokens.weight").view(torch.int32))
+        if not same:
+            raise CheckpointError("TiedHeadMismatch", [(
+                "lm_head.weight", "differs from model.embed_tokens.weight although the "
+                "embeddings are tied")])
+    return DecoderWeights(embed=embed, final_norm=norm("model.norm.weight"), layers=layers,
+                          lm_head=lm_head)

@@ -357,8 +357,10 @@ def decoder_forward(ids, embed, layers, final_norm, lm_head, cos, sin, q_heads, 
     + 2 kv_heads) head_dim, hidden] (the q, k and v projections' rows in that
     order), qkv_bias, o_weight, o_bias, post_attention_norm, gate_up_weight
     [2 intermediate, hidden] (gate rows then up rows), gate_up_bias,
-    down_weight, down_bias (biases may be None). lm_head None: tied to embed.
-    cos, sin: [len(ids), head_dim]."""
+    down_weight, down_bias (biases may be None), and optionally q_norm and
+    k_norm [head_dim]: RMSNorm scales applied to every query and key head
+    before the rotation (attention_impl's QK-norm, root.zig:501-530).
+    lm_head None: tied to embed. cos, sin: [len(ids), head_dim]."""
     t = len(ids)
     hidden = round_bf16(embed[np.asarray(ids)])
     qw, kvw = q_heads * head_dim, kv_heads * head_dim
@@ -373,6 +375,11 @@ def decoder_forward(ids, embed, layers, final_norm, lm_head, cos, sin, q_heads, 
         q = proj(n, wq, bq, 0, qw)
         k = proj(n, wq, bq, qw, qw + kvw)
         v = proj(n, wq, bq, qw + kvw, qw + 2 * kvw)
+        if layer.get("q_norm") is not None:
+            q = rms_norm(q.reshape(t * q_heads, head_dim), layer["q_norm"], eps,
+                         bf16=True).reshape(t, qw)
+            k = rms_norm(k.reshape(t * kv_heads, head_dim), layer["k_norm"], eps,
+                         bf16=True).reshape(t, kvw)
         q = rotate_heads(q, cos, sin, q_heads, head_dim, bf16=True)
         k = rotate_heads(k, cos, sin, kv_heads, head_dim, bf16=True)
         ctx = attention_core(q, k, v, mask, q_heads, kv_heads, head_dim, bf16=True)

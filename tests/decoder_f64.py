@@ -9,8 +9,10 @@ import numpy as np
 
 def forward_f64(ids, embed, layers, final_norm, lm_head, cos, sin, hq, hkv, hd, eps, window=0,
                 skip=None):
-    """skip: None, "rope" or "residual" (a planted mistake, to show that a
-    test's bound tells the composition apart from a wrong one)."""
+    """skip: None, "rope", "residual" or "qk_norm" (a planted mistake, to
+    show that a test's bound tells the composition apart from a wrong one).
+    A layer with q_norm / k_norm [head_dim] scales RMS-normalizes every
+    query and key head before the rotation (Qwen3)."""
     x = embed[np.asarray(ids)].astype(np.float64)
     t = len(ids)
     qi, ki = np.meshgrid(np.arange(t), np.arange(t), indexing="ij")
@@ -27,6 +29,12 @@ def forward_f64(ids, embed, layers, final_norm, lm_head, cos, sin, hq, hkv, hd, 
             out[:, h * hd:(h + 1) * hd] = s * cos + rot * sin
         return out
 
+    def head_rms(v, heads, w):
+        out = v.copy()
+        for h in range(heads):
+            out[:, h * hd:(h + 1) * hd] = rms(v[:, h * hd:(h + 1) * hd], w)
+        return out
+
     def bias(b):
         return 0.0 if b is None else b.astype(np.float64)
 
@@ -36,6 +44,8 @@ def forward_f64(ids, embed, layers, final_norm, lm_head, cos, sin, hq, hkv, hd, 
         q = qkv[:, :hq * hd]
         k = qkv[:, hq * hd:(hq + hkv) * hd]
         v = qkv[:, (hq + hkv) * hd:]
+        if layer.get("q_norm") is not None and skip != "qk_norm":
+            q, k = head_rms(q, hq, layer["q_norm"]), head_rms(k, hkv, layer["k_norm"])
         if skip != "rope":
             q, k = rope(q, hq), rope(k, hkv)
         ctx = np.zeros((t, hq * hd))
@@ -59,9 +69,10 @@ def forward_f64(ids, embed, layers, final_norm, lm_head, cos, sin, hq, hkv, hd, 
 
 
 def random_model(rng, round_bf16, hidden, inter, vocab, hq, hkv, hd, layers, std=0.05,
-                 biases=False):
+                 biases=False, qk_norm=False):
     """bf16-valued float32 weights: projections ~N(0, std), embeddings
-    ~N(0, 5 std), norm scales ~1 + N(0, 0.1)."""
+    ~N(0, 5 std), norm scales ~1 + N(0, 0.1); with qk_norm, per-head query
+    and key norm scales ~1.2 + N(0, 0.2)."""
     def w(*shape, s=std):
         return round_bf16((rng.standard_normal(shape) * s).astype(np.float32))
 
@@ -82,4 +93,7 @@ def random_model(rng, round_bf16, hidden, inter, vocab, hq, hkv, hd, layers, std
             down_weight=w(hidden, inter),
             down_bias=w(hidden, s=0.05) if biases else None,
         ))
+        if qk_norm:
+            for name in ("q_norm", "k_norm"):
+                ls[-1][name] = round_bf16((1.2 + 0.2 * rng.standard_normal(hd)).astype(np.float32))
     return w(vocab, hidden, s=5 * std), ls, norm()

@@ -35,17 +35,23 @@ def _dev_f32(a, cuda):
     return torch.from_numpy(np.ascontiguousarray(a, np.float32)).to(cuda)
 
 
-@pytest.mark.parametrize("hd,window,biases,batch,seq", [(64, 0, False, 2, 96),
-                                                        (64, 0, True, 1, 130),
-                                                        (128, 20, False, 2, 70)])
-def test_decoder_forward_against_oracle(ncm, oracle, cuda, hd, window, biases, batch, seq):
+@pytest.mark.parametrize("hd,window,biases,batch,seq,qk_norm", [(64, 0, False, 2, 96, False),
+                                                                (64, 0, True, 1, 130, False),
+                                                                (128, 20, False, 2, 70, False),
+                                                                (128, 0, True, 2, 77, True),
+                                                                (64, 0, False, 1, 40, True)])
+def test_decoder_forward_against_oracle(ncm, oracle, cuda, hd, window, biases, batch, seq,
+                                        qk_norm):
+    """qk_norm: the Qwen3 layout, per-head RMSNorm of queries and keys
+    before the rotation (packages/kernels/root.zig:501-530)."""
     import torch
     from ncmorph_amd import decoder, kernels
 
+    print(f"decoder case hd={hd} window={window} biases={biases} qk_norm={qk_norm}", flush=True)
     rng = np.random.default_rng(hd + window + batch)
     hidden, inter, vocab, hq, hkv, nl = 256, 512, 300, 4, 2, 2
     embed, layers, fnorm = random_model(rng, oracle.round_bf16, hidden, inter, vocab, hq, hkv,
-                                        hd, nl, biases=biases)
+                                        hd, nl, biases=biases, qk_norm=qk_norm)
     spec = decoder.DecoderSpec(hidden=hidden, intermediate=inter, vocab=vocab, q_heads=hq,
                                kv_heads=hkv, head_dim=hd, layers=nl, window=window)
     cos, sin = decoder.rope_tables(spec, seq)

@@ -9,12 +9,13 @@ import pytest
 from .decoder_f64 import forward_f64, random_model
 
 
-@pytest.mark.parametrize("biases,window", [(False, 0), (True, 0), (False, 9)])
-def test_oracle_decoder_against_f64(oracle, biases, window):
+@pytest.mark.parametrize("biases,window,qk_norm", [(False, 0, False), (True, 0, False),
+                                                   (False, 9, False), (False, 0, True)])
+def test_oracle_decoder_against_f64(oracle, biases, window, qk_norm):
     rng = np.random.default_rng(5 + window + biases)
     hidden, inter, vocab, hq, hkv, hd, nl, t = 256, 512, 300, 4, 2, 64, 2, 48
     embed, layers, fnorm = random_model(rng, oracle.round_bf16, hidden, inter, vocab, hq, hkv,
-                                        hd, nl, biases=biases)
+                                        hd, nl, biases=biases, qk_norm=qk_norm)
     cos, sin = oracle.rope_tables(oracle.rope_llama3(hd, 500000.0, 32.0, 1.0, 4.0, 8192), t)
     ids = rng.integers(0, vocab, t)
     got = oracle.decoder_forward(ids, embed, layers, fnorm, None, cos, sin, hq, hkv, hd, 1e-5,
@@ -25,7 +26,7 @@ def test_oracle_decoder_against_f64(oracle, biases, window):
     # bf16 roundings throughout two layers: a few parts in a thousand.
     assert np.max(np.abs(got - ref)) <= 0.02 * scale
     # The bound separates the right composition from plausible wrong ones.
-    for mistake in ("rope", "residual"):
+    for mistake in ("rope", "residual") + (("qk_norm",) if qk_norm else ()):
         assert np.max(np.abs(forward_f64(*args, skip=mistake) - ref)) > 0.05 * scale
 
 

@@ -41,7 +41,8 @@ def test_upload_bytes_identical(ncm, cuda, tmp_path):
         assert f.find("empty").shape == (0, 4)
 
 
-def _write_checkpoint(path, embed, layers, fnorm, hq, hkv, hd, shards=1, f32_keys=()):
+def _write_checkpoint(path, embed, layers, fnorm, hq, hkv, hd, shards=1, f32_keys=(),
+                      f16_keys=(), lm_head=None):
     tensors = {"model.embed_tokens.weight": embed}
     qw, kw = hq * hd, hkv * hd
     inter = layers[0]["gate_up_weight"].shape[0] // 2
@@ -67,12 +68,21 @@ def _write_checkpoint(path, embed, layers, fnorm, hq, hkv, hd, shards=1, f32_key
             tensors[p + "mlp.up_proj.bias"] = L["gate_up_bias"][inter:]
         if L.get("down_bias") is not None:
             tensors[p + "mlp.down_proj.bias"] = L["down_bias"]
+        if L.get("q_norm") is not None:
+            tensors[p + "self_attn.q_norm.weight"] = L["q_norm"]
+            tensors[p + "self_attn.k_norm.weight"] = L["k_norm"]
     tensors["model.norm.weight"] = fnorm
+    if lm_head is not None:
+        tensors["lm_head.weight"] = lm_head
 
     def entry(name, a):
         a = np.ascontiguousarray(a, np.float32)
         if name in f32_keys:
             return ("F32", a.shape, a.tobytes())
+        if name in f16_keys:
+            h = a.astype(np.float16)
+            assert np.array_equal(h.astype(np.float32), a)  # exact in f16
+            return ("F16", a.shape, h.tobytes())
         return ("BF16", a.shape, synth.bf16_bits(a).tobytes())
 
     names = list(tensors)
@@ -128,3 +138,72 @@ def test_checkpoint_loads_into_decoder(ncm, oracle, cuda, tmp_path, shards, bias
     b = decoder.forward(spec, w, ids, cd, sd)
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+def _direct_weights(cuda, embed, layers, fnorm, inter, lm_head=None):
+    """The same weights handed to the decoder directly, in its layout."""
+    import torch
+    from ncmorph_amd import decoder, kernels
+
+    def dev16(a):
+        return torch.from_numpy(synth.bf16_bits(np.ascontiguousarray(a, np.float32))
+                                .view(np.int16).copy()).to(cuda).view(torch.bfloat16)
+
+    direct = []
+    for L in layers:
+        d = {k: (torch.from_numpy(v).to(cuda) if k.endswith("norm") else
+                 (None if v is None else dev16(v))) for k, v in L.items()}
+        d["gate_up_weight"] = dev16(kernels.interleave_gate_up(L["gate_up_weight"][:inter],
+                                                                L["gate_up_weight"][inter:]))
+        direct.append(d)
+    return decoder.DecoderWeights(embed=dev16(embed), final_norm=torch.from_numpy(fnorm).to(cuda),
+                                  layers=direct, lm_head=None if lm_head is None else
+                                  dev16(lm_head))
+
+
+def test_qwen3_checkpoint_with_config(ncm, oracle, cuda, tmp_path):
+    """load_checkpoint on a Qwen3-layout directory (config.json, QK-norm
+    scales, tied embeddings with a stored equal lm_head, F16 norm scales):
+    the manifest passes, the weights load (reads counted) and the forward
+    gives the bits of the same weights handed over directly. A stored
+    lm_head that differs from the tied embeddings in one element is refused
+    as TiedHeadMismatch (src/loader.zig:259-267)."""
+    import torch
+    from ncmorph_amd import decoder
+
+    rng = np.random.default_rng(11)
+    hidden, inter, vocab, hq, hkv, hd, nl = 256, 512, 300, 4, 2, 64, 2
+    embed, layers, fnorm = random_model(rng, oracle.round_bf16, hidden, inter, vocab, hq, hkv,
+                                        hd, nl, qk_norm=True)
+    cfg = {"architectures": ["Qwen3ForCausalLM"], "model_type": "qwen3", "vocab_size": vocab,
+           "hidden_size": hidden, "intermediate_size": inter, "num_hidden_layers": nl,
+           "num_attention_heads": hq, "num_key_value_heads": hkv, "head_dim": hd,
+           "rms_norm_eps": 1e-6, "rope_theta": 1000000.0, "tie_word_embeddings": True,
+           "attention_bias": False, "use_sliding_window": False}
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    f16 = ("model.norm.weight", "model.layers.1.self_attn.q_norm.weight")
+    _write_checkpoint(str(tmp_path), embed, layers, fnorm, hq, hkv, hd, shards=2,
+                      f16_keys=f16, lm_head=embed)
+    reads = [0]
+    mc, spec, loaded = decoder.load_checkpoint(str(tmp_path), cuda, read_count=reads)
+    assert mc.family == "Qwen3" and spec.head_dim == hd and spec.tie_word_embeddings
+    assert reads[0] >= nl * 11 + 2
+    assert loaded.lm_head is None
+    w = _direct_weights(cuda, embed, layers, fnorm, inter)
+    cos, sin = decoder.rope_tables(spec, 33)
+    cd, sd = torch.from_numpy(cos).to(cuda), torch.from_numpy(sin).to(cuda)
+    ids = rng.integers(0, vocab, (1, 33))
+    a = decoder.forward(spec, loaded, ids, cd, sd)
+    b = decoder.forward(spec, w, ids, cd, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+    bad = embed.copy()
+    bad[7, 3] = oracle.round_bf16(np.array([bad[7, 3] + 0.5], np.float32))[0]
+    d2 = tmp_path / "mismatch"
+    d2.mkdir()
+    (d2 / "config.json").write_text(json.dumps(cfg))
+    _write_checkpoint(str(d2), embed, layers, fnorm, hq, hkv, hd, lm_head=bad)
+    with pytest.raises(decoder.CheckpointError) as e:
+        decoder.load_checkpoint(str(d2), cuda)
+    assert e.value.kind == "TiedHeadMismatch"
