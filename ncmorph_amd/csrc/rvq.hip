@@ -362,6 +362,8 @@ __device__ __forceinline__ void dist_epilogue(const GemmAcc<S>& acc, const DistA
     }
 }
 
+constexpr int kDistGroup = 8;
+
 // ONE: each workgroup has one code tile (ntv == 1), so the per-row state
 // (offsets, top-4 keys) is created after the main loop and holds no registers
 // during it.
@@ -369,9 +371,19 @@ template <class S, bool ONE>
 __global__ __launch_bounds__(S::NT)
 __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void rvq_dist_kernel(DistArgs a) {
     extern __shared__ __attribute__((aligned(16))) char lds[];
+    // XCD-aware grouped order: each XCD receives a contiguous run of logical
+    // ids, and a run of kDistGroup x nranges ids covers kDistGroup row tiles
+    // (fastest) by every code range, so the 32 workgroups an XCD runs at
+    // once share 8 row tiles and 4 code tiles in its L2.
     const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
-    const int range = logical % a.cg.nranges;
-    const int rt = logical / a.cg.nranges;
+    const int nr = a.cg.nranges;
+    const int row_tiles = (int)gridDim.x / nr;
+    const int per_group = kDistGroup * nr;
+    const int grp = logical / per_group;
+    const int gm = min(kDistGroup, row_tiles - grp * kDistGroup);
+    const int in_g = logical - grp * per_group;
+    const int rt = grp * kDistGroup + in_g % gm;
+    const int range = in_g / gm;
     const int64_t row0 = (int64_t)rt * S::BN;
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
