@@ -456,9 +456,13 @@ int ncm_attention_bf16_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t* k,
     if (batch > 65535 || q_heads > 65535 || seq_len > (int64_t(1) << 31)) return NCM_E_SHAPE;
     int rc = ctx_bind(ctx);
     if (rc) return rc;
+    void* vt = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::attention_workspace_bytes(batch, seq_len, kv_heads, head_dim),
+                           &vt);
+    if (rc) return rc;
     hipError_t e = ncm::launch_attention_bf16(q, k, v, out, batch, seq_len, q_heads, kv_heads,
                                               head_dim, q_stride, kv_stride, out_stride, window,
-                                              out_mode, ctx->stream);
+                                              out_mode, (uint16_t*)vt, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "attention launch");
     return NCM_OK;
 }
@@ -485,10 +489,14 @@ int ncm_attention_bf16_seg_dev(ncm_ctx_t* ctx, const uint16_t* q, const uint16_t
     if (batch > 65535 || q_heads > 65535 || seq_len > (int64_t(1) << 30)) return NCM_E_SHAPE;
     int rc = ctx_bind(ctx);
     if (rc) return rc;
+    void* vt = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::attention_workspace_bytes(batch, seq_len, kv_heads, head_dim),
+                           &vt);
+    if (rc) return rc;
     hipError_t e = ncm::launch_attention_bf16_seg(q, k, v, out, batch, seq_len, q_heads, kv_heads,
                                                   head_dim, q_stride, kv_stride, out_stride,
                                                   prefix_len, seg_lo, seg_hi, prefix_pad_bits,
-                                                  out_mode, ctx->stream);
+                                                  out_mode, (uint16_t*)vt, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "attention (level mask) launch");
     return NCM_OK;
 }

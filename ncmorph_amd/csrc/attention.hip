@@ -1,6 +1,7 @@
-// Causal bf16 attention for the decoder's prefill (packages/kernels/root.zig:
-// 536-578, softmax :272-284, mask :380-399), after the q/k/v projections and
-// the rotation. Per query and head, in the reference's bf16 mode:
+// bf16 attention after the q/k/v projections and the rotation
+// (packages/kernels/root.zig:536-578, softmax :272-284, causal mask
+// :380-399), causal or with NCM's prefix + level mask. Per query and head, in
+// the reference's bf16 mode:
 //   s_k = round(round(q . k_k) * 1/sqrt(head_dim))   (k allowed by the mask)
 //   p_k = round(exp(s_k - max s) / sum exp(s - max s))
 //   context = round(sum_k p_k v_k)
@@ -12,132 +13,64 @@
 // the other side of a bf16 rounding boundary now and then. Results agree
 // with the reference within a few bf16 steps, not bit for bit.
 //
-// Two passes over the key blocks of one (sequence, head, 128 queries)
-// workgroup: pass 1 finds max s and the softmax sum; pass 2 recomputes the
-// scores, forms the bf16 probabilities and accumulates P V. Keys are
-// processed in blocks of 64: K rows staged in LDS (row-padded), V staged
-// transposed (one LDS row per head dimension) so that each lane's eight
-// P-operand keys are two 8-byte LDS reads.
+// Two passes over the key blocks of one (sequence, head, 32 NWV queries)
+// workgroup of NWV wavefronts (32 queries each): pass 1 finds max s and the
+// softmax sum; pass 2 recomputes the scores, forms the bf16 probabilities and
+// accumulates P V. The probabilities need the final sum before they are
+// rounded, hence the two passes. Keys are processed in blocks of 64, loaded
+// global -> LDS directly (buffer loads into LDS, two stages: the next block's
+// loads fly while the current block is computed, one barrier per block):
+// K rows as stored, and V from a transposed copy V^T [batch][kv head][dim]
+// [keys, padded to 64] that attention_vt_kernel writes first. LDS rows keep
+// 16-byte chunks XOR-swizzled by row so that the fragment reads of 16
+// consecutive rows hit 16 distinct bank groups.
 //
 // Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16_bf16,
-// one 32-key tile at a time (the running max and sum are updated per tile):
-// lane l then holds query l % 32 and keys 8 (i / 4) + 4 (l / 32) + i % 4 of a
-// 32-key tile in element i. Elements 8j .. 8j+7 of that fragment are exactly
-// the A operand of P V for the keys 16j + {4h .. 4h+3, 8+4h .. 8+4h+3}
-// (h = l / 32); the V operand is read for the same keys, so the sum runs
-// over the right pairs without moving P between lanes.
+// one 32-key tile at a time (the running max and sum are updated per tile).
+// The A operand's row m of a tile is key perm(m), perm swapping bits 2 and 3
+// of m; lane l then holds query l % 32 and key perm(8 (i / 4) + 4 (l / 32) +
+// i % 4) in element i, which for elements 8j .. 8j+7 is keys 16j + 8 (l / 32)
+// .. + 7: exactly the A operand of P V for the k-step of keys 16j .. 16j + 15,
+// whose B operand (8 consecutive keys of one dim per lane) is then one
+// 16-byte chunk of a V^T row.
 #include "common.h"
+#include "gemm_core.h"
 #include "linear.h"
 
 namespace ncm {
 
 namespace {
 
-constexpr int kBq = 128;  // queries per workgroup (32 per wave)
-constexpr int kBk = 64;   // keys per block
+constexpr int kBk = 64;  // keys per block
 
-__device__ __forceinline__ float round_bf16_f(float v) {
-    return __uint_as_float(bf16_bits_rne(v) << 16);
-}
-
-template <int HD>
-struct AttnLds {
-    static constexpr int KROW = HD * 2 + 16;   // bytes per staged K row
-    static constexpr int VROW = kBk * 2 + 8;   // bytes per staged V^T row (one dim)
-    static constexpr int K_BYTES = kBk * KROW;
-    static constexpr int V_BYTES = HD * VROW;
+// LDS layout of one stage: the K block [kBk keys][HD] (rows of 2 HD bytes)
+// then the V^T block [HD dims][kBk keys] (rows of 128 bytes); chunk c of row
+// r sits in slot c ^ ((r >> SWZ) & (CH - 1)). A direct-to-LDS instruction
+// fills 1 KB: RPI consecutive rows.
+template <int HD, int NWV>
+struct AttnTile {
+    static constexpr int KRB = 2 * HD;
+    static constexpr int KCH = KRB / 16;
+    static constexpr int KSWZ = KRB == 256 ? 0 : 1;
+    static constexpr int KRPI = 1024 / KRB;
+    static constexpr int K_BYTES = kBk * KRB;
+    static constexpr int K_DMA = kBk / KRPI / NWV;  // K instructions per wavefront
+    static constexpr int VRB = 2 * kBk;
+    static constexpr int VCH = VRB / 16;
+    static constexpr int VSWZ = 1;
+    static constexpr int VRPI = 1024 / VRB;
+    static constexpr int V_BYTES = HD * VRB;
+    static constexpr int V_DMA = HD / VRPI / NWV;
+    static constexpr int STAGE = K_BYTES + V_BYTES;
+    static constexpr int LDS = 2 * STAGE;
+    static_assert(K_DMA >= 1 && K_DMA * KRPI * NWV == kBk, "K loader shape");
+    static_assert(V_DMA >= 1 && V_DMA * VRPI * NWV == HD, "V loader shape");
+    static_assert(LDS <= 64 * 1024, "at least two workgroups per CU");
 };
 
-// K block [kBk keys][HD] -> registers -> LDS rows; keys at or past `valid`
-// are zero. The load for the next block is issued before the current block's
-// compute and stored to LDS after it, so its latency overlaps the MFMA work.
-template <int HD>
-struct KRegs {
-    static constexpr int CPR = HD / 8;  // 16-byte chunks per row
-    static constexpr int N = kBk * CPR / 256;
-    u32x4_t r[N];
-};
-
-template <int HD>
-__device__ __forceinline__ void load_k(KRegs<HD>& R, const uint16_t* kbase, int64_t kv_stride,
-                                       int64_t key0, int64_t valid) {
-    constexpr int CPR = KRegs<HD>::CPR;
-#pragma unroll
-    for (int j = 0; j < KRegs<HD>::N; ++j) {
-        const int chunk = threadIdx.x + 256 * j;
-        const int row = chunk / CPR, cc = chunk % CPR;
-        R.r[j] = u32x4_t{0u, 0u, 0u, 0u};
-        if (key0 + row < valid) R.r[j] = *(const u32x4_t*)(kbase + (key0 + row) * kv_stride + 8 * cc);
-    }
-}
-
-template <int HD>
-__device__ __forceinline__ void store_k(char* kl, const KRegs<HD>& R) {
-    constexpr int CPR = KRegs<HD>::CPR;
-#pragma unroll
-    for (int j = 0; j < KRegs<HD>::N; ++j) {
-        const int chunk = threadIdx.x + 256 * j;
-        const int row = chunk / CPR, cc = chunk % CPR;
-        *(u32x4_t*)(kl + row * AttnLds<HD>::KROW + 16 * cc) = R.r[j];
-    }
-}
-
-// V block [kBk keys][HD] -> LDS V^T [HD][kBk] (keys at or past `valid` zero).
-// Task (key pair kp, dim chunk dc): two 16-byte global loads, eight 4-byte
-// LDS stores; consecutive threads take consecutive key pairs, so a wave's
-// stores to one V^T row are contiguous.
-template <int HD>
-struct VRegs {
-    static constexpr int N = (kBk / 2) * (HD / 8) / 256;
-    u32x4_t a[N], b[N];
-};
-
-template <int HD>
-__device__ __forceinline__ void load_v(VRegs<HD>& R, const uint16_t* vbase, int64_t kv_stride,
-                                       int64_t key0, int64_t valid) {
-#pragma unroll
-    for (int j = 0; j < VRegs<HD>::N; ++j) {
-        const int task = threadIdx.x + 256 * j;
-        const int kp = task % (kBk / 2), dc = task / (kBk / 2);
-        const int64_t k0 = key0 + 2 * kp;
-        R.a[j] = u32x4_t{0u, 0u, 0u, 0u};
-        R.b[j] = u32x4_t{0u, 0u, 0u, 0u};
-        if (k0 < valid) R.a[j] = *(const u32x4_t*)(vbase + k0 * kv_stride + 8 * dc);
-        if (k0 + 1 < valid) R.b[j] = *(const u32x4_t*)(vbase + (k0 + 1) * kv_stride + 8 * dc);
-    }
-}
-
-template <int HD>
-__device__ __forceinline__ void store_v(char* vl, const VRegs<HD>& R) {
-#pragma unroll
-    for (int j = 0; j < VRegs<HD>::N; ++j) {
-        const int task = threadIdx.x + 256 * j;
-        const int kp = task % (kBk / 2), dc = task / (kBk / 2);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const uint32_t lo = (R.a[j][e] & 0xFFFFu) | (R.b[j][e] << 16);
-            const uint32_t hi = (R.a[j][e] >> 16) | (R.b[j][e] & 0xFFFF0000u);
-            *(uint32_t*)(vl + (8 * dc + 2 * e) * AttnLds<HD>::VROW + 4 * kp) = lo;
-            *(uint32_t*)(vl + (8 * dc + 2 * e + 1) * AttnLds<HD>::VROW + 4 * kp) = hi;
-        }
-    }
-}
-
-// One S^T tile for one wave: keys key0 + 32 t + [0, 32) x its 32 queries.
-template <int HD>
-__device__ __forceinline__ f32x16_t score_tile(const char* kl, const u32x4_t (&qf)[HD / 16],
-                                               int t, int lane) {
-    const int c = lane & 31, hl = lane >> 5;
-    f32x16_t a = {};
-#pragma unroll
-    for (int s = 0; s < HD / 16; ++s) {
-        const u32x4_t kf =
-            *(const u32x4_t*)(kl + (32 * t + c) * AttnLds<HD>::KROW + (16 * s + 8 * hl) * 2);
-        a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
-                                                    __builtin_bit_cast(bf16x8_t, qf[s]), a, 0,
-                                                    0, 0);
-    }
-    return a;
+// Row m of a 32-key score tile holds key perm(m): bits 2 and 3 swapped.
+__device__ __forceinline__ int key_perm(int m) {
+    return (m & ~0xC) | ((m & 4) << 1) | ((m & 8) >> 1);
 }
 
 __device__ __forceinline__ int wave_min_i(int v) {
@@ -153,6 +86,43 @@ __device__ __forceinline__ int wave_max_i(int v) {
 
 }  // namespace
 
+// V [batch * T rows, row stride kv_stride, head h at column h * HD] ->
+// V^T [batch][kv_heads][HD][Tp] (Tp = T rounded up to kBk, keys >= T zero),
+// through 64 x 64 LDS tiles. Grid: (Tp / 64, kv_heads * HD / 64, batch).
+__global__ __launch_bounds__(256) void attention_vt_kernel(const uint16_t* __restrict__ v,
+                                                           uint16_t* __restrict__ vt, int64_t T,
+                                                           int64_t Tp, int64_t kv_stride,
+                                                           int64_t kv_width) {
+    __shared__ uint16_t tile[64][64 + 8];
+    const int64_t key0 = (int64_t)blockIdx.x * 64;
+    const int64_t col0 = (int64_t)blockIdx.y * 64;  // column in [0, kv_heads * HD)
+    const int64_t b = blockIdx.z;
+    const int tid = threadIdx.x;
+    // Load: thread t takes key key0 + (t / 8) + 32 p, columns col0 + 8 (t % 8) .. + 7.
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int kr = tid / 8 + 32 * p, cc = 8 * (tid % 8);
+        u32x4_t x = {0u, 0u, 0u, 0u};
+        if (key0 + kr < T) x = *(const u32x4_t*)(v + (b * T + key0 + kr) * kv_stride + col0 + cc);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            tile[kr][cc + 2 * e] = (uint16_t)(x[e] & 0xFFFFu);
+            tile[kr][cc + 2 * e + 1] = (uint16_t)(x[e] >> 16);
+        }
+    }
+    __syncthreads();
+    // Store: thread t takes column col0 + (t / 8) + 32 p, keys key0 + 8 (t % 8) .. + 7.
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        const int c = tid / 8 + 32 * p, k8 = 8 * (tid % 8);
+        u32x4_t o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            o[e] = (uint32_t)tile[k8 + 2 * e][c] | ((uint32_t)tile[k8 + 2 * e + 1][c] << 16);
+        *(u32x4_t*)(vt + (b * kv_width + col0 + c) * Tp + key0 + k8) = o;
+    }
+}
+
 // Prefix + level-block mask (MASK = 1): key k is allowed for query q when k
 // is a prefix key (k < prefix) that is not padded, or k lies in q's own
 // range [seg_lo[q], seg_hi[q]) (NCM's block-diagonal mask,
@@ -166,28 +136,85 @@ struct SegArgs {
     const uint64_t* pad;
 };
 
-template <int HD, int OUT_MODE, int MASK, bool POW2 = (HD == 64)>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu((HD == 64 || MASK == 1) ? 2 : 1, 4)))
-void attention_bf16_kernel(
+template <int HD, int OUT_MODE, int MASK, int NWV, bool POW2 = (HD == 64)>
+__global__ __launch_bounds__(64 * NWV)
+__attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-    const uint16_t* __restrict__ v, void* __restrict__ out, int64_t T, int group,
-    int64_t q_stride, int64_t kv_stride, int64_t out_stride, int64_t window, float scale,
-    SegArgs sa) {
-    __shared__ int seg_red[8];
-    using L = AttnLds<HD>;
-    __shared__ __attribute__((aligned(16))) char kl[L::K_BYTES];
-    __shared__ __attribute__((aligned(16))) char vl[L::V_BYTES];
+    const uint16_t* __restrict__ vt, void* __restrict__ out, int64_t T, int64_t Tp, int group,
+    int kv_heads, int64_t q_stride, int64_t kv_stride, int64_t out_stride, int64_t window,
+    float scale, SegArgs sa) {
+    using L = AttnTile<HD, NWV>;
+    constexpr int kBq = 32 * NWV;  // queries per workgroup
+    __shared__ int seg_red[2 * NWV];
+    __shared__ __attribute__((aligned(1024))) char lds[L::LDS];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 31, hl = lane >> 5;
     const int64_t b = blockIdx.z;
     const int h = blockIdx.y, kvh = h / group;
+
+    // K rows of this (sequence, kv head): keys >= T load as zero (out of the
+    // resource's range). V^T rows: Tp keys each, zero past T.
+    const uint16_t* kbase = k + b * T * kv_stride + (int64_t)kvh * HD;
+    const __amdgpu_buffer_rsrc_t rsk =
+        make_rsrc(kbase, (uint32_t)(((T - 1) * kv_stride + HD) * 2));
+    const uint16_t* vbase = vt + ((b * kv_heads + kvh) * HD) * Tp;
+    const __amdgpu_buffer_rsrc_t rsv = make_rsrc(vbase, (uint32_t)(HD * Tp * 2));
+
+    // Direct-to-LDS loads of block kb into stage st: wave w's instruction p
+    // fills 1 KB of rows; lane l takes row (p NWV + w) RPI + l / CH, slot
+    // l % CH, i.e. global chunk slot ^ swizzle(row).
+    auto load_k = [&](int st, int64_t kb) {
+        char* dst0 = lds + st * L::STAGE;
+#pragma unroll
+        for (int p = 0; p < L::K_DMA; ++p) {
+            const int ins = p * NWV + wave;
+            const int row = ins * L::KRPI + lane / L::KCH;
+            const int ch = (lane % L::KCH) ^ ((row >> L::KSWZ) & (L::KCH - 1));
+            const uint32_t off = (uint32_t)((kb * kBk + row) * kv_stride * 2 + ch * 16);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsk, (__attribute__((address_space(3))) void*)(dst0 + ins * 1024), 16, off, 0, 0,
+                0);
+        }
+    };
+    auto load_v = [&](int st, int64_t kb) {
+        char* dst0 = lds + st * L::STAGE + L::K_BYTES;
+#pragma unroll
+        for (int p = 0; p < L::V_DMA; ++p) {
+            const int ins = p * NWV + wave;
+            const int row = ins * L::VRPI + lane / L::VCH;
+            const int ch = (lane % L::VCH) ^ ((row >> L::VSWZ) & (L::VCH - 1));
+            const uint32_t off = (uint32_t)((row * Tp + kb * kBk) * 2 + ch * 16);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                rsv, (__attribute__((address_space(3))) void*)(dst0 + ins * 1024), 16, off, 0, 0,
+                0);
+        }
+    };
+    // Lane-constant parts of the fragment addresses: K row perm(c) of a tile
+    // (its swizzle term), V^T row c of a 32-dim block.
+    const int krow = key_perm(c);
+    const int kswz = (krow >> L::KSWZ) & (L::KCH - 1);
+    const int vswz = (c >> L::VSWZ) & (L::VCH - 1);
+    // S^T tile t (keys 32 t .. + 31 of the block) x the wave's 32 queries.
+    auto score_tile = [&](const char* kl, const u32x4_t (&qf)[HD / 16], int t) {
+        f32x16_t a = {};
+        const char* rowp = kl + (32 * t + krow) * L::KRB;
+#pragma unroll
+        for (int s = 0; s < HD / 16; ++s) {
+            const u32x4_t kf = *(const u32x4_t*)(rowp + (((2 * s + hl) ^ kswz) * 16));
+            a = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, kf),
+                                                        __builtin_bit_cast(bf16x8_t, qf[s]), a,
+                                                        0, 0, 0);
+        }
+        return a;
+    };
+
     // Causal balance: workgroup x takes query block nqb - 1 - x (the most
     // keys) and then block x (the fewest), so every workgroup walks about
     // the same number of key blocks (the middle block of an odd count is
-    // taken once).
-    // Level mask: one query block per workgroup, the last (longest level)
-    // blocks first.
+    // taken once). Level mask: one query block per workgroup, the last
+    // (longest level) blocks first.
     const int nqb = (int)((T + kBq - 1) / kBq);
     for (int part = 0; part < 2; ++part) {
     const int qbi = part == 0 ? nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
@@ -195,8 +222,6 @@ void attention_bf16_kernel(
     const int64_t q0 = (int64_t)qbi * kBq;
     const int64_t qw0 = q0 + 32 * wave;
     const int64_t qq = qw0 + c;  // the query of this lane's score column
-    const uint16_t* kbase = k + b * T * kv_stride + (int64_t)kvh * HD;
-    const uint16_t* vbase = v + b * T * kv_stride + (int64_t)kvh * HD;
 
     // Q as the B operand of K Q^T: query qq, dims 16 s + 8 hl .. + 7.
     u32x4_t qf[HD / 16];
@@ -246,7 +271,7 @@ void attention_bf16_kernel(
         __syncthreads();
         int g_lo = 0x7FFFFFFF, g_hi = 0;
 #pragma unroll
-        for (int w = 0; w < 4; ++w) {
+        for (int w = 0; w < NWV; ++w) {
             g_lo = min(g_lo, seg_red[2 * w]);
             g_hi = max(g_hi, seg_red[2 * w + 1]);
         }
@@ -287,7 +312,6 @@ void attention_bf16_kernel(
                (key0 >= sa.prefix && key0 >= w_maxlo && key0 + kBk <= w_minhi &&
                 wq_last == qw0 + 31);
     };
-    const int koff = 4 * hl;  // + 32 t + 8 (i / 4) + i % 4: the key of element i of tile t
     // bf16 RNE without the NaN canonicalisation of bf16_bits_rne: exact for
     // every finite or infinite value (scores and probabilities here; a NaN
     // input propagates as some NaN or garbage, where the reference's whole
@@ -328,49 +352,51 @@ void attention_bf16_kernel(
     // s: a tile value after to_scores (for POW2 the rounded sum; the scale
     // sits in sl).
     auto expo = [&](float s, float nm_) { return fmaf(s, sl, nm_); };
-    // Per-element mask inside a block: key offset kr (element i of tile t) is
-    // allowed for query offset rq when kr <= rq, kr < rt (keys before T) and
-    // kr > rw (inside the window).
-    auto kr_of = [&](int t, int i) { return 32 * t + 8 * (i / 4) + (i % 4) + koff; };
+    // The key offset in its block of element i of score tile t.
+    auto kr_of = [&](int t, int i) { return 32 * t + key_perm(8 * (i / 4) + 4 * hl + (i % 4)); };
+    // Per-element mask inside a block. Causal: key offset kk is allowed when
+    // kk <= rq, kk < rt (keys before T) and kk > rw (inside the window).
+    // MASK 1: kk < rp is a prefix key (allowed unless its pad bit is set),
+    // else allowed when rlo <= kk < rhi (offsets clamped to [-1, kBk]).
+    auto apply_mask = [&](f32x16_t& acc, int64_t key0, int t) {
+        const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
+        const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
+        auto clampk = [](int64_t x) { return (int)(x < -1 ? -1 : (x > kBk ? kBk : x)); };
+        const int rp = MASK == 1 ? clampk(sa.prefix - key0) : 0;
+        const int rlo = MASK == 1 ? clampk(seg_lo_q - key0) : 0;
+        const int rhi = MASK == 1 ? clampk(seg_hi_q - key0) : 0;
+        const uint64_t pbits = pad_bits(key0);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int kk = kr_of(t, i);
+            bool ok;
+            if (MASK == 0)
+                ok = kk <= rq && kk < rt && kk > rw;
+            else
+                ok = kk < rp ? ((pbits >> kk) & 1ull) == 0ull : (kk >= rlo && kk < rhi);
+            acc[i] = ok ? acc[i] : -INFINITY;
+        }
+    };
 
     // ---- pass 1: running max and softmax sum per query. score() is
     // monotone in the accumulated dot product, so the block maximum is taken
     // on the raw sums and scored once.
     float m = -INFINITY, lsum = 0.0f;
-    KRegs<HD> kr;
-    load_k<HD>(kr, kbase, kv_stride, kb_begin * kBk, T);
+    __syncthreads();  // the previous part has finished reading both stages
+    load_k(0, kb_begin);
+    int cur = 0;
     for (int64_t kb = kb_begin; kb < kb_end; kb = next_kb(kb)) {
         const int64_t key0 = kb * kBk;
         const int64_t kb_next = next_kb(kb);
-        store_k<HD>(kl, kr);
-        lds_barrier();
-        if (kb_next < kb_end) load_k<HD>(kr, kbase, kv_stride, kb_next * kBk, T);
+        wait_barrier<0>();  // block kb has landed; stage cur ^ 1 is free
+        if (kb_next < kb_end) load_k(cur ^ 1, kb_next);
+        const char* kl = lds + cur * L::STAGE;
         if (wave_sees(key0)) {
             const bool full = block_full(key0);
-            // Causal: key offset kr is allowed when kr <= rq, kr < rt (keys
-            // before T) and kr > rw (inside the window). MASK 1: kr < rp is a
-            // prefix key (allowed unless its pad bit is set), else allowed
-            // when rlo <= kr < rhi (offsets clamped to [-1, kBk]).
-            const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
-            const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
-            auto clampk = [](int64_t x) { return (int)(x < -1 ? -1 : (x > kBk ? kBk : x)); };
-            const int rp = MASK == 1 ? clampk(sa.prefix - key0) : 0;
-            const int rlo = MASK == 1 ? clampk(seg_lo_q - key0) : 0;
-            const int rhi = MASK == 1 ? clampk(seg_hi_q - key0) : 0;
-            const uint64_t pbits = pad_bits(key0);
-            auto ok = [&](int kk) {
-                if (MASK == 0) return kk <= rq && kk < rt && kk > rw;
-                return kk < rp ? ((pbits >> kk) & 1ull) == 0ull : (kk >= rlo && kk < rhi);
-            };
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                f32x16_t acc = score_tile<HD>(kl, qf, t, lane);
-                if (!full)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int k = kr_of(t, i);
-                        acc[i] = ok(k) ? acc[i] : -INFINITY;
-                    }
+                f32x16_t acc = score_tile(kl, qf, t);
+                if (!full) apply_mask(acc, key0, t);
                 float mb = -INFINITY;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mb = fmaxf(mb, acc[i]);
@@ -382,16 +408,16 @@ void attention_bf16_kernel(
                     const float alpha =
                         m == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(fmaf(m, kLog2e, nm));
                     to_scores(acc);
-                    float part = 0.0f;
+                    float part_sum = 0.0f;
 #pragma unroll
                     for (int i = 0; i < 16; ++i)
-                        part = part + __builtin_amdgcn_exp2f(expo(acc[i], nm));
-                    lsum = fmaf(lsum, alpha, part);
+                        part_sum = part_sum + __builtin_amdgcn_exp2f(expo(acc[i], nm));
+                    lsum = fmaf(lsum, alpha, part_sum);
                     m = mn;
                 }
             }
         }
-        lds_barrier();
+        cur ^= 1;
     }
     const float ltot = lsum + __shfl_xor(lsum, 32, 64);
     // A query with no allowed key (a prefix query whose prefix is all
@@ -406,45 +432,26 @@ void attention_bf16_kernel(
     f32x16_t o[NT];
 #pragma unroll
     for (int n = 0; n < NT; ++n) o[n] = f32x16_t{};
-    VRegs<HD> vr;
-    load_k<HD>(kr, kbase, kv_stride, kb_begin * kBk, T);
-    load_v<HD>(vr, vbase, kv_stride, kb_begin * kBk, T);
+    __syncthreads();  // pass 1 has finished reading both stages
+    load_k(0, kb_begin);
+    load_v(0, kb_begin);
+    cur = 0;
     for (int64_t kb = kb_begin; kb < kb_end; kb = next_kb(kb)) {
         const int64_t key0 = kb * kBk;
         const int64_t kb_next = next_kb(kb);
-        store_k<HD>(kl, kr);
-        store_v<HD>(vl, vr);
-        lds_barrier();
+        wait_barrier<0>();
         if (kb_next < kb_end) {
-            load_k<HD>(kr, kbase, kv_stride, kb_next * kBk, T);
-            load_v<HD>(vr, vbase, kv_stride, kb_next * kBk, T);
+            load_k(cur ^ 1, kb_next);
+            load_v(cur ^ 1, kb_next);
         }
+        const char* kl = lds + cur * L::STAGE;
+        const char* vl = kl + L::K_BYTES;
         if (wave_sees(key0)) {
             const bool full = block_full(key0);
-            // Causal: key offset kr is allowed when kr <= rq, kr < rt (keys
-            // before T) and kr > rw (inside the window). MASK 1: kr < rp is a
-            // prefix key (allowed unless its pad bit is set), else allowed
-            // when rlo <= kr < rhi (offsets clamped to [-1, kBk]).
-            const int rq = (int)(qq - key0), rt = (int)(T - key0 < kBk ? T - key0 : kBk);
-            const int rw = window > 0 ? (int)(rq - window) : -(1 << 30);
-            auto clampk = [](int64_t x) { return (int)(x < -1 ? -1 : (x > kBk ? kBk : x)); };
-            const int rp = MASK == 1 ? clampk(sa.prefix - key0) : 0;
-            const int rlo = MASK == 1 ? clampk(seg_lo_q - key0) : 0;
-            const int rhi = MASK == 1 ? clampk(seg_hi_q - key0) : 0;
-            const uint64_t pbits = pad_bits(key0);
-            auto ok = [&](int kk) {
-                if (MASK == 0) return kk <= rq && kk < rt && kk > rw;
-                return kk < rp ? ((pbits >> kk) & 1ull) == 0ull : (kk >= rlo && kk < rhi);
-            };
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                f32x16_t acc = score_tile<HD>(kl, qf, t, lane);
-                if (!full)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) {
-                        const int k = kr_of(t, i);
-                        acc[i] = ok(k) ? acc[i] : -INFINITY;
-                    }
+                f32x16_t acc = score_tile(kl, qf, t);
+                if (!full) apply_mask(acc, key0, t);
                 // p = round_bf16(e / sum), packed two per register.
                 to_scores(acc);
                 float pf[16];
@@ -457,13 +464,12 @@ void attention_bf16_kernel(
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
                         pa[e] = bf16x2_rne(pf[8 * j + 2 * e], pf[8 * j + 2 * e + 1]);
-                    const int kofs = (32 * t + 16 * j + 4 * hl) * 2;
+                    // V^T rows 32 n + c, keys 32 t + 16 j + 8 hl .. + 7: chunk 4 t + 2 j + hl.
+                    const int vslot = (4 * t + 2 * j + hl) ^ vswz;
 #pragma unroll
                     for (int n = 0; n < NT; ++n) {
-                        const char* vp = vl + (32 * n + c) * L::VROW + kofs;
-                        const u32x2_t v0 = *(const u32x2_t*)vp;
-                        const u32x2_t v1 = *(const u32x2_t*)(vp + 16);
-                        const u32x4_t vb = {v0[0], v0[1], v1[0], v1[1]};
+                        const u32x4_t vb =
+                            *(const u32x4_t*)(vl + (32 * n + c) * L::VRB + vslot * 16);
                         o[n] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
                             __builtin_bit_cast(bf16x8_t, pa), __builtin_bit_cast(bf16x8_t, vb),
                             o[n], 0, 0, 0);
@@ -471,8 +477,13 @@ void attention_bf16_kernel(
                 }
             }
         }
-        lds_barrier();
+        cur ^= 1;
     }
+    // No load may still be writing LDS when the workgroup ends (a walk with
+    // no key block issued its first loads and never waited for them).
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm_lgkm0(0));
+    asm volatile("" ::: "memory");
 
     // context = round_bf16(sum); D row 8 (i / 4) + 4 hl + i % 4 = query, column = dim.
     if (wave_live) {
@@ -493,30 +504,54 @@ void attention_bf16_kernel(
     }  // part
 }
 
+int64_t attention_vt_padded(int64_t seq_len) { return (seq_len + kBk - 1) / kBk * kBk; }
+
+size_t attention_workspace_bytes(int64_t batch, int64_t seq_len, int kv_heads, int head_dim) {
+    return (size_t)batch * kv_heads * head_dim * attention_vt_padded(seq_len) * 2;
+}
+
+namespace {
+
+// Waves per workgroup (measured at the decoder's 4 x 1024 causal prefill and
+// NCM's 8224-position level attention): 2 for head_dim 64, 4 for head_dim
+// 128. Both kernels hold about 200 VGPRs (two wavefronts per SIMD); small
+// workgroups keep the per-block barrier short.
+template <int HD>
+constexpr int attn_waves() { return HD == 64 ? 2 : 4; }
+
 template <int HD, int MASK>
-static hipError_t launch_attn_hd(const uint16_t* q, const uint16_t* k, const uint16_t* v,
-                                 void* out, int64_t batch, int64_t T, int hq, int hkv,
-                                 int64_t q_stride, int64_t kv_stride, int64_t out_stride,
-                                 int64_t window, SegArgs sa, int out_mode, hipStream_t stream) {
-    const int64_t nqb = (T + kBq - 1) / kBq;
+hipError_t launch_attn_hd(const uint16_t* q, const uint16_t* k, const uint16_t* v, void* out,
+                          int64_t batch, int64_t T, int hq, int hkv, int64_t q_stride,
+                          int64_t kv_stride, int64_t out_stride, int64_t window, SegArgs sa,
+                          int out_mode, uint16_t* vt, hipStream_t stream) {
+    constexpr int NWV = attn_waves<HD>();
+    const int64_t Tp = attention_vt_padded(T);
+    hipLaunchKernelGGL(attention_vt_kernel,
+                       dim3((unsigned)(Tp / 64), (unsigned)(hkv * HD / 64), (unsigned)batch),
+                       dim3(256), 0, stream, v, vt, T, Tp, kv_stride, (int64_t)hkv * HD);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    const int64_t nqb = (T + 32 * NWV - 1) / (32 * NWV);
     const dim3 grid((unsigned)(MASK == 0 ? (nqb + 1) / 2 : nqb), (unsigned)hq, (unsigned)batch);
     const float scale = 1.0f / sqrtf((float)HD);
     const int group = hq / hkv;
     if (out_mode == NCM_OUT_BF16)
-        hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16, MASK>), grid, dim3(256), 0,
-                           stream, q, k, v, out, T, group, q_stride, kv_stride, out_stride, window,
-                           scale, sa);
+        hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16, MASK, NWV>), grid,
+                           dim3(64 * NWV), 0, stream, q, k, vt, out, T, Tp, group, hkv, q_stride,
+                           kv_stride, out_stride, window, scale, sa);
     else
-        hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16_F32, MASK>), grid, dim3(256),
-                           0, stream, q, k, v, out, T, group, q_stride, kv_stride, out_stride,
-                           window, scale, sa);
+        hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16_F32, MASK, NWV>), grid,
+                           dim3(64 * NWV), 0, stream, q, k, vt, out, T, Tp, group, hkv, q_stride,
+                           kv_stride, out_stride, window, scale, sa);
     return hipGetLastError();
 }
+
+}  // namespace
 
 hipError_t launch_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                  void* out, int64_t batch, int64_t seq_len, int q_heads,
                                  int kv_heads, int head_dim, int64_t q_stride, int64_t kv_stride,
-                                 int64_t out_stride, int64_t window, int out_mode,
+                                 int64_t out_stride, int64_t window, int out_mode, uint16_t* vt,
                                  hipStream_t stream) {
     // A window of seq_len or more admits every causal key.
     if (window >= seq_len) window = 0;
@@ -524,11 +559,12 @@ hipError_t launch_attention_bf16(const uint16_t* q, const uint16_t* k, const uin
     switch (head_dim) {
         case 64:
             return launch_attn_hd<64, 0>(q, k, v, out, batch, seq_len, q_heads, kv_heads, q_stride,
-                                         kv_stride, out_stride, window, none, out_mode, stream);
+                                         kv_stride, out_stride, window, none, out_mode, vt,
+                                         stream);
         case 128:
             return launch_attn_hd<128, 0>(q, k, v, out, batch, seq_len, q_heads, kv_heads,
                                           q_stride, kv_stride, out_stride, window, none, out_mode,
-                                          stream);
+                                          vt, stream);
         default:
             return hipErrorInvalidValue;
     }
@@ -539,15 +575,16 @@ hipError_t launch_attention_bf16_seg(const uint16_t* q, const uint16_t* k, const
                                      int kv_heads, int head_dim, int64_t q_stride,
                                      int64_t kv_stride, int64_t out_stride, int64_t prefix,
                                      const int32_t* seg_lo, const int32_t* seg_hi,
-                                     const uint64_t* pad, int out_mode, hipStream_t stream) {
+                                     const uint64_t* pad, int out_mode, uint16_t* vt,
+                                     hipStream_t stream) {
     const SegArgs sa{prefix, seg_lo, seg_hi, pad};
     switch (head_dim) {
         case 64:
             return launch_attn_hd<64, 1>(q, k, v, out, batch, seq_len, q_heads, kv_heads, q_stride,
-                                         kv_stride, out_stride, 0, sa, out_mode, stream);
+                                         kv_stride, out_stride, 0, sa, out_mode, vt, stream);
         case 128:
             return launch_attn_hd<128, 1>(q, k, v, out, batch, seq_len, q_heads, kv_heads,
-                                          q_stride, kv_stride, out_stride, 0, sa, out_mode,
+                                          q_stride, kv_stride, out_stride, 0, sa, out_mode, vt,
                                           stream);
         default:
             return hipErrorInvalidValue;

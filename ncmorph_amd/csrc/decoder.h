@@ -32,6 +32,7 @@ struct LayerStack {
     uint16_t* qkv;
     uint16_t* ctx;
     uint16_t* act;
+    uint16_t* vt;  // attention_workspace_bytes(batch, seq, kv_heads, head_dim)
 };
 hipError_t run_layers(const LayerStack& a, hipStream_t st);
 

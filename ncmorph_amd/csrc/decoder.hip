@@ -55,7 +55,7 @@ size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 
 struct Plan {
     int64_t T, qkv_w, q_w;
-    size_t o_hidden, o_normed, o_qkv, o_ctx, o_act, o_ids, total;
+    size_t o_hidden, o_normed, o_qkv, o_ctx, o_act, o_ids, o_vt, total;
 };
 
 Plan plan(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq) {
@@ -70,6 +70,7 @@ Plan plan(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq) {
     p.o_ctx = off;    off += up((size_t)p.T * p.q_w * 2);
     p.o_act = off;    off += up((size_t)p.T * s.intermediate * 2);
     p.o_ids = off;    off += up((size_t)p.T * 8);
+    p.o_vt = off;     off += up(attention_workspace_bytes(batch, seq, s.kv_heads, s.head_dim));
     p.total = off;
     return p;
 }
@@ -120,11 +121,12 @@ hipError_t run_layers(const LayerStack& a, hipStream_t st) {
         if (a.seg_lo)
             NCM_TRY(launch_attention_bf16_seg(a.qkv, kp, vp, a.ctx, a.batch, a.seq, s.q_heads,
                                               s.kv_heads, hd, qkv_w, qkv_w, q_w, a.prefix,
-                                              a.seg_lo, a.seg_hi, a.pad, NCM_OUT_BF16, st));
+                                              a.seg_lo, a.seg_hi, a.pad, NCM_OUT_BF16, a.vt,
+                                              st));
         else
             NCM_TRY(launch_attention_bf16(a.qkv, kp, vp, a.ctx, a.batch, a.seq, s.q_heads,
                                           s.kv_heads, hd, qkv_w, qkv_w, q_w, s.window,
-                                          NCM_OUT_BF16, st));
+                                          NCM_OUT_BF16, a.vt, st));
         NCM_TRY(launch_linear_residual(a.ctx, L.o_weight, L.o_bias, a.hidden, a.hidden, T, q_w, H,
                                        NCM_OUT_BF16_F32, st));
         NCM_TRY(launch_rms_norm_rows(a.hidden, L.post_attention_norm, a.normed, T, H, s.rms_eps,
@@ -158,6 +160,7 @@ hipError_t decoder_forward(const ncm_decoder_shape_t& s, const ncm_decoder_layer
     a.qkv = (uint16_t*)(w + p.o_qkv);
     a.ctx = (uint16_t*)(w + p.o_ctx);
     a.act = (uint16_t*)(w + p.o_act);
+    a.vt = (uint16_t*)(w + p.o_vt);
     int64_t* ids = (int64_t*)(w + p.o_ids);
     const int64_t T = p.T, H = s.hidden;
 

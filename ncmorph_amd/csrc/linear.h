@@ -64,11 +64,14 @@ hipError_t launch_rope_rotate(uint16_t* x, int64_t rows, int64_t row_stride, int
                               int64_t seq_len, const float* cosine, const float* sine,
                               hipStream_t stream);
 // Causal (optionally windowed) bf16 attention over `batch` sequences of
-// seq_len tokens; see attention.hip.
+// seq_len tokens; see attention.hip. vt: device scratch of
+// attention_workspace_bytes(batch, seq_len, kv_heads, head_dim) bytes,
+// 16-byte aligned (the transposed V).
+size_t attention_workspace_bytes(int64_t batch, int64_t seq_len, int kv_heads, int head_dim);
 hipError_t launch_attention_bf16(const uint16_t* q, const uint16_t* k, const uint16_t* v,
                                  void* out, int64_t batch, int64_t seq_len, int q_heads,
                                  int kv_heads, int head_dim, int64_t q_stride, int64_t kv_stride,
-                                 int64_t out_stride, int64_t window, int out_mode,
+                                 int64_t out_stride, int64_t window, int out_mode, uint16_t* vt,
                                  hipStream_t stream);
 
 // The same attention with the prefix + level-block mask (see attention.hip).
@@ -77,7 +80,8 @@ hipError_t launch_attention_bf16_seg(const uint16_t* q, const uint16_t* k, const
                                      int kv_heads, int head_dim, int64_t q_stride,
                                      int64_t kv_stride, int64_t out_stride, int64_t prefix,
                                      const int32_t* seg_lo, const int32_t* seg_hi,
-                                     const uint64_t* pad, int out_mode, hipStream_t stream);
+                                     const uint64_t* pad, int out_mode, uint16_t* vt,
+                                     hipStream_t stream);
 
 hipError_t launch_bf16_from_f32(const float* src, uint16_t* dst, int64_t n, int flush,
                                 hipStream_t stream);

@@ -98,7 +98,7 @@ size_t up(size_t n) { return (n + kAlign - 1) / kAlign * kAlign; }
 struct NcmPlan {
     int64_t S, T, max_level;
     size_t o_rows, o_rows16, o_col, o_convy, o_hidden, o_normed, o_qkv, o_ctx, o_act, o_ids,
-        o_seg_lo, o_seg_hi, o_pad, total;
+        o_seg_lo, o_seg_hi, o_pad, o_vt, total;
 };
 
 NcmPlan ncm_plan(const ncm_ncm_shape_t& s, bool convs) {
@@ -127,6 +127,7 @@ NcmPlan ncm_plan(const ncm_ncm_shape_t& s, bool convs) {
     p.o_seg_lo = carve((size_t)p.S * 4);
     p.o_seg_hi = carve((size_t)p.S * 4);
     p.o_pad = carve((size_t)((s.prefix_length + 63) / 64 + 1) * 8);
+    p.o_vt = carve(attention_workspace_bytes(1, p.S, s.kv_heads, s.head_dim));
     p.total = off;
     return p;
 }
@@ -244,6 +245,7 @@ hipError_t ncm_forward(const ncm_ncm_shape_t& s, const ncm_decoder_layer_t* laye
     a.qkv = (uint16_t*)(base + p.o_qkv);
     a.ctx = (uint16_t*)(base + p.o_ctx);
     a.act = (uint16_t*)(base + p.o_act);
+    a.vt = (uint16_t*)(base + p.o_vt);
 
     NCM_TRY(launch_linear(rows16, w.input_projection, w.input_projection_bias, a.hidden, S, vq, H,
                           NCM_OUT_BF16_F32, -1, st));
