@@ -71,6 +71,20 @@ def linear_inputs(torch, dev):
     return xs, ws, ys
 
 
+def _ramp(torch, fn, ms=150.0):
+    """Runs fn, untimed, until about `ms` of wall time has passed: the GPU
+    raises its engine clock over roughly 100 ms of sustained load, and a
+    section that follows host-only work (a CPU baseline) starts from a lower
+    clock."""
+    t0 = time.perf_counter()
+    n = 1
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        n *= 2
+
+
 def run_linear(torch, steps, warmup):
     from ncmorph_amd import kernels
 
@@ -176,9 +190,7 @@ def run_decoder_ops(torch, reps=20):
              t * h * 4 + h * 4 + t * h * 2),
             ("silu_mul_bf16", lambda: kernels.silu_mul(gate, up, "bf16", out=y_m),
              2 * t * inter * 4 + t * inter * 2)):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
+        _ramp(torch, fn)
         e0, e1 = _events(torch)
         e0.record()
         for _ in range(reps):
@@ -226,7 +238,7 @@ def run_decoder(torch, reps=10, warmup=3):
                          device=dev)
     for _ in range(warmup):
         decoder.forward(spec, w, ids, cd, sd, logits=logits)
-    torch.cuda.synchronize()
+    _ramp(torch, lambda: decoder.forward(spec, w, ids, cd, sd, logits=logits))
     e0, e1 = _events(torch)
     e0.record()
     for _ in range(reps):
@@ -366,9 +378,7 @@ def run_ncm_attention(torch, reps=10):
         kernels.attention_bf16_seg(q, k, v, 1, seq, hq, hkv, hd, NCM_PREFIX, dl, dh, None,
                                    out_mode="bf16", out=out)
 
-    for _ in range(3):
-        run()
-    torch.cuda.synchronize()
+    _ramp(torch, run)
     e0, e1 = _events(torch)
     e0.record()
     for _ in range(reps):
@@ -405,9 +415,7 @@ def run_ncm_tied_head(torch, reps=5):
     def run():
         kernels.tied_head_logits_levels(z, cb, csq, NCM_LEVELS, out=out)
 
-    for _ in range(2):
-        run()
-    torch.cuda.synchronize()
+    _ramp(torch, run)
     e0, e1 = _events(torch)
     e0.record()
     for _ in range(reps):
@@ -585,8 +593,12 @@ def cpu_rvq_baseline():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # The GPU raises its engine clock over roughly 100 ms of sustained load;
+    # the default warmup (500 linear steps, then 100 RVQ encodes) lets it
+    # reach its steady state before the timed steps, which a short warmup
+    # would measure on the ramp instead.
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--only", choices=["linear", "rvq", "decoder", "ncm", "all", "copy"],
                     default="all",
                     help="copy: a plain 256 MiB device copy, the reference point for "
