@@ -64,7 +64,9 @@ int ncm_init(int device, ncm_ctx_t** out);
 int ncm_destroy(ncm_ctx_t* ctx);
 /* Route the context's work to a stream (a hipStream_t passed as void*;
  * NULL is HIP's default stream). A new context uses a non-blocking stream
- * of its own. */
+ * of its own. The context's entry points share one device workspace: when
+ * the stream changes, work queued on the new stream waits for the work
+ * already queued on the previous one. */
 int ncm_set_stream(ncm_ctx_t* ctx, void* stream);
 void* ncm_get_stream(ncm_ctx_t* ctx);
 int ncm_synchronize(ncm_ctx_t* ctx);

@@ -24,6 +24,7 @@ struct ncm_ctx {
     hipStream_t stream = nullptr;
     void* ws = nullptr;  // grow-only device workspace
     size_t ws_bytes = 0;
+    hipEvent_t handoff = nullptr;  // orders a new stream after the previous one
 };
 
 namespace {
@@ -195,6 +196,7 @@ int ncm_destroy(ncm_ctx_t* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->handoff) (void)hipEventDestroy(ctx->handoff);
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return NCM_OK;
@@ -203,7 +205,19 @@ int ncm_destroy(ncm_ctx_t* ctx) {
 int ncm_set_stream(ncm_ctx_t* ctx, void* stream) {
     if (!ctx) return NCM_E_NULL;
     // NULL selects HIP's default (null) stream, as everywhere in HIP.
-    ctx->stream = (hipStream_t)stream;
+    hipStream_t next = (hipStream_t)stream;
+    if (next != ctx->stream && ctx->ws) {
+        // Every entry point shares the one workspace: work queued on the new
+        // stream waits for everything already queued on the previous one, so
+        // two streams never use the workspace at the same time.
+        int rc = ctx_bind(ctx);
+        if (rc) return rc;
+        if (!ctx->handoff)
+            NCM_HIP(hipEventCreateWithFlags(&ctx->handoff, hipEventDisableTiming));
+        NCM_HIP(hipEventRecord(ctx->handoff, ctx->stream));
+        NCM_HIP(hipStreamWaitEvent(next, ctx->handoff, 0));
+    }
+    ctx->stream = next;
     return NCM_OK;
 }
 

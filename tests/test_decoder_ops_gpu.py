@@ -45,7 +45,8 @@ def test_rms_norm_dropin_kats_and_random(ncm, oracle, cuda):
         assert np.array_equal(y.view(np.uint32), ref.view(np.uint32)), x.size
 
 
-@pytest.mark.parametrize("rows,width", [(64, 2048), (5, 11), (3, 2050), (4096, 2048)])
+@pytest.mark.parametrize("rows,width", [(64, 2048), (5, 11), (3, 2050), (4096, 2048),
+                                        (3, 6144), (3, 8192), (2, 16384), (2, 8204)])
 def test_rms_norm_rows_device(ncm, oracle, cuda, rows, width):
     import torch
     from ncmorph_amd import kernels
@@ -96,3 +97,59 @@ def test_silu_mul_device(ncm, oracle, cuda):
     steps = _bf16_steps(y, ref)
     assert np.mean(steps == 0) >= 0.999 and steps.max() <= 2
     assert np.array_equal(yb.view(np.uint16).astype(np.uint32) << 16, y.view(np.uint32))
+
+
+def _same_bits_or_both_nan(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | (a.view(np.uint32) == b.view(np.uint32))))
+
+
+@pytest.mark.parametrize("width", [2048, 8192, 16384])
+def test_rms_norm_rows_special_values(ncm, oracle, cuda, width):
+    """Rows whose rounding inputs are subnormal (tiny x, tiny weights), and
+    rows holding a NaN, an infinity or both signs of infinity, bit for bit
+    against the oracle (NaN rows: NaN where the oracle has NaN). Covers the
+    staged (width <= 8192) and global-read (16384) vector paths."""
+    import torch
+    from ncmorph_amd import kernels
+
+    rng = np.random.default_rng(width)
+    base = rng.standard_normal(width).astype(np.float32)
+    rows = [base * np.float32(1e-39),                      # x subnormal: sum of squares 0
+            base * np.float32(1e-20),                      # squares subnormal
+            base.copy(), base.copy(), base.copy(), base.copy()]
+    rows[3][7] = np.nan
+    rows[4][5] = np.inf
+    rows[5][1], rows[5][2] = np.inf, -np.inf
+    x = oracle.round_bf16(np.stack(rows).astype(np.float32))
+    weights = [oracle.round_bf16((rng.standard_normal(width) * 0.1 + 1).astype(np.float32)),
+               oracle.round_bf16((rng.standard_normal(width) * 1e-38).astype(np.float32))]
+    for w in weights:
+        xd, wd = torch.from_numpy(x).to(cuda), torch.from_numpy(w).to(cuda)
+        y = kernels.rms_norm_rows(xd, wd, 1e-5).cpu().numpy()
+        for r in range(x.shape[0]):
+            ref = oracle.rms_norm(x[r], w, 1e-5, bf16=True)
+            assert _same_bits_or_both_nan(y[r], ref), r
+
+
+def test_silu_mul_special_values(ncm, oracle, cuda):
+    """round(silu_bf16(gate) * up) with up around 1e-39 (subnormal products
+    and roundings), gate at +-inf, large magnitudes and NaN: within the SiLU
+    test's step bound of the oracle, NaN exactly where the oracle has NaN."""
+    import torch
+    from ncmorph_amd import kernels
+
+    rng = np.random.default_rng(8)
+    n = 4096
+    g = oracle.round_bf16((rng.standard_normal(n) * 3).astype(np.float32))
+    u = oracle.round_bf16((rng.standard_normal(n) * 1e-39).astype(np.float32))
+    g[:8] = [np.inf, -np.inf, np.nan, 1e30, -1e30, 0.0, -0.0, 88.0]
+    u[8:16] = [np.inf, -np.inf, np.nan, 1e30, 0.0, -0.0, 1e-45, 3e-38]
+    gd, ud = torch.from_numpy(g).to(cuda), torch.from_numpy(u).to(cuda)
+    y = kernels.silu_mul(gd, ud).cpu().numpy()
+    ref = oracle.silu_mul_bf16(g, u)
+    assert np.array_equal(np.isnan(y), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    steps = _bf16_steps(y[ok], ref[ok])
+    assert steps.max() <= 2 and np.mean(steps == 0) >= 0.99
