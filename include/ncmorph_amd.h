@@ -187,18 +187,20 @@ int ncm_bf16_from_f32_dev(ncm_ctx_t* ctx, const float* src, uint16_t* dst, int64
 /* bf16 bits -> f32, exact (packages/bf16/root.zig:25-37). Device pointers. */
 int ncm_bf16_widen_dev(ncm_ctx_t* ctx, const uint16_t* src, float* dst, int64_t n);
 
-/* Device RMSNorm, bf16 mode, of each of `rows` rows of x [rows, width] (f32)
- * with weight [width] (f32): the decoder's normalize_rows
- * (src/decoder.zig:168, root.zig:246-254), one row per wavefront, same bits
- * as ncm_rms_norm_bf16. out_mode NCM_OUT_BF16_F32 (y float) or NCM_OUT_BF16
- * (y uint16 bits, ready for ncm_linear_bf16). When width % 4 == 0, x and
- * weight must be 16-byte aligned. */
+/* Device RMSNorm of each of `rows` rows of x [rows, width] (f32) with weight
+ * [width] (f32): the decoder's normalize_rows (src/decoder.zig:168), one row
+ * per wavefront. out_mode NCM_OUT_BF16_F32 (y float) or NCM_OUT_BF16 (y
+ * uint16 bits, ready for ncm_linear_bf16): the bf16 mode (rms_norm_bf16,
+ * root.zig:246-254), same bits as ncm_rms_norm_bf16; NCM_OUT_F32 (y float):
+ * the f32 mode (rms_norm, root.zig:226-239), same bits as the reference. y
+ * may be x. When width % 4 == 0, x and weight must be 16-byte aligned. */
 int ncm_rms_norm_rows_dev(ncm_ctx_t* ctx, const float* x, const float* weight, void* y,
                           int64_t rows, int64_t width, float epsilon, int out_mode);
 
-/* Device MLP activation, bf16 mode (src/decoder.zig:210-211):
- * y[i] = round_bf16(silu_bf16(gate[i]) * up[i]); up NULL gives silu_bf16
- * alone. out_mode NCM_OUT_BF16_F32 or NCM_OUT_BF16. */
+/* Device MLP activation (src/decoder.zig:210-211). out_mode NCM_OUT_BF16_F32
+ * or NCM_OUT_BF16: bf16 mode, y[i] = round_bf16(silu_bf16(gate[i]) * up[i]);
+ * NCM_OUT_F32: f32 mode, y[i] = silu(gate[i]) * up[i] (root.zig:255-261).
+ * up NULL gives the SiLU alone; y may be gate. */
 int ncm_silu_mul_dev(ncm_ctx_t* ctx, const float* gate, const float* up, void* y, int64_t n,
                      int out_mode);
 
@@ -349,6 +351,66 @@ int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
                             const float* final_norm, const uint16_t* lm_head,
                             const float* cosine, const float* sine, const int64_t* token_ids,
                             int64_t batch, int64_t seq_len, float* logits);
+
+/* One layer's device weights in the f32 mode (decoder.zig:10-20,
+ * attention_weights_t of root.zig:351-362), all float: qkv_weight holds the
+ * q rows [q_heads * head_dim], then the k rows, then the v rows [kv_heads *
+ * head_dim each], each `hidden` wide (q|k|v biases in the same order);
+ * gate, up and down as stored ([intermediate, hidden], [intermediate,
+ * hidden], [hidden, intermediate]). NULL = no bias; q_norm / k_norm: both
+ * NULL or both [head_dim]. */
+typedef struct ncm_decoder_layer_f32 {
+    const float* input_norm;           /* [hidden] */
+    const float* qkv_weight;           /* [(q_heads + 2 kv_heads) head_dim, hidden] */
+    const float* qkv_bias;             /* [(q_heads + 2 kv_heads) head_dim] or NULL */
+    const float* o_weight;             /* [hidden, q_heads head_dim] */
+    const float* o_bias;               /* [hidden] or NULL */
+    const float* post_attention_norm;  /* [hidden] */
+    const float* gate_weight;          /* [intermediate, hidden] */
+    const float* gate_bias;            /* [intermediate] or NULL */
+    const float* up_weight;            /* [intermediate, hidden] */
+    const float* up_bias;              /* [intermediate] or NULL */
+    const float* down_weight;          /* [hidden, intermediate] */
+    const float* down_bias;            /* [hidden] or NULL */
+    const float* q_norm;               /* [head_dim] or NULL */
+    const float* k_norm;               /* [head_dim] or NULL */
+} ncm_decoder_layer_f32_t;
+
+/* The per-stage trace of forward_with_trace (decoder_trace_t,
+ * src/decoder.zig:30-47): device float buffers, each NULL (not kept) or
+ * [layers, batch * seq_len, width] layer-major (block_input: [batch *
+ * seq_len, hidden]); width is hidden, q_heads * head_dim (attention_context)
+ * or intermediate (gate_projection, up_projection, gate_up_product). */
+typedef struct ncm_decoder_trace {
+    float* block_input;
+    float* input_norm;
+    float* attention_context;
+    float* attention_output;
+    float* attention_residual;
+    float* post_attention_norm;
+    float* gate_projection;
+    float* up_projection;
+    float* gate_up_product;
+    float* mlp_output;
+    float* block_output;
+} ncm_decoder_trace_t;
+
+/* The prefill forward in the reference's f32 mode (forward_with_trace with
+ * bf16_compute false, decoder.zig:62-228: rms_norm, kernels.matmul + bias,
+ * f32 rotate_head and attention, silu, unrounded adds), for `batch`
+ * sequences of seq_len tokens. Arguments as ncm_decoder_forward_dev with
+ * float weights (embed and lm_head float [vocab, hidden], lm_head NULL for
+ * tied embeddings); trace: NULL or the stages to keep. hidden,
+ * intermediate and head_dim must be multiples of 4 (head_dim <= 256) and
+ * q_heads * head_dim too; logits: float [batch * seq_len, vocab]. The
+ * projections sum on the fp32 MFMA in its own order; the attention sums in
+ * the reference's dimension and key order; exp is the device's. */
+int ncm_decoder_forward_f32_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
+                                const ncm_decoder_layer_f32_t* layers, const float* embed,
+                                const float* final_norm, const float* lm_head,
+                                const float* cosine, const float* sine,
+                                const int64_t* token_ids, int64_t batch, int64_t seq_len,
+                                float* logits, const ncm_decoder_trace_t* trace);
 
 /* ---- NCM level-parallel body (src/ncm_model.zig) ---- */
 

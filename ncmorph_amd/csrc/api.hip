@@ -404,7 +404,8 @@ int ncm_rms_norm_rows_dev(ncm_ctx_t* ctx, const float* x, const float* weight, v
                           int64_t rows, int64_t width, float epsilon, int out_mode) {
     if (!ctx) return NCM_E_NULL;
     if (rows < 0 || width < 0) return NCM_E_SHAPE;
-    if (out_mode != NCM_OUT_BF16_F32 && out_mode != NCM_OUT_BF16) return NCM_E_ARG;
+    if (out_mode != NCM_OUT_F32 && out_mode != NCM_OUT_BF16_F32 && out_mode != NCM_OUT_BF16)
+        return NCM_E_ARG;
     if (rows == 0) return NCM_OK;
     if (width == 0) return NCM_E_SHAPE;  // root.zig:247: nonempty rows
     if (!x || !weight || !y) return NCM_E_NULL;
@@ -421,7 +422,8 @@ int ncm_silu_mul_dev(ncm_ctx_t* ctx, const float* gate, const float* up, void* y
                      int out_mode) {
     if (!ctx) return NCM_E_NULL;
     if (n < 0) return NCM_E_SHAPE;
-    if (out_mode != NCM_OUT_BF16_F32 && out_mode != NCM_OUT_BF16) return NCM_E_ARG;
+    if (out_mode != NCM_OUT_F32 && out_mode != NCM_OUT_BF16_F32 && out_mode != NCM_OUT_BF16)
+        return NCM_E_ARG;
     if (n == 0) return NCM_OK;
     if (!gate || !y) return NCM_E_NULL;
     int rc = ctx_bind(ctx);
@@ -600,6 +602,55 @@ int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
     hipError_t e = ncm::decoder_forward(s, layers, embed, final_norm, lm_head, cosine, sine,
                                         token_ids, batch, seq_len, logits, ws, ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "decoder forward");
+    return NCM_OK;
+}
+
+int ncm_decoder_forward_f32_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
+                                const ncm_decoder_layer_f32_t* layers, const float* embed,
+                                const float* final_norm, const float* lm_head,
+                                const float* cosine, const float* sine,
+                                const int64_t* token_ids, int64_t batch, int64_t seq_len,
+                                float* logits, const ncm_decoder_trace_t* trace) {
+    if (!ctx || !shape) return NCM_E_NULL;
+    const ncm_decoder_shape_t& s = *shape;
+    if (batch < 0 || seq_len < 0) return NCM_E_SHAPE;
+    if (batch == 0 || seq_len == 0) return NCM_E_ARG;  // EmptyInput
+    if (s.hidden <= 0 || s.intermediate <= 0 || s.vocab <= 0 || s.layers < 0 || s.window < 0)
+        return NCM_E_SHAPE;
+    if (s.q_heads <= 0 || s.kv_heads <= 0 || s.q_heads % s.kv_heads) return NCM_E_SHAPE;
+    // Device limits: 16-byte rows for the fp32 MFMA linear and the attention.
+    if (s.head_dim <= 0 || s.head_dim % 4 || s.head_dim > 256) return NCM_E_SHAPE;
+    if (s.hidden % 4 || s.intermediate % 4) return NCM_E_SHAPE;
+    if (s.hidden > (int64_t(1) << 20) || s.intermediate > (int64_t(1) << 20) ||
+        s.vocab > (int64_t(1) << 31) || (int64_t)s.q_heads * s.head_dim > (int64_t(1) << 20))
+        return NCM_E_SHAPE;
+    if (batch > 65535 || seq_len > (int64_t(1) << 31) - 1 || batch * seq_len > (int64_t(1) << 31))
+        return NCM_E_SHAPE;
+    if (!embed || !final_norm || !cosine || !sine || !token_ids || !logits) return NCM_E_NULL;
+    if (s.layers > 0 && !layers) return NCM_E_NULL;
+    if ((uintptr_t)embed % 16 || (lm_head && (uintptr_t)lm_head % 16)) return NCM_E_ARG;
+    for (int l = 0; l < s.layers; ++l) {
+        const ncm_decoder_layer_f32_t& L = layers[l];
+        if (!L.input_norm || !L.qkv_weight || !L.o_weight || !L.post_attention_norm ||
+            !L.gate_weight || !L.up_weight || !L.down_weight)
+            return NCM_E_NULL;
+        if (!L.q_norm != !L.k_norm) return NCM_E_ARG;
+        const float* ws_[] = {L.qkv_weight, L.o_weight, L.gate_weight, L.up_weight,
+                              L.down_weight};
+        for (const float* p : ws_)
+            if ((uintptr_t)p % 16) return NCM_E_ARG;
+    }
+    for (int64_t i = 0; i < batch * seq_len; ++i)
+        if (token_ids[i] < 0 || token_ids[i] >= s.vocab) return NCM_E_ARG;  // TokenIdOutOfRange
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::decoder_f32_workspace_bytes(s, batch, seq_len), &ws);
+    if (rc) return rc;
+    hipError_t e = ncm::decoder_forward_f32(s, layers, embed, final_norm, lm_head, cosine, sine,
+                                            token_ids, batch, seq_len, logits, trace, ws,
+                                            ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "f32 decoder forward");
     return NCM_OK;
 }
 

@@ -43,4 +43,14 @@ hipError_t decoder_forward(const ncm_decoder_shape_t& s, const ncm_decoder_layer
                            const int64_t* host_ids, int64_t batch, int64_t seq, float* logits,
                            void* ws, hipStream_t st);
 
+// f32 mode (decoder_f32.hip): workspace bytes and the forward. All pointers
+// device memory except `layers` (host array) and `host_ids`; trace may be
+// null.
+size_t decoder_f32_workspace_bytes(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq);
+hipError_t decoder_forward_f32(const ncm_decoder_shape_t& s, const ncm_decoder_layer_f32_t* layers,
+                               const float* embed, const float* final_norm, const float* lm_head,
+                               const float* cosine, const float* sine, const int64_t* host_ids,
+                               int64_t batch, int64_t seq, float* logits,
+                               const ncm_decoder_trace_t* trace, void* ws, hipStream_t st);
+
 }  // namespace ncm

@@ -104,8 +104,15 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
     const float mean = sum / (float)n;
     const float inv = 1.0f / sqrtf(mean + epsilon);
 
-    // round_bf16(round_bf16(x * inv) * round_bf16(weight)) (root.zig:250-252).
+    // f32 mode (OUT_MODE NCM_OUT_F32, rms_norm, root.zig:226-239):
+    // (x * inv) * weight. bf16 mode: round_bf16(round_bf16(x * inv) *
+    // round_bf16(weight)) (root.zig:250-252).
     auto out1 = [&](int64_t i, float v, float wv) {
+        if (OUT_MODE == NCM_OUT_F32) {
+            const float normalized = v * inv;
+            ((float*)y)[row * n + i] = normalized * wv;
+            return;
+        }
         const float normalized = __uint_as_float(bf16_bits_rne(v * inv) << 16);
         const uint32_t bits = bf16_bits_rne(normalized * __uint_as_float(bf16_bits_rne(wv) << 16));
         if (OUT_MODE == NCM_OUT_BF16)
@@ -113,7 +120,9 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
         else
             ((float*)y)[row * n + i] = __uint_as_float(bits << 16);
     };
-    if ((n & 3) == 0) {
+    if (OUT_MODE == NCM_OUT_F32) {
+        for (int64_t i = lane; i < n; i += 64) out1(i, xr[i], weight[i]);
+    } else if ((n & 3) == 0) {
         // Four elements per lane and step: one 8-byte (bf16) or 16-byte
         // (bf16 values as fp32) store when y is aligned for it.
         const bool yvec = ((uintptr_t)y & (OUT_MODE == NCM_OUT_BF16 ? 7 : 15)) == 0;
@@ -165,6 +174,21 @@ template <int OUT_MODE>
 __global__ __launch_bounds__(256) void silu_mul_kernel(const float* __restrict__ gate,
                                                        const float* __restrict__ up,
                                                        void* __restrict__ y, int64_t n) {
+    if (OUT_MODE == NCM_OUT_F32) {
+        // f32 mode: silu(g) = g * (1 / (1 + exp(-g))) (root.zig:255-261), then
+        // the product with up unrounded (src/decoder.zig:210-211).
+        const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int64_t i = i0 + e;
+            if (i >= n) break;
+            const float v = gate[i];
+            const float sigmoid = 1.0f / (1.0f + expf(-v));
+            const float a = v * sigmoid;
+            ((float*)y)[i] = up ? a * up[i] : a;
+        }
+        return;
+    }
     auto act = [](float v, float u) {
         const float a = __uint_as_float(bf16_bits_rne(v / (1.0f + expf(-v))) << 16);
         return bf16_bits_rne(a * u);
@@ -351,6 +375,9 @@ static hipError_t launch_rms_t(const float* x, const float* weight, void* y, int
 hipError_t launch_rms_norm_rows(const float* x, const float* weight, void* y, int64_t rows,
                                 int64_t n, float epsilon, int out_mode, hipStream_t stream) {
     const bool stage = n % 4 == 0 && n <= kRmsStageMax;
+    if (out_mode == NCM_OUT_F32)
+        return stage ? launch_rms_t<NCM_OUT_F32, true>(x, weight, y, rows, n, epsilon, stream)
+                     : launch_rms_t<NCM_OUT_F32, false>(x, weight, y, rows, n, epsilon, stream);
     if (out_mode == NCM_OUT_BF16)
         return stage ? launch_rms_t<NCM_OUT_BF16, true>(x, weight, y, rows, n, epsilon, stream)
                      : launch_rms_t<NCM_OUT_BF16, false>(x, weight, y, rows, n, epsilon, stream);
@@ -361,7 +388,10 @@ hipError_t launch_rms_norm_rows(const float* x, const float* weight, void* y, in
 hipError_t launch_silu_mul(const float* gate, const float* up, void* y, int64_t n, int out_mode,
                            hipStream_t stream) {
     const dim3 grid((unsigned)((n + 1023) / 1024));
-    if (out_mode == NCM_OUT_BF16)
+    if (out_mode == NCM_OUT_F32)
+        hipLaunchKernelGGL(silu_mul_kernel<NCM_OUT_F32>, grid, dim3(256), 0, stream, gate, up, y,
+                           n);
+    else if (out_mode == NCM_OUT_BF16)
         hipLaunchKernelGGL(silu_mul_kernel<NCM_OUT_BF16>, grid, dim3(256), 0, stream, gate, up, y,
                            n);
     else

@@ -103,6 +103,9 @@ class DecoderWeights:
     final_norm: object
     layers: list = field(default_factory=list)
     lm_head: object = None
+    # "bf16": the layout above (forward); "f32": float32 tensors with the
+    # layer names of _LAYER_F32_FIELDS (forward_f32).
+    mode: str = "bf16"
 
 
 def random_weights(spec: DecoderSpec, device, seed: int = 0, std: float = 0.02,
@@ -247,6 +250,86 @@ def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine,
     return logits
 
 
+_LAYER_F32_FIELDS = ("input_norm", "qkv_weight", "qkv_bias", "o_weight", "o_bias",
+                     "post_attention_norm", "gate_weight", "gate_bias", "up_weight", "up_bias",
+                     "down_weight", "down_bias", "q_norm", "k_norm")
+TRACE_FIELDS = ("block_input", "input_norm", "attention_context", "attention_output",
+                "attention_residual", "post_attention_norm", "gate_projection",
+                "up_projection", "gate_up_product", "mlp_output", "block_output")
+
+
+class _LayerF32(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in _LAYER_F32_FIELDS]
+
+
+class _Trace(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in TRACE_FIELDS]
+
+
+def forward_f32(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine,
+                logits=None, trace: bool = False, ctx=None):
+    """The f32-mode prefill forward (forward_with_trace with bf16_compute
+    false, src/decoder.zig:62-228) of every row of token_ids (int [batch,
+    seq]): logits float32 [batch * seq, vocab], and with trace=True also a
+    dict of the stages of decoder_trace_t (decoder.zig:30-47), each float32
+    [layers, batch * seq, width] (block_input [batch * seq, hidden]).
+    weights: float32 device tensors; layers[i] maps the names of
+    _LAYER_F32_FIELDS (qkv_weight = q, k and v rows concatenated; gate, up
+    and down as stored; biases and q_norm / k_norm may be None)."""
+    import torch
+
+    ids = np.ascontiguousarray(token_ids, dtype=np.int64)
+    if ids.ndim != 2:
+        raise ValueError("token_ids must be [batch, seq]")
+    batch, seq = ids.shape
+    dev = weights.embed.device
+    H, I, hd = spec.hidden, spec.intermediate, spec.head_dim
+    qkv, qw = (spec.q_heads + 2 * spec.kv_heads) * hd, spec.q_heads * hd
+    W = "decoder_forward_f32"
+    a = _ck.Args(W)
+    a.dev(cosine, "cosine", _ck.F32, (seq, hd))
+    a.dev(sine, "sine", _ck.F32, (seq, hd))
+    if logits is None:
+        logits = torch.empty((batch * seq, spec.vocab), dtype=torch.float32, device=dev)
+    a.dev(logits, "logits", _ck.F32, (batch * seq, spec.vocab))
+    a.dev(weights.embed, "embed", _ck.F32, (spec.vocab, H))
+    a.dev(weights.lm_head, "lm_head", _ck.F32, (spec.vocab, H), optional=True)
+    a.dev(weights.final_norm, "final_norm", _ck.F32, (H,))
+    if len(weights.layers) != spec.layers:
+        raise NcmError(-3, W, "one weight dict per layer")
+    shapes = {"input_norm": (H,), "qkv_weight": (qkv, H), "qkv_bias": (qkv,), "o_weight": (H, qw),
+              "o_bias": (H,), "post_attention_norm": (H,), "gate_weight": (I, H),
+              "gate_bias": (I,), "up_weight": (I, H), "up_bias": (I,), "down_weight": (H, I),
+              "down_bias": (H,), "q_norm": (hd,), "k_norm": (hd,)}
+    optional = {"qkv_bias", "o_bias", "gate_bias", "up_bias", "down_bias", "q_norm", "k_norm"}
+    for i, layer in enumerate(weights.layers):
+        for f in _LAYER_F32_FIELDS:
+            a.dev(layer.get(f), f"layers[{i}].{f}", _ck.F32, shapes[f], optional=f in optional)
+    tr = None
+    if trace:
+        T = batch * seq
+        widths = {"attention_context": qw, "gate_projection": I, "up_projection": I,
+                  "gate_up_product": I}
+        tr = {f: torch.empty((T, H) if f == "block_input" else
+                             (spec.layers, T, widths.get(f, H)), dtype=torch.float32, device=dev)
+              for f in TRACE_FIELDS}
+    a.done()
+    shape = _Shape(H, I, spec.vocab, spec.q_heads, spec.kv_heads, hd, spec.layers, spec.window,
+                   spec.rms_eps)
+    arr = (_LayerF32 * max(1, spec.layers))()
+    for i, layer in enumerate(weights.layers):
+        arr[i] = _LayerF32(*[_ptr(layer.get(n)) for n in _LAYER_F32_FIELDS])
+    ctr = _Trace(*[_ptr(tr[f]) for f in TRACE_FIELDS]) if tr else None
+    ctx = ctx or default_context(dev.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_decoder_forward_f32_dev(ctx.handle, C.byref(shape), arr, _ptr(weights.embed),
+                                            _ptr(weights.final_norm), _ptr(weights.lm_head),
+                                            _ptr(cosine), _ptr(sine),
+                                            ids.ctypes.data_as(C.c_void_p), batch, seq,
+                                            _ptr(logits), C.byref(ctr) if ctr else None), W)
+    return (logits, tr) if trace else logits
+
+
 def _hf_names(i: int) -> dict:
     p = f"model.layers.{i}."
     return {"input_norm": p + "input_layernorm.weight",
@@ -277,15 +360,17 @@ _PICKLE_WEIGHTS = ("pytorch_model.bin", "pytorch_model.bin.index.json", "model.b
                    "model.bin.index.json", "pytorch_model.pt")
 
 
-def load_checkpoint(path: str, device, read_count: list | None = None):
+def load_checkpoint(path: str, device, read_count: list | None = None, mode: str = "auto"):
     """(ConfigSpec, DecoderSpec, DecoderWeights) of a Transformers checkpoint
     directory: config.json, then model.safetensors or a sharded
     model.safetensors.index.json (load_checkpoint_report_impl,
     src/loader.zig:95-202). config.json is parsed with the reference's rules
     (hf_config.parse_config) and every shard header is checked against the
     spec's tensor manifest and the index before the first tensor data read;
-    any problem raises CheckpointError. read_count: a one-element list that
-    counts tensor data reads."""
+    any problem raises CheckpointError. mode "auto" picks the reference's
+    arithmetic (bf16_compute when every tensor is BF16, src/loader.zig:
+    191-199, else the f32 mode); "bf16" or "f32" forces one. read_count: a
+    one-element list that counts tensor data reads."""
     import os
 
     from . import hf_config
@@ -299,7 +384,7 @@ def load_checkpoint(path: str, device, read_count: list | None = None):
     if cfg is None:
         raise CheckpointError("InvalidConfig", problems)
     spec = cfg.decoder_spec()
-    return cfg, spec, _load(spec, cfg, path, device, read_count)
+    return cfg, spec, _load(spec, cfg, path, device, read_count, mode)
 
 
 def _manifest_spec(spec: DecoderSpec, present) -> "hf_config.ConfigSpec":
@@ -321,7 +406,7 @@ def _manifest_spec(spec: DecoderSpec, present) -> "hf_config.ConfigSpec":
 
 
 def load_safetensors(spec: DecoderSpec, path: str, device,
-                     read_count: list | None = None) -> DecoderWeights:
+                     read_count: list | None = None, mode: str = "bf16") -> DecoderWeights:
     """Device weights of a Llama-layout checkpoint (Transformers names:
     model.embed_tokens, model.layers.N.{input_layernorm, self_attn.{q,k,v,o}_proj,
     self_attn.{q,k}_norm, post_attention_layernorm, mlp.{gate,up,down}_proj},
@@ -329,11 +414,20 @@ def load_safetensors(spec: DecoderSpec, path: str, device,
     .safetensors file or a directory with model.safetensors or a sharded
     model.safetensors.index.json. The manifest is checked before any data
     read as in load_checkpoint, with the optional tensors that layer 0
-    holds."""
-    return _load(spec, None, path, device, read_count)
+    holds; mode as load_checkpoint's (default "bf16")."""
+    return _load(spec, None, path, device, read_count, mode)
 
 
-def _load(spec: DecoderSpec, cfg, path: str, device, read_count):
+def run(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine, logits=None,
+        ctx=None):
+    """Logits of the forward that matches the weights' mode: forward (bf16)
+    or forward_f32."""
+    if weights.mode == "f32":
+        return forward_f32(spec, weights, token_ids, cosine, sine, logits=logits, ctx=ctx)
+    return forward(spec, weights, token_ids, cosine, sine, logits=logits, ctx=ctx)
+
+
+def _load(spec: DecoderSpec, cfg, path: str, device, read_count, mode="bf16"):
     """Manifest first, then the reads (src/loader.zig:95-202, 225-276).
 
     Every shard header is parsed, then checked against the manifest of
@@ -396,7 +490,14 @@ def _load(spec: DecoderSpec, cfg, path: str, device, read_count):
             problems += hf_config.check_index(entries, shards)
         if problems:
             raise CheckpointError("InvalidManifest", problems)
-        weights = _read_weights(spec, mspec, files, where, device, read_count, torch, kernels)
+        if mode not in ("auto", "bf16", "f32"):
+            raise ValueError(f"mode must be auto, bf16 or f32, not {mode!r}")
+        if mode == "auto":
+            all_bf16 = all(t.dtype == "BF16" for t in present
+                           if not t.name.endswith(hf_config.INV_FREQ))
+            mode = "bf16" if all_bf16 else "f32"
+        weights = _read_weights(spec, mspec, files, where, device, read_count, torch, kernels,
+                                mode)
         torch.cuda.current_stream(device).synchronize()
         return weights
     finally:
@@ -404,8 +505,10 @@ def _load(spec: DecoderSpec, cfg, path: str, device, read_count):
             f.close()
 
 
-def _read_weights(spec, mspec, files, where, device, read_count, torch, kernels):
-    """The tensor reads of a checkpoint whose manifest passed."""
+def _read_weights(spec, mspec, files, where, device, read_count, torch, kernels, mode):
+    """The tensor reads of a checkpoint whose manifest passed, into the
+    bf16 layout or (mode "f32") float32 tensors decoded as the reference's
+    decode_chunk does (src/loader.zig:323-345)."""
 
     def handle(name):
         f = files[where[name]]
@@ -456,6 +559,56 @@ def _read_weights(spec, mspec, files, where, device, read_count, torch, kernels)
         return load_into(name, out) if name in where else None
 
     qw, kw = spec.q_heads * spec.head_dim, spec.kv_heads * spec.head_dim
+
+    def tied_check():
+        # The reference compares the decoded f32 values bit for bit.
+        same = torch.equal(as_f32("lm_head.weight").view(torch.int32),
+                           as_f32("model.embed_tokens.weight").view(torch.int32))
+        if not same:
+            raise CheckpointError("TiedHeadMismatch", [(
+                "lm_head.weight", "differs from model.embed_tokens.weight although the "
+                "embeddings are tied")])
+
+    if mode == "f32":
+        def f32(name, *shape):
+            return as_f32(name).view(*shape)
+
+        def opt(name, *shape):
+            return f32(name, *shape) if name in where else None
+
+        layers = []
+        for i in range(spec.layers):
+            n = _hf_names(i)
+            qkv_b = None
+            if n["q"] + ".bias" in where:
+                qkv_b = torch.cat([as_f32(n[p] + ".bias") for p in ("q", "k", "v")])
+            layers.append({
+                "input_norm": norm(n["input_norm"]),
+                "qkv_weight": torch.cat([f32(n["q"] + ".weight", qw, spec.hidden),
+                                         f32(n["k"] + ".weight", kw, spec.hidden),
+                                         f32(n["v"] + ".weight", kw, spec.hidden)]),
+                "qkv_bias": qkv_b,
+                "o_weight": f32(n["o"] + ".weight", spec.hidden, qw),
+                "o_bias": opt(n["o"] + ".bias", spec.hidden),
+                "post_attention_norm": norm(n["post_attention_norm"]),
+                "gate_weight": f32(n["gate"] + ".weight", spec.intermediate, spec.hidden),
+                "gate_bias": opt(n["gate"] + ".bias", spec.intermediate),
+                "up_weight": f32(n["up"] + ".weight", spec.intermediate, spec.hidden),
+                "up_bias": opt(n["up"] + ".bias", spec.intermediate),
+                "down_weight": f32(n["down"] + ".weight", spec.hidden, spec.intermediate),
+                "down_bias": opt(n["down"] + ".bias", spec.hidden),
+                "q_norm": norm(n["q_norm"]) if mspec.qk_norm else None,
+                "k_norm": norm(n["k_norm"]) if mspec.qk_norm else None,
+            })
+        embed = f32("model.embed_tokens.weight", spec.vocab, spec.hidden)
+        lm_head = None
+        if not spec.tie_word_embeddings:
+            lm_head = f32("lm_head.weight", spec.vocab, spec.hidden)
+        elif "lm_head.weight" in where:
+            tied_check()
+        return DecoderWeights(embed=embed, final_norm=norm("model.norm.weight"), layers=layers,
+                              lm_head=lm_head, mode="f32")
+
     layers = []
     for i in range(spec.layers):
         n = _hf_names(i)
@@ -494,12 +647,6 @@ def _read_weights(spec, mspec, files, where, device, read_count, torch, kernels)
     if not spec.tie_word_embeddings:
         lm_head = load_into("lm_head.weight", bf16(spec.vocab, spec.hidden))
     elif "lm_head.weight" in where:
-        # The reference compares the decoded f32 values bit for bit.
-        same = torch.equal(as_f32("lm_head.weight").view(torch.int32),
-                           as_f32("model.embed_tokens.weight").view(torch.int32))
-        if not same:
-            raise CheckpointError("TiedHeadMismatch", [(
-                "lm_head.weight", "differs from model.embed_tokens.weight although the "
-                "embeddings are tied")])
+        tied_check()
     return DecoderWeights(embed=embed, final_norm=norm("model.norm.weight"), layers=layers,
                           lm_head=lm_head)

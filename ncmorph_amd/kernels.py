@@ -294,17 +294,16 @@ def bf16_widen(src, ctx=None):
 
 
 def rms_norm_rows(x, weight, epsilon: float, out_mode: str = "bf16_f32", out=None, ctx=None):
-    """RMSNorm (bf16 mode) of every row of x (float32 [rows, width]) with
-    weight (float32 [width]) on torch's current stream; out_mode "bf16_f32"
-    (float32 holding bf16 values) or "bf16" (torch.bfloat16)."""
+    """RMSNorm of every row of x (float32 [rows, width]) with weight (float32
+    [width]) on torch's current stream: bf16 mode with out_mode "bf16_f32"
+    (float32 holding bf16 values) or "bf16" (torch.bfloat16); the f32 mode
+    (rms_norm, root.zig:226-239) with out_mode "f32"."""
     import torch
 
     W = "rms_norm_rows"
     a = _ck.Args(W)
     rows_, width = _ck.dims(x, "x", W, 2)
     mode = _mode(out_mode, W)
-    if mode == NCM_OUT_F32:
-        raise NcmError(-7, W, 'out_mode must be "bf16_f32" or "bf16"')
     dv = x.device
     px = a.dev(x, "x", _ck.F32, (rows_, width))
     pw = a.dev(weight, "weight", _ck.F32, (width,))
@@ -320,14 +319,13 @@ def rms_norm_rows(x, weight, epsilon: float, out_mode: str = "bf16_f32", out=Non
 
 def silu_mul(gate, up=None, out_mode: str = "bf16_f32", out=None, ctx=None):
     """round_bf16(silu_bf16(gate) * up) elementwise (up None: silu_bf16) on
-    torch's current stream; gate, up float32 of one shape."""
+    torch's current stream, or with out_mode "f32" the f32 mode silu(gate) *
+    up (root.zig:255-261); gate, up float32 of one shape."""
     import torch
 
     W = "silu_mul"
     a = _ck.Args(W)
     mode = _mode(out_mode, W)
-    if mode == NCM_OUT_F32:
-        raise NcmError(-7, W, 'out_mode must be "bf16_f32" or "bf16"')
     if gate is None:
         raise NcmError(-1, W, "gate is required")
     dv = gate.device

@@ -350,51 +350,82 @@ def rope_tables(inv, positions: int):
 
 
 def decoder_forward(ids, embed, layers, final_norm, lm_head, cos, sin, q_heads, kv_heads,
-                    head_dim, eps, window=0):
-    """forward_with_trace with bf16_compute (src/decoder.zig:62-228) for one
-    sequence, composed of the restatements above. Weights are float32
-    (bf16 values); each layer is a dict with input_norm, qkv_weight [(q_heads
-    + 2 kv_heads) head_dim, hidden] (the q, k and v projections' rows in that
-    order), qkv_bias, o_weight, o_bias, post_attention_norm, gate_up_weight
-    [2 intermediate, hidden] (gate rows then up rows), gate_up_bias,
-    down_weight, down_bias (biases may be None), and optionally q_norm and
-    k_norm [head_dim]: RMSNorm scales applied to every query and key head
-    before the rotation (attention_impl's QK-norm, root.zig:501-530).
-    lm_head None: tied to embed. cos, sin: [len(ids), head_dim]."""
+                    head_dim, eps, window=0, bf16=True, trace=None):
+    """forward_with_trace (src/decoder.zig:62-228) for one sequence, composed
+    of the restatements above: bf16_compute (bf16=True) or the f32 mode.
+    Weights are float32 (bf16 values in bf16 mode); each layer is a dict with
+    input_norm, qkv_weight [(q_heads + 2 kv_heads) head_dim, hidden] (the q,
+    k and v projections' rows in that order), qkv_bias, o_weight, o_bias,
+    post_attention_norm, gate_up_weight [2 intermediate, hidden] (gate rows
+    then up rows), gate_up_bias, down_weight, down_bias (biases may be None),
+    and optionally q_norm and k_norm [head_dim]: RMSNorm scales applied to
+    every query and key head before the rotation (attention_impl's QK-norm,
+    root.zig:501-530). lm_head None: tied to embed. cos, sin: [len(ids),
+    head_dim]. trace: a dict that receives the stages of decoder_trace_t
+    (decoder.zig:30-47), each [layers, tokens, width] (block_input [tokens,
+    hidden])."""
     t = len(ids)
-    hidden = round_bf16(embed[np.asarray(ids)])
+    rb = round_bf16 if bf16 else (lambda a: np.asarray(a, np.float32))
+    hidden = rb(np.asarray(embed, np.float32)[np.asarray(ids)])
     qw, kvw = q_heads * head_dim, kv_heads * head_dim
     mask = causal_mask(t, window)
+    stages = {k: [] for k in ("input_norm", "attention_context", "attention_output",
+                              "attention_residual", "post_attention_norm", "gate_projection",
+                              "up_projection", "gate_up_product", "mlp_output",
+                              "block_output")}
+    if trace is not None:
+        trace["block_input"] = hidden.copy()
 
-    def proj(x, w, b, lo, hi):
-        return matmul_bf16(x, w[lo:hi], None if b is None else b[lo:hi])
+    def proj(x, w, b, lo=None, hi=None):
+        w = np.asarray(w, np.float32)
+        if lo is not None:
+            w = w[lo:hi]
+            b = None if b is None else np.asarray(b, np.float32)[lo:hi]
+        if bf16:
+            return matmul_bf16(x, w, b)
+        y = matmul_reference(x, w)   # kernels.matmul, then the bias (root.zig:583-609)
+        return y if b is None else (y + np.asarray(b, np.float32)[None, :]).astype(np.float32)
 
     for layer in layers:
-        n = rms_norm(hidden, layer["input_norm"], eps, bf16=True)
+        n = rms_norm(hidden, layer["input_norm"], eps, bf16=bf16)
+        stages["input_norm"].append(n)
         wq, bq = layer["qkv_weight"], layer.get("qkv_bias")
         q = proj(n, wq, bq, 0, qw)
         k = proj(n, wq, bq, qw, qw + kvw)
         v = proj(n, wq, bq, qw + kvw, qw + 2 * kvw)
         if layer.get("q_norm") is not None:
             q = rms_norm(q.reshape(t * q_heads, head_dim), layer["q_norm"], eps,
-                         bf16=True).reshape(t, qw)
+                         bf16=bf16).reshape(t, qw)
             k = rms_norm(k.reshape(t * kv_heads, head_dim), layer["k_norm"], eps,
-                         bf16=True).reshape(t, kvw)
-        q = rotate_heads(q, cos, sin, q_heads, head_dim, bf16=True)
-        k = rotate_heads(k, cos, sin, kv_heads, head_dim, bf16=True)
-        ctx = attention_core(q, k, v, mask, q_heads, kv_heads, head_dim, bf16=True)
-        attn = matmul_bf16(ctx, layer["o_weight"], layer.get("o_bias"))
-        hidden = round_bf16(hidden + attn)
-        n = rms_norm(hidden, layer["post_attention_norm"], eps, bf16=True)
+                         bf16=bf16).reshape(t, kvw)
+        q = rotate_heads(q, cos, sin, q_heads, head_dim, bf16=bf16)
+        k = rotate_heads(k, cos, sin, kv_heads, head_dim, bf16=bf16)
+        ctx = attention_core(q, k, v, mask, q_heads, kv_heads, head_dim, bf16=bf16)
+        stages["attention_context"].append(ctx)
+        attn = proj(ctx, layer["o_weight"], layer.get("o_bias"))
+        stages["attention_output"].append(attn)
+        hidden = rb(hidden + attn)
+        stages["attention_residual"].append(hidden)
+        n = rms_norm(hidden, layer["post_attention_norm"], eps, bf16=bf16)
+        stages["post_attention_norm"].append(n)
         inter = layer["gate_up_weight"].shape[0] // 2
         wg, bg = layer["gate_up_weight"], layer.get("gate_up_bias")
         gate = proj(n, wg, bg, 0, inter)
         up = proj(n, wg, bg, inter, 2 * inter)
-        act = silu_mul_bf16(gate, up)
-        mlp = matmul_bf16(act, layer["down_weight"], layer.get("down_bias"))
-        hidden = round_bf16(hidden + mlp)
-    n = rms_norm(hidden, final_norm, eps, bf16=True)
-    return matmul_bf16(n, embed if lm_head is None else lm_head)
+        stages["gate_projection"].append(gate)
+        stages["up_projection"].append(up)
+        act = silu_mul_bf16(gate, up) if bf16 else (silu(gate) * up).astype(np.float32)
+        stages["gate_up_product"].append(act)
+        mlp = proj(act, layer["down_weight"], layer.get("down_bias"))
+        stages["mlp_output"].append(mlp)
+        hidden = rb(hidden + mlp)
+        stages["block_output"].append(hidden)
+    n = rms_norm(hidden, final_norm, eps, bf16=bf16)
+    if trace is not None:
+        for key, vals in stages.items():
+            trace[key] = np.stack(vals) if vals else np.zeros((0, t, 0), np.float32)
+    head = embed if lm_head is None else lm_head
+    return matmul_bf16(n, head) if bf16 else matmul_reference(n, head)
 
 
 # ------------------------------------------------------------ NCM body

@@ -10,6 +10,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 STRUCTS = {
     "ncm_decoder_shape_t": ("decoder", "_Shape"),
     "ncm_decoder_layer_t": ("decoder", "_Layer"),
+    "ncm_decoder_layer_f32_t": ("decoder", "_LayerF32"),
+    "ncm_decoder_trace_t": ("decoder", "_Trace"),
     "ncm_ncm_shape_t": ("ncm", "_Shape"),
     "ncm_ncm_weights_t": ("ncm", "_Weights"),
 }

@@ -46,8 +46,9 @@ def test_linear_checks():
 
 def test_elementwise_checks():
     _raises(NCM_E_SHAPE, kernels.rms_norm_rows, z(3, 8, dtype=f32), z(7, dtype=f32), 1e-5)
+    # the f32 mode writes float32: a bf16 out is refused
     _raises(NCM_E_ARG, kernels.rms_norm_rows, z(3, 8, dtype=f32), z(8, dtype=f32), 1e-5,
-            out_mode="f32")
+            out_mode="f32", out=z(3, 8))
     _raises(NCM_E_SHAPE, kernels.rms_norm_rows, z(3, 8, dtype=f32), z(8, dtype=f32), 1e-5,
             out=z(3, 8, dtype=f32)[:2])
     # up shorter than gate; a bf16 out for the float mode

@@ -185,7 +185,10 @@ def test_qwen3_checkpoint_with_config(ncm, oracle, cuda, tmp_path):
     _write_checkpoint(str(tmp_path), embed, layers, fnorm, hq, hkv, hd, shards=2,
                       f16_keys=f16, lm_head=embed)
     reads = [0]
-    mc, spec, loaded = decoder.load_checkpoint(str(tmp_path), cuda, read_count=reads)
+    # F16 tensors would select the f32 mode (as the reference's loader); the
+    # bf16 layout is asked for explicitly.
+    mc, spec, loaded = decoder.load_checkpoint(str(tmp_path), cuda, read_count=reads,
+                                               mode="bf16")
     assert mc.family == "Qwen3" and spec.head_dim == hd and spec.tie_word_embeddings
     assert reads[0] >= nl * 11 + 2
     assert loaded.lm_head is None
@@ -207,3 +210,52 @@ def test_qwen3_checkpoint_with_config(ncm, oracle, cuda, tmp_path):
     with pytest.raises(decoder.CheckpointError) as e:
         decoder.load_checkpoint(str(d2), cuda)
     assert e.value.kind == "TiedHeadMismatch"
+
+
+def test_f32_checkpoint_loads_in_f32_mode(ncm, oracle, cuda, tmp_path):
+    """A checkpoint holding F32 tensors loads in the reference's f32 mode
+    (bf16_compute only when every tensor is BF16, src/loader.zig:191-199):
+    load_checkpoint picks it, and the f32 forward of the loaded weights gives
+    the bits of the same weights handed over directly; mode="bf16" forces
+    the bf16 layout."""
+    import torch
+    from ncmorph_amd import decoder
+
+    rng = np.random.default_rng(13)
+    hidden, inter, vocab, hq, hkv, hd, nl = 128, 256, 200, 4, 2, 32, 2
+    embed, layers, fnorm = random_model(rng, lambda a: np.asarray(a, np.float32), hidden, inter,
+                                        vocab, hq, hkv, hd, nl, biases=True)
+    cfg = {"architectures": ["LlamaForCausalLM"], "model_type": "llama", "vocab_size": vocab,
+           "hidden_size": hidden, "intermediate_size": inter, "num_hidden_layers": nl,
+           "num_attention_heads": hq, "num_key_value_heads": hkv, "rms_norm_eps": 1e-5,
+           "rope_theta": 10000.0, "attention_bias": True, "mlp_bias": True,
+           "tie_word_embeddings": False}
+    (tmp_path / "config.json").write_text(json.dumps(cfg))
+    everything = ["model.embed_tokens.weight", "model.norm.weight", "lm_head.weight"]
+    for i in range(nl):
+        p = f"model.layers.{i}."
+        everything += [p + s for s in (
+            "input_layernorm.weight", "post_attention_layernorm.weight",
+            "self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+            "self_attn.q_proj.bias", "self_attn.k_proj.bias", "self_attn.v_proj.bias",
+            "self_attn.o_proj.weight", "self_attn.o_proj.bias", "mlp.gate_proj.weight",
+            "mlp.up_proj.weight", "mlp.down_proj.weight", "mlp.gate_proj.bias",
+            "mlp.up_proj.bias", "mlp.down_proj.bias")]
+    head = (rng.standard_normal((vocab, hidden)) * 0.05).astype(np.float32)
+    _write_checkpoint(str(tmp_path), embed, layers, fnorm, hq, hkv, hd, f32_keys=everything,
+                      lm_head=head)
+    cfg_spec, spec, w = decoder.load_checkpoint(str(tmp_path), cuda)
+    assert w.mode == "f32" and w.layers[0]["qkv_weight"].dtype == torch.float32
+    from .test_decoder_f32_gpu import _f32_weights
+
+    direct = _f32_weights(decoder, cuda, embed, layers, fnorm, lm_head=head)
+    cos, sin = oracle.rope_tables(oracle.rope_default_frequencies(hd, 10000.0), 29)
+    cd = torch.from_numpy(cos).to(cuda)
+    sd = torch.from_numpy(sin).to(cuda)
+    ids = rng.integers(0, vocab, (2, 29))
+    a = decoder.run(spec, w, ids, cd, sd)
+    b = decoder.forward_f32(spec, direct, ids, cd, sd)
+    torch.cuda.synchronize()
+    assert torch.equal(a.view(torch.int32), b.view(torch.int32))
+    _, _, w16 = decoder.load_checkpoint(str(tmp_path), cuda, mode="bf16")
+    assert w16.mode == "bf16" and w16.layers[0]["qkv_weight"].dtype == torch.bfloat16
