@@ -595,6 +595,89 @@ int ncm_st_index_entry(const ncm_st_index_t* ix, int64_t i, const char** tensor,
 /* NCM_E_ARG when the index has no metadata.total_size. */
 int ncm_st_index_total_size(const ncm_st_index_t* ix, uint64_t* total);
 
+/* ------------------------------------------------------------------------
+ * The upstream VQ-VAE tokenizer (inference): encoder, multiscale residual
+ * quantizer and decoder of research/reference/vq_forward_semantics.md, in
+ * the configuration of the released WMT14 tokenizer
+ * (research/converter/wmt14_tokenizer_keys.md) or any other of that module.
+ * The reference has no code for it (ROADMAP.md:259-261 plans a Zig port,
+ * packages/vq); these entry points follow the conventions of the kernels
+ * module (caller-owned device buffers, explicit sizes, int status).
+ * Float32 arithmetic throughout, in the device's summation order.
+ * ------------------------------------------------------------------------ */
+#define NCM_VQ_TOK_MAX_LEVELS 64
+#define NCM_VQ_TOK_MAX_STAGES 8
+
+/* Shapes, switches and device weights of one tokenizer. Conv weights are
+ * packed by ncm_vq_tok_pack_conv_dev from their PyTorch layouts. */
+typedef struct ncm_vq_tok {
+    int64_t embed_dim;       /* D: a multiple of 4 * groups */
+    int64_t in_vocab;        /* C: token table rows */
+    int64_t context_length;  /* wpe rows, >= the sequence length */
+    int32_t n_levels;        /* K, 1 .. NCM_VQ_TOK_MAX_LEVELS */
+    int32_t groups;          /* GroupNorm groups of the pre-quant and cascade norms */
+    /* Positions of each level, increasing; the last one is the sequence
+     * length L (the levels of vq.levels, models/quant.py:285-292). */
+    int64_t level_len[NCM_VQ_TOK_MAX_LEVELS];
+    int64_t level_vocab[NCM_VQ_TOK_MAX_LEVELS];  /* V_l: codebook rows */
+    float group_eps;         /* GroupNorm epsilon (1e-5) */
+    float resi_ratio;        /* Phi blend ratio r (0.5) */
+    /* Level 0 through the learned conv cascade (learned_l1_sampling with
+     * learned_l1_cascade): n_stages kernel = stride = stage_stride[i] convs
+     * whose strides multiply to L / level_len[0]; GroupNorm after every
+     * inner down stage and up stage (cascade_norm) and after the last down
+     * stage (cascade_norm_final). 0: level 0 pools by area and upsamples
+     * linearly like the other levels. */
+    int32_t learned_level0;
+    int32_t n_stages;
+    int64_t stage_stride[NCM_VQ_TOK_MAX_STAGES];
+    int32_t cascade_norm;
+    int32_t cascade_norm_final;
+    /* Device weights (float32, 16-byte aligned). */
+    const float* wte;                                 /* [C, D] (encode only) */
+    const float* wpe;                                 /* [context_length, D] */
+    const float* codebook[NCM_VQ_TOK_MAX_LEVELS];     /* [V_l, D] */
+    /* Phi of each level (quant_resi.l): Conv1d(D, D, 3, padding 1) packed
+     * [D, 3 D] and its bias [D]; weight NULL: no Phi (Q = the upsampled
+     * codes). */
+    const float* resi_weight[NCM_VQ_TOK_MAX_LEVELS];
+    const float* resi_bias[NCM_VQ_TOK_MAX_LEVELS];
+    const float* down_weight[NCM_VQ_TOK_MAX_STAGES];  /* packed [D, s D] */
+    const float* down_bias[NCM_VQ_TOK_MAX_STAGES];    /* [D] */
+    const float* up_weight[NCM_VQ_TOK_MAX_STAGES];    /* packed [s D, D] */
+    const float* up_bias[NCM_VQ_TOK_MAX_STAGES];      /* [D] */
+} ncm_vq_tok_t;
+
+/* Repacks a conv weight for ncm_vq_tok_t: transposed 0 takes a Conv1d
+ * weight (out = c, in = c, k) to dst[o, j c + i] = src[o, i, j] ([c, k c]);
+ * transposed 1 a ConvTranspose1d weight (in = c, out = c, k) to
+ * dst[j c + o, i] = src[i, o, j] ([k c, c]). Device buffers of c c k floats. */
+int ncm_vq_tok_pack_conv_dev(ncm_ctx_t* ctx, const float* src, float* dst, int64_t c, int64_t k,
+                             int transposed);
+
+/* Tokenizer encode in eval mode for `batch` sequences of L = level_len[K-1]
+ * token ids (host int64 [batch, L], each in [0, C): NCM_E_ARG otherwise,
+ * before any device work): z = GroupNorm(wte[ids] + wpe) (the encoder and
+ * pre-quant norm, vq_forward_semantics.md:38-49), then the quantizer loop
+ * (models/quant.py:448-549, vq_forward_semantics.md:59-76): per level l,
+ * u = Down_l(r), codes = argmin_k |u - e_k|^2 (lowest index on ties), Q =
+ * Phi_l(Up_l(e[codes])), zhat += Q, r -= Q. codes: int32 [batch, sum_l
+ * level_len[l]], level 0 first; zhat (NULL: not kept) and latent (z, NULL:
+ * not kept): float [batch, L, D]. The search computes |e|^2 - 2 u.e on the
+ * fp32 MFMA, so a code may differ from PyTorch's where two distances agree
+ * to float32 rounding. */
+int ncm_vq_tok_encode_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const int64_t* token_ids,
+                          int64_t batch, int32_t* codes, float* zhat, float* latent);
+
+/* The quantizer alone from a latent z (device float [batch, L, D]). */
+int ncm_vq_tok_quantize_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const float* latent,
+                            int64_t batch, int32_t* codes, float* zhat);
+
+/* zhat = sum_l Phi_l(Up_l(e_l[codes_l])) (the decoder's input in eval mode);
+ * codes as ncm_vq_tok_encode_dev writes them, each clamped to [0, V_l). */
+int ncm_vq_tok_reconstruct_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const int32_t* codes,
+                               int64_t batch, float* zhat);
+
 #ifdef __cplusplus
 }
 #endif

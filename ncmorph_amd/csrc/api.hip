@@ -17,6 +17,7 @@
 #include "ncm_body.h"
 #include "rvq.h"
 #include "status.h"
+#include "vq_tok.h"
 
 struct ncm_ctx {
     int device = 0;
@@ -946,6 +947,137 @@ int ncm_rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t
     if (rc) return rc;
     return ncm::rvq_encode(ctx, x, b, t, d, levels, strides, codebooks, csq, v, codes, recon,
                            gap, force_codes, n_flagged);
+}
+
+// Shape, switch and weight checks shared by the tokenizer entry points.
+static int vq_tok_check(const ncm_vq_tok_t* t, bool need_embed) {
+    if (!t) return NCM_E_NULL;
+    if (t->n_levels < 1 || t->n_levels > NCM_VQ_TOK_MAX_LEVELS) return NCM_E_SHAPE;
+    if (t->groups < 1 || t->embed_dim <= 0 || t->embed_dim % (4 * t->groups) ||
+        t->embed_dim > (1 << 16))
+        return NCM_E_SHAPE;
+    const int64_t L = t->level_len[t->n_levels - 1];
+    if (L < 1 || L > (1 << 20)) return NCM_E_SHAPE;
+    for (int l = 0; l < t->n_levels; ++l) {
+        if (t->level_len[l] < 1 || t->level_len[l] > L) return NCM_E_SHAPE;
+        if (l > 0 && t->level_len[l] <= t->level_len[l - 1]) return NCM_E_SHAPE;
+        if (t->level_vocab[l] < 1 || t->level_vocab[l] > (int64_t(1) << 30)) return NCM_E_SHAPE;
+        if (!t->codebook[l]) return NCM_E_NULL;
+        if ((uintptr_t)t->codebook[l] % 16) return NCM_E_ARG;
+        if (t->resi_weight[l] && (!t->resi_bias[l] || (uintptr_t)t->resi_weight[l] % 16))
+            return NCM_E_ARG;
+    }
+    if (t->learned_level0) {
+        if (t->n_stages < 0 || t->n_stages > NCM_VQ_TOK_MAX_STAGES) return NCM_E_SHAPE;
+        if (L % t->level_len[0]) return NCM_E_SHAPE;
+        int64_t prod = 1;
+        for (int i = 0; i < t->n_stages; ++i) {
+            if (t->stage_stride[i] < 1 || t->stage_stride[i] > 64) return NCM_E_SHAPE;
+            prod *= t->stage_stride[i];
+            if (!t->down_weight[i] || !t->down_bias[i] || !t->up_weight[i] || !t->up_bias[i])
+                return NCM_E_NULL;
+            if ((uintptr_t)t->down_weight[i] % 16 || (uintptr_t)t->up_weight[i] % 16)
+                return NCM_E_ARG;
+        }
+        if (prod != L / t->level_len[0]) return NCM_E_SHAPE;
+    }
+    if (need_embed) {
+        if (!t->wte || !t->wpe) return NCM_E_NULL;
+        if ((uintptr_t)t->wte % 16 || (uintptr_t)t->wpe % 16) return NCM_E_ARG;
+        if (t->in_vocab < 1 || t->in_vocab > (int64_t(1) << 31) || t->context_length < L)
+            return NCM_E_SHAPE;
+        if (!(t->group_eps >= 0.0f)) return NCM_E_ARG;
+    }
+    return NCM_OK;
+}
+
+static int vq_tok_batch_ok(const ncm_vq_tok_t* t, int64_t batch) {
+    if (batch < 0) return NCM_E_SHAPE;
+    if (batch == 0) return NCM_E_ARG;  // EmptyInput
+    if (batch > 65535) return NCM_E_SHAPE;
+    int64_t nsum = 0;
+    for (int l = 0; l < t->n_levels; ++l) nsum += t->level_len[l];
+    const int64_t L = t->level_len[t->n_levels - 1];
+    // Activation buffers below 2^31 elements, codes below 2^31 entries.
+    if (batch * (L + 2) * t->embed_dim >= (int64_t(1) << 31) || batch * nsum >= (int64_t(1) << 31))
+        return NCM_E_SHAPE;
+    return NCM_OK;
+}
+
+static int vq_tok_run(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const int32_t* ids,
+                      const float* latent_in, int64_t batch, int32_t* codes, float* zhat,
+                      float* latent_out) {
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::vq_tok_workspace_bytes(*tok, batch, zhat == nullptr), &ws);
+    if (rc) return rc;
+    hipError_t e = ncm::vq_tok_encode(*tok, ids, latent_in, batch, codes, zhat, latent_out, ws,
+                                      ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "vq tokenizer encode");
+    return NCM_OK;
+}
+
+int ncm_vq_tok_pack_conv_dev(ncm_ctx_t* ctx, const float* src, float* dst, int64_t c, int64_t k,
+                             int transposed) {
+    if (!ctx) return NCM_E_NULL;
+    if (!src || !dst) return NCM_E_NULL;
+    if (c <= 0 || k <= 0 || c > (1 << 16) || k > 64) return NCM_E_SHAPE;
+    if (transposed != 0 && transposed != 1) return NCM_E_ARG;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::vq_tok_pack_conv(src, dst, c, k, transposed, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "vq tokenizer conv pack");
+    return NCM_OK;
+}
+
+int ncm_vq_tok_encode_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const int64_t* token_ids,
+                          int64_t batch, int32_t* codes, float* zhat, float* latent) {
+    if (!ctx) return NCM_E_NULL;
+    int rc = vq_tok_check(tok, true);
+    if (rc) return rc;
+    rc = vq_tok_batch_ok(tok, batch);
+    if (rc) return rc;
+    if (!token_ids || !codes) return NCM_E_NULL;
+    if ((zhat && (uintptr_t)zhat % 16) || (latent && (uintptr_t)latent % 16)) return NCM_E_ARG;
+    const int64_t L = tok->level_len[tok->n_levels - 1];
+    std::vector<int32_t> ids((size_t)(batch * L));
+    for (int64_t i = 0; i < batch * L; ++i) {
+        if (token_ids[i] < 0 || token_ids[i] >= tok->in_vocab) return NCM_E_ARG;
+        ids[(size_t)i] = (int32_t)token_ids[i];
+    }
+    return vq_tok_run(ctx, tok, ids.data(), nullptr, batch, codes, zhat, latent);
+}
+
+int ncm_vq_tok_quantize_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const float* latent,
+                            int64_t batch, int32_t* codes, float* zhat) {
+    if (!ctx) return NCM_E_NULL;
+    int rc = vq_tok_check(tok, false);
+    if (rc) return rc;
+    rc = vq_tok_batch_ok(tok, batch);
+    if (rc) return rc;
+    if (!latent || !codes) return NCM_E_NULL;
+    if ((uintptr_t)latent % 16 || (zhat && (uintptr_t)zhat % 16)) return NCM_E_ARG;
+    return vq_tok_run(ctx, tok, nullptr, latent, batch, codes, zhat, nullptr);
+}
+
+int ncm_vq_tok_reconstruct_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const int32_t* codes,
+                               int64_t batch, float* zhat) {
+    if (!ctx) return NCM_E_NULL;
+    int rc = vq_tok_check(tok, false);
+    if (rc) return rc;
+    rc = vq_tok_batch_ok(tok, batch);
+    if (rc) return rc;
+    if (!codes || !zhat) return NCM_E_NULL;
+    if ((uintptr_t)zhat % 16) return NCM_E_ARG;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::vq_tok_workspace_bytes(*tok, batch, false), &ws);
+    if (rc) return rc;
+    hipError_t e = ncm::vq_tok_reconstruct(*tok, codes, batch, zhat, ws, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "vq tokenizer reconstruct");
+    return NCM_OK;
 }
 
 int ncm_rvq_decode(ncm_ctx_t* ctx, const int32_t* codes, int64_t b, int64_t t, int64_t d,
