@@ -678,6 +678,42 @@ int ncm_vq_tok_quantize_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const float
 int ncm_vq_tok_reconstruct_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const int32_t* codes,
                                int64_t batch, float* zhat);
 
+/* The tokenizer's decoder (models/vae.py:198-258 in eval mode,
+ * vq_forward_semantics.md:84-94): x = zhat; x += c_proj(attn(LN_1(x)));
+ * x += mlp.c_proj(GELU(mlp.c_fc(LN_2(x)))); logits = output_layer(ln_f(x)).
+ * Attention is bidirectional over the L positions, n_head heads of D /
+ * n_head, with q and k RMS-normalised per head when q_norm / k_norm are set
+ * (both or neither). Device float32 weights in PyTorch's Linear layout [out,
+ * in]; LayerNorm biases may be NULL (ln_f has none). */
+typedef struct ncm_vq_tok_decoder {
+    int32_t n_head;
+    float ln_eps;                /* LayerNorm epsilon (1e-6) */
+    float qk_eps;                /* q / k RMSNorm epsilon (1e-6) */
+    const float* ln1_weight;     /* [D] */
+    const float* ln1_bias;       /* [D] or NULL */
+    const float* attn_weight;    /* c_attn [3 D, D]: q, k, v rows */
+    const float* attn_bias;      /* [3 D] or NULL */
+    const float* proj_weight;    /* attn.c_proj [D, D] */
+    const float* proj_bias;      /* [D] or NULL */
+    const float* q_norm;         /* [D / n_head] or NULL */
+    const float* k_norm;         /* [D / n_head] or NULL */
+    const float* ln2_weight;     /* [D] */
+    const float* ln2_bias;       /* [D] or NULL */
+    const float* fc_weight;      /* mlp.c_fc [4 D, D] */
+    const float* fc_bias;        /* [4 D] or NULL */
+    const float* fc_proj_weight; /* mlp.c_proj [D, 4 D] */
+    const float* fc_proj_bias;   /* [D] or NULL */
+    const float* lnf_weight;     /* ln_f [D] (no bias) */
+    const float* out_weight;     /* output_layer [C, D] (no bias) */
+} ncm_vq_tok_decoder_t;
+
+/* logits (float [batch, L, C], C = tok->in_vocab) of the decoder on zhat
+ * (float [batch, L, D], as ncm_vq_tok_encode_dev or
+ * ncm_vq_tok_reconstruct_dev write it). Only the shapes of tok are read. */
+int ncm_vq_tok_decode_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok,
+                          const ncm_vq_tok_decoder_t* dec, const float* zhat, int64_t batch,
+                          float* logits);
+
 #ifdef __cplusplus
 }
 #endif

@@ -73,6 +73,7 @@ SIGNATURES = [
     ("ncm_vq_tok_encode_dev", i32, [vp, vp, vp, i64, vp, vp, vp]),
     ("ncm_vq_tok_quantize_dev", i32, [vp, vp, vp, i64, vp, vp]),
     ("ncm_vq_tok_reconstruct_dev", i32, [vp, vp, vp, i64, vp]),
+    ("ncm_vq_tok_decode_dev", i32, [vp, vp, vp, vp, i64, vp]),
     ("ncm_st_parse", i32, [vp, sz, C.c_uint64, C.POINTER(vp)]),
     ("ncm_st_open", i32, [C.c_char_p, C.POINTER(vp)]),
     ("ncm_st_close", i32, [vp]),

@@ -1080,6 +1080,44 @@ int ncm_vq_tok_reconstruct_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const in
     return NCM_OK;
 }
 
+int ncm_vq_tok_decode_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok,
+                          const ncm_vq_tok_decoder_t* dec, const float* zhat, int64_t batch,
+                          float* logits) {
+    if (!ctx || !tok || !dec) return NCM_E_NULL;
+    if (tok->n_levels < 1 || tok->n_levels > NCM_VQ_TOK_MAX_LEVELS) return NCM_E_SHAPE;
+    const int64_t L = tok->level_len[tok->n_levels - 1], D = tok->embed_dim;
+    const int64_t C = tok->in_vocab;
+    if (L < 1 || L > 4096 || D < 4 || D % 4 || D > (1 << 16) || C < 1 || C % 4 ||
+        C > (int64_t(1) << 31))
+        return NCM_E_SHAPE;
+    if (dec->n_head < 1 || D % dec->n_head || (D / dec->n_head) % 4 || D / dec->n_head > 256)
+        return NCM_E_SHAPE;
+    if (batch < 0) return NCM_E_SHAPE;
+    if (batch == 0) return NCM_E_ARG;
+    if (batch > 65535 || batch * L * 4 * D >= (int64_t(1) << 31) ||
+        batch * L * C >= (int64_t(1) << 40))
+        return NCM_E_SHAPE;
+    if (!zhat || !logits) return NCM_E_NULL;
+    if (!dec->ln1_weight || !dec->attn_weight || !dec->proj_weight || !dec->ln2_weight ||
+        !dec->fc_weight || !dec->fc_proj_weight || !dec->lnf_weight || !dec->out_weight)
+        return NCM_E_NULL;
+    if (!dec->q_norm != !dec->k_norm) return NCM_E_ARG;
+    if (!(dec->ln_eps >= 0.0f) || !(dec->qk_eps >= 0.0f)) return NCM_E_ARG;
+    const void* al[] = {zhat, logits, dec->ln1_weight, dec->ln1_bias, dec->attn_weight,
+                        dec->proj_weight, dec->ln2_weight, dec->ln2_bias, dec->fc_weight,
+                        dec->fc_proj_weight, dec->lnf_weight, dec->out_weight};
+    for (const void* q : al)
+        if ((uintptr_t)q % 16) return NCM_E_ARG;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::vq_tok_decoder_workspace_bytes(*tok, batch), &ws);
+    if (rc) return rc;
+    hipError_t e = ncm::vq_tok_decode(*tok, *dec, zhat, batch, logits, ws, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "vq tokenizer decode");
+    return NCM_OK;
+}
+
 int ncm_rvq_decode(ncm_ctx_t* ctx, const int32_t* codes, int64_t b, int64_t t, int64_t d,
                    int64_t levels, const int32_t* strides, const uint16_t* codebooks, int64_t v,
                    float* recon) {

@@ -24,4 +24,10 @@ hipError_t vq_tok_encode(const ncm_vq_tok_t& t, const int32_t* ids_host, const f
 hipError_t vq_tok_reconstruct(const ncm_vq_tok_t& t, const int32_t* codes, int64_t batch,
                               float* zhat, void* ws, hipStream_t st);
 
+// The decoder block, ln_f and the output layer on zhat [batch, L, D] ->
+// logits [batch, L, C].
+size_t vq_tok_decoder_workspace_bytes(const ncm_vq_tok_t& t, int64_t batch);
+hipError_t vq_tok_decode(const ncm_vq_tok_t& t, const ncm_vq_tok_decoder_t& dec, const float* zhat,
+                         int64_t batch, float* logits, void* ws, hipStream_t st);
+
 }  // namespace ncm

@@ -39,13 +39,16 @@ constexpr int kNT = 256;
 enum { kEpiStage = 0, kEpiPhi = 1, kEpiDist = 2 };
 
 struct VtEpi {
-    // kEpiStage: y = acc + bias[n % bias_len]; pad_len > 0 stores flat row
+    // kEpiStage: y = act(acc + bias[n % bias_len]) (+ res, [M, N], may be
+    // y); bias NULL: none; act 1: exact GELU. pad_len > 0 stores flat row
     // R = (m N + n) / D of [rows, D] at padded row R + 2 (R / pad_len) + 1.
     const float* bias;
     int64_t bias_len;
     float* y;
     int64_t pad_len;
     int64_t d;
+    const float* res;
+    int act;
     // kEpiPhi: Q = (1 - ratio) h + ratio (acc + bias); zhat (+)= Q; r -= Q.
     const float* hpad;
     float* zhat;
@@ -65,6 +68,16 @@ __device__ __forceinline__ unsigned long long dist_key(float v, int64_t col) {
     b = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
     if (v != v) b = 0;
     return ((unsigned long long)b << 32) | (uint32_t)col;
+}
+
+// Exact GELU (nn.GELU's default): x Phi(x) with the device library's erff.
+__device__ __forceinline__ float gelu_exact(float x) {
+    return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+}
+
+__device__ __forceinline__ float stage_value(const VtEpi& ep, float acc, int64_t n) {
+    const float v = ep.bias ? acc + ep.bias[n % ep.bias_len] : acc;
+    return ep.act == 1 ? gelu_exact(v) : v;
 }
 
 __device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
@@ -139,7 +152,8 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void vt_gemm_kernel(
             }
             f32x4_t o;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) o[j] = v[j] + ep.bias[(n + j) % ep.bias_len];
+            for (int j = 0; j < 4; ++j) o[j] = stage_value(ep, v[j], n + j);
+            if (ep.res) o += *(const f32x4_t*)(ep.res + dst);
             *(f32x4_t*)(ep.y + dst) = o;
         } else {
             // Virtual row m = b (L + 2) + t; t >= L straddles two sequences.
@@ -209,7 +223,8 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void vt_gemm_kernel(
                         const int64_t row = dst / ep.d;
                         dst = (row + 2 * (row / ep.pad_len) + 1) * ep.d + dst % ep.d;
                     }
-                    ep.y[dst] = v + ep.bias[n % ep.bias_len];
+                    const float o = stage_value(ep, v, n);
+                    ep.y[dst] = ep.res ? ep.res[dst] + o : o;
                 } else {
                     const int64_t b = m / (ep.seq + 2);
                     const int64_t t = m - b * (ep.seq + 2);
@@ -702,6 +717,116 @@ hipError_t quantize_body(const ncm_vq_tok_t& t, const Ws& w, int32_t* codes, flo
     return hipSuccess;
 }
 
+// ------------------------------------------------------------------ decoder
+// The VQ-VAE decoder in eval mode (models/vae.py:198-258,
+// vq_forward_semantics.md:84-94): one pre-LN block (bidirectional attention
+// with per-head RMSNorm on q and k, a GELU MLP), ln_f, the output layer.
+
+// LayerNorm of one row per wavefront: (x - mean) / sqrt(var + eps) * w (+ b),
+// biased variance, two passes over the row (models/vae.py:6-13).
+__global__ __launch_bounds__(kNT) void vt_layer_norm_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ w,
+                                                            const float* __restrict__ bias,
+                                                            float* __restrict__ y, int64_t rows,
+                                                            int64_t D, float eps) {
+    const int64_t row = blockIdx.x * (int64_t)(kNT / 64) + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const int lane = threadIdx.x & 63;
+    const float* xr = x + row * D;
+    float s = 0.0f;
+    for (int64_t c = 4 * lane; c < D; c += 256) {
+        const f32x4_t v = *(const f32x4_t*)(xr + c);
+        s += (v[0] + v[1]) + (v[2] + v[3]);
+    }
+    const float mean = wave_sum_xor(s) / (float)D;
+    float q = 0.0f;
+    for (int64_t c = 4 * lane; c < D; c += 256) {
+        const f32x4_t v = *(const f32x4_t*)(xr + c);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) q += (v[j] - mean) * (v[j] - mean);
+    }
+    const float inv = 1.0f / sqrtf(wave_sum_xor(q) / (float)D + eps);
+    for (int64_t c = 4 * lane; c < D; c += 256) {
+        const f32x4_t v = *(const f32x4_t*)(xr + c);
+        const f32x4_t wv = *(const f32x4_t*)(w + c);
+        f32x4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = (v[j] - mean) * inv * wv[j];
+        if (bias) o += *(const f32x4_t*)(bias + c);
+        *(f32x4_t*)(y + row * D + c) = o;
+    }
+}
+
+// Per-head RMSNorm of q and k in place (models/vae.py:16-26, :60-62):
+// x / sqrt(mean(x^2) + eps) * w over each head_dim slice; one wavefront per
+// (row, head) of q (blockIdx.y 0) or k (1). qkv rows are [q | k | v], 3 D.
+__global__ __launch_bounds__(64) void vt_qk_norm_kernel(float* qkv, const float* __restrict__ wq,
+                                                        const float* __restrict__ wk, int64_t D,
+                                                        int heads, int hd, float eps) {
+    const int64_t row = blockIdx.x;
+    const int which = blockIdx.y / heads;
+    const int h = blockIdx.y % heads;
+    const int lane = threadIdx.x;
+    float* p = qkv + row * 3 * D + which * D + (int64_t)h * hd;
+    const float* w = which ? wk : wq;
+    float s = 0.0f;
+    for (int d = lane; d < hd; d += 64) s += p[d] * p[d];
+    const float inv = 1.0f / sqrtf(wave_sum_xor(s) / (float)hd + eps);
+    for (int d = lane; d < hd; d += 64) p[d] = p[d] * inv * w[d];
+}
+
+// Bidirectional softmax attention, one wavefront per (query, head,
+// sequence): scores q.k / sqrt(hd) for every key (lane = key), the maximum,
+// exp and their sum, then out[d] = sum_j p_j v_j[d] / sum (lane = d).
+// Scores in LDS (up to kAttnMaxT keys).
+constexpr int kAttnMaxT = 4096;
+__global__ __launch_bounds__(64) void vt_attention_kernel(const float* __restrict__ qkv,
+                                                          float* __restrict__ out, int64_t T,
+                                                          int64_t D, int hd, float scale) {
+    __shared__ float sc[kAttnMaxT];
+    __shared__ float qs[256];
+    const int64_t t = blockIdx.x;
+    const int h = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    const int lane = threadIdx.x;
+    const float* base = qkv + b * T * 3 * D;
+    const float* q = base + t * 3 * D + (int64_t)h * hd;
+    for (int d = lane; d < hd; d += 64) qs[d] = q[d];
+    __syncthreads();
+    float mx = -__builtin_inff();
+    for (int64_t j = lane; j < T; j += 64) {
+        const float* k = base + j * 3 * D + D + (int64_t)h * hd;
+        float dot = 0.0f;
+        for (int d = 0; d < hd; d += 4) {
+            const f32x4_t kv = *(const f32x4_t*)(k + d);
+            dot += qs[d] * kv[0];
+            dot += qs[d + 1] * kv[1];
+            dot += qs[d + 2] * kv[2];
+            dot += qs[d + 3] * kv[3];
+        }
+        const float v = dot * scale;
+        sc[j] = v;
+        mx = fmaxf(mx, v);
+    }
+    // wavefront maximum
+    for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off));
+    float sum = 0.0f;
+    for (int64_t j = lane; j < T; j += 64) {
+        const float e = expf(sc[j] - mx);
+        sc[j] = e;
+        sum += e;
+    }
+    sum = wave_sum_xor(sum);
+    __syncthreads();
+    const float inv = 1.0f / sum;
+    for (int d = lane; d < hd; d += 64) {
+        float acc = 0.0f;
+        for (int64_t j = 0; j < T; ++j)
+            acc += sc[j] * base[j * 3 * D + 2 * D + (int64_t)h * hd + d];
+        out[(b * T + t) * D + (int64_t)h * hd + d] = acc * inv;
+    }
+}
+
 }  // namespace
 
 size_t vq_tok_workspace_bytes(const ncm_vq_tok_t& t, int64_t batch, bool need_zhat) {
@@ -734,6 +859,58 @@ hipError_t vq_tok_encode(const ncm_vq_tok_t& t, const int32_t* ids_host, const f
                               hipMemcpyDeviceToDevice, st));
     }
     return quantize_body(t, w, codes, zh, st);
+}
+
+size_t vq_tok_decoder_workspace_bytes(const ncm_vq_tok_t& t, int64_t batch) {
+    const int64_t M = batch * t.level_len[t.n_levels - 1], D = t.embed_dim;
+    // x, h (D each), qkv (3 D), attention output (D), MLP hidden (4 D)
+    return align256((size_t)(M * D) * 4) * 3 + align256((size_t)(M * 3 * D) * 4) +
+           align256((size_t)(M * 4 * D) * 4);
+}
+
+hipError_t vq_tok_decode(const ncm_vq_tok_t& t, const ncm_vq_tok_decoder_t& dec, const float* zhat,
+                         int64_t batch, float* logits, void* ws, hipStream_t st) {
+    const int64_t L = t.level_len[t.n_levels - 1], D = t.embed_dim, M = batch * L;
+    const int64_t C = t.in_vocab;
+    char* p = (char*)ws;
+    auto take = [&](int64_t floats) {
+        float* q = (float*)p;
+        p += align256((size_t)floats * 4);
+        return q;
+    };
+    float* x = take(M * D);
+    float* h = take(M * D);
+    float* a = take(M * D);
+    float* qkv = take(M * 3 * D);
+    float* f = take(M * 4 * D);
+    auto gemm = [&](const float* in, const float* w, const float* bias, float* y, int64_t K,
+                    int64_t N, const float* res, int act) {
+        VtEpi ep{};
+        ep.bias = bias; ep.bias_len = N; ep.y = y; ep.d = N; ep.res = res; ep.act = act;
+        return launch_vt_gemm<kEpiStage>(in, K, M, w, M, K, N, ep, st);
+    };
+    auto ln = [&](const float* in, const float* w, const float* b, float* y) {
+        hipLaunchKernelGGL(vt_layer_norm_kernel, dim3((unsigned)((M + 3) / 4)), dim3(kNT), 0, st,
+                           in, w, b, y, M, D, dec.ln_eps);
+        return hipGetLastError();
+    };
+    const int hd = (int)(D / dec.n_head);
+    VT_TRY(ln(zhat, dec.ln1_weight, dec.ln1_bias, h));
+    VT_TRY(gemm(h, dec.attn_weight, dec.attn_bias, qkv, D, 3 * D, nullptr, 0));
+    if (dec.q_norm) {
+        hipLaunchKernelGGL(vt_qk_norm_kernel, dim3((unsigned)M, 2 * dec.n_head), dim3(64), 0, st,
+                           qkv, dec.q_norm, dec.k_norm, D, dec.n_head, hd, dec.qk_eps);
+        VT_TRY(hipGetLastError());
+    }
+    hipLaunchKernelGGL(vt_attention_kernel, dim3((unsigned)L, dec.n_head, (unsigned)batch),
+                       dim3(64), 0, st, qkv, a, L, D, hd, 1.0f / sqrtf((float)hd));
+    VT_TRY(hipGetLastError());
+    VT_TRY(gemm(a, dec.proj_weight, dec.proj_bias, x, D, D, zhat, 0));        // x = zhat + proj
+    VT_TRY(ln(x, dec.ln2_weight, dec.ln2_bias, h));
+    VT_TRY(gemm(h, dec.fc_weight, dec.fc_bias, f, D, 4 * D, nullptr, 1));     // GELU
+    VT_TRY(gemm(f, dec.fc_proj_weight, dec.fc_proj_bias, x, 4 * D, D, x, 0)); // x += mlp
+    VT_TRY(ln(x, dec.lnf_weight, nullptr, h));
+    return gemm(h, dec.out_weight, nullptr, logits, D, C, nullptr, 0);
 }
 
 hipError_t vq_tok_reconstruct(const ncm_vq_tok_t& t, const int32_t* codes, int64_t batch,

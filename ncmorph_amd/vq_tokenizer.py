@@ -156,6 +156,35 @@ class _Tok(C.Structure):
     ]
 
 
+class _Dec(C.Structure):
+    _fields_ = [("n_head", C.c_int32), ("ln_eps", C.c_float), ("qk_eps", C.c_float)] + [
+        (f, C.c_void_p) for f in (
+            "ln1_weight", "ln1_bias", "attn_weight", "attn_bias", "proj_weight", "proj_bias",
+            "q_norm", "k_norm", "ln2_weight", "ln2_bias", "fc_weight", "fc_bias",
+            "fc_proj_weight", "fc_proj_bias", "lnf_weight", "out_weight")]
+
+
+# _Dec field -> (state_dict name, shape factory of (D, hd, C))
+_DEC_NAMES = {
+    "ln1_weight": ("decoder.middle_block.ln_1.weight", lambda d, h, c: (d,)),
+    "ln1_bias": ("decoder.middle_block.ln_1.bias", lambda d, h, c: (d,)),
+    "attn_weight": ("decoder.middle_block.attn.c_attn.weight", lambda d, h, c: (3 * d, d)),
+    "attn_bias": ("decoder.middle_block.attn.c_attn.bias", lambda d, h, c: (3 * d,)),
+    "proj_weight": ("decoder.middle_block.attn.c_proj.weight", lambda d, h, c: (d, d)),
+    "proj_bias": ("decoder.middle_block.attn.c_proj.bias", lambda d, h, c: (d,)),
+    "q_norm": ("decoder.middle_block.attn.q_norm.weight", lambda d, h, c: (h,)),
+    "k_norm": ("decoder.middle_block.attn.k_norm.weight", lambda d, h, c: (h,)),
+    "ln2_weight": ("decoder.middle_block.ln_2.weight", lambda d, h, c: (d,)),
+    "ln2_bias": ("decoder.middle_block.ln_2.bias", lambda d, h, c: (d,)),
+    "fc_weight": ("decoder.middle_block.mlp.c_fc.weight", lambda d, h, c: (4 * d, d)),
+    "fc_bias": ("decoder.middle_block.mlp.c_fc.bias", lambda d, h, c: (4 * d,)),
+    "fc_proj_weight": ("decoder.middle_block.mlp.c_proj.weight", lambda d, h, c: (d, 4 * d)),
+    "fc_proj_bias": ("decoder.middle_block.mlp.c_proj.bias", lambda d, h, c: (d,)),
+    "lnf_weight": ("decoder.ln_f.weight", lambda d, h, c: (d,)),
+    "out_weight": ("decoder.output_layer.weight", lambda d, h, c: (c, d)),
+}
+
+
 class TokenizerError(ValueError):
     """A checkpoint whose names, shapes or dtypes do not match the config."""
 
@@ -232,6 +261,14 @@ class Tokenizer:
             t.wte = get("encoder.wte.weight", (cfg.in_vocab, d)).data_ptr()
             t.wpe = get("encoder.wpe.weight", (cfg.context_length, d)).data_ptr()
         self.desc = t
+        self.dec = None
+        if "decoder.output_layer.weight" in state:
+            dd = _Dec()
+            dd.n_head, dd.ln_eps, dd.qk_eps = cfg.n_head, cfg.ln_eps, cfg.qk_eps
+            for f, (name, shape) in _DEC_NAMES.items():
+                if name in state:
+                    setattr(dd, f, get(name, shape(d, d // cfg.n_head, cfg.in_vocab)).data_ptr())
+            self.dec = dd
 
     # ---------------------------------------------------------------- calls
     def _outputs(self, B, zhat, W):
@@ -305,6 +342,29 @@ class Tokenizer:
         self.ctx.bind_stream()
         check(lib().ncm_vq_tok_reconstruct_dev(self.ctx.handle, C.byref(self.desc), pc, B, pz), W)
         return zhat
+
+
+    def decode(self, zhat, logits=None):
+        """logits float32 [B, L, C] of the decoder block, ln_f and the output
+        layer on zhat float32 [B, L, D]."""
+        import torch
+
+        W = "vq_tok_decode"
+        cfg = self.cfg
+        if self.dec is None:
+            raise NcmError(NCM_E_ARG, W, "the tokenizer was built without decoder weights")
+        B, _, _ = _ck.dims(zhat, "zhat", W, 3)
+        if logits is None:
+            logits = torch.empty((B, cfg.seq_len, cfg.in_vocab), dtype=torch.float32,
+                                 device=self.device)
+        a = _ck.Args(W)
+        pz = a.dev(zhat, "zhat", _ck.F32, (B, cfg.seq_len, cfg.embed_dim))
+        pl = a.dev(logits, "logits", _ck.F32, (B, cfg.seq_len, cfg.in_vocab))
+        a.done()
+        self.ctx.bind_stream()
+        check(lib().ncm_vq_tok_decode_dev(self.ctx.handle, C.byref(self.desc), C.byref(self.dec),
+                                          pz, B, pl), W)
+        return logits
 
 
 # ------------------------------------------------------------------ loading

@@ -15,6 +15,7 @@ STRUCTS = {
     "ncm_ncm_shape_t": ("ncm", "_Shape"),
     "ncm_ncm_weights_t": ("ncm", "_Weights"),
     "ncm_vq_tok_t": ("vq_tokenizer", "_Tok"),
+    "ncm_vq_tok_decoder_t": ("vq_tokenizer", "_Dec"),
 }
 
 

@@ -210,3 +210,72 @@ def test_wmt14_full_size_properties():
     z = a["latent"][:4].cpu().numpy().astype(np.float64)
     _check_codes(ocfg, qw, z, codes[:4], a["zhat"][:4].cpu().numpy())
     assert torch.equal(tok.reconstruct(a["codes"]), a["zhat"])
+
+
+@pytest.mark.parametrize("ocfg,batch", [
+    (SMALL_WMT, 2),
+    (vo.TokenizerConfig(embed_dim=96, in_vocab=52, context_length=24, levels=(1, 3, 7, 16),
+                        vocab_sizes=(40, 300, 33, 129), groups=4, learned_level0=False,
+                        n_head=3), 3),
+])
+def test_decoder_matches_oracle(ocfg, batch):
+    torch = _torch()
+    ocfg, enc, qw, dec, tok = _model(ocfg, seed=21)
+    rng = np.random.default_rng(21)
+    zhat = rng.standard_normal((batch, ocfg.seq_len, ocfg.embed_dim)).astype(np.float32)
+    print(f"vq_tok decode B={batch} D={ocfg.embed_dim}", flush=True)
+    logits = tok.decode(torch.from_numpy(zhat).cuda()).cpu().numpy()
+    want = vo.decoder_forward(ocfg, dec, zhat)
+    np.testing.assert_allclose(logits, want, rtol=1e-4, atol=1e-4)
+
+
+def test_codes_to_logits_full_wmt14_vocab():
+    """Codes -> reconstruction -> logits over the full 151680-token output
+    layer for two sequences, against the oracle on the device's zhat."""
+    torch = _torch()
+    ocfg, enc, qw, dec, tok = _model(vo.WMT14, seed=12)
+    rng = np.random.default_rng(12)
+    ids = rng.integers(0, ocfg.in_vocab, size=(2, 64))
+    out = tok.encode(ids)
+    zhat = tok.reconstruct(out["codes"])
+    logits = tok.decode(zhat)
+    torch.cuda.synchronize()
+    want = vo.decoder_forward(ocfg, dec, zhat.cpu().numpy())
+    np.testing.assert_allclose(logits.cpu().numpy(), want, rtol=1e-4, atol=1e-4)
+
+
+def test_load_round_trip(tmp_path):
+    """A checkpoint with every state_dict entry (float tensors stored F32,
+    codebooks BF16, hit counters I64) loads and encodes exactly as the
+    tokenizer built from the same values."""
+    torch = _torch()
+    from ncmorph_amd import vq_tokenizer as vt
+    from ncmorph_amd.safetensors import write_file
+
+    ocfg = vo.TokenizerConfig(embed_dim=64, in_vocab=40, context_length=32,
+                              levels=(2, 8, 16, 32), vocab_sizes=(16, 64, 32, 128), n_head=2)
+    _, enc, qw, dec, tok = _model(ocfg, seed=8)
+    pcfg = tok.cfg
+    tensors = {}
+    for name, shape, dt in vt.state_dict_entries(pcfg):
+        if dt == "int64":
+            tensors[name] = ("I64", shape, np.zeros(shape, np.int64).tobytes())
+        elif name.startswith("vq.ema_"):
+            tensors[name] = ("F32", shape, np.zeros(shape, np.float32).tobytes())
+        elif name.startswith("vq.embeddings."):
+            bits = tok.state[name].cpu().numpy().view(np.uint32)
+            # round to bf16 (values chosen to be bf16 already: truncate then
+            # compare against the same truncation on the device tokenizer)
+            b16 = (bits >> 16).astype(np.uint16)
+            tok.state[name].copy_(torch.from_numpy((b16.astype(np.uint32) << 16).view(np.float32)))
+            tensors[name] = ("BF16", shape, b16.tobytes())
+        else:
+            tensors[name] = ("F32", shape, tok.state[name].cpu().numpy().tobytes())
+    path = tmp_path / "tokenizer.safetensors"
+    write_file(str(path), tensors)
+    loaded = vt.load(str(path), pcfg, device="cuda:0")
+    ids = np.random.default_rng(0).integers(0, 40, size=(3, 32))
+    a = tok.encode(ids)
+    b = loaded.encode(ids)
+    assert torch.equal(a["codes"], b["codes"]) and torch.equal(a["zhat"], b["zhat"])
+    assert torch.equal(tok.decode(a["zhat"]), loaded.decode(b["zhat"]))
