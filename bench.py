@@ -431,6 +431,102 @@ def run_ncm_tied_head(torch, reps=5):
                          "unit": "TFLOP/s", "frac": round(tf / BF16_PEAK_TFLOPS, 4)}}
 
 
+VQ_TOK_BATCH = 1024
+VQ_TOK_DECODE_BATCH = 64
+FP32_PEAK_TFLOPS = 157.3  # MI355X dense fp32 MFMA
+
+
+def run_vq_tokenizer(torch, reps=20):
+    """The upstream VQ-VAE tokenizer at the released WMT14 configuration
+    (D 384, 64 positions, 11 levels 1..64 of 4096 codes, learned level-0
+    cascade of three stride-4 stages with GroupNorms, Phi blend convs),
+    random-init float32 weights: encode (token ids -> codes + zhat) of 1024
+    sequences, and the decoder (zhat -> logits over 151680 tokens) of 64.
+    Flops: 2 per multiply-add of the code searches, Phi convs and cascade
+    (encode) and of the decoder's linears and attention (decode)."""
+    from ncmorph_amd import vq_tokenizer as vt
+
+    dev = torch.device("cuda", 0)
+    cfg = vt.WMT14
+    tok = vt.Tokenizer(cfg, vt.random_state(cfg, dev, seed=31))
+    ids = np.random.default_rng(32).integers(0, cfg.in_vocab, (VQ_TOK_BATCH, cfg.seq_len))
+    B = VQ_TOK_BATCH
+    codes = torch.empty((B, cfg.codes_per_sequence), dtype=torch.int32, device=dev)
+    zhat = torch.empty((B, cfg.seq_len, cfg.embed_dim), dtype=torch.float32, device=dev)
+    latent = tok.encode(ids, want_latent=True)["latent"]
+
+    def enc():
+        tok.quantize(latent)
+
+    _ramp(torch, enc)
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        enc()
+    e1.record()
+    torch.cuda.synchronize()
+    q_sec = e0.elapsed_time(e1) * 1e-3 / reps
+    e0.record()
+    for _ in range(reps):
+        tok.encode(ids)
+    e1.record()
+    torch.cuda.synchronize()
+    e_sec = e0.elapsed_time(e1) * 1e-3 / reps
+    del codes, zhat
+    fl = vt.flops_per_sequence(cfg)
+    tf = fl["total"] * B / q_sec / 1e12
+    # decoder
+    Bd = VQ_TOK_DECODE_BATCH
+    zd = latent[:Bd].contiguous()
+    logits = torch.empty((Bd, cfg.seq_len, cfg.in_vocab), dtype=torch.float32, device=dev)
+    tok.decode(zd, logits)
+    _ramp(torch, lambda: tok.decode(zd, logits))
+    e0.record()
+    for _ in range(reps):
+        tok.decode(zd, logits)
+    e1.record()
+    torch.cuda.synchronize()
+    d_sec = e0.elapsed_time(e1) * 1e-3 / reps
+    d, L, c = cfg.embed_dim, cfg.seq_len, cfg.in_vocab
+    d_flops = Bd * (2 * L * d * (3 * d + d + 8 * d + c) + 4 * L * L * d)
+    d_tf = d_flops / d_sec / 1e12
+    tokens = B * L
+    return {"metric": "VQ tokenizer quantize tokens/s", "value": round(tokens / q_sec, 1),
+            "unit": "tokens/s", "ms_per_quantize": round(q_sec * 1e3, 4),
+            "encode_with_ids_tokens_per_s": round(tokens / e_sec, 1),
+            "config": {"workload": "upstream VQ-VAE tokenizer, WMT14 configuration, fp32",
+                       "batch": B, "seq_len": L, "d": d, "levels": list(cfg.levels),
+                       "codes": cfg.vocab_sizes[0], "cascade": cfg.cascade_strides()},
+            "flops_per_sequence": fl,
+            "roofline": {"bound": "mfma", "achieved": round(tf, 2), "peak": FP32_PEAK_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(tf / FP32_PEAK_TFLOPS, 4)},
+            "decode": {"batch": Bd, "ms": round(d_sec * 1e3, 4),
+                       "tokens_per_s": round(Bd * L / d_sec, 1), "flops": d_flops,
+                       "roofline": {"bound": "mfma", "achieved": round(d_tf, 2),
+                                    "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                    "frac": round(d_tf / FP32_PEAK_TFLOPS, 4)}}}
+
+
+def cpu_vq_tokenizer_baseline(seqs=24):
+    """The float64 oracle's quantizer (numpy, BLAS held to one thread) on
+    `seqs` sequences of the WMT14 configuration with random weights."""
+    from threadpoolctl import threadpool_limits
+
+    from oracle import vq_tokenizer as vo
+
+    cfg = vo.WMT14
+    enc, qw, _ = vo.random_weights(cfg, seed=31, vocab_cap=1024)
+    ids = np.random.default_rng(32).integers(0, 1024, (seqs, cfg.seq_len))
+    z = vo.encode_front(cfg, ids, enc["wte"], enc["wpe"])
+    with threadpool_limits(limits=1):
+        t0 = time.perf_counter()
+        vo.quantize(cfg, qw, z)
+        dt = time.perf_counter() - t0
+    return {"value": seqs * cfg.seq_len / dt, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "sample": f"{seqs} sequences of 64 tokens, all 11 levels, float64 numpy oracle, "
+                      "1 BLAS thread"}
+
+
 def run_weight_upload(torch, mib=512):
     """Device weight path: one bf16 tensor of `mib` MiB in a safetensors file
     (written first, so it is in the page cache) copied to HBM as stored
@@ -599,7 +695,7 @@ def main():
     # would measure on the ramp instead.
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=500)
-    ap.add_argument("--only", choices=["linear", "rvq", "decoder", "ncm", "all", "copy"],
+    ap.add_argument("--only", choices=["linear", "rvq", "decoder", "ncm", "vqtok", "all", "copy"],
                     default="all",
                     help="copy: a plain 256 MiB device copy, the reference point for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
@@ -686,6 +782,11 @@ def main():
                 res["cpu_baseline"] = rvq["cpu_baseline"]
     if args.only == "ncm":
         res["ncm_level_step"] = run_ncm_step(torch)
+    if args.only in ("vqtok", "all"):
+        vq = run_vq_tokenizer(torch)
+        if not args.no_cpu:
+            vq["cpu_baseline"] = cpu_vq_tokenizer_baseline()
+        res["vq_tokenizer"] = vq
     if args.only in ("decoder", "all"):
         dec = run_decoder(torch)
         dec["weight_upload"] = run_weight_upload(torch)

@@ -418,6 +418,38 @@ def load(path: str, cfg: TokenizerConfig = WMT14, device=None, ctx=None) -> Toke
     return Tokenizer(cfg, state, ctx)
 
 
+def random_state(cfg: TokenizerConfig, device, seed: int = 0, decoder: bool = True) -> dict:
+    """Random-initialised float32 device weights of every inference entry:
+    N(0, 1) token, position and codebook tables (models/quant.py:299),
+    uniform(+-1/sqrt(fan_in)) conv and linear weights and biases (PyTorch's
+    default scale), LayerNorm / RMSNorm weights near 1."""
+    import torch
+
+    g = torch.Generator(device=device).manual_seed(seed)
+    st = {}
+    for name, shape, dt in state_dict_entries(cfg):
+        if dt != "float32" or name.startswith("vq.ema_"):
+            continue
+        if name.startswith("decoder.") and not decoder:
+            continue
+        if name.endswith(("wte.weight", "wpe.weight")) or "embeddings" in name:
+            t = torch.randn(shape, device=device, generator=g)
+        elif "norm" in name or "ln_" in name:
+            t = (1.0 + 0.1 * torch.randn(shape, device=device, generator=g)
+                 if name.endswith("weight") else 0.1 * torch.randn(shape, device=device, generator=g))
+        else:
+            if "quant_resi" in name or "learned_" in name:
+                fan_in = cfg.embed_dim * (3 if "quant_resi" in name else cfg.cascade_base)
+            elif name.endswith(".bias"):
+                fan_in = cfg.embed_dim * (4 if "mlp.c_proj" in name else 1)
+            else:
+                fan_in = shape[-1]
+            bound = fan_in ** -0.5
+            t = (torch.rand(shape, device=device, generator=g) * 2.0 - 1.0) * bound
+        st[name] = t.contiguous()
+    return st
+
+
 def flops_per_sequence(cfg: TokenizerConfig) -> dict:
     """Algorithmic multiply-add flops (2 per MAC) of one sequence's encode:
     the nearest-code searches, the Phi convs and the level-0 cascade."""
