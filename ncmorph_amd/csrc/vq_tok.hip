@@ -33,7 +33,10 @@ namespace ncm {
 
 namespace {
 
-using VtTile = GemmShape<128, 128, 32, 2, 2, 2, 5, true, 2, true>;
+// 128 x 128 x 16 fp32 tile, 4 wavefronts of 64 x 64, two LDS stages (32 KB):
+// four workgroups per CU, 118 VGPRs (measured faster than 32-deep K tiles with
+// two workgroups per CU, deeper pipelines and 8-wavefront tiles).
+using VtTile = GemmShape<128, 128, 16, 2, 2, 4, 5, true, 2, true>;
 constexpr int kNT = 256;
 
 enum { kEpiStage = 0, kEpiPhi = 1, kEpiDist = 2 };
@@ -114,31 +117,49 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void vt_gemm_kernel(
     const int wn = wave / S::WGM;
 
     if constexpr (EPI == kEpiDist) {
-        // Per row: the minimum key over this wave's columns, reduced over the
-        // 32 lanes that hold the row, then one atomic per row and wave.
+        // Per row: the minimum key over this wavefront's columns. A lane
+        // holds 16 rows per 32-row block (element i: row 8 (i / 4) + 4 (lane /
+        // 32) + i % 4) of one column per 32-column block; the 32 lanes of a
+        // half share the rows. Transposed reduction over those 32 lanes: at
+        // each xor step a lane keeps half of its rows and sends the other
+        // half to its partner, so 16 rows take 8 + 4 + 2 + 1 exchanges; the
+        // last step (xor 1) pairs lanes that hold the same row. Lane q ends
+        // with row i = q / 2 (even lanes issue the atomic).
+        const int q = lane & 31;
 #pragma unroll
         for (int mb = 0; mb < S::MB; ++mb) {
+            unsigned long long k16[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 unsigned long long best = ~0ull;
 #pragma unroll
                 for (int nb = 0; nb < S::NB; ++nb) {
-                    const int64_t n = n0 + wn * S::WN + nb * 32 + (lane & 31);
+                    const int64_t n = n0 + wn * S::WN + nb * 32 + q;
                     if (n < N) {
-                        const float v = ep.csq[n] - 2.0f * acc.v[mb][nb][i];
-                        const unsigned long long k = dist_key(v, n);
+                        const unsigned long long k =
+                            dist_key(ep.csq[n] - 2.0f * acc.v[mb][nb][i], n);
                         best = k < best ? k : best;
                     }
                 }
-#pragma unroll
-                for (int off = 16; off >= 1; off >>= 1) {
-                    const unsigned long long o = shfl_xor_u64(best, off);
-                    best = o < best ? o : best;
-                }
-                const int64_t m =
-                    m0 + wm * S::WM + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
-                if ((lane & 31) == 0 && m < M && best != ~0ull) atomicMin(ep.keys + m, best);
+                k16[i] = best;
             }
+#pragma unroll
+            for (int half = 8; half >= 1; half >>= 1) {
+                // xor 2 * half: bit b of q chooses which half of the rows stays.
+                const bool up = (q & (2 * half)) != 0;
+#pragma unroll
+                for (int t = 0; t < half; ++t) {
+                    const unsigned long long send = up ? k16[t] : k16[t + half];
+                    const unsigned long long keep = up ? k16[t + half] : k16[t];
+                    const unsigned long long recv = shfl_xor_u64(send, 2 * half);
+                    k16[t] = recv < keep ? recv : keep;
+                }
+            }
+            const unsigned long long o = shfl_xor_u64(k16[0], 1);
+            const unsigned long long best = o < k16[0] ? o : k16[0];
+            const int i = q >> 1;
+            const int64_t m = m0 + wm * S::WM + mb * 32 + 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3);
+            if ((q & 1) == 0 && m < M && best != ~0ull) atomicMin(ep.keys + m, best);
         }
         return;
     }
