@@ -374,6 +374,10 @@ typedef struct ncm_decoder_layer_f32 {
     const float* down_bias;            /* [hidden] or NULL */
     const float* q_norm;               /* [head_dim] or NULL */
     const float* k_norm;               /* [head_dim] or NULL */
+    /* rms_norm_rows_with_bias (src/ncm_norm.zig:22-49): biases added after
+     * the input and post-attention norms, or NULL (the decoder has none). */
+    const float* input_norm_bias;      /* [hidden] or NULL */
+    const float* post_attention_norm_bias; /* [hidden] or NULL */
 } ncm_decoder_layer_f32_t;
 
 /* The per-stage trace of forward_with_trace (decoder_trace_t,
@@ -487,6 +491,38 @@ int ncm_ncm_forward_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
                         const int64_t* prefix_ids, const uint8_t* prefix_pad_mask,
                         int64_t pad_len, const float* target_inputs, const float* cosine,
                         const float* sine, float* output);
+
+/* weights_t (src/ncm_model.zig:61-72) for the f32 body: every tensor float.
+ * conv_weight / conv_bias as in ncm_ncm_weights_t. */
+typedef struct ncm_ncm_weights_f32 {
+    const float* prefix_token_embedding; /* [prefix_vocab, vq_width] */
+    const float* input_projection;       /* [hidden, vq_width] */
+    const float* input_projection_bias;  /* [hidden] or NULL */
+    const float* level_embedding;        /* [n_levels, hidden] */
+    const float* l0_queries;             /* [level_lengths[0], vq_width] or NULL */
+    const float* final_norm;             /* [hidden] */
+    const float* final_norm_bias;        /* [hidden] or NULL */
+    const float* const* conv_weight;
+    const float* const* conv_bias;
+} ncm_ncm_weights_f32_t;
+
+/* The NCM body forward in the reference's own arithmetic: f32 throughout
+ * (kernels.matmul + bias, src/ncm_model.zig:278-294; rms_norm_rows_with_bias;
+ * f32 RoPE at the restarting positions; f32 attention with the level mask,
+ * each dot product in dimension order and the softmax sum and context in
+ * key order; silu(gate) * up; unrounded adds). Arguments, checks and output
+ * layout as ncm_ncm_forward_dev, with float weights and
+ * ncm_decoder_layer_f32_t layers (fused q|k|v rows, gate / up / down as
+ * stored, norm biases as input_norm_bias / post_attention_norm_bias).
+ * hidden, vq_width, intermediate and head_dim must be multiples of 4,
+ * head_dim <= 256. The projections sum on the fp32 MFMA in its own order,
+ * so results agree with the reference to fp32 rounding, not bit for bit. */
+int ncm_ncm_forward_f32_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
+                            const ncm_decoder_layer_f32_t* layers,
+                            const ncm_ncm_weights_f32_t* weights, const int64_t* prefix_ids,
+                            const uint8_t* prefix_pad_mask, int64_t pad_len,
+                            const float* target_inputs, const float* cosine, const float* sine,
+                            float* output);
 
 /* ---- multiscale residual vector quantization ---- */
 

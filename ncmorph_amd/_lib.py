@@ -64,6 +64,7 @@ SIGNATURES = [
     ("ncm_decoder_forward_dev", i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]),
     ("ncm_decoder_forward_f32_dev", i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp, vp]),
     ("ncm_ncm_forward_dev", i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp]),
+    ("ncm_ncm_forward_f32_dev", i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp]),
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
     ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
     ("ncm_rvq_encode_noalloc", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp,

@@ -717,6 +717,82 @@ int ncm_ncm_forward_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
     return NCM_OK;
 }
 
+// ncm_ncm_forward_f32_dev: the checks of forward_with_trace in its order (as
+// ncm_ncm_forward_dev), then the f32 path's device limits.
+int ncm_ncm_forward_f32_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
+                            const ncm_decoder_layer_f32_t* layers,
+                            const ncm_ncm_weights_f32_t* weights, const int64_t* prefix_ids,
+                            const uint8_t* prefix_pad_mask, int64_t pad_len,
+                            const float* target_inputs, const float* cosine, const float* sine,
+                            float* output) {
+    if (!ctx || !shape || !weights) return NCM_E_NULL;
+    const ncm_ncm_shape_t& s = *shape;
+    if (s.prefix_length < 0 || s.n_levels < 0 || s.n_levels > NCM_MAX_LEVELS) return NCM_E_SHAPE;
+    if (pad_len != 0 && pad_len != s.prefix_length) return NCM_E_LENGTH;  // InvalidPrefixMask
+    if (s.n_levels == 0) return NCM_E_ARG;                                // InvalidNcmMode
+    if (s.hidden <= 0 || s.vq_width <= 0 || s.head_dim <= 0 || s.intermediate <= 0 ||
+        s.q_heads <= 0 || s.kv_heads <= 0 || s.head_dim % 2 || s.q_heads % s.kv_heads)
+        return NCM_E_SHAPE;  // InvalidNcmDimensions
+    if (s.layers <= 0) return NCM_E_LENGTH;  // InvalidNcmTensorSize
+    if (s.mask_mode < NCM_MASK_BLOCK_DIAGONAL || s.mask_mode > NCM_MASK_CAUSAL || s.window < 0)
+        return NCM_E_ARG;
+    int64_t S = s.prefix_length;
+    for (int l = 0; l < s.n_levels; ++l) {
+        if (s.level_lengths[l] < 0 || __builtin_add_overflow(S, s.level_lengths[l], &S))
+            return NCM_E_SHAPE;
+    }
+    // Device limits: 16-byte rows for the fp32 MFMA and the attention.
+    if (s.head_dim % 4 || s.head_dim > 256) return NCM_E_SHAPE;
+    if (s.hidden % 4 || s.vq_width % 4 || s.intermediate % 4) return NCM_E_SHAPE;
+    if (S > (int64_t(1) << 30) || s.hidden > (int64_t(1) << 21) ||
+        s.vq_width > (int64_t(1) << 19) || s.intermediate > (int64_t(1) << 20) ||
+        (int64_t)s.q_heads * s.head_dim > (int64_t(1) << 21))
+        return NCM_E_SHAPE;
+    if (S == s.prefix_length) return NCM_E_ARG;  // no target position
+    const bool convs = weights->conv_weight || weights->conv_bias;
+    if (!weights->prefix_token_embedding && s.prefix_length > 0) return NCM_E_NULL;
+    if (!weights->input_projection || !weights->final_norm) return NCM_E_NULL;
+    if (s.use_level_encoding && !weights->level_embedding) return NCM_E_NULL;
+    if (s.query_level0 && !weights->l0_queries && s.level_lengths[0] > 0) return NCM_E_NULL;
+    if (convs) {
+        if (!weights->conv_weight || !weights->conv_bias) return NCM_E_NULL;
+        for (int l = 0; l < s.n_levels; ++l)
+            if (!weights->conv_weight[l] || !weights->conv_bias[l]) return NCM_E_NULL;
+    }
+    if (!target_inputs || !cosine || !sine || !output || !layers) return NCM_E_NULL;
+    if (pad_len > 0 && !prefix_pad_mask) return NCM_E_NULL;
+    if (s.prefix_length > 0 && !prefix_ids) return NCM_E_NULL;
+    if ((uintptr_t)weights->input_projection % 16 || (uintptr_t)target_inputs % 16 ||
+        (uintptr_t)output % 16)
+        return NCM_E_ARG;
+    if (convs)
+        for (int l = 0; l < s.n_levels; ++l)
+            if ((uintptr_t)weights->conv_weight[l] % 16) return NCM_E_ARG;
+    for (int l = 0; l < s.layers; ++l) {
+        const ncm_decoder_layer_f32_t& L = layers[l];
+        if (!L.input_norm || !L.qkv_weight || !L.o_weight || !L.post_attention_norm ||
+            !L.gate_weight || !L.up_weight || !L.down_weight)
+            return NCM_E_NULL;
+        if (!L.q_norm != !L.k_norm) return NCM_E_ARG;
+        const float* ws_[] = {L.qkv_weight, L.o_weight, L.gate_weight, L.up_weight,
+                              L.down_weight};
+        for (const float* q : ws_)
+            if ((uintptr_t)q % 16) return NCM_E_ARG;
+    }
+    for (int64_t i = 0; i < s.prefix_length; ++i)
+        if (prefix_ids[i] < 0 || prefix_ids[i] >= s.prefix_vocab)
+            return NCM_E_ARG;  // PrefixTokenOutOfRange
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    void* ws = nullptr;
+    rc = ncm_ctx_workspace(ctx, ncm::ncm_f32_workspace_bytes(s, convs), &ws);
+    if (rc) return rc;
+    hipError_t e = ncm::ncm_forward_f32(s, layers, *weights, prefix_ids, prefix_pad_mask, pad_len,
+                                        target_inputs, cosine, sine, output, ws, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "ncm forward (f32)");
+    return NCM_OK;
+}
+
 // ------------------------------------------------------------------ drop-ins
 
 namespace {

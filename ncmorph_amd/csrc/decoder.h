@@ -53,4 +53,34 @@ hipError_t decoder_forward_f32(const ncm_decoder_shape_t& s, const ncm_decoder_l
                                int64_t batch, int64_t seq, float* logits,
                                const ncm_decoder_trace_t* trace, void* ws, hipStream_t st);
 
+// The f32 layer stack (decoder_f32.hip) over `batch` sequences of `seq`
+// rows: hidden [batch * seq, hidden] fp32 updated in place. Attention:
+// causal with shape->window, or, when seg_lo is set, the prefix + level-block
+// mask (prefix keys without their pad bit, then keys [seg_lo, seg_hi) of the
+// query's row). cosine / sine: [seq, head_dim], table row = row % seq.
+// Scratch (fp32): normed [rows, hidden], q [rows, q_heads head_dim], k, v
+// [rows, kv_heads head_dim], ctx [rows, q_heads head_dim], proj [rows,
+// hidden], gate, up [rows, intermediate]. trace may be null.
+struct LayerStackF32 {
+    const ncm_decoder_shape_t* shape;
+    const ncm_decoder_layer_f32_t* layers;  // host array [shape->layers]
+    int64_t batch, seq;
+    const float* cosine;
+    const float* sine;
+    int64_t prefix;
+    const int32_t* seg_lo;
+    const int32_t* seg_hi;
+    const uint64_t* pad;
+    float *hidden, *normed, *q, *k, *v, *ctx, *proj, *gate, *up;
+    const ncm_decoder_trace_t* trace;
+};
+hipError_t run_layers_f32(const LayerStackF32& a, hipStream_t st);
+
+// y [rows, n] = x [rows, k] w^T (+ bias) on the fp32 MFMA (k % 4 == 0).
+hipError_t project_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows,
+                       int64_t k, int64_t n, hipStream_t st);
+// y[r, c] += a[r, c] (a_rows == rows) or a[c] (a_rows == 1).
+hipError_t launch_add_f32(float* y, const float* a, int64_t rows, int64_t n, int64_t a_rows,
+                          hipStream_t st);
+
 }  // namespace ncm

@@ -48,15 +48,6 @@ __global__ __launch_bounds__(256) void add_f32_kernel(float* __restrict__ y,
     y[i] = y[i] + av;
 }
 
-hipError_t launch_add_f32(float* y, const float* a, int64_t rows, int64_t n, int64_t a_rows,
-                          hipStream_t st) {
-    const int64_t total = rows * n;
-    if (total == 0) return hipSuccess;
-    hipLaunchKernelGGL(add_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, y,
-                       a, rows, n, a_rows);
-    return hipGetLastError();
-}
-
 // rotate_head in f32 mode (root.zig:615-634), in place: row r, head h at
 // x[r * row_stride + h * hd ..]; table row r % seq_len. One thread per pair.
 __global__ __launch_bounds__(256) void rope_rotate_f32_kernel(float* __restrict__ x, int64_t rows,
@@ -97,18 +88,23 @@ hipError_t launch_rope_rotate_f32(float* x, int64_t rows, int64_t row_stride, in
 constexpr int kAttnF32MaxHd = 256;
 
 // f32-mode attention of one (sequence, query, head) per wavefront, four
-// heads per workgroup: grid (seq_len, ceil(q_heads / 4), batch). Keys
-// [k_lo, query] (causal, optionally windowed), 64 per chunk, one per lane.
-// Three walks over the keys: the maximum score; the softmax sum, added in key
-// order (every lane adds the chunk's exponentials in lane order); then
-// p = exp(s - max) / sum and the context, lane = dimension, adding p_k v_k
-// in key order. A score is the dot product in dimension order, then times
-// 1 / sqrt(hd). Keys after the query (probability 0) add nothing, as in the
-// reference unless V holds an infinity or NaN there.
+// heads per workgroup: grid (seq_len, ceil(q_heads / 4), batch). Allowed
+// keys, in increasing order: causal, [k_lo, query] (optionally windowed); or
+// with the level mask (seg_lo set), the prefix keys 0 .. prefix-1 whose pad
+// bit is clear, then [seg_lo[q], seg_hi[q]) (at or after the prefix). They
+// are walked 64 per chunk, one per lane, three times: the maximum score; the
+// softmax sum, added in key order (every lane adds the chunk's exponentials
+// in lane order); then p = exp(s - max) / sum and the context, lane =
+// dimension, adding p_k v_k in key order. A score is the dot product in
+// dimension order, then times 1 / sqrt(hd). Masked keys (probability 0) add
+// nothing, as in the reference unless V holds an infinity or NaN there; a
+// query with no allowed key gets a zero context (root.zig:563-565).
 __global__ __launch_bounds__(256) void attention_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     float* __restrict__ out, int64_t T, int q_heads, int group, int hd, int64_t q_stride,
-    int64_t kv_stride, int64_t out_stride, int64_t window, float scale) {
+    int64_t kv_stride, int64_t out_stride, int64_t window, float scale, int64_t prefix,
+    const int32_t* __restrict__ seg_lo, const int32_t* __restrict__ seg_hi,
+    const uint64_t* __restrict__ pad) {
     const int lane = threadIdx.x & 63;
     const int h = blockIdx.y * 4 + (threadIdx.x >> 6);
     if (h >= q_heads) return;
@@ -124,9 +120,24 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(
         const int d = s * 64 + lane;
         qv[s] = d < hd ? qrow[d] : 0.0f;
     }
-    int64_t k_lo = window > 0 ? qi - window + 1 : 0;
-    if (k_lo < 0) k_lo = 0;
-    const int64_t k_hi = qi + 1;  // keys [k_lo, k_hi)
+    // Key j of the walk (j in [0, nkeys)) and whether it is allowed.
+    int64_t nkeys, k_lo = 0, lo = 0, P = 0;
+    if (seg_lo) {
+        P = prefix;
+        lo = seg_lo[b * T + qi];
+        const int64_t hi = seg_hi[b * T + qi];
+        nkeys = P + (hi > lo ? hi - lo : 0);
+    } else {
+        k_lo = window > 0 ? qi - window + 1 : 0;
+        if (k_lo < 0) k_lo = 0;
+        nkeys = qi + 1 - k_lo;
+    }
+    auto key_of = [&](int64_t j) { return seg_lo ? (j < P ? j : lo + (j - P)) : k_lo + j; };
+    auto allowed = [&](int64_t j) {
+        if (j >= nkeys) return false;
+        if (seg_lo && j < P && pad) return ((pad[j >> 6] >> (j & 63)) & 1ull) == 0ull;
+        return true;
+    };
     // q . k in dimension order (separate multiply and add), then * scale;
     // the q values come from their lanes, the k row in 16-byte loads.
     auto score_of = [&](int64_t key) {
@@ -148,37 +159,45 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(
     };
     // Walk 1: the maximum.
     float m = -INFINITY;
-    for (int64_t c0 = k_lo; c0 < k_hi; c0 += 64) {
-        const int64_t key = c0 + lane;
-        const float s = key < k_hi ? score_of(key) : -INFINITY;
+    for (int64_t c0 = 0; c0 < nkeys; c0 += 64) {
+        const int64_t j = c0 + lane;
+        const float s = allowed(j) ? score_of(key_of(j)) : -INFINITY;
         m = fmaxf(m, s);
     }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    // Walk 2: the sum, in key order.
-    float sum = 0.0f;
-    for (int64_t c0 = k_lo; c0 < k_hi; c0 += 64) {
-        const int64_t key = c0 + lane;
-        const float e = key < k_hi ? expf(score_of(key) - m) : 0.0f;
-        const int n = (int)(k_hi - c0 < 64 ? k_hi - c0 : 64);
-        for (int j = 0; j < n; ++j)
-            sum = sum + __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(e), j));
-    }
-    // Walk 3: probabilities and the context, lane = dimension.
     float acc[kAttnF32MaxHd / 64];
 #pragma unroll
     for (int s = 0; s < kAttnF32MaxHd / 64; ++s) acc[s] = 0.0f;
-    for (int64_t c0 = k_lo; c0 < k_hi; c0 += 64) {
-        const int64_t key = c0 + lane;
-        const float p = key < k_hi ? expf(score_of(key) - m) / sum : 0.0f;
-        const int n = (int)(k_hi - c0 < 64 ? k_hi - c0 : 64);
-        for (int j = 0; j < n; ++j) {
-            const float pj = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p), j));
-            const float* vr = vbase + (c0 + j) * kv_stride;
+    if (m != -INFINITY) {
+        // Walk 2: the sum, in key order.
+        float sum = 0.0f;
+        for (int64_t c0 = 0; c0 < nkeys; c0 += 64) {
+            const int64_t j = c0 + lane;
+            const bool ok = allowed(j);
+            const float e = ok ? expf(score_of(key_of(j)) - m) : 0.0f;
+            const uint64_t okm = __ballot(ok);
+            const int n = (int)(nkeys - c0 < 64 ? nkeys - c0 : 64);
+            for (int jj = 0; jj < n; ++jj)
+                if ((okm >> jj) & 1ull)
+                    sum = sum + __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(e), jj));
+        }
+        // Walk 3: probabilities and the context, lane = dimension.
+        for (int64_t c0 = 0; c0 < nkeys; c0 += 64) {
+            const int64_t j = c0 + lane;
+            const bool ok = allowed(j);
+            const float p = ok ? expf(score_of(key_of(j)) - m) / sum : 0.0f;
+            const uint64_t okm = __ballot(ok);
+            const int n = (int)(nkeys - c0 < 64 ? nkeys - c0 : 64);
+            for (int jj = 0; jj < n; ++jj) {
+                if (!((okm >> jj) & 1ull)) continue;
+                const float pj = __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(p), jj));
+                const float* vr = vbase + key_of(c0 + jj) * kv_stride;
 #pragma unroll
-            for (int s = 0; s < kAttnF32MaxHd / 64; ++s) {
-                const int d = s * 64 + lane;
-                if (d < hd) acc[s] = acc[s] + pj * vr[d];
+                for (int s = 0; s < kAttnF32MaxHd / 64; ++s) {
+                    const int d = s * 64 + lane;
+                    if (d < hd) acc[s] = acc[s] + pj * vr[d];
+                }
             }
         }
     }
@@ -193,12 +212,13 @@ __global__ __launch_bounds__(256) void attention_f32_kernel(
 hipError_t launch_attention_f32(const float* q, const float* k, const float* v, float* out,
                                 int64_t batch, int64_t T, int q_heads, int kv_heads, int hd,
                                 int64_t q_stride, int64_t kv_stride, int64_t out_stride,
-                                int64_t window, hipStream_t st) {
+                                int64_t window, int64_t prefix, const int32_t* seg_lo,
+                                const int32_t* seg_hi, const uint64_t* pad, hipStream_t st) {
     if (window >= T) window = 0;
     const dim3 grid((unsigned)T, (unsigned)((q_heads + 3) / 4), (unsigned)batch);
     hipLaunchKernelGGL(attention_f32_kernel, grid, dim3(256), 0, st, q, k, v, out, T, q_heads,
                        q_heads / kv_heads, hd, q_stride, kv_stride, out_stride, window,
-                       1.0f / sqrtf((float)hd));
+                       1.0f / sqrtf((float)hd), prefix, seg_lo, seg_hi, pad);
     return hipGetLastError();
 }
 
@@ -236,14 +256,6 @@ PlanF32 plan_f32(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq) {
         if (e_ != hipSuccess) return e_;               \
     } while (0)
 
-// y [rows, n] = x [rows, k] w^T (+ bias), f32.
-hipError_t project_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows,
-                       int64_t k, int64_t n, hipStream_t st) {
-    NCM_TRY(launch_linear_f32(x, w, y, rows, k, n, st));
-    if (bias) NCM_TRY(launch_add_f32(y, bias, rows, n, 1, st));
-    return hipSuccess;
-}
-
 // Copies one stage [T, width] into trace layer `layer` (layer-major).
 hipError_t trace_copy(float* dst, int layer, const float* src, int64_t T, int64_t width,
                       hipStream_t st) {
@@ -254,6 +266,80 @@ hipError_t trace_copy(float* dst, int layer, const float* src, int64_t T, int64_
 }
 
 }  // namespace
+
+hipError_t launch_add_f32(float* y, const float* a, int64_t rows, int64_t n, int64_t a_rows,
+                          hipStream_t st) {
+    const int64_t total = rows * n;
+    if (total == 0) return hipSuccess;
+    hipLaunchKernelGGL(add_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, y,
+                       a, rows, n, a_rows);
+    return hipGetLastError();
+}
+
+// y [rows, n] = x [rows, k] w^T (+ bias), f32.
+hipError_t project_f32(const float* x, const float* w, const float* bias, float* y, int64_t rows,
+                       int64_t k, int64_t n, hipStream_t st) {
+    NCM_TRY(launch_linear_f32(x, w, y, rows, k, n, st));
+    if (bias) NCM_TRY(launch_add_f32(y, bias, rows, n, 1, st));
+    return hipSuccess;
+}
+
+hipError_t run_layers_f32(const LayerStackF32& a, hipStream_t st) {
+    const ncm_decoder_shape_t& s = *a.shape;
+    const int64_t T = a.batch * a.seq, H = s.hidden, I = s.intermediate;
+    const int hd = s.head_dim;
+    const int64_t q_w = (int64_t)s.q_heads * hd, kv_w = (int64_t)s.kv_heads * hd;
+    const ncm_decoder_trace_t none{};
+    const ncm_decoder_trace_t& tr = a.trace ? *a.trace : none;
+    float *hidden = a.hidden, *normed = a.normed, *q = a.q, *k = a.k, *v = a.v, *ctx = a.ctx;
+    float *proj = a.proj, *gate = a.gate, *up = a.up;
+    for (int l = 0; l < s.layers; ++l) {
+        const ncm_decoder_layer_f32_t& L = a.layers[l];
+        NCM_TRY(launch_rms_norm_rows(hidden, L.input_norm, normed, T, H, s.rms_eps, NCM_OUT_F32,
+                                     st));
+        if (L.input_norm_bias) NCM_TRY(launch_add_f32(normed, L.input_norm_bias, T, H, 1, st));
+        NCM_TRY(trace_copy(tr.input_norm, l, normed, T, H, st));
+        const float* wq = L.qkv_weight;
+        const float* wk = wq + q_w * H;
+        const float* wv = wk + kv_w * H;
+        const float* bq = L.qkv_bias;
+        NCM_TRY(project_f32(normed, wq, bq, q, T, H, q_w, st));
+        NCM_TRY(project_f32(normed, wk, bq ? bq + q_w : nullptr, k, T, H, kv_w, st));
+        NCM_TRY(project_f32(normed, wv, bq ? bq + q_w + kv_w : nullptr, v, T, H, kv_w, st));
+        if (L.q_norm) {  // QK-norm (f32 rms_norm of every head) before the rotation
+            NCM_TRY(launch_rms_norm_rows(q, L.q_norm, q, T * s.q_heads, hd, s.rms_eps,
+                                         NCM_OUT_F32, st));
+            NCM_TRY(launch_rms_norm_rows(k, L.k_norm, k, T * s.kv_heads, hd, s.rms_eps,
+                                         NCM_OUT_F32, st));
+        }
+        NCM_TRY(launch_rope_rotate_f32(q, T, q_w, s.q_heads, hd, a.seq, a.cosine, a.sine, st));
+        NCM_TRY(launch_rope_rotate_f32(k, T, kv_w, s.kv_heads, hd, a.seq, a.cosine, a.sine, st));
+        NCM_TRY(launch_attention_f32(q, k, v, ctx, a.batch, a.seq, s.q_heads, s.kv_heads, hd, q_w,
+                                     kv_w, q_w, a.seg_lo ? 0 : s.window, a.prefix, a.seg_lo,
+                                     a.seg_hi, a.pad, st));
+        NCM_TRY(trace_copy(tr.attention_context, l, ctx, T, q_w, st));
+        NCM_TRY(project_f32(ctx, L.o_weight, L.o_bias, proj, T, q_w, H, st));
+        NCM_TRY(trace_copy(tr.attention_output, l, proj, T, H, st));
+        NCM_TRY(launch_add_f32(hidden, proj, T, H, T, st));
+        NCM_TRY(trace_copy(tr.attention_residual, l, hidden, T, H, st));
+        NCM_TRY(launch_rms_norm_rows(hidden, L.post_attention_norm, normed, T, H, s.rms_eps,
+                                     NCM_OUT_F32, st));
+        if (L.post_attention_norm_bias)
+            NCM_TRY(launch_add_f32(normed, L.post_attention_norm_bias, T, H, 1, st));
+        NCM_TRY(trace_copy(tr.post_attention_norm, l, normed, T, H, st));
+        NCM_TRY(project_f32(normed, L.gate_weight, L.gate_bias, gate, T, H, I, st));
+        NCM_TRY(trace_copy(tr.gate_projection, l, gate, T, I, st));
+        NCM_TRY(project_f32(normed, L.up_weight, L.up_bias, up, T, H, I, st));
+        NCM_TRY(trace_copy(tr.up_projection, l, up, T, I, st));
+        NCM_TRY(launch_silu_mul(gate, up, gate, T * I, NCM_OUT_F32, st));
+        NCM_TRY(trace_copy(tr.gate_up_product, l, gate, T, I, st));
+        NCM_TRY(project_f32(gate, L.down_weight, L.down_bias, proj, T, I, H, st));
+        NCM_TRY(trace_copy(tr.mlp_output, l, proj, T, H, st));
+        NCM_TRY(launch_add_f32(hidden, proj, T, H, T, st));
+        NCM_TRY(trace_copy(tr.block_output, l, hidden, T, H, st));
+    }
+    return hipSuccess;
+}
 
 size_t decoder_f32_workspace_bytes(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq) {
     return plan_f32(s, batch, seq).total;
@@ -276,8 +362,7 @@ hipError_t decoder_forward_f32(const ncm_decoder_shape_t& s, const ncm_decoder_l
     float* gate = (float*)(w + p.o_gate);
     float* up = (float*)(w + p.o_up);
     int64_t* ids = (int64_t*)(w + p.o_ids);
-    const int64_t T = p.T, H = s.hidden, I = s.intermediate;
-    const int hd = s.head_dim;
+    const int64_t T = p.T, H = s.hidden;
     const ncm_decoder_trace_t none{};
     const ncm_decoder_trace_t& tr = trace ? *trace : none;
 
@@ -288,47 +373,17 @@ hipError_t decoder_forward_f32(const ncm_decoder_shape_t& s, const ncm_decoder_l
         NCM_TRY(hipGetLastError());
     }
     NCM_TRY(trace_copy(tr.block_input, 0, hidden, T, H, st));
-    for (int l = 0; l < s.layers; ++l) {
-        const ncm_decoder_layer_f32_t& L = layers[l];
-        NCM_TRY(launch_rms_norm_rows(hidden, L.input_norm, normed, T, H, s.rms_eps, NCM_OUT_F32,
-                                     st));
-        NCM_TRY(trace_copy(tr.input_norm, l, normed, T, H, st));
-        const float* wq = L.qkv_weight;
-        const float* wk = wq + p.q_w * H;
-        const float* wv = wk + p.kv_w * H;
-        const float* bq = L.qkv_bias;
-        NCM_TRY(project_f32(normed, wq, bq, q, T, H, p.q_w, st));
-        NCM_TRY(project_f32(normed, wk, bq ? bq + p.q_w : nullptr, k, T, H, p.kv_w, st));
-        NCM_TRY(project_f32(normed, wv, bq ? bq + p.q_w + p.kv_w : nullptr, v, T, H, p.kv_w, st));
-        if (L.q_norm) {  // QK-norm (f32 rms_norm of every head) before the rotation
-            NCM_TRY(launch_rms_norm_rows(q, L.q_norm, q, T * s.q_heads, hd, s.rms_eps,
-                                         NCM_OUT_F32, st));
-            NCM_TRY(launch_rms_norm_rows(k, L.k_norm, k, T * s.kv_heads, hd, s.rms_eps,
-                                         NCM_OUT_F32, st));
-        }
-        NCM_TRY(launch_rope_rotate_f32(q, T, p.q_w, s.q_heads, hd, seq, cosine, sine, st));
-        NCM_TRY(launch_rope_rotate_f32(k, T, p.kv_w, s.kv_heads, hd, seq, cosine, sine, st));
-        NCM_TRY(launch_attention_f32(q, k, v, ctx, batch, seq, s.q_heads, s.kv_heads, hd, p.q_w,
-                                     p.kv_w, p.q_w, s.window, st));
-        NCM_TRY(trace_copy(tr.attention_context, l, ctx, T, p.q_w, st));
-        NCM_TRY(project_f32(ctx, L.o_weight, L.o_bias, proj, T, p.q_w, H, st));
-        NCM_TRY(trace_copy(tr.attention_output, l, proj, T, H, st));
-        NCM_TRY(launch_add_f32(hidden, proj, T, H, T, st));
-        NCM_TRY(trace_copy(tr.attention_residual, l, hidden, T, H, st));
-        NCM_TRY(launch_rms_norm_rows(hidden, L.post_attention_norm, normed, T, H, s.rms_eps,
-                                     NCM_OUT_F32, st));
-        NCM_TRY(trace_copy(tr.post_attention_norm, l, normed, T, H, st));
-        NCM_TRY(project_f32(normed, L.gate_weight, L.gate_bias, gate, T, H, I, st));
-        NCM_TRY(trace_copy(tr.gate_projection, l, gate, T, I, st));
-        NCM_TRY(project_f32(normed, L.up_weight, L.up_bias, up, T, H, I, st));
-        NCM_TRY(trace_copy(tr.up_projection, l, up, T, I, st));
-        NCM_TRY(launch_silu_mul(gate, up, gate, T * I, NCM_OUT_F32, st));
-        NCM_TRY(trace_copy(tr.gate_up_product, l, gate, T, I, st));
-        NCM_TRY(project_f32(gate, L.down_weight, L.down_bias, proj, T, I, H, st));
-        NCM_TRY(trace_copy(tr.mlp_output, l, proj, T, H, st));
-        NCM_TRY(launch_add_f32(hidden, proj, T, H, T, st));
-        NCM_TRY(trace_copy(tr.block_output, l, hidden, T, H, st));
-    }
+    LayerStackF32 a{};
+    a.shape = &s;
+    a.layers = layers;
+    a.batch = batch;
+    a.seq = seq;
+    a.cosine = cosine;
+    a.sine = sine;
+    a.hidden = hidden; a.normed = normed; a.q = q; a.k = k; a.v = v; a.ctx = ctx;
+    a.proj = proj; a.gate = gate; a.up = up;
+    a.trace = trace;
+    NCM_TRY(run_layers_f32(a, st));
     NCM_TRY(launch_rms_norm_rows(hidden, final_norm, normed, T, H, s.rms_eps, NCM_OUT_F32, st));
     NCM_TRY(launch_linear_f32(normed, lm_head ? lm_head : embed, logits, T, H, s.vocab, st));
     return hipSuccess;

@@ -20,4 +20,13 @@ hipError_t ncm_forward(const ncm_ncm_shape_t& s, const ncm_decoder_layer_t* laye
                        const float* cosine, const float* sine, float* output, void* ws,
                        hipStream_t st);
 
+// The same body in the reference's f32 arithmetic (float weights,
+// ncm_decoder_layer_f32_t layers); same pointer conventions.
+size_t ncm_f32_workspace_bytes(const ncm_ncm_shape_t& s, bool convs);
+hipError_t ncm_forward_f32(const ncm_ncm_shape_t& s, const ncm_decoder_layer_f32_t* layers,
+                           const ncm_ncm_weights_f32_t& w, const int64_t* host_ids,
+                           const uint8_t* host_pad, int64_t pad_len, const float* target,
+                           const float* cosine, const float* sine, float* output, void* ws,
+                           hipStream_t st);
+
 }  // namespace ncm

@@ -252,7 +252,8 @@ def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine,
 
 _LAYER_F32_FIELDS = ("input_norm", "qkv_weight", "qkv_bias", "o_weight", "o_bias",
                      "post_attention_norm", "gate_weight", "gate_bias", "up_weight", "up_bias",
-                     "down_weight", "down_bias", "q_norm", "k_norm")
+                     "down_weight", "down_bias", "q_norm", "k_norm", "input_norm_bias",
+                     "post_attention_norm_bias")
 TRACE_FIELDS = ("block_input", "input_norm", "attention_context", "attention_output",
                 "attention_residual", "post_attention_norm", "gate_projection",
                 "up_projection", "gate_up_product", "mlp_output", "block_output")
@@ -300,8 +301,10 @@ def forward_f32(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, s
     shapes = {"input_norm": (H,), "qkv_weight": (qkv, H), "qkv_bias": (qkv,), "o_weight": (H, qw),
               "o_bias": (H,), "post_attention_norm": (H,), "gate_weight": (I, H),
               "gate_bias": (I,), "up_weight": (I, H), "up_bias": (I,), "down_weight": (H, I),
-              "down_bias": (H,), "q_norm": (hd,), "k_norm": (hd,)}
-    optional = {"qkv_bias", "o_bias", "gate_bias", "up_bias", "down_bias", "q_norm", "k_norm"}
+              "down_bias": (H,), "q_norm": (hd,), "k_norm": (hd,), "input_norm_bias": (H,),
+              "post_attention_norm_bias": (H,)}
+    optional = {"qkv_bias", "o_bias", "gate_bias", "up_bias", "down_bias", "q_norm", "k_norm",
+                "input_norm_bias", "post_attention_norm_bias"}
     for i, layer in enumerate(weights.layers):
         for f in _LAYER_F32_FIELDS:
             a.dev(layer.get(f), f"layers[{i}].{f}", _ck.F32, shapes[f], optional=f in optional)

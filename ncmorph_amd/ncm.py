@@ -306,3 +306,131 @@ def code_head_logits(spec: NcmSpec, hidden, z_weights, codebooks, csq, log_inv_t
         off += n
     return kernels.tied_head_logits_levels(z, codebooks, csq, list(spec.level_lengths),
                                            log_inv_t=log_inv_t, bias=bias, ctx=ctx)
+
+
+class _WeightsF32(C.Structure):
+    _fields_ = [("prefix_token_embedding", C.c_void_p), ("input_projection", C.c_void_p),
+                ("input_projection_bias", C.c_void_p), ("level_embedding", C.c_void_p),
+                ("l0_queries", C.c_void_p), ("final_norm", C.c_void_p),
+                ("final_norm_bias", C.c_void_p), ("conv_weight", C.c_void_p),
+                ("conv_bias", C.c_void_p)]
+
+
+def device_weights_f32(spec: NcmSpec, ref: dict, device) -> NcmWeights:
+    """Float32 device weights for forward_f32 from the reference's weights_t
+    layout (numpy float32 arrays, per-layer dicts with the layer_weights_t
+    names): fused q|k|v rows, gate / up / down as stored, the ln biases as
+    the norm biases."""
+    import torch
+
+    def f32(a):
+        return None if a is None else torch.from_numpy(
+            np.ascontiguousarray(a, np.float32)).to(device)
+
+    layers = []
+    for L in ref["layers"]:
+        layers.append({
+            "input_norm": f32(L["ln_1_weight"]), "qkv_weight": f32(L["fused_qkv_weight"]),
+            "qkv_bias": f32(L.get("fused_qkv_bias")), "o_weight": f32(L["output_weight"]),
+            "o_bias": f32(L.get("output_bias")), "post_attention_norm": f32(L["ln_2_weight"]),
+            "gate_weight": f32(L["gate_weight"]), "gate_bias": f32(L.get("gate_bias")),
+            "up_weight": f32(L["up_weight"]), "up_bias": f32(L.get("up_bias")),
+            "down_weight": f32(L["down_weight"]), "down_bias": f32(L.get("down_bias")),
+            "q_norm": f32(L.get("query_norm_weight")), "k_norm": f32(L.get("key_norm_weight")),
+            "input_norm_bias": f32(L.get("ln_1_bias")),
+            "post_attention_norm_bias": f32(L.get("ln_2_bias")),
+        })
+    convs = [dict(weight=f32(c["weight"]), bias=f32(c["bias"]))
+             for c in (ref.get("post_upsample_convs") or [])]
+    return NcmWeights(
+        prefix_token_embedding=f32(ref["prefix_token_embedding"]),
+        input_projection=f32(ref["input_projection"]),
+        input_projection_bias=f32(ref.get("input_projection_bias")),
+        level_embedding=f32(ref["level_embedding"]),
+        l0_queries=f32(ref.get("l0_queries")),
+        final_norm=f32(ref["final_norm_weight"]),
+        final_norm_bias=f32(ref.get("final_norm_bias")),
+        layers=layers, convs=convs)
+
+
+def forward_f32(spec: NcmSpec, weights: NcmWeights, prefix_ids, target_inputs, cosine, sine,
+                prefix_pad_mask=None, out=None, ctx=None):
+    """The NCM body in the reference's f32 arithmetic (forward_with_trace,
+    src/ncm_model.zig:89-250): final-normalized hidden states float32 [S,
+    hidden]. Arguments as forward, with float32 weights (device_weights_f32;
+    layers[i] maps the names of decoder._LAYER_F32_FIELDS)."""
+    import torch
+
+    W = "ncm_forward_f32"
+    if len(spec.level_lengths) > MAX_LEVELS or spec.mask not in MASK_MODES:
+        raise NcmError(-2, W, "too many levels or an unknown mask")
+    ids = np.ascontiguousarray(prefix_ids, dtype=np.int64).ravel()
+    if ids.size != spec.prefix_length:
+        raise NcmError(-3, W, "prefix_ids must hold prefix_length ids")
+    pad = None if prefix_pad_mask is None else np.ascontiguousarray(prefix_pad_mask, np.uint8)
+    S, T = spec.seq_len, int(sum(spec.level_lengths))
+    H, I, hd, vq = spec.hidden, spec.intermediate, spec.head_dim, spec.vq_width
+    qkv, qw = (spec.q_heads + 2 * spec.kv_heads) * hd, spec.q_heads * hd
+    nl = len(spec.level_lengths)
+    a = _ck.Args(W)
+    a.dev(target_inputs, "target_inputs", _ck.F32, (T, vq))
+    a.dev(cosine, "cosine", _ck.F32, (S, hd))
+    a.dev(sine, "sine", _ck.F32, (S, hd))
+    a.dev(weights.prefix_token_embedding, "prefix_token_embedding", _ck.F32,
+          (spec.prefix_vocab, vq))
+    a.dev(weights.input_projection, "input_projection", _ck.F32, (H, vq))
+    a.dev(weights.input_projection_bias, "input_projection_bias", _ck.F32, (H,), optional=True)
+    a.dev(weights.level_embedding, "level_embedding", _ck.F32, (nl, H),
+          optional=not spec.use_level_encoding)
+    a.dev(weights.l0_queries, "l0_queries", _ck.F32, (spec.level_lengths[0], vq),
+          optional=not spec.query_level0)
+    a.dev(weights.final_norm, "final_norm", _ck.F32, (H,))
+    a.dev(weights.final_norm_bias, "final_norm_bias", _ck.F32, (H,), optional=True)
+    if len(weights.layers) != spec.layers:
+        raise NcmError(-3, W, "one weight dict per layer")
+    shapes = {"input_norm": (H,), "qkv_weight": (qkv, H), "qkv_bias": (qkv,), "o_weight": (H, qw),
+              "o_bias": (H,), "post_attention_norm": (H,), "gate_weight": (I, H),
+              "gate_bias": (I,), "up_weight": (I, H), "up_bias": (I,), "down_weight": (H, I),
+              "down_bias": (H,), "q_norm": (hd,), "k_norm": (hd,), "input_norm_bias": (H,),
+              "post_attention_norm_bias": (H,)}
+    required = {"input_norm", "qkv_weight", "o_weight", "post_attention_norm", "gate_weight",
+                "up_weight", "down_weight"}
+    for i, L in enumerate(weights.layers):
+        for f in _dec._LAYER_F32_FIELDS:
+            a.dev(L.get(f), f"layers[{i}].{f}", _ck.F32, shapes[f], optional=f not in required)
+    if weights.convs and len(weights.convs) != nl:
+        raise NcmError(-3, W, "one convolution per level, or none")
+    for i, c in enumerate(weights.convs):
+        a.dev(c["weight"], f"convs[{i}].weight", _ck.F32, (vq, vq, 3))
+        a.dev(c["bias"], f"convs[{i}].bias", _ck.F32, (vq,))
+    if out is None:
+        out = torch.empty((S, H), dtype=torch.float32, device=target_inputs.device)
+    po = a.dev(out, "out", _ck.F32, (S, H))
+    a.done()
+
+    ptr = lambda t: None if t is None else t.data_ptr()
+    shape = _Shape(H, vq, I, spec.q_heads, spec.kv_heads, hd, spec.layers, spec.prefix_length,
+                   spec.prefix_vocab, nl, MASK_MODES[spec.mask], int(spec.query_level0),
+                   int(spec.use_level_encoding), spec.window, spec.rms_eps, 0)
+    for l, n in enumerate(spec.level_lengths):
+        shape.level_lengths[l] = int(n)
+    cw = cb = None
+    if weights.convs:
+        cw = (C.c_void_p * nl)(*[ptr(c["weight"]) for c in weights.convs])
+        cb = (C.c_void_p * nl)(*[ptr(c["bias"]) for c in weights.convs])
+    wts = _WeightsF32(ptr(weights.prefix_token_embedding), ptr(weights.input_projection),
+                      ptr(weights.input_projection_bias), ptr(weights.level_embedding),
+                      ptr(weights.l0_queries), ptr(weights.final_norm),
+                      ptr(weights.final_norm_bias), C.cast(cw, C.c_void_p) if cw else None,
+                      C.cast(cb, C.c_void_p) if cb else None)
+    arr = (_dec._LayerF32 * spec.layers)()
+    for i, L in enumerate(weights.layers):
+        arr[i] = _dec._LayerF32(*[ptr(L.get(n)) for n in _dec._LAYER_F32_FIELDS])
+    ctx = ctx or default_context(target_inputs.device.index or 0)
+    ctx.bind_stream()
+    check(lib().ncm_ncm_forward_f32_dev(
+        ctx.handle, C.byref(shape), arr, C.byref(wts), ids.ctypes.data_as(C.c_void_p),
+        None if pad is None else pad.ctypes.data_as(C.c_void_p), 0 if pad is None else pad.size,
+        C.c_void_p(target_inputs.data_ptr()), C.c_void_p(cosine.data_ptr()),
+        C.c_void_p(sine.data_ptr()), po), W)
+    return out

@@ -14,6 +14,7 @@ STRUCTS = {
     "ncm_decoder_trace_t": ("decoder", "_Trace"),
     "ncm_ncm_shape_t": ("ncm", "_Shape"),
     "ncm_ncm_weights_t": ("ncm", "_Weights"),
+    "ncm_ncm_weights_f32_t": ("ncm", "_WeightsF32"),
     "ncm_vq_tok_t": ("vq_tokenizer", "_Tok"),
     "ncm_vq_tok_decoder_t": ("vq_tokenizer", "_Dec"),
 }
