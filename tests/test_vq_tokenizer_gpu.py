@@ -279,3 +279,21 @@ def test_load_round_trip(tmp_path):
     b = loaded.encode(ids)
     assert torch.equal(a["codes"], b["codes"]) and torch.equal(a["zhat"], b["zhat"])
     assert torch.equal(tok.decode(a["zhat"]), loaded.decode(b["zhat"]))
+
+
+def test_owt_full_size_replay():
+    """The OWT tokenizer of vq_forward_semantics.md section 1 at its full
+    shapes (1024 positions, 32 levels of (k + 1)^2 positions, 8192 codes, a
+    five-stage cascade without norms) on one sequence: the oracle replay of
+    every level and the reconstruction identity."""
+    torch = _torch()
+    ocfg = dataclasses.replace(vo.OWT, in_vocab=512)
+    ocfg, enc, qw, dec, tok = _model(ocfg, seed=13)
+    rng = np.random.default_rng(13)
+    ids = rng.integers(0, ocfg.in_vocab, size=(1, 1024))
+    print("vq_tok OWT B=1", flush=True)
+    out = tok.encode(ids, want_latent=True)
+    torch.cuda.synchronize()
+    z = out["latent"].cpu().numpy().astype(np.float64)
+    _check_codes(ocfg, qw, z, out["codes"].cpu().numpy(), out["zhat"].cpu().numpy())
+    assert torch.equal(tok.reconstruct(out["codes"]), out["zhat"])
