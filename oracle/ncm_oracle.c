@@ -157,6 +157,61 @@ void ncmo_matmul_bf16(const float* input, const float* weights, const float* bia
                           output_width, 0, token_count);
 }
 
+/* The same arithmetic with the output columns split over `threads` POSIX
+ * threads: every element is computed exactly as ncmo_matmul_bf16 computes
+ * it, so the results are bit-identical (a speed-up for large checks only). */
+struct mm_job {
+    const float *input, *weights, *bias;
+    float *output, *sum_out;
+    size_t token_count, input_width, output_width, o_begin, o_end, kb;
+};
+
+static void* mm_worker(void* arg) {
+    const struct mm_job* j = (const struct mm_job*)arg;
+    for (size_t t = 0; t < j->token_count; ++t) {
+        for (size_t o = j->o_begin; o < j->o_end; ++o) {
+            float sum = j->kb ? bf16_dot_f32(j->input + t * j->input_width,
+                                             j->weights + o * j->input_width, j->input_width,
+                                             j->kb)
+                              : 0.0f;
+            if (j->bias) sum += ncmo_round_bf16(j->bias[o]);
+            if (j->sum_out) j->sum_out[t * j->output_width + o] = sum;
+            j->output[t * j->output_width + o] = ncmo_round_bf16(sum);
+        }
+    }
+    return NULL;
+}
+
+void ncmo_matmul_bf16_mt(const float* input, const float* weights, const float* bias,
+                         float* output, float* sum_out, size_t token_count, size_t input_width,
+                         size_t output_width, int threads) {
+    if (threads < 2 || output_width < 64) {
+        ncmo_matmul_bf16(input, weights, bias, output, sum_out, token_count, input_width,
+                         output_width);
+        return;
+    }
+    if (threads > 64) threads = 64;
+    pthread_t tids[64];
+    struct mm_job jobs[64];
+    const size_t kb = reduction_block(input_width);
+    int started = 0;
+    for (int w = 0; w < threads; ++w) {
+        const size_t o0 = output_width * (size_t)w / (size_t)threads;
+        const size_t o1 = output_width * (size_t)(w + 1) / (size_t)threads;
+        jobs[w] = (struct mm_job){input, weights, bias, output, sum_out, token_count,
+                                  input_width, output_width, o0, o1, kb};
+        if (pthread_create(&tids[w], NULL, mm_worker, &jobs[w]) != 0) {
+            mm_worker(&jobs[w]);
+            tids[w] = 0;
+        } else {
+            ++started;
+        }
+    }
+    for (int w = 0; w < threads; ++w)
+        if (tids[w]) pthread_join(tids[w], NULL);
+    (void)started;
+}
+
 void ncmo_matmul_bf16_u16_rows(const uint16_t* input, const uint16_t* weights,
                                const uint16_t* bias, float* output, float* sum_out,
                                size_t token_count, size_t input_width, size_t output_width,

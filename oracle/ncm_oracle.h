@@ -56,6 +56,9 @@ void ncmo_matmul_bf16_rows(const float* input, const float* weights, const float
 void ncmo_matmul_bf16(const float* input, const float* weights, const float* bias,
                       float* output, float* sum_out, size_t token_count, size_t input_width,
                       size_t output_width);
+void ncmo_matmul_bf16_mt(const float* input, const float* weights, const float* bias,
+                         float* output, float* sum_out, size_t token_count, size_t input_width,
+                         size_t output_width, int threads);
 /* Same, operands given as bf16 bit patterns (already rounded). */
 void ncmo_matmul_bf16_u16_rows(const uint16_t* input, const uint16_t* weights,
                                const uint16_t* bias, float* output, float* sum_out,

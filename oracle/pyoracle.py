@@ -49,6 +49,7 @@ def lib():
         L.ncmo_bf16_from_f32_array.argtypes = [f32p, u16p, sz]
         L.ncmo_widen_little_endian.argtypes = [f32p, u8p, sz]
         L.ncmo_matmul_bf16.argtypes = [f32p, f32p, vp, f32p, vp, sz, sz, sz]
+        L.ncmo_matmul_bf16_mt.argtypes = [f32p, f32p, vp, f32p, vp, sz, sz, sz, C.c_int]
         L.ncmo_matmul_bf16_rows.argtypes = [f32p, f32p, vp, f32p, vp, sz, sz, sz, sz, sz]
         L.ncmo_matmul_bf16_u16_rows.argtypes = [u16p, u16p, vp, f32p, vp, sz, sz, sz, sz, sz]
         L.ncmo_matmul_reference.argtypes = [f32p, f32p, f32p, sz, sz, sz]
@@ -123,8 +124,23 @@ def matmul_bf16(x, w, bias=None, token_count=None, input_width=None, output_widt
     out = np.empty((T, N), np.float32)
     s = np.empty((T, N), np.float32) if want_sum else None
     b = None if bias is None else np.ascontiguousarray(bias, np.float32)
-    lib().ncmo_matmul_bf16(x.ravel(), w.ravel(), _ptr(b), out, _ptr(s), T, K, N)
+    if _THREADS > 1:
+        lib().ncmo_matmul_bf16_mt(x.ravel(), w.ravel(), _ptr(b), out, _ptr(s), T, K, N,
+                                  _THREADS)
+    else:
+        lib().ncmo_matmul_bf16(x.ravel(), w.ravel(), _ptr(b), out, _ptr(s), T, K, N)
     return (out, s) if want_sum else out
+
+
+_THREADS = 1
+
+
+def set_threads(n: int) -> int:
+    """Threads for matmul_bf16 (and so decoder_forward): output columns split
+    over POSIX threads, bit-identical results. Returns the previous value."""
+    global _THREADS
+    prev, _THREADS = _THREADS, max(1, int(n))
+    return prev
 
 
 def matmul_bf16_u16_rows(x_bits, w_bits, row_begin, row_end, bias_bits=None):

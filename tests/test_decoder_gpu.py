@@ -120,3 +120,62 @@ def test_decoder_llama_1b_shape_batch_invariant(ncm, cuda):
     # Logits are bf16 values and not degenerate.
     assert torch.equal(a, a.to(torch.bfloat16).float())
     assert float(a.std()) > 0
+
+
+def test_decoder_llama_1b_full_size_against_oracle(ncm, oracle, cuda):
+    """The whole Llama-3.2-1B shape (16 layers, hidden 2048, 32 / 8 heads of
+    64, SwiGLU 8192, tied 128256-row head) on 4 tokens against the oracle's
+    composition of the reference's bf16 ops (its matmul_bf16 split over host
+    threads, bit-identical to one thread): the same bar as the small shapes,
+    |dev - oracle| <= BAR_1B max|logits|, with rounding differences now
+    carried through 16 layers."""
+    import os
+
+    import torch
+    from ncmorph_amd import decoder, kernels
+
+    spec = decoder.LLAMA_3_2_1B
+    H, I, V = spec.hidden, spec.intermediate, spec.vocab
+    g = torch.Generator().manual_seed(21)
+
+    def w(*shape, s=0.02):  # bf16-valued float32 (torch rounds to nearest even)
+        return (torch.randn(*shape, generator=g) * s).to(torch.bfloat16).float().numpy()
+
+    def norm():
+        return (1.0 + 0.1 * torch.randn(H, generator=g)).to(torch.bfloat16).float().numpy()
+
+    embed = w(V, H, s=0.5)
+    layers = [dict(input_norm=norm(), qkv_weight=w((spec.q_heads + 2 * spec.kv_heads) * 64, H),
+                   o_weight=w(H, spec.q_heads * 64), post_attention_norm=norm(),
+                   gate_up_weight=w(2 * I, H), down_weight=w(H, I)) for _ in range(spec.layers)]
+    fnorm = norm()
+    seq = 4
+    cos, sin = decoder.rope_tables(spec, seq)
+    dl = []
+    for L in layers:
+        d = {k: (_dev_f32(v, cuda) if k.endswith("norm") else _dev_bf16(v, cuda))
+             for k, v in L.items() if k != "gate_up_weight"}
+        d["gate_up_weight"] = _dev_bf16(kernels.interleave_gate_up(L["gate_up_weight"][:I],
+                                                                   L["gate_up_weight"][I:]), cuda)
+        dl.append(d)
+    wd = decoder.DecoderWeights(embed=_dev_bf16(embed, cuda), final_norm=_dev_f32(fnorm, cuda),
+                                layers=dl)
+    ids = np.random.default_rng(22).integers(0, V, (1, seq))
+    print("decoder 1B full size, 4 tokens", flush=True)
+    got = decoder.forward(spec, wd, ids, _dev_f32(cos, cuda), _dev_f32(sin, cuda))
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    prev = oracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    try:
+        ref = oracle.decoder_forward(ids[0], embed, layers, fnorm, None, cos, sin,
+                                     spec.q_heads, spec.kv_heads, 64, 1e-5)
+    finally:
+        oracle.set_threads(prev)
+    scale = np.max(np.abs(ref))
+    err = np.abs(got - ref)
+    print("max / mean error relative to max|logits|:", err.max() / scale, err.mean() / scale,
+          "bit-identical:", np.mean(got == ref), flush=True)
+    assert err.max() <= BAR_1B * scale, err.max() / scale
+
+
+BAR_1B = 0.03  # measured 0.0153 (mean 0.0024) on the MI355X

@@ -92,3 +92,18 @@ def test_u16_path_matches_f32_path(oracle):
     y, s = oracle.matmul_bf16(x, w, want_sum=True)
     y2, s2 = oracle.matmul_bf16_u16_rows(oracle.bf16_from_f32(x), oracle.bf16_from_f32(w), 0, 4)
     assert np.array_equal(y, y2) and np.array_equal(s, s2)
+
+
+def test_threaded_matmul_is_bit_identical(oracle):
+    """The column-split threaded matmul gives the single-threaded bits."""
+    rng = np.random.default_rng(9)
+    x = oracle.round_bf16(rng.standard_normal((7, 2050)).astype(np.float32))
+    w = oracle.round_bf16(rng.standard_normal((301, 2050)).astype(np.float32))
+    b = oracle.round_bf16(rng.standard_normal(301).astype(np.float32))
+    one = oracle.matmul_bf16(x, w, b)
+    prev = oracle.set_threads(5)
+    try:
+        many = oracle.matmul_bf16(x, w, b)
+    finally:
+        oracle.set_threads(prev)
+    assert np.array_equal(one.view(np.uint32), many.view(np.uint32))

@@ -155,8 +155,10 @@ def test_decode_matches_oracle(ncm, oracle, cuda):
 
 def test_large_config_properties(ncm, oracle, cuda):
     """16 x 2048 x 2048, 8 levels, 4096 codes: codes in range, decode equals
-    the encode's reconstruction, and sampled rows of every level agree with
-    the oracle's exhaustive search given the GPU's earlier codes."""
+    the encode's reconstruction, sampled rows of every level agree with the
+    oracle's exhaustive search given the GPU's earlier codes, and sequence 0
+    (every level, 4080 codes, and its reconstruction) equals the oracle's
+    own encode bit for bit."""
     import torch
     from ncmorph_amd import vq
 
@@ -193,3 +195,14 @@ def test_large_config_properties(ncm, oracle, cuda):
         assert np.all(ogap[~np.isfinite(g)] >= 1e-5)
         off += per_b
     print("near-ties (gap < 1e-5):", int((gap < 1e-5).sum()), "of", gap.size)
+    # One whole sequence against the oracle's own exhaustive encode (no
+    # teacher forcing): all 4080 codes and the 2048 x 2048 reconstruction
+    # bit for bit.
+    import os
+
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    ref = oracle.rvq_encode(np.ascontiguousarray(x[:1]), cb, c["strides"], csq=csq,
+                            want_gap=False, threads=threads)
+    assert np.array_equal(ref["codes"][0], codes[0]), int(np.sum(ref["codes"][0] != codes[0]))
+    assert np.array_equal(ref["recon"][0].view(np.uint32),
+                          r["recon"][0].cpu().numpy().view(np.uint32))
