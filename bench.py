@@ -125,8 +125,21 @@ def run_linear(torch, steps, warmup):
     n, k = LINEAR_NK[0]
     ref = xs[k].float() @ ws[(n, k)].float().T
     err = float((ys[(n, k)] - ref).abs().max())
+    # Same-box reference point, outside the timed region: torch's bf16
+    # linear (hipBLASLt; bf16 output, half of this path's output bytes).
+    vendor = {}
+    for (n, k) in LINEAR_NK:
+        run = lambda: torch.nn.functional.linear(xs[k], ws[(n, k)])  # noqa: E731
+        _ramp(torch, run, ms=50.0)
+        e0, e1 = _events(torch)
+        e0.record()
+        for _ in range(20):
+            run()
+        e1.record()
+        torch.cuda.synchronize()
+        vendor[(n, k)] = e0.elapsed_time(e1) / 20 * 1e-3
     return {"step_s": gpu_s / steps, "wall_s": wall, "flops_per_step": flops,
-            "per_shape_s": per_shape, "max_abs_err_vs_fp32": err}
+            "per_shape_s": per_shape, "max_abs_err_vs_fp32": err, "vendor_per_shape_s": vendor}
 
 
 def run_rvq(torch, reps, warmup):
@@ -746,6 +759,9 @@ def main():
                 "frac": round(2.0 * LINEAR_M * n * k / t / 1e12 / BF16_PEAK_TFLOPS, 4)}
             for (n, k), t in lin["per_shape_s"].items()}
         res["linear_max_abs_err_vs_fp32"] = lin["max_abs_err_vs_fp32"]
+        res["linear_hipblaslt_bf16_out_per_shape_us"] = {
+            f"{LINEAR_M}x{n}x{k}": round(t * 1e6, 2) for (n, k), t in
+            lin["vendor_per_shape_s"].items()}
         if not args.no_cpu:
             res["cpu_baseline"] = cpu_linear_baseline()
             res["cpu_baseline_ncores"] = cpu_linear_baseline_ncores()
