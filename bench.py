@@ -127,19 +127,30 @@ def run_linear(torch, steps, warmup):
     err = float((ys[(n, k)] - ref).abs().max())
     # Same-box reference point, outside the timed region: torch's bf16
     # linear (hipBLASLt; bf16 output, half of this path's output bytes).
-    vendor = {}
-    for (n, k) in LINEAR_NK:
-        run = lambda: torch.nn.functional.linear(xs[k], ws[(n, k)])  # noqa: E731
-        _ramp(torch, run, ms=50.0)
-        e0, e1 = _events(torch)
-        e0.record()
-        for _ in range(20):
-            run()
-        e1.record()
-        torch.cuda.synchronize()
-        vendor[(n, k)] = e0.elapsed_time(e1) / 20 * 1e-3
+    # Also torch.mm with out_dtype=float32 (hipBLASLt with this path's fp32
+    # output), where this torch build has it.
+    def vendor_times(fn):
+        out = {}
+        for (n, k) in LINEAR_NK:
+            run = lambda: fn(xs[k], ws[(n, k)])  # noqa: E731
+            _ramp(torch, run, ms=50.0)
+            e0, e1 = _events(torch)
+            e0.record()
+            for _ in range(20):
+                run()
+            e1.record()
+            torch.cuda.synchronize()
+            out[(n, k)] = e0.elapsed_time(e1) / 20 * 1e-3
+        return out
+
+    vendor = vendor_times(torch.nn.functional.linear)
+    try:
+        vendor_f32 = vendor_times(lambda a, b: torch.mm(a, b.t(), out_dtype=torch.float32))
+    except (RuntimeError, TypeError):
+        vendor_f32 = None
     return {"step_s": gpu_s / steps, "wall_s": wall, "flops_per_step": flops,
-            "per_shape_s": per_shape, "max_abs_err_vs_fp32": err, "vendor_per_shape_s": vendor}
+            "per_shape_s": per_shape, "max_abs_err_vs_fp32": err, "vendor_per_shape_s": vendor,
+            "vendor_f32_per_shape_s": vendor_f32}
 
 
 def run_rvq(torch, reps, warmup):
@@ -762,6 +773,9 @@ def main():
         res["linear_hipblaslt_bf16_out_per_shape_us"] = {
             f"{LINEAR_M}x{n}x{k}": round(t * 1e6, 2) for (n, k), t in
             lin["vendor_per_shape_s"].items()}
+        res["linear_hipblaslt_f32_out_per_shape_us"] = None if lin["vendor_f32_per_shape_s"] is None \
+            else {f"{LINEAR_M}x{n}x{k}": round(t * 1e6, 2) for (n, k), t in
+                  lin["vendor_f32_per_shape_s"].items()}
         if not args.no_cpu:
             res["cpu_baseline"] = cpu_linear_baseline()
             res["cpu_baseline_ncores"] = cpu_linear_baseline_ncores()

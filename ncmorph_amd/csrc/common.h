@@ -50,6 +50,27 @@ __device__ __forceinline__ float flush_subnormal(float v) {
     return (b & 0x7F800000u) == 0 ? __uint_as_float(b & 0x80000000u) : v;
 }
 
+// round(silu_bf16(gate) * up) of two elements from their accumulators
+// (packages/kernels/root.zig:265-270, src/decoder.zig:210-211): the gate and
+// up projections' bits (bf16(flush(acc + bias))), a = rb(g / (1 + expf(-g)))
+// with rb(v) = v rounded to a bf16 value, then round(a * up); the roundings
+// two values per v_cvt_pk_bf16_f32, bit for bit the same as bf16_bits_rne
+// (the unfused SiLU x up kernel's arithmetic).
+__device__ __forceinline__ void swiglu_bits2(float ga0, float ua0, float ga1, float ua1,
+                                             float bg, float bu, uint32_t& o0, uint32_t& o1) {
+    // Intermediate roundings without the NaN rule: a NaN stays a NaN through
+    // the products and the quotient, and the final rounding maps it to 0x7FC0.
+    const uint32_t p0 = bf16x2_rne(flush_subnormal(ga0 + bg), flush_subnormal(ua0 + bu));
+    const uint32_t p1 = bf16x2_rne(flush_subnormal(ga1 + bg), flush_subnormal(ua1 + bu));
+    const float g0 = __uint_as_float(p0 << 16), u0 = __uint_as_float(p0 & 0xFFFF0000u);
+    const float g1 = __uint_as_float(p1 << 16), u1 = __uint_as_float(p1 & 0xFFFF0000u);
+    const uint32_t a = bf16x2_rne(g0 / (1.0f + expf(-g0)), g1 / (1.0f + expf(-g1)));
+    const uint32_t r = bf16x2_bits_rne(__uint_as_float(a << 16) * u0,
+                                       __uint_as_float(a & 0xFFFF0000u) * u1);
+    o0 = r & 0xFFFFu;
+    o1 = r >> 16;
+}
+
 __device__ __forceinline__ float bf16_lo_to_f32(uint32_t packed) {
     return __uint_as_float(packed << 16);
 }

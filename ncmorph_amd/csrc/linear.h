@@ -32,6 +32,21 @@ hipError_t launch_linear_rope64(const uint16_t* x, const uint16_t* w, const uint
                                 int64_t seq_len, const float* cosine, const float* sine,
                                 hipStream_t stream);
 
+// Rows past the last full 256-row tile that launch_linear,
+// launch_linear_residual and launch_linear_swiglu (automatic tile choice)
+// hand to linear_tail.hip, or 0: M % 256 when it is at most 64, the
+// 256 x 256 tile is chosen for M and for M - M % 256, K % 2048 == 0,
+// N % 16 == 0, and the partial row tile would cost the whole chip an extra
+// round (N: the weight's rows).
+int64_t linear_tail_rows(int64_t M, int64_t N, int64_t K);
+// The R rows of such a tail (x, y, residual pointing at its first row):
+// out_mode / bias / residual as launch_linear(_residual); swiglu: N is the
+// feature count (weight rows 2 N, interleaved as launch_linear_swiglu),
+// y [R, N] bf16 bits.
+hipError_t launch_linear_tail(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                              const float* residual, void* y, int64_t R, int64_t K, int64_t N,
+                              int out_mode, bool swiglu, hipStream_t st);
+
 // fp32 operands, fp32 output; K % 4 == 0, 16-byte aligned x and w.
 hipError_t launch_linear_f32(const float* x, const float* w, float* y, int64_t M, int64_t K,
                              int64_t N, hipStream_t stream);

@@ -259,6 +259,19 @@ hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* b
         return e ? atoi(e) : -1;
     }();
     if (config < 0) config = env_cfg;
+    if (config < 0) {
+        // A partial last row tile that would add a round: its rows go to the
+        // tail kernel.
+        const int64_t r = linear_tail_rows(M, N, K);
+        if (r > 0) {
+            const int64_t mm = M - r;
+            hipError_t e = launch_linear(x, w, bias, y, mm, K, N, out_mode, 0, stream);
+            if (e != hipSuccess) return e;
+            const size_t esz = out_mode == NCM_OUT_BF16 ? 2 : 4;
+            return launch_linear_tail(x + mm * K, w, bias, nullptr, (char*)y + mm * N * esz, r,
+                                      K, N, out_mode, false, stream);
+        }
+    }
     switch (linear_tile_config(M, N, K, config)) {
         case 0: return launch_linear_s<Lin0>(x, w, bias, y, M, K, N, out_mode, stream);
         case 1: return launch_linear_s<Lin1>(x, w, bias, y, M, K, N, out_mode, stream);
@@ -297,7 +310,18 @@ static hipError_t launch_linear_res_s(const uint16_t* x, const uint16_t* w, cons
 hipError_t launch_linear_residual(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                                   const float* residual, void* y, int64_t M, int64_t K,
                                   int64_t N, int out_mode, hipStream_t stream) {
-    // The automatic tile choice only (configurations 0, 1, 2 and 5).
+    // The automatic tile choice only (configurations 0, 1, 2 and 5), with
+    // the tail rows of linear_tail_rows on the tail kernel.
+    const int64_t r = linear_tail_rows(M, N, K);
+    if (r > 0) {
+        const int64_t mm = M - r;
+        hipError_t e =
+            launch_linear_residual(x, w, bias, residual, y, mm, K, N, out_mode, stream);
+        if (e != hipSuccess) return e;
+        const size_t esz = out_mode == NCM_OUT_BF16 ? 2 : 4;
+        return launch_linear_tail(x + mm * K, w, bias, residual + mm * N,
+                                  (char*)y + mm * N * esz, r, K, N, out_mode, false, stream);
+    }
     switch (linear_tile_config(M, N, K, -1)) {
         case 0: return launch_linear_res_s<Lin0>(x, w, bias, residual, y, M, K, N, out_mode, stream);
         case 1: return launch_linear_res_s<Lin1>(x, w, bias, residual, y, M, K, N, out_mode, stream);

@@ -29,29 +29,9 @@ struct PairArgs {
     int64_t rot_cols;  // columns [0, rot_cols) are rotated
 };
 
-// rb(v): v rounded to a bf16 value (RNE, NaN -> 0x7FC0), as an fp32. The
-// projections' output value of one accumulator: bf16(flush(acc + bias)).
-// Both are computed two values at a time with bf16x2_bits_rne below.
-
-// round(silu_bf16(gate) * up) of two elements from their accumulators
-// (root.zig:265-270, decoder.zig:210-211): the gate and up projections' bits
-// (bf16(flush(acc + bias))), a = rb(g / (1 + expf(-g))), round(a * up); the
-// roundings two values per v_cvt_pk_bf16_f32, bit for bit the same as
-// bf16_bits_rne (the unfused SiLU x up kernel's arithmetic).
-__device__ __forceinline__ void swiglu_bits2(float ga0, float ua0, float ga1, float ua1,
-                                             float bg, float bu, uint32_t& o0, uint32_t& o1) {
-    // Intermediate roundings without the NaN rule: a NaN stays a NaN through
-    // the products and the quotient, and the final rounding maps it to 0x7FC0.
-    const uint32_t p0 = bf16x2_rne(flush_subnormal(ga0 + bg), flush_subnormal(ua0 + bu));
-    const uint32_t p1 = bf16x2_rne(flush_subnormal(ga1 + bg), flush_subnormal(ua1 + bu));
-    const float g0 = __uint_as_float(p0 << 16), u0 = __uint_as_float(p0 & 0xFFFF0000u);
-    const float g1 = __uint_as_float(p1 << 16), u1 = __uint_as_float(p1 & 0xFFFF0000u);
-    const uint32_t a = bf16x2_rne(g0 / (1.0f + expf(-g0)), g1 / (1.0f + expf(-g1)));
-    const uint32_t r = bf16x2_bits_rne(__uint_as_float(a << 16) * u0,
-                                       __uint_as_float(a & 0xFFFF0000u) * u1);
-    o0 = r & 0xFFFFu;
-    o1 = r >> 16;
-}
+// The projections' output value of one accumulator is bf16(flush(acc +
+// bias)), computed two values at a time with bf16x2_bits_rne (SwiGLU:
+// swiglu_bits2 in common.h).
 
 }  // namespace
 
@@ -262,6 +242,15 @@ hipError_t launch_linear_swiglu(const uint16_t* x, const uint16_t* w, const uint
                                 uint16_t* y, int64_t M, int64_t K, int64_t N2,
                                 hipStream_t stream) {
     if (N2 % 64) return hipErrorInvalidValue;
+    const int64_t r = linear_tail_rows(M, N2, K);
+    if (r > 0) {
+        const int64_t mm = M - r;
+        hipError_t e = launch_pair<kEpiSwiGLU>(x, w, bias, y, mm, K, N2,
+                                               PairArgs{nullptr, nullptr, 1, 0}, stream);
+        if (e != hipSuccess) return e;
+        return launch_linear_tail(x + mm * K, w, bias, nullptr, y + mm * (N2 / 2), r, K, N2 / 2,
+                                  NCM_OUT_BF16, true, stream);
+    }
     return launch_pair<kEpiSwiGLU>(x, w, bias, y, M, K, N2, PairArgs{nullptr, nullptr, 1, 0},
                                    stream);
 }
