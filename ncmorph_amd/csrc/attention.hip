@@ -142,7 +142,7 @@ __attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ vt, void* __restrict__ out, int64_t T, int64_t Tp, int group,
     int kv_heads, int64_t q_stride, int64_t kv_stride, int64_t out_stride, int64_t window,
-    float scale, SegArgs sa) {
+    float scale, SegArgs sa, int n_xb) {
     using L = AttnTile<HD, NWV>;
     constexpr int kBq = 32 * NWV;  // queries per workgroup
     __shared__ int seg_red[2 * NWV];
@@ -151,8 +151,18 @@ __attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int c = lane & 31, hl = lane >> 5;
-    const int64_t b = blockIdx.z;
-    const int h = blockIdx.y, kvh = h / group;
+    // Workgroup -> (sequence b, kv head, query block xb, head hg of the kv
+    // head's group), the kv head slowest but for the sequence and the group's
+    // heads fastest: with the XCD remap, each XCD walks a contiguous run of
+    // this order, so the K and V^T blocks it streams belong to few kv heads
+    // (one per XCD for 8 kv heads and one sequence) and the group's heads read
+    // the same blocks at about the same time, from the XCD's L2.
+    const int logical = xcd_remap((int)blockIdx.x, (int)gridDim.x);
+    const int hg = logical % group;
+    const int xb = (logical / group) % n_xb;
+    const int kvh = (logical / group / n_xb) % kv_heads;
+    const int64_t b = logical / group / n_xb / kv_heads;
+    const int h = kvh * group + hg;
 
     // K rows of this (sequence, kv head): keys >= T load as zero (out of the
     // resource's range). V^T rows: Tp keys each, zero past T.
@@ -217,8 +227,8 @@ __attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
     // (longest level) blocks first.
     const int nqb = (int)((T + kBq - 1) / kBq);
     for (int part = 0; part < 2; ++part) {
-    const int qbi = part == 0 ? nqb - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    if (part == 1 && (MASK == 1 || qbi == nqb - 1 - (int)blockIdx.x)) break;
+    const int qbi = part == 0 ? nqb - 1 - xb : xb;
+    if (part == 1 && (MASK == 1 || qbi == nqb - 1 - xb)) break;
     const int64_t q0 = (int64_t)qbi * kBq;
     const int64_t qw0 = q0 + 32 * wave;
     const int64_t qq = qw0 + c;  // the query of this lane's score column
@@ -393,14 +403,24 @@ __attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
         const char* kl = lds + cur * L::STAGE;
         if (wave_sees(key0)) {
             const bool full = block_full(key0);
+            // Both tiles' scores first: the second tile's MFMAs run while
+            // the first tile's softmax work issues.
+            f32x16_t accs[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) accs[t] = score_tile(kl, qf, t);
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                f32x16_t acc = score_tile(kl, qf, t);
+                f32x16_t& acc = accs[t];
                 if (!full) apply_mask(acc, key0, t);
                 float mb = -INFINITY;
 #pragma unroll
                 for (int i = 0; i < 16; ++i) mb = fmaxf(mb, acc[i]);
-                mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+                {
+                    // Max with the other half-wave's value (the same 32 keys'
+                    // other 16 rows): a VALU lane swap, no LDS round trip.
+                    const u32x2_t sw = swap32(__float_as_uint(mb));
+                    mb = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+                }
                 mb = POW2 ? rnd(mb) * scale : score(mb);
                 const float mn = fmaxf(m, mb);
                 if (mn != -INFINITY) {
@@ -419,7 +439,13 @@ __attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
         }
         cur ^= 1;
     }
-    const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+    float ltot;
+    {
+        // lsum plus the other half-wave's lsum (the same sum in both
+        // halves: the add commutes).
+        const u32x2_t sw = swap32(__float_as_uint(lsum));
+        ltot = __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+    }
     // A query with no allowed key (a prefix query whose prefix is all
     // padding) gets zero probabilities, hence a zero context, as the
     // reference (root.zig:563-565).
@@ -448,9 +474,12 @@ __attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
         const char* vl = kl + L::K_BYTES;
         if (wave_sees(key0)) {
             const bool full = block_full(key0);
+            f32x16_t accs[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) accs[t] = score_tile(kl, qf, t);
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
-                f32x16_t acc = score_tile(kl, qf, t);
+                f32x16_t& acc = accs[t];
                 if (!full) apply_mask(acc, key0, t);
                 // p = round_bf16(e / sum), packed two per register.
                 to_scores(acc);
@@ -532,17 +561,18 @@ hipError_t launch_attn_hd(const uint16_t* q, const uint16_t* k, const uint16_t* 
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     const int64_t nqb = (T + 32 * NWV - 1) / (32 * NWV);
-    const dim3 grid((unsigned)(MASK == 0 ? (nqb + 1) / 2 : nqb), (unsigned)hq, (unsigned)batch);
+    const int n_xb = (int)(MASK == 0 ? (nqb + 1) / 2 : nqb);
+    const dim3 grid((unsigned)((int64_t)n_xb * hq * batch));
     const float scale = 1.0f / sqrtf((float)HD);
     const int group = hq / hkv;
     if (out_mode == NCM_OUT_BF16)
         hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16, MASK, NWV>), grid,
                            dim3(64 * NWV), 0, stream, q, k, vt, out, T, Tp, group, hkv, q_stride,
-                           kv_stride, out_stride, window, scale, sa);
+                           kv_stride, out_stride, window, scale, sa, n_xb);
     else
         hipLaunchKernelGGL((attention_bf16_kernel<HD, NCM_OUT_BF16_F32, MASK, NWV>), grid,
                            dim3(64 * NWV), 0, stream, q, k, vt, out, T, Tp, group, hkv, q_stride,
-                           kv_stride, out_stride, window, scale, sa);
+                           kv_stride, out_stride, window, scale, sa, n_xb);
     return hipGetLastError();
 }
 
