@@ -95,8 +95,24 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
     if (row >= rows) return;
     const float* xr = x + row * n;
     if (STAGE) {
+        // Eight 16-byte loads per lane in flight, then their LDS writes (a
+        // loop of load, wait, write would wait out the memory latency once per
+        // kilobyte of the row). Lanes past the row load its last chunk again
+        // and write nothing.
         float* sr = stage + (threadIdx.x >> 6) * n;
-        for (int64_t i = 4 * lane; i < n; i += 256) *(f32x4_t*)(sr + i) = *(const f32x4_t*)(xr + i);
+        for (int64_t base = 4 * lane; base < n; base += 8 * 256) {
+            f32x4_t t[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int64_t i = base + 256 * j;
+                t[j] = *(const f32x4_t*)(xr + (i < n ? i : n - 4));
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int64_t i = base + 256 * j;
+                if (i < n) *(f32x4_t*)(sr + i) = t[j];
+            }
+        }
         asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // this wave's row is in LDS
         xr = sr;
     }
@@ -126,9 +142,7 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
         // Four elements per lane and step: one 8-byte (bf16) or 16-byte
         // (bf16 values as fp32) store when y is aligned for it.
         const bool yvec = ((uintptr_t)y & (OUT_MODE == NCM_OUT_BF16 ? 7 : 15)) == 0;
-        for (int64_t i = 4 * lane; i < n; i += 256) {
-            const f32x4_t v = *(const f32x4_t*)(xr + i);
-            const f32x4_t wv = *(const f32x4_t*)(weight + i);
+        auto emit = [&](int64_t i, const f32x4_t v, const f32x4_t wv) {
             // The same roundings two elements per v_cvt_pk_bf16_f32; the NaN
             // rule on the stored one (a NaN stays a NaN through the product).
             uint32_t bits[4];
@@ -161,6 +175,21 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
                 for (int e = 0; e < 4; ++e) o[e] = __uint_as_float(bits[e] << 16);
                 *(f32x4_t*)((float*)y + row * n + i) = o;
             }
+        };
+        // Four steps' loads (x from LDS or global, the weight from global)
+        // issued together; lanes past the row load its last chunk and store
+        // nothing.
+        for (int64_t base = 4 * lane; base < n; base += 4 * 256) {
+            f32x4_t vq[4], wq[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t i = base + 256 * j < n ? base + 256 * j : n - 4;
+                vq[j] = *(const f32x4_t*)(xr + i);
+                wq[j] = *(const f32x4_t*)(weight + i);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (base + 256 * j < n) emit(base + 256 * j, vq[j], wq[j]);
         }
     } else {
         for (int64_t i = lane; i < n; i += 64) out1(i, xr[i], weight[i]);

@@ -11,9 +11,10 @@
 // features, i.e. their 16 gate and 16 up weight rows) of all R rows over the
 // whole K; its 8 wavefronts take one eighth of K each, in 128-element steps
 // of v_mfma_f32_16x16x32_bf16 (A = x rows, B = weight rows, operands loaded
-// straight from global memory, lane group g holding k = 32 g .. 32 g + 31 of
-// a step, MFMA i using 8 i .. 8 i + 7 of them), and the eight partial sums
-// are added in wavefront order through LDS. The epilogue is the tile
+// straight from global memory: MFMA i of a step covers k = 32 i .. 32 i + 31,
+// lane group g holding 32 i + 8 g .. + 7, so each load instruction reads 64
+// contiguous bytes of 16 rows), and the eight partial sums are added in
+// wavefront order through LDS. The epilogue is the tile
 // kernels' own: bias, bf16 rounding, residual add (linear_kernel) or
 // swiglu_bits2 (linear_pair_kernel). Every output is the same function of
 // its row of x and its weight row(s) wherever the row sits in the batch, but
@@ -60,7 +61,7 @@ __global__ __launch_bounds__(64 * kTailWaves) void linear_tail_kernel(
     // Rows >= R lie past the resource: they load as zero.
     const __amdgpu_buffer_rsrc_t rsx = make_rsrc(x, (uint32_t)(R * K * 2));
     const int64_t kq = K / kTailWaves;
-    const uint32_t kb0 = (uint32_t)((wave * kq + 32 * grp) * 2);
+    const uint32_t kb0 = (uint32_t)((wave * kq + 8 * grp) * 2);
     const uint32_t goff = (uint32_t)(r16 * K * 2) + kb0;
     const uint32_t uoff = (uint32_t)((32 + r16) * K * 2) + kb0;
     uint32_t aoff[RB];
@@ -75,10 +76,10 @@ __global__ __launch_bounds__(64 * kTailWaves) void linear_tail_kernel(
         const uint32_t kb = step < steps ? (uint32_t)step * (kTailStepK * 2) : kOobOffset;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            b.g[i] = buffer_load_b128(rsw, goff + kb + 16 * i);
-            if (SWIGLU) b.u[i] = buffer_load_b128(rsw, uoff + kb + 16 * i);
+            b.g[i] = buffer_load_b128(rsw, goff + kb + 64 * i);
+            if (SWIGLU) b.u[i] = buffer_load_b128(rsw, uoff + kb + 64 * i);
 #pragma unroll
-            for (int rb = 0; rb < RB; ++rb) b.a[rb][i] = buffer_load_b128(rsx, aoff[rb] + kb + 16 * i);
+            for (int rb = 0; rb < RB; ++rb) b.a[rb][i] = buffer_load_b128(rsx, aoff[rb] + kb + 64 * i);
         }
     };
     f32x4_t acc[NACC][RB];
