@@ -304,9 +304,65 @@ __global__ __launch_bounds__(256) void rope_rotate_kernel(uint16_t* __restrict__
     e[half] = (uint16_t)bf16_bits_rne(left2 + right2);
 }
 
+// The same rotation, four consecutive pairs per thread (8-byte element and
+// 16-byte table loads, 32-bit index arithmetic): hd % 8 == 0, row_stride % 4
+// == 0, x 8-byte and the tables 16-byte aligned, rows * heads * hd / 8 <
+// 2^31.
+__global__ __launch_bounds__(256) void rope_rotate4_kernel(uint16_t* __restrict__ x, int rows,
+                                                           int64_t row_stride, int heads, int hd,
+                                                           int seq_len,
+                                                           const float* __restrict__ cosine,
+                                                           const float* __restrict__ sine) {
+    const int half = hd >> 1, groups = half >> 2;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= rows * heads * groups) return;
+    const int i = 4 * (idx % groups);
+    const int rh = idx / groups;
+    const int h = rh % heads;
+    const int r = rh / heads;
+    const int pos = r % seq_len;
+    auto rb = [](float v) { return __uint_as_float(bf16_bits_rne(v) << 16); };
+    uint16_t* e = x + (int64_t)r * row_stride + (int64_t)h * hd + i;
+    const u32x2_t fa = *(const u32x2_t*)e;
+    const u32x2_t fb = *(const u32x2_t*)(e + half);
+    const float* ct = cosine + (int64_t)pos * hd + i;
+    const float* st = sine + (int64_t)pos * hd + i;
+    const f32x4_t c1 = *(const f32x4_t*)ct, s1 = *(const f32x4_t*)st;
+    const f32x4_t c2 = *(const f32x4_t*)(ct + half), s2 = *(const f32x4_t*)(st + half);
+    uint32_t o1[4], o2[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t wa = fa[j >> 1], wb = fb[j >> 1];
+        const float first = __uint_as_float((j & 1) ? (wa & 0xFFFF0000u) : (wa << 16));
+        const float second = __uint_as_float((j & 1) ? (wb & 0xFFFF0000u) : (wb << 16));
+        const float left = rb(first * rb(c1[j]));
+        const float right = rb(-second * rb(s1[j]));
+        const float right2 = rb(first * rb(s2[j]));
+        const float left2 = rb(second * rb(c2[j]));
+        o1[j] = bf16_bits_rne(left + right);
+        o2[j] = bf16_bits_rne(left2 + right2);
+    }
+    u32x2_t w1, w2;
+    w1[0] = o1[0] | (o1[1] << 16);
+    w1[1] = o1[2] | (o1[3] << 16);
+    w2[0] = o2[0] | (o2[1] << 16);
+    w2[1] = o2[2] | (o2[3] << 16);
+    *(u32x2_t*)e = w1;
+    *(u32x2_t*)(e + half) = w2;
+}
+
 hipError_t launch_rope_rotate(uint16_t* x, int64_t rows, int64_t row_stride, int heads, int hd,
                               int64_t seq_len, const float* cosine, const float* sine,
                               hipStream_t stream) {
+    const int64_t n4 = rows * heads * (hd / 8);
+    if (hd % 8 == 0 && row_stride % 4 == 0 && ((uintptr_t)x & 7) == 0 &&
+        ((uintptr_t)cosine & 15) == 0 && ((uintptr_t)sine & 15) == 0 && n4 < ((int64_t)1 << 31) &&
+        seq_len < ((int64_t)1 << 31)) {
+        hipLaunchKernelGGL(rope_rotate4_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
+                           stream, x, (int)rows, row_stride, heads, hd, (int)seq_len, cosine,
+                           sine);
+        return hipGetLastError();
+    }
     const int64_t n = rows * heads * (hd / 2);
     hipLaunchKernelGGL(rope_rotate_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream,
                        x, rows, row_stride, heads, hd, seq_len, cosine, sine);

@@ -42,8 +42,10 @@ def _tables(oracle, positions, hd):
     return oracle.rope_tables(inv, positions)
 
 
-@pytest.mark.parametrize("batch,seq,hq,hkv,hd", [(2, 1024, 32, 8, 64), (1, 37, 2, 1, 128)])
+@pytest.mark.parametrize("batch,seq,hq,hkv,hd", [(2, 1024, 32, 8, 64), (1, 37, 2, 1, 128),
+                                                 (1, 19, 3, 1, 12)])
 def test_rope_rotate_bit_identical(ncm, oracle, cuda, batch, seq, hq, hkv, hd):
+    """Four pairs per thread when hd % 8 == 0 (64, 128), one otherwise (12)."""
     import torch
     from ncmorph_amd import kernels
 
