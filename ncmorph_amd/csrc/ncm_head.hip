@@ -173,6 +173,23 @@ static hipError_t launch_head_t(HeadArgs& a, hipStream_t st) {
     return hipGetLastError();
 }
 
+// Levels [l0, l1) of a as a launch of their own (rows keep their places in
+// y; codebooks, norms, biases and scales from level l0 on).
+static HeadArgs sub_levels(const HeadArgs& a, int l0, int l1) {
+    HeadArgs b = a;
+    b.levels = l1 - l0;
+    b.cb = a.cb + (int64_t)l0 * a.v * a.d;
+    b.csq = a.csq + (int64_t)l0 * a.v;
+    b.bias = a.bias ? a.bias + (int64_t)l0 * a.v : nullptr;
+    b.scale = a.scale + l0;
+    for (int l = 0; l < b.levels; ++l) {
+        b.row0[l] = a.row0[l0 + l];
+        b.rows[l] = a.rows[l0 + l];
+        b.log_inv_t[l] = a.log_inv_t[l0 + l];
+    }
+    return b;
+}
+
 hipError_t launch_tied_head(const uint16_t* z, const uint16_t* cb, const float* csq,
                             const float* bias, const float* log_inv_t, const int64_t* rows,
                             int levels, float* scale, float* y, int64_t d, int64_t v,
@@ -200,7 +217,27 @@ hipError_t launch_tied_head(const uint16_t* z, const uint16_t* cb, const float* 
     using H1 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
     using H2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
     const int64_t cus = 256;
-    if (tiles_big * 4 >= cus * 3) return launch_head_t<H0>(a, st);
+    if (tiles_big * 4 >= cus * 3) {
+        // The leading levels that do not fill a 256-row tile (the NCM step's
+        // 32 ... 128-position levels) go to a launch of their own on 128 x
+        // 128 tiles when, without their tiles, the 256 x 256 tiles of the
+        // rest need fewer rounds of the CUs: the small launch then takes a
+        // fraction of a round instead of a whole one.
+        int split = 0;
+        int64_t rest = tiles_big, small = 0;
+        while (split < levels - 1 && rows[split] < 256) {
+            rest -= ((rows[split] + 255) / 256) * ((v + 255) / 256);
+            small += ((rows[split] + 127) / 128) * ((v + 127) / 128);
+            ++split;
+        }
+        if (split > 0 && small <= cus && (rest + cus - 1) / cus < (tiles_big + cus - 1) / cus) {
+            HeadArgs lo = sub_levels(a, 0, split), hi = sub_levels(a, split, levels);
+            hipError_t e2 = launch_head_t<H1>(lo, st);
+            if (e2 != hipSuccess) return e2;
+            return launch_head_t<H0>(hi, st);
+        }
+        return launch_head_t<H0>(a, st);
+    }
     if (tiles_small <= cus) return launch_head_t<H1>(a, st);
     return launch_head_t<H2>(a, st);
 }

@@ -112,3 +112,45 @@ def test_tied_head_levels_one_launch(ncm, oracle, cuda):
             err = np.abs(got[off:off + n].astype(np.float64) - ref)
             assert np.all(err <= bound), (l, float(np.max(err / bound)))
         off += n
+
+
+def test_tied_head_levels_split_launch(ncm, oracle, cuda):
+    """The NCM layout's growing levels (32 ... 1024 rows, 8192 codes): the
+    levels below 256 rows run as a launch of 128 x 128 tiles of their own
+    (their 256 x 256 tiles would add a round), the rest on 256 x 256 tiles;
+    sampled rows of every level against the oracle's bound, and the argmax of
+    rows with a clear top-2 gap against the exact nearest code."""
+    import torch
+    from ncmorph_amd import kernels, vq
+
+    rng = np.random.default_rng(321)
+    d, v = 512, 8192
+    level_rows = [32, 64, 128, 256, 512, 1024]
+    lit = [0.1 * l for l in range(len(level_rows))]
+    L = len(level_rows)
+    zb = synth.bf16_bits(rng.standard_normal((sum(level_rows), d)).astype(np.float32))
+    eb = synth.bf16_bits((rng.standard_normal((L, v, d)) / np.sqrt(d)).astype(np.float32))
+    zd, ed = _bf16_dev(zb, cuda), _bf16_dev(eb, cuda)
+    csq = vq.prepare(ed)
+    got = kernels.tied_head_logits_levels(zd, ed, csq, level_rows, lit)
+    torch.cuda.synchronize()
+    got = got.cpu().numpy()
+    off = 0
+    for l, n in enumerate(level_rows):
+        sel = off + np.sort(rng.choice(n, size=min(n, 24), replace=False))
+        z = synth.bf16_to_f32(zb[sel])
+        E = synth.bf16_to_f32(eb[l])
+        ref, mag = oracle.tied_head_logits_f64(z, E, lit[l], None)
+        esq = np.sum(E.astype(np.float64) ** 2, axis=1)
+        scale = np.exp(lit[l]) / esq.mean()
+        t = np.abs(ref) / scale
+        bound = (scale * ((d + 4) * 2.0**-24 * mag + d * 2.0**-24 * esq[None, :] + 2.0**-22 * t)
+                 + 2.0**-21 * np.abs(ref) + 1e-30)
+        err = np.abs(got[sel].astype(np.float64) - ref)
+        assert np.all(err <= bound), (l, float(np.max(err / bound)))
+        r = vq.encode(zd[off:off + n].float().view(1, n, d), ed[l].view(1, v, d), (1,),
+                      csq=csq[l].view(1, v), want_gap=True)
+        codes = r["codes"].cpu().numpy()[0]
+        clear = r["gap"].cpu().numpy()[0] > 1e-4
+        assert np.array_equal(np.argmax(got[off:off + n], axis=1)[clear], codes[clear]), l
+        off += n
