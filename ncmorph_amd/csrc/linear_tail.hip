@@ -223,8 +223,10 @@ hipError_t launch_tail_rb(const uint16_t* x, const uint16_t* w, const uint16_t* 
 
 int64_t linear_tail_rows(int64_t M, int64_t N, int64_t K) {
     const int64_t r = M % 256;
+    // K <= 2^22: every buffer offset the kernel forms, the out-of-range one
+    // included, stays far below 2^32.
     if (r == 0 || r > kTailMaxRows || M < 256 || K % kTailKMultiple != 0 || N % 16 != 0 ||
-        K > (int64_t)1 << 24)
+        K > (int64_t)1 << 22)
         return 0;
     const int64_t m_main = M - r;
     if (linear_tile_config(M, N, K, -1) != 0 || linear_tile_config(m_main, N, K, -1) != 0)
@@ -239,7 +241,8 @@ int64_t linear_tail_rows(int64_t M, int64_t N, int64_t K) {
 hipError_t launch_linear_tail(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
                               const float* residual, void* y, int64_t R, int64_t K, int64_t N,
                               int out_mode, bool swiglu, hipStream_t st) {
-    if (R <= 0 || R > kTailMaxRows || K % kTailKMultiple != 0 || N % 16 != 0)
+    if (R <= 0 || R > kTailMaxRows || K % kTailKMultiple != 0 || N % 16 != 0 ||
+        K > (int64_t)1 << 22)
         return hipErrorInvalidValue;
     if (R <= 16) return launch_tail_rb<1>(x, w, bias, residual, y, R, K, N, out_mode, swiglu, st);
     if (R <= 32) return launch_tail_rb<2>(x, w, bias, residual, y, R, K, N, out_mode, swiglu, st);
