@@ -117,3 +117,44 @@ def test_tail_epilogues_bit_for_bit(ncm, cuda):
     ref = kernels.silu_mul(gate, up, out_mode="bf16")
     torch.cuda.synchronize()
     assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
+
+
+def test_tail_special_values(ncm, cuda):
+    """NaN, +-inf and overflowing projections in the tail rows: the bf16 and
+    residual epilogues against the tail's own fp32 output, and the fused
+    SwiGLU tail against the plain tail + SiLU x up (every NaN -> 0x7FC0)."""
+    import torch
+    from ncmorph_amd import kernels
+
+    m, n, k = 2048 + 16, 8192, 2048
+    rng = np.random.default_rng(57)
+    xf = rng.standard_normal((m, k)).astype(np.float32)
+    xf[2049, 3] = np.nan
+    xf[2050, 5] = np.inf
+    xf[2051, 0] = -np.inf
+    xf[2052, :] = np.float32(3e38)
+    xb = synth.bf16_bits(xf)
+    wb = synth.bf16_bits((rng.standard_normal((n, k)) * 0.02).astype(np.float32))
+    x, w = _dev(xb, cuda), _dev(wb, cuda)
+    y32 = kernels.linear_bf16(x, w)
+    y16 = kernels.linear_bf16(x, w, out_mode="bf16")
+    res = torch.from_numpy(rng.standard_normal((m, n)).astype(np.float32)).to(cuda)
+    yresb = kernels.linear_bf16_residual(x, w, res, out_mode="bf16_f32")
+    fused = kernels.linear_bf16_swiglu(x, w)
+    proj = kernels.linear_bf16(x, w, out_mode="bf16_f32")
+    torch.cuda.synchronize()
+    y32n = y32.cpu().numpy()
+    tail = y32n[2048:]
+    assert np.isnan(tail[1]).all() and np.isinf(tail[2]).any() and np.isinf(tail[3]).any()
+    assert np.array_equal(y16.cpu().numpy().view(np.uint16), synth.bf16_bits(y32n))
+    r = res.cpu().numpy()
+    want = synth.bf16_to_f32(synth.bf16_bits(r + synth.bf16_to_f32(synth.bf16_bits(y32n))))
+    got = yresb.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    cols = np.arange(n).reshape(-1, 64)
+    gate = proj[:, torch.from_numpy(cols[:, :32].ravel()).to(cuda)].contiguous()
+    up = proj[:, torch.from_numpy(cols[:, 32:].ravel()).to(cuda)].contiguous()
+    ref = kernels.silu_mul(gate, up, out_mode="bf16")
+    torch.cuda.synchronize()
+    assert torch.isnan(fused[2049].float()).any()
+    assert torch.equal(fused.view(torch.int16), ref.view(torch.int16))
