@@ -5,6 +5,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <condition_variable>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -26,6 +27,11 @@ struct ncm_ctx {
     void* ws = nullptr;  // grow-only device workspace
     size_t ws_bytes = 0;
     hipEvent_t handoff = nullptr;  // orders a new stream after the previous one
+    // Pinned staging of host -> device uploads (two buffers of stage_bytes,
+    // each with the event of its last copy), kept until ncm_destroy.
+    void* stage[2] = {nullptr, nullptr};
+    hipEvent_t stage_done[2] = {nullptr, nullptr};
+    size_t stage_bytes = 0;
 };
 
 namespace {
@@ -86,56 +92,118 @@ int ncm_ctx_device(ncm_ctx_t* ctx) { return ctx->device; }
 
 void ncm_set_error_detail(const std::string& what) { g_last_error = what; }
 
+// memcpy of one buffer by a pool of threads (one thread moves ~10-15 GB/s
+// from the page cache; the host link takes several times that): the caller
+// copies the first slice, the workers the others.
+class CopyPool {
+  public:
+    explicit CopyPool(int threads) : n_(threads < 1 ? 1 : threads) {
+        for (int t = 1; t < n_; ++t) th_.emplace_back([this, t] { work(t); });
+    }
+    ~CopyPool() {
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            stop_ = true;
+        }
+        go_.notify_all();
+        for (auto& t : th_) t.join();
+    }
+    void copy(char* to, const char* from, size_t len) {
+        const size_t slice = (len + n_ - 1) / n_;
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            to_ = to; from_ = from; len_ = len; slice_ = slice;
+            pending_ = n_ - 1;
+            ++gen_;
+        }
+        go_.notify_all();
+        std::memcpy(to, from, std::min(len, slice));
+        std::unique_lock<std::mutex> lk(mu_);
+        done_.wait(lk, [this] { return pending_ == 0; });
+    }
+
+  private:
+    void work(int t) {
+        uint64_t seen = 0;
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            go_.wait(lk, [&] { return stop_ || gen_ != seen; });
+            if (stop_) return;
+            seen = gen_;
+            char* to = to_;
+            const char* from = from_;
+            const size_t a = (size_t)t * slice_, len = len_;
+            lk.unlock();
+            if (a < len) std::memcpy(to + a, from + a, std::min(len, a + slice_) - a);
+            lk.lock();
+            if (--pending_ == 0) done_.notify_one();
+        }
+    }
+    int n_;
+    std::vector<std::thread> th_;
+    std::mutex mu_;
+    std::condition_variable go_, done_;
+    char* to_ = nullptr;
+    const char* from_ = nullptr;
+    size_t len_ = 0, slice_ = 0;
+    uint64_t gen_ = 0;
+    int pending_ = 0;
+    bool stop_ = false;
+};
+
 int ncm_upload_host_bytes(ncm_ctx_t* ctx, const void* src, void* dst, size_t n) {
     int rc = ctx_bind(ctx);
     if (rc) return rc;
-    // Two pinned staging buffers, refilled from the (mapped, pageable) source
-    // while the previous chunk's copy runs.
+    // The context's two pinned staging buffers, refilled from the (mapped,
+    // pageable) source while the other one's copy runs; allocated when an
+    // upload needs more than they hold (at least doubling, at most 64 MiB
+    // each) and kept, since pinning memory costs milliseconds per call.
     constexpr size_t kChunk = 64u << 20;
-    constexpr int kCopyThreads = 8;
-    void* stage[2] = {nullptr, nullptr};
-    hipEvent_t done[2] = {nullptr, nullptr};
-    auto cleanup = [&]() {
-        for (int b = 0; b < 2; ++b) {
-            if (done[b]) { (void)hipEventSynchronize(done[b]); (void)hipEventDestroy(done[b]); }
-            if (stage[b]) (void)hipHostFree(stage[b]);
-        }
-    };
     const size_t chunk = n < kChunk ? n : kChunk;
-    for (int b = 0; b < 2; ++b) {
-        if (hipHostMalloc(&stage[b], chunk, hipHostMallocDefault) != hipSuccess ||
-            hipEventCreateWithFlags(&done[b], hipEventDisableTiming) != hipSuccess) {
-            (void)hipGetLastError();
-            cleanup();
-            g_last_error = "pinned staging allocation failed";
-            return NCM_E_NOMEM;
+    if (ctx->stage_bytes < chunk) {
+        const size_t want = std::max(chunk, std::min(kChunk, 2 * ctx->stage_bytes));
+        for (int b = 0; b < 2; ++b) {
+            if (ctx->stage_done[b]) (void)hipEventSynchronize(ctx->stage_done[b]);
+            if (ctx->stage[b]) (void)hipHostFree(ctx->stage[b]);
+            ctx->stage[b] = nullptr;
         }
+        ctx->stage_bytes = 0;
+        for (int b = 0; b < 2; ++b) {
+            if (hipHostMalloc(&ctx->stage[b], want, hipHostMallocDefault) != hipSuccess) {
+                (void)hipGetLastError();
+                for (int c = 0; c < 2; ++c) {
+                    if (ctx->stage[c]) (void)hipHostFree(ctx->stage[c]);
+                    ctx->stage[c] = nullptr;
+                }
+                g_last_error = "pinned staging allocation failed";
+                return NCM_E_NOMEM;
+            }
+        }
+        ctx->stage_bytes = want;
     }
+    for (int b = 0; b < 2; ++b)
+        if (!ctx->stage_done[b])
+            NCM_HIP(hipEventCreateWithFlags(&ctx->stage_done[b], hipEventDisableTiming));
+    // At most 16 copy threads (the host's share for one GPU), fewer on a
+    // smaller host, one for small uploads.
+    const unsigned hw = std::thread::hardware_concurrency();
+    const int threads = n < (4u << 20) ? 1 : (int)std::min<unsigned>(16u, hw ? hw : 1u);
+    CopyPool pool(threads);
     size_t off = 0;
     for (int b = 0; off < n; b ^= 1) {
         const size_t len = n - off < chunk ? n - off : chunk;
-        hipError_t e = hipEventSynchronize(done[b]);  // the buffer's previous copy is done
+        hipError_t e = hipEventSynchronize(ctx->stage_done[b]);  // the buffer's last copy is done
         if (e == hipSuccess) {
-            // Page-cache -> pinned copy in parallel slices (one thread moves
-            // ~10-15 GB/s; the host link takes several times that).
-            const char* from = (const char*)src + off;
-            char* to = (char*)stage[b];
-            const size_t slice = (len + kCopyThreads - 1) / kCopyThreads;
-            std::vector<std::thread> pool;
-            for (int t = 1; t < kCopyThreads && t * slice < len; ++t)
-                pool.emplace_back([=] {
-                    const size_t a = t * slice, z = std::min(len, a + slice);
-                    std::memcpy(to + a, from + a, z - a);
-                });
-            std::memcpy(to, from, std::min(len, slice));
-            for (auto& th : pool) th.join();
-            e = hipMemcpyAsync((char*)dst + off, stage[b], len, hipMemcpyHostToDevice, ctx->stream);
+            pool.copy((char*)ctx->stage[b], (const char*)src + off, len);
+            e = hipMemcpyAsync((char*)dst + off, ctx->stage[b], len, hipMemcpyHostToDevice,
+                               ctx->stream);
         }
-        if (e == hipSuccess) e = hipEventRecord(done[b], ctx->stream);
-        if (e != hipSuccess) { cleanup(); return fail_hip(e, "upload"); }
+        if (e == hipSuccess) e = hipEventRecord(ctx->stage_done[b], ctx->stream);
+        if (e != hipSuccess) return fail_hip(e, "upload");
         off += len;
     }
-    cleanup();  // waits for the last copies: the staging memory is freed
+    // The device holds the bytes when the call returns.
+    for (int b = 0; b < 2; ++b) NCM_HIP(hipEventSynchronize(ctx->stage_done[b]));
     return NCM_OK;
 }
 
@@ -198,6 +266,13 @@ int ncm_destroy(ncm_ctx_t* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->handoff) (void)hipEventDestroy(ctx->handoff);
+    for (int b = 0; b < 2; ++b) {
+        if (ctx->stage_done[b]) {
+            (void)hipEventSynchronize(ctx->stage_done[b]);
+            (void)hipEventDestroy(ctx->stage_done[b]);
+        }
+        if (ctx->stage[b]) (void)hipHostFree(ctx->stage[b]);
+    }
     if (ctx->own_stream) (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
     return NCM_OK;

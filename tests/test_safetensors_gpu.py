@@ -41,6 +41,26 @@ def test_upload_bytes_identical(ncm, cuda, tmp_path):
         assert f.find("empty").shape == (0, 4)
 
 
+def test_upload_staging_reuse(ncm, cuda, tmp_path):
+    """One context's pinned staging grows and is reused: uploads of growing,
+    shrinking and odd sizes in a row (one and several copy threads, one and
+    several chunks) all arrive bytes identical."""
+    import torch
+
+    rng = np.random.default_rng(2)
+    sizes = [1000, 3 << 20, (5 << 20) + 3, 70 << 20, 17, (130 << 20) + 1]
+    arrays = {f"t{i}": rng.integers(0, 256, n, dtype=np.uint8) for i, n in enumerate(sizes)}
+    p = str(tmp_path / "w.safetensors")
+    st.write_file(p, {k: ("U8", (a.size,), a.tobytes()) for k, a in arrays.items()})
+    with st.SafetensorsFile(p) as f:
+        for rep in range(2):
+            for k, a in arrays.items():
+                out = torch.empty(a.size, dtype=torch.uint8, device=cuda)
+                f.upload(k, out)
+                torch.cuda.synchronize()
+                assert np.array_equal(out.cpu().numpy(), a), (rep, k)
+
+
 def _write_checkpoint(path, embed, layers, fnorm, hq, hkv, hd, shards=1, f32_keys=(),
                       f16_keys=(), lm_head=None):
     tensors = {"model.embed_tokens.weight": embed}
