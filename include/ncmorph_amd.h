@@ -615,8 +615,10 @@ int ncm_st_find(const ncm_st_file_t* f, const char* name, ncm_st_tensor_t* out);
 const char* ncm_st_dtype_name(int dtype);
 int ncm_st_dtype_bits(int dtype);
 /* Copies a tensor's stored bytes to device memory (dst_bytes must equal its
- * size), stream-ordered on the context's stream through pinned staging
- * buffers: bf16 weights reach the device as stored, without the loader's
+ * size) on the context's stream through the context's two pinned staging
+ * buffers (up to 64 MiB each, allocated by the first upload that needs them
+ * and kept until ncm_destroy); the bytes are on the device when the call
+ * returns. bf16 weights reach the device as stored, without the loader's
  * widen to f32 (src/loader.zig:339-342). The file must come from
  * ncm_st_open. */
 int ncm_st_upload(ncm_ctx_t* ctx, const ncm_st_file_t* f, const char* name, void* dst,
