@@ -14,9 +14,9 @@ namespace ncm {
 // vector sum, lanes into the scalar sum) run in the reference's order on
 // values gathered by shuffles. Every product and sum is a separate fp32 op
 // (built with -ffp-contract=off), as in the reference.
-// STAGE: the row is first copied to LDS with 16-byte loads by all 64 lanes
-// (n % 4 == 0, n <= kRmsStageMax), and both passes read it from there.
-constexpr int64_t kRmsStageMax = 8192;
+// Both passes read the row from global memory (the second mostly from the
+// L2): staging it in LDS first measured slower at widths 2048-8192, since the
+// 16 KB-per-row stages held the kernel to two workgroups per CU.
 
 // The pinned sum of squares of one row (root.zig:152-227) by one
 // wavefront: lane c < 32 runs chain (r = c / 8, l = c % 8) with its four
@@ -84,38 +84,15 @@ __device__ __forceinline__ float rms_sum_squares(const float* xr, int64_t n, int
     return sum;
 }
 
-template <int OUT_MODE, bool STAGE>
+template <int OUT_MODE>
 __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restrict__ x,
                                                             const float* __restrict__ weight,
                                                             void* __restrict__ y, int64_t rows,
                                                             int64_t n, float epsilon) {
-    extern __shared__ __attribute__((aligned(16))) float stage[];
     const int lane = threadIdx.x & 63;
     const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float* xr = x + row * n;
-    if (STAGE) {
-        // Eight 16-byte loads per lane in flight, then their LDS writes (a
-        // loop of load, wait, write would wait out the memory latency once per
-        // kilobyte of the row). Lanes past the row load its last chunk again
-        // and write nothing.
-        float* sr = stage + (threadIdx.x >> 6) * n;
-        for (int64_t base = 4 * lane; base < n; base += 8 * 256) {
-            f32x4_t t[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int64_t i = base + 256 * j;
-                t[j] = *(const f32x4_t*)(xr + (i < n ? i : n - 4));
-            }
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int64_t i = base + 256 * j;
-                if (i < n) *(f32x4_t*)(sr + i) = t[j];
-            }
-        }
-        asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");  // this wave's row is in LDS
-        xr = sr;
-    }
     const float sum = rms_sum_squares(xr, n, lane);
     const float mean = sum / (float)n;
     const float inv = 1.0f / sqrtf(mean + epsilon);
@@ -437,37 +414,21 @@ hipError_t launch_bias_round(void* y, const float* bias, int64_t rows, int64_t n
     return hipGetLastError();
 }
 
-template <int OUT_MODE, bool STAGE>
+template <int OUT_MODE>
 static hipError_t launch_rms_t(const float* x, const float* weight, void* y, int64_t rows,
                                int64_t n, float epsilon, hipStream_t stream) {
-    auto kern = rms_norm_rows_kernel<OUT_MODE, STAGE>;
-    const size_t lds = STAGE ? (size_t)4 * n * sizeof(float) : 0;
-    if (STAGE && lds > 64 * 1024) {
-        static bool attr_set = false;
-        if (!attr_set) {
-            hipError_t e = hipFuncSetAttribute((const void*)kern,
-                                               hipFuncAttributeMaxDynamicSharedMemorySize,
-                                               (int)(4 * kRmsStageMax * sizeof(float)));
-            if (e != hipSuccess) return e;
-            attr_set = true;
-        }
-    }
-    hipLaunchKernelGGL(kern, dim3((unsigned)((rows + 3) / 4)), dim3(256), lds, stream, x, weight,
-                       y, rows, n, epsilon);
+    hipLaunchKernelGGL(rms_norm_rows_kernel<OUT_MODE>, dim3((unsigned)((rows + 3) / 4)),
+                       dim3(256), 0, stream, x, weight, y, rows, n, epsilon);
     return hipGetLastError();
 }
 
 hipError_t launch_rms_norm_rows(const float* x, const float* weight, void* y, int64_t rows,
                                 int64_t n, float epsilon, int out_mode, hipStream_t stream) {
-    const bool stage = n % 4 == 0 && n <= kRmsStageMax;
     if (out_mode == NCM_OUT_F32)
-        return stage ? launch_rms_t<NCM_OUT_F32, true>(x, weight, y, rows, n, epsilon, stream)
-                     : launch_rms_t<NCM_OUT_F32, false>(x, weight, y, rows, n, epsilon, stream);
+        return launch_rms_t<NCM_OUT_F32>(x, weight, y, rows, n, epsilon, stream);
     if (out_mode == NCM_OUT_BF16)
-        return stage ? launch_rms_t<NCM_OUT_BF16, true>(x, weight, y, rows, n, epsilon, stream)
-                     : launch_rms_t<NCM_OUT_BF16, false>(x, weight, y, rows, n, epsilon, stream);
-    return stage ? launch_rms_t<NCM_OUT_BF16_F32, true>(x, weight, y, rows, n, epsilon, stream)
-                 : launch_rms_t<NCM_OUT_BF16_F32, false>(x, weight, y, rows, n, epsilon, stream);
+        return launch_rms_t<NCM_OUT_BF16>(x, weight, y, rows, n, epsilon, stream);
+    return launch_rms_t<NCM_OUT_BF16_F32>(x, weight, y, rows, n, epsilon, stream);
 }
 
 hipError_t launch_silu_mul(const float* gate, const float* up, void* y, int64_t n, int out_mode,

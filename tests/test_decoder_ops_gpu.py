@@ -109,8 +109,8 @@ def _same_bits_or_both_nan(a, b):
 def test_rms_norm_rows_special_values(ncm, oracle, cuda, width):
     """Rows whose rounding inputs are subnormal (tiny x, tiny weights), and
     rows holding a NaN, an infinity or both signs of infinity, bit for bit
-    against the oracle (NaN rows: NaN where the oracle has NaN). Covers the
-    staged (width <= 8192) and global-read (16384) vector paths."""
+    against the oracle (NaN rows: NaN where the oracle has NaN), at widths
+    from the decoder's to past the largest hidden size."""
     import torch
     from ncmorph_amd import kernels
 
