@@ -98,7 +98,17 @@ void ncm_set_error_detail(const std::string& what) { g_last_error = what; }
 class CopyPool {
   public:
     explicit CopyPool(int threads) : n_(threads < 1 ? 1 : threads) {
-        for (int t = 1; t < n_; ++t) th_.emplace_back([this, t] { work(t); });
+        // A thread that cannot be started leaves its slices to the others
+        // (n_ counts the threads that run, the caller included).
+        int started = 1;
+        try {
+            for (int t = 1; t < n_; ++t) {
+                th_.emplace_back([this, t] { work(t); });
+                ++started;
+            }
+        } catch (...) {
+        }
+        n_ = started;
     }
     ~CopyPool() {
         {

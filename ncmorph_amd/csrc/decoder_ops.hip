@@ -291,8 +291,9 @@ __global__ __launch_bounds__(256) void rope_rotate4_kernel(uint16_t* __restrict_
                                                            const float* __restrict__ cosine,
                                                            const float* __restrict__ sine) {
     const int half = hd >> 1, groups = half >> 2;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx >= rows * heads * groups) return;
+    const int64_t idx64 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx64 >= (int64_t)rows * heads * groups) return;
+    const int idx = (int)idx64;  // < 2^31 (checked by the launcher)
     const int i = 4 * (idx % groups);
     const int rh = idx / groups;
     const int h = rh % heads;
