@@ -704,14 +704,18 @@ __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const 
     }
 }
 
-// KEEP_D: D_l stays in registers from the residual to the finish (one memory
-// round trip less, more registers: the small levels, whose few rows leave
-// occupancy to spare).
-template <int NCH, int KS, bool KEEP_D>
+// Where D_l waits between the residual and the finish (DMODE): 0 reloaded
+// from global memory; 1 kept in registers (one memory round trip less, more
+// registers: the small levels, whose few rows leave occupancy to spare); 2
+// kept in LDS, 1 KB per 256 elements and wavefront (the large levels at d <=
+// 2048: their 32 KB per workgroup fits the three workgroups per CU that the
+// registers allow).
+template <int NCH, int KS, int DMODE>
 __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     constexpr int kKeySlots = KS;
     __shared__ int32_t cand_list[4][kKeySlots * 64];
     __shared__ int32_t inc_list[4][kKeySlots * 16];
+    __shared__ f32x4_t d_stash[4][DMODE == 2 ? NCH * 64 : 1];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -722,6 +726,15 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
 
     RowVec<NCH> u, D;
     load_residual<NCH>(a, row, lane, u, D);
+    if constexpr (DMODE == 2) {
+        // Each lane stashes, and later reads back, its own elements.
+#pragma unroll
+        for (int m = 0; m < NCH; ++m) {
+            f32x4_t v;
+            v[0] = D.v[m][0]; v[1] = D.v[m][1]; v[2] = D.v[m][2]; v[3] = D.v[m][3];
+            d_stash[wave][m * 64 + lane] = v;
+        }
+    }
     const int nk = a.cg.nchunk * 4;
     const uint32_t* ck = a.cand + row * (int64_t)nk;
     uint32_t key[kKeySlots];
@@ -833,7 +846,14 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
             }
         }
     }
-    finish_row<NCH, KEEP_D>(a, row, b, best_row, have_row, st.unorm2, lane, D);
+    if constexpr (DMODE == 2) {
+#pragma unroll
+        for (int m = 0; m < NCH; ++m) {
+            const f32x4_t v = d_stash[wave][m * 64 + lane];
+            D.v[m][0] = v[0]; D.v[m][1] = v[1]; D.v[m][2] = v[2]; D.v[m][3] = v[3];
+        }
+    }
+    finish_row<NCH, DMODE != 0>(a, row, b, best_row, have_row, st.unorm2, lane, D);
 }
 
 // ------------------------------------------------------------ host side
@@ -862,7 +882,8 @@ using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 2>;
 //             key slots per row.
 using DistTiny = GemmShape<64, 64, 64, 2, 2, 2, 8, true, 4>;
 constexpr int64_t kCus = 256;
-// Levels with at most this many rows rescore with KEEP_D.
+// Levels with at most this many rows keep D_l in registers through the
+// rescore.
 constexpr int64_t kSmallLevelRows = 4096;
 
 static int nch_for(int64_t d) {
@@ -881,13 +902,13 @@ static hipError_t launch_row_kernels(const PrepArgs* pa, const RowArgs* ra, int6
     if (pa)
         hipLaunchKernelGGL(rvq_prep_kernel<NCH>, grid, dim3(256), 0, st, *pa);
     else if (ra->cg.nchunk > kMaxChunks)
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlotsWide, true>), grid, dim3(256), 0, st,
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlotsWide, 1>), grid, dim3(256), 0, st,
                            *ra);
     else if (rows <= kSmallLevelRows)
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, true>), grid, dim3(256), 0, st, *ra);
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, 1>), grid, dim3(256), 0, st, *ra);
     else
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, false>), grid, dim3(256), 0, st,
-                           *ra);
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, NCH <= 8 ? 2 : 0>), grid, dim3(256),
+                           0, st, *ra);
     return hipGetLastError();
 }
 
