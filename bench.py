@@ -39,7 +39,7 @@ LINEAR_NK = [(2048, 2048), (8192, 2048), (2048, 8192)]
 # one whole encode; the summaries and commands are in
 # profiles/linear_bf16_1b_shapes.md and profiles/rvq_encode_b16_t2048_d2048_l8_v4096.md.
 LINEAR_TRAFFIC_BYTES_PER_LAUNCH = 155.3e6
-RVQ_TRAFFIC_BYTES_PER_ENCODE = 5320e6
+RVQ_TRAFFIC_BYTES_PER_ENCODE = 5099e6
 NEAR_TIE_REL = 1e-5  # relative top-2 distance gap under which a code is a near-tie
 
 
