@@ -38,7 +38,7 @@ def _d53(y, xb, wb, bb=None, rows=None):
     return np.all(np.abs(y - ref) <= (k + 2) * 2.0**-24 * asum)
 
 
-@pytest.mark.parametrize("tail", [16, 32, 64])
+@pytest.mark.parametrize("tail", [1, 16, 32, 33, 64])
 def test_tail_rows_against_bound_oracle_and_other_batches(ncm, oracle, cuda, tail):
     import torch
     from ncmorph_amd import kernels
