@@ -423,8 +423,8 @@ def run_ncm_tied_head(torch, reps=5):
     (PROJECT.md:222): for each of the 8 levels (the level lengths of
     run_ncm_attention), logits [n_l, 8192] = (2 z E_l^T - ||E_l||^2) *
     exp(log_inv_T) / mean ||E_l||^2 with z bf16 [n_l, 4096] and the level's
-    bf16 codebook E_l [8192, 4096] ~N(0, 1/4096), all levels in one launch.
-    Flops: 2 V d per row."""
+    bf16 codebook E_l [8192, 4096] ~N(0, 1/4096), all levels in one call
+    (ncm_tied_head_logits_levels). Flops: 2 V d per row."""
     from ncmorph_amd import kernels, vq
 
     dev = torch.device("cuda", 0)
