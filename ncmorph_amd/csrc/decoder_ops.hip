@@ -22,9 +22,14 @@ namespace ncm {
 // wavefront: lane c < 32 runs chain (r = c / 8, l = c % 8) with its four
 // levels in registers, and the merges that cross chains run in the
 // reference's order on values gathered by shuffles. Every lane returns the
-// same bits. xr: the row in global memory or LDS.
-__device__ __forceinline__ float rms_sum_squares(const float* xr, int64_t n, int lane) {
-    const bool chain = lane < 32;
+// same bits. xr: the row in global memory or LDS. TWO: each half-wavefront
+// runs the 32 chains of its own row (xr: that half's row; live: whether it
+// exists) and returns that row's sum.
+template <bool TWO = false>
+__device__ __forceinline__ float rms_sum_squares(const float* xr, int64_t n, int lane,
+                                                 bool live = true) {
+    const bool chain = TWO ? live : lane < 32;
+    const int base = TWO ? (lane & 32) : 0;
     const int r = (lane >> 3) & 3, l = lane & 7;
 
     const int64_t vectors = n / 8, groups = vectors / 4;
@@ -69,34 +74,29 @@ __device__ __forceinline__ float rms_sum_squares(const float* xr, int64_t n, int
     if (r == 0)  // vector tail, into row 0's chains
         for (int64_t vi = groups * 4; vi < vectors; ++vi) a0 = a0 + sq(vi);
     // vector_sum[l] = ((acc[0][0][l] + acc[0][1][l]) + acc[0][2][l]) + acc[0][3][l]
-    const float r1 = __shfl(a0, l + 8, 64), r2 = __shfl(a0, l + 16, 64), r3 = __shfl(a0, l + 24, 64);
+    const float r1 = __shfl(a0, base + l + 8, 64), r2 = __shfl(a0, base + l + 16, 64),
+                r3 = __shfl(a0, base + l + 24, 64);
     float vs = a0;
     vs = vs + r1;
     vs = vs + r2;
     vs = vs + r3;
     float sum = 0.0f;
     for (int64_t i = vectors * 8; i < n; ++i) {
-        const float v = xr[i];
+        const float v = live ? xr[i] : 0.0f;
         sum = sum + v * v;
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) sum = sum + __shfl(vs, k, 64);
+    for (int k = 0; k < 8; ++k) sum = sum + __shfl(vs, base + k, 64);
     return sum;
 }
 
+// The output pass of one row by one wavefront, given 1 / rms.
 template <int OUT_MODE>
-__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restrict__ x,
-                                                            const float* __restrict__ weight,
-                                                            void* __restrict__ y, int64_t rows,
-                                                            int64_t n, float epsilon) {
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= rows) return;
+__device__ __forceinline__ void rms_write_row(const float* __restrict__ x,
+                                              const float* __restrict__ weight,
+                                              void* __restrict__ y, int64_t row, int64_t n,
+                                              float inv, int lane) {
     const float* xr = x + row * n;
-    const float sum = rms_sum_squares(xr, n, lane);
-    const float mean = sum / (float)n;
-    const float inv = 1.0f / sqrtf(mean + epsilon);
-
     // f32 mode (OUT_MODE NCM_OUT_F32, rms_norm, root.zig:226-239):
     // (x * inv) * weight. bf16 mode: round_bf16(round_bf16(x * inv) *
     // round_bf16(weight)) (root.zig:250-252).
@@ -170,6 +170,38 @@ __global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restr
         }
     } else {
         for (int64_t i = lane; i < n; i += 64) out1(i, xr[i], weight[i]);
+    }
+}
+
+// TWO: two rows per wavefront (the first in lanes 0-31's chains, the second
+// in lanes 32-63's), then the output pass of each in turn by the whole
+// wavefront: used when the rows outnumber the wavefronts the chip holds at
+// once, where one row per wavefront would leave the last few rows a second
+// round of their own.
+template <int OUT_MODE, bool TWO>
+__global__ __launch_bounds__(256) void rms_norm_rows_kernel(const float* __restrict__ x,
+                                                            const float* __restrict__ weight,
+                                                            void* __restrict__ y, int64_t rows,
+                                                            int64_t n, float epsilon) {
+    const int lane = threadIdx.x & 63;
+    const int64_t wrow = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int64_t row0 = TWO ? 2 * wrow : wrow;
+    if (row0 >= rows) return;
+    if constexpr (TWO) {
+        const int h = lane >> 5;
+        const bool live = row0 + h < rows;
+        const float sum =
+            rms_sum_squares<true>(x + (row0 + (live ? h : 0)) * n, n, lane, live);
+        const float mean = sum / (float)n;
+        const float inv = 1.0f / sqrtf(mean + epsilon);
+        const float inv0 = __shfl(inv, 0, 64), inv1 = __shfl(inv, 32, 64);
+        rms_write_row<OUT_MODE>(x, weight, y, row0, n, inv0, lane);
+        if (row0 + 1 < rows) rms_write_row<OUT_MODE>(x, weight, y, row0 + 1, n, inv1, lane);
+    } else {
+        const float sum = rms_sum_squares(x + row0 * n, n, lane);
+        const float mean = sum / (float)n;
+        const float inv = 1.0f / sqrtf(mean + epsilon);
+        rms_write_row<OUT_MODE>(x, weight, y, row0, n, inv, lane);
     }
 }
 
@@ -418,8 +450,16 @@ hipError_t launch_bias_round(void* y, const float* bias, int64_t rows, int64_t n
 template <int OUT_MODE>
 static hipError_t launch_rms_t(const float* x, const float* weight, void* y, int64_t rows,
                                int64_t n, float epsilon, hipStream_t stream) {
-    hipLaunchKernelGGL(rms_norm_rows_kernel<OUT_MODE>, dim3((unsigned)((rows + 3) / 4)),
-                       dim3(256), 0, stream, x, weight, y, rows, n, epsilon);
+    // Wavefronts resident at once: 8 per SIMD on 256 CUs.
+    constexpr int64_t kResidentWaves = 256 * 4 * 8;
+    if (rows > kResidentWaves)
+        hipLaunchKernelGGL((rms_norm_rows_kernel<OUT_MODE, true>),
+                           dim3((unsigned)((rows + 7) / 8)), dim3(256), 0, stream, x, weight, y,
+                           rows, n, epsilon);
+    else
+        hipLaunchKernelGGL((rms_norm_rows_kernel<OUT_MODE, false>),
+                           dim3((unsigned)((rows + 3) / 4)), dim3(256), 0, stream, x, weight, y,
+                           rows, n, epsilon);
     return hipGetLastError();
 }
 
