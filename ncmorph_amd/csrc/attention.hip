@@ -9,8 +9,9 @@
 // fp32 products; the MFMA sums them in its own order instead of the
 // reference's key order, and the softmax sum is kept online. exp(x) is
 // computed as exp2(x log2 e) (v_exp_f32, relative error ~2^-20 at |x| ~ 20)
-// and the division as a product with 1 / sum, so a probability can land on
-// the other side of a bf16 rounding boundary now and then. Results agree
+// and the division by the sum as a term - log2(sum) of the same exponent
+// (v_log_f32), so a probability can land on the other side of a bf16
+// rounding boundary now and then. Results agree
 // with the reference within a few bf16 steps, not bit for bit.
 //
 // Two passes over the key blocks of one (sequence, head, 32 NWV queries)
@@ -449,9 +450,10 @@ __attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
     // A query with no allowed key (a prefix query whose prefix is all
     // padding) gets zero probabilities, hence a zero context, as the
     // reference (root.zig:563-565).
+    // p = exp2(s log2 e - m log2 e - log2 sum): the division by the sum
+    // folded into the exponent (no product per score); -inf gives p = 0.
     const bool any_key = ltot > 0.0f;
-    const float inv_l = any_key ? 1.0f / ltot : 0.0f;
-    const float nm = any_key ? -m * kLog2e : 0.0f;  // m is a score: -m log2 e as in pass 1
+    const float nm = any_key ? -m * kLog2e - __builtin_amdgcn_logf(ltot) : -INFINITY;
 
     // ---- pass 2: bf16 probabilities and P V.
     constexpr int NT = HD / 32;
@@ -486,7 +488,7 @@ __attribute__((amdgpu_waves_per_eu(2, 4))) void attention_bf16_kernel(
                 float pf[16];
 #pragma unroll
                 for (int i = 0; i < 16; ++i)
-                    pf[i] = __builtin_amdgcn_exp2f(expo(acc[i], nm)) * inv_l;
+                    pf[i] = __builtin_amdgcn_exp2f(expo(acc[i], nm));
 #pragma unroll
                 for (int j = 0; j < 2; ++j) {
                     u32x4_t pa;
