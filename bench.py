@@ -719,7 +719,8 @@ def main():
     # would measure on the ramp instead.
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=500)
-    ap.add_argument("--only", choices=["linear", "rvq", "decoder", "ncm", "vqtok", "all", "copy"],
+    ap.add_argument("--only", choices=["linear", "rvq", "decoder", "ncm", "attention", "vqtok", "all",
+                                       "copy"],
                     default="all",
                     help="copy: a plain 256 MiB device copy, the reference point for "
                          "the FETCH_SIZE / WRITE_SIZE counters")
@@ -812,6 +813,8 @@ def main():
                 res["cpu_baseline"] = rvq["cpu_baseline"]
     if args.only == "ncm":
         res["ncm_level_step"] = run_ncm_step(torch)
+    if args.only == "attention":
+        res["ncm_level_attention"] = run_ncm_attention(torch)
     if args.only in ("vqtok", "all"):
         vq = run_vq_tokenizer(torch)
         if not args.no_cpu:
