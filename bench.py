@@ -71,11 +71,16 @@ def linear_inputs(torch, dev):
     return xs, ws, ys
 
 
-def _ramp(torch, fn, ms=150.0):
-    """Runs fn, untimed, until about `ms` of wall time has passed: the GPU
-    raises its engine clock over roughly 100 ms of sustained load, and a
-    section that follows host-only work (a CPU baseline) starts from a lower
-    clock."""
+# Untimed clock-settling run before every timed loop, ours and hipBLASLt's
+# alike: the GPU raises its engine clock over roughly 100 ms of sustained
+# load, so a loop timed right after set-up, host-only work (a CPU baseline)
+# or a short warmup measures the ramp instead of the steady clock.
+RAMP_MS = 200.0
+SHAPE_RAMP_MS = 50.0
+
+
+def _ramp(torch, fn, ms=RAMP_MS):
+    """Runs fn, untimed, until about `ms` of wall time has passed."""
     t0 = time.perf_counter()
     n = 1
     while (time.perf_counter() - t0) * 1e3 < ms:
@@ -95,21 +100,25 @@ def run_linear(torch, steps, warmup):
         for (n, k) in LINEAR_NK:
             kernels.linear_bf16(xs[k], ws[(n, k)], out=ys[(n, k)])
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
-    # Per-shape launch durations (events on the launch stream).
+    # Per-shape launch durations (events on the launch stream), each shape
+    # after the same 50 ms ramp that the hipBLASLt shapes get below.
     per_shape = {}
     for (n, k) in LINEAR_NK:
+        run = lambda: kernels.linear_bf16(xs[k], ws[(n, k)], out=ys[(n, k)])  # noqa: E731
+        _ramp(torch, run, ms=SHAPE_RAMP_MS)
         e0, e1 = _events(torch)
         reps = 20
         e0.record()
         for _ in range(reps):
-            kernels.linear_bf16(xs[k], ws[(n, k)], out=ys[(n, k)])
+            run()
         e1.record()
         torch.cuda.synchronize()
         per_shape[(n, k)] = e0.elapsed_time(e1) / reps * 1e-3
-    # Timed region: exactly `steps` steps, synchronized on both sides.
+    # Clock ramp, then `warmup` untimed steps, then the timed region:
+    # exactly `steps` steps, synchronized on both sides.
+    _ramp(torch, step)
+    for _ in range(warmup):
+        step()
     torch.cuda.synchronize()
     e0, e1 = _events(torch)
     t0 = time.perf_counter()
@@ -133,7 +142,7 @@ def run_linear(torch, steps, warmup):
         out = {}
         for (n, k) in LINEAR_NK:
             run = lambda: fn(xs[k], ws[(n, k)])  # noqa: E731
-            _ramp(torch, run, ms=50.0)
+            _ramp(torch, run, ms=SHAPE_RAMP_MS)
             e0, e1 = _events(torch)
             e0.record()
             for _ in range(20):
@@ -164,11 +173,19 @@ def run_rvq(torch, reps, warmup):
     del x
     csq = vq.prepare(cbd)
     out = {}
-    r = vq.encode(xd, cbd, c["strides"], csq=csq, want_gap=False, count_flagged=True)
+    r = vq.encode(xd, cbd, c["strides"], csq=csq, want_gap=False, level_counts=True)
     n_flagged = r["n_flagged"]
+    level_rows = [c["b"] * c["t"] // s for s in c["strides"]]
+    rescored = [{"rows": n, "scored": sc, "share": round(sc / n, 4), "flagged": fl}
+                for n, sc, fl in zip(level_rows, r["scored"], r["flagged"])]
     out = {"codes": r["codes"], "recon": r["recon"]}
-    for _ in range(warmup):
+
+    def enc():
         vq.encode(xd, cbd, c["strides"], csq=csq, want_gap=False, out=out)
+
+    _ramp(torch, enc)
+    for _ in range(warmup):
+        enc()
     torch.cuda.synchronize()
     e0, e1 = _events(torch)
     e0.record()
@@ -189,7 +206,7 @@ def run_rvq(torch, reps, warmup):
     bytes_alg = (c["b"] * c["t"] * c["d"] * 4 + c["levels"] * c["v"] * c["d"] * 2 +
                  rows * 4 + c["b"] * c["t"] * c["d"] * 4)
     return {"encode_s": t, "tokens": c["b"] * c["t"], "flops": flops, "bytes": bytes_alg,
-            "n_flagged": n_flagged, "near_ties": near, "codes": rows}
+            "n_flagged": n_flagged, "near_ties": near, "codes": rows, "rescored": rescored}
 
 
 def run_decoder_ops(torch, reps=20):
@@ -713,12 +730,10 @@ def cpu_rvq_baseline():
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    # The GPU raises its engine clock over roughly 100 ms of sustained load;
-    # the default warmup (500 linear steps, then 100 RVQ encodes) lets it
-    # reach its steady state before the timed steps, which a short warmup
-    # would measure on the ramp instead.
+    # Every timed section first runs its own work untimed for RAMP_MS (the
+    # engine clock's ramp), then its warmup, then exactly its timed steps.
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--only", choices=["linear", "rvq", "decoder", "ncm", "attention", "vqtok", "all",
                                        "copy"],
                     default="all",
@@ -783,7 +798,7 @@ def main():
     if args.only in ("linear", "all"):
         res["decoder_ops"] = run_decoder_ops(torch)
     if args.only in ("rvq", "all"):
-        rv = run_rvq(torch, max(3, args.steps // 10), max(1, args.warmup // 5))
+        rv = run_rvq(torch, max(10, args.steps // 2), max(1, args.warmup // 5))
         tps = rv["tokens"] / rv["encode_s"]
         tf = rv["flops"] / rv["encode_s"] / 1e12
         gbs = rv["bytes"] / rv["encode_s"] / 1e9
@@ -799,6 +814,10 @@ def main():
                             "hbm_gbs_algorithmic": round(gbs, 1),
                             "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
                "flagged_rows": rv["n_flagged"],
+               # Per level: rows that needed any exact distance (the rest had
+               # one candidate under the error bound) and rows with an
+               # incomplete candidate chunk.
+               "rescored_rows_per_level": rv["rescored"],
                "near_ties": {"count": rv["near_ties"], "codes": rv["codes"],
                              "rel_gap_below": NEAR_TIE_REL}}
         if not args.no_cpu:

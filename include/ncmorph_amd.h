@@ -550,6 +550,18 @@ int ncm_rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t
                    const float* csq, int64_t v, int32_t* codes, float* recon, float* gap,
                    const int32_t* force_codes, int64_t* n_flagged);
 
+/* ncm_rvq_encode that also reports, per level, how the exact pass went. No
+ * counterpart in the reference (which has no RVQ code); for callers that
+ * profile or tune the encode. flagged and scored (host, int64 [levels])
+ * receive the rows with an incomplete candidate chunk (every code of the
+ * chunk rescored) and the rows that needed any exact distance (every other
+ * row had exactly one candidate under its error bound, which is then the
+ * exact argmin without a rescore). Synchronizes the context's stream. */
+int ncm_rvq_encode_counts(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d,
+                          int64_t levels, const int32_t* strides, const uint16_t* codebooks,
+                          const float* csq, int64_t v, int32_t* codes, float* recon, float* gap,
+                          const int32_t* force_codes, int64_t* flagged, int64_t* scored);
+
 /* Allocation-free variant of ncm_rvq_encode. No counterpart in the
  * reference: it exists for callers that cannot allocate device memory (code
  * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).

@@ -67,6 +67,8 @@ SIGNATURES = [
     ("ncm_ncm_forward_f32_dev", i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp]),
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
     ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
+    ("ncm_rvq_encode_counts", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp,
+                                    vp, vp]),
     ("ncm_rvq_encode_noalloc", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp,
                                      vp]),
     ("ncm_rvq_decode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, i64, vp]),

@@ -1110,6 +1110,27 @@ int ncm_rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t
                            gap, force_codes, n_flagged);
 }
 
+int ncm_rvq_encode_counts(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d,
+                          int64_t levels, const int32_t* strides, const uint16_t* codebooks,
+                          const float* csq, int64_t v, int32_t* codes, float* recon, float* gap,
+                          const int32_t* force_codes, int64_t* flagged, int64_t* scored) {
+    if (!ctx) return NCM_E_NULL;
+    if (!x || !strides || !codebooks || !csq || !codes || !flagged || !scored) return NCM_E_NULL;
+    int rc = ncm::rvq_check_shape(b, t, d, levels, strides, v);
+    if (rc) return rc;
+    rc = ctx_bind(ctx);
+    if (rc) return rc;
+    ncm::RvqCounts counts{};
+    rc = ncm::rvq_encode(ctx, x, b, t, d, levels, strides, codebooks, csq, v, codes, recon, gap,
+                         force_codes, nullptr, &counts);
+    if (rc) return rc;
+    for (int64_t l = 0; l < levels; ++l) {
+        flagged[l] = counts.flagged[l];
+        scored[l] = counts.scored[l];
+    }
+    return NCM_OK;
+}
+
 // Shape, switch and weight checks shared by the tokenizer entry points.
 static int vq_tok_check(const ncm_vq_tok_t* t, bool need_embed) {
     if (!t) return NCM_E_NULL;

@@ -33,6 +33,15 @@ struct RvqGeom {
     int64_t pyr_off[kMaxPyr];  // float offset of the stride-2^j pool (j >= 1)
 };
 
+// Per-level counters of one encode: rows with an incomplete candidate chunk
+// (every code of the chunk rescored) and rows that needed any exact
+// distance (the others had one candidate under the threshold).
+struct RvqCounts {
+    int64_t levels;
+    int64_t flagged[kMaxLevels];
+    int64_t scored[kMaxLevels];
+};
+
 int rvq_check_shape(int64_t b, int64_t t, int64_t d, int64_t levels, const int32_t* strides,
                     int64_t v);
 LevelTable make_level_table(int64_t t, int64_t levels, const int32_t* strides);
@@ -45,7 +54,7 @@ hipError_t launch_rvq_decode(const int32_t* codes, int64_t b, int64_t t, int64_t
 int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
                const int32_t* strides, const uint16_t* codebooks, const float* csq, int64_t v,
                int32_t* codes, float* recon, float* gap, const int32_t* force_codes,
-               int64_t* n_flagged);
+               int64_t* n_flagged, RvqCounts* counts = nullptr);
 // Device bytes of the workspace one encode of this shape uses.
 int rvq_workspace_bytes(int64_t b, int64_t t, int64_t d, int64_t levels, const int32_t* strides,
                         int64_t v, size_t* bytes);
@@ -54,6 +63,7 @@ int rvq_workspace_bytes(int64_t b, int64_t t, int64_t d, int64_t levels, const i
 int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int64_t b,
                   int64_t t, int64_t d, int64_t levels, const int32_t* strides,
                   const uint16_t* codebooks, const float* csq, int64_t v, int32_t* codes,
-                  float* recon, float* gap, const int32_t* force_codes, int64_t* n_flagged);
+                  float* recon, float* gap, const int32_t* force_codes, int64_t* n_flagged,
+                  RvqCounts* counts = nullptr);
 
 }  // namespace ncm

@@ -235,14 +235,15 @@ __global__ void rvq_pyramid_kernel(const float* __restrict__ src, int64_t rows, 
 
 // ------------------------------------------------- per-encode set-up kernel
 
-// cmax[l] = sqrt(max_k csq[l, k]) (rounded up); zeroes the flag counters.
+// cmax[l] = sqrt(max_k csq[l, k]) (rounded up); zeroes the level's two
+// counters (counts[l], counts[levels + l]).
 // One 1024-thread block per level; each thread issues its (up to) four loads
 // of a pass together, so the block waits for one memory round trip per
 // 4096 codes.
 constexpr int kSetupThreads = 1024;
 __global__ __launch_bounds__(kSetupThreads) void rvq_setup_kernel(const float* __restrict__ csq,
-                                                                 int64_t v, float* cmax,
-                                                                 int32_t* flag_count) {
+                                                                 int64_t v, int64_t levels,
+                                                                 float* cmax, int32_t* counts) {
     const int l = blockIdx.x;
     const float* row = csq + (int64_t)l * v;
     float m = 0.0f;
@@ -265,7 +266,8 @@ __global__ __launch_bounds__(kSetupThreads) void rvq_setup_kernel(const float* _
         float r = red[0];
         for (int w = 1; w < kSetupThreads / 64; ++w) r = fmaxf(r, red[w]);
         cmax[l] = sqrtf(r) * 1.00001f;
-        flag_count[l] = 0;
+        counts[l] = 0;
+        counts[levels + l] = 0;
     }
 }
 
@@ -483,7 +485,11 @@ struct RowArgs {
     uint16_t* ubuf;              // level l+1 bf16 rows
     float* rowc_out;             // level l+1 offsets
     float* recon;                // last level only, nullable
-    int32_t* flag_count;         // this level's counter
+    int32_t* flag_count;         // this level's counter of rows with an
+                                 // incomplete chunk
+    int32_t* score_count;        // nullable: this level's counter of rows
+                                 // with any exact distance (diagnostics:
+                                 // one same-address atomic per such row)
     int level;
     int64_t n_rows;
     int64_t d_div;               // level-l rows per D_l row (s_{l-1} / s_l)
@@ -814,6 +820,7 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
         // needed (the gap is +inf, as for any single rescored candidate).
         b.code = list[0];
     } else {
+        if (a.score_count && lane == 0) atomicAdd(a.score_count, 1);
         score_list<NCH>(u, cbl, csql, list, nsel, d, lane, b, best_row);
         have_row = nsel > 0;
     }
@@ -1040,7 +1047,9 @@ static int rvq_layout(int64_t b, int64_t t, int64_t d, int64_t levels, const int
     lay.rc1 = carve((size_t)max_rows * 4);
     lay.cand = carve((size_t)max_cand * 4);
     lay.cmax = carve((size_t)levels * 4);
-    lay.fc = carve((size_t)levels * 4);
+    // Per level: rows with an incomplete chunk, then rows with any exact
+    // distance.
+    lay.fc = carve((size_t)levels * 2 * 4);
     lay.total = off;
     return NCM_OK;
 }
@@ -1058,7 +1067,7 @@ int rvq_workspace_bytes(int64_t b, int64_t t, int64_t d, int64_t levels, const i
 int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, int64_t levels,
                const int32_t* strides, const uint16_t* codebooks, const float* csq, int64_t v,
                int32_t* codes, float* recon, float* gap, const int32_t* force_codes,
-               int64_t* n_flagged) {
+               int64_t* n_flagged, RvqCounts* counts) {
     size_t bytes = 0;
     int rc = rvq_workspace_bytes(b, t, d, levels, strides, v, &bytes);
     if (rc) return rc;
@@ -1066,13 +1075,14 @@ int rvq_encode(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d, 
     rc = ncm_ctx_workspace(ctx, bytes, &ws);
     if (rc) return rc;
     return rvq_encode_ws(ncm_ctx_stream(ctx), ws, bytes, x, b, t, d, levels, strides, codebooks,
-                         csq, v, codes, recon, gap, force_codes, n_flagged);
+                         csq, v, codes, recon, gap, force_codes, n_flagged, counts);
 }
 
 int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int64_t b,
                   int64_t t, int64_t d, int64_t levels, const int32_t* strides,
                   const uint16_t* codebooks, const float* csq, int64_t v, int32_t* codes,
-                  float* recon, float* gap, const int32_t* force_codes, int64_t* n_flagged) {
+                  float* recon, float* gap, const int32_t* force_codes, int64_t* n_flagged,
+                  RvqCounts* counts) {
     RvqGeom g;
     RvqLayout lay;
     int rc = rvq_layout(b, t, d, levels, strides, v, g, lay);
@@ -1087,12 +1097,12 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
     float* rowc[2] = {(float*)(W + lay.rc0), (float*)(W + lay.rc1)};
     uint32_t* cand = (uint32_t*)(W + lay.cand);
     float* cmax = (float*)(W + lay.cmax);
-    int32_t* fcount = (int32_t*)(W + lay.fc);
+    int32_t* fcount = (int32_t*)(W + lay.fc);  // [levels] flagged, [levels] scored
     // D_{l+1} (coarse reconstruction) is written by level l into dbuf[(l+1)&1].
     float* dbuf[2] = {(float*)(W + lay.d0), (float*)(W + lay.d1)};
 
     hipLaunchKernelGGL(rvq_setup_kernel, dim3((unsigned)levels), dim3(kSetupThreads), 0, st, csq,
-                       v, cmax, fcount);
+                       v, levels, cmax, fcount);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return NCM_E_HIP;
 
@@ -1164,19 +1174,27 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
         ra.ubuf = ubuf; ra.rowc_out = rowc[(l + 1) & 1];
         ra.recon = l + 1 == levels ? recon : nullptr;
         ra.flag_count = fcount + l;
+        ra.score_count = counts ? fcount + levels + l : nullptr;
         ra.level = (int)l; ra.n_rows = n; ra.cg = cg;
         e = launch_rows(nch, nullptr, &ra, n, st);
         if (e != hipSuccess) return NCM_E_HIP;
     }
 
-    if (n_flagged) {
-        int32_t host[kMaxLevels];
-        e = hipMemcpyAsync(host, fcount, levels * 4, hipMemcpyDeviceToHost, st);
+    if (n_flagged || counts) {
+        int32_t host[2 * kMaxLevels];
+        e = hipMemcpyAsync(host, fcount, levels * 2 * 4, hipMemcpyDeviceToHost, st);
         if (e == hipSuccess) e = hipStreamSynchronize(st);
         if (e != hipSuccess) return NCM_E_HIP;
         int64_t s = 0;
         for (int64_t l = 0; l < levels; ++l) s += host[l];
-        *n_flagged = s;
+        if (n_flagged) *n_flagged = s;
+        if (counts) {
+            counts->levels = levels;
+            for (int64_t l = 0; l < levels; ++l) {
+                counts->flagged[l] = host[l];
+                counts->scored[l] = host[levels + l];
+            }
+        }
     }
     return NCM_OK;
 }

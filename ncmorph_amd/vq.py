@@ -45,12 +45,15 @@ def prepare(codebooks, ctx=None):
 
 
 def encode(x, codebooks, strides, csq=None, want_recon=True, want_gap=True, force_codes=None,
-           count_flagged=False, out=None, ctx=None):
+           count_flagged=False, out=None, ctx=None, level_counts=False):
     """x: float32 [b, t, d]; codebooks: bfloat16 [levels, v, d]; csq float32
     [levels, v] (prepare) or None; force_codes int32 [b, sum t/s] or None.
     out: optional dict of preallocated outputs (codes int32 [b, sum t/s],
     recon float32 [b, t, d], gap float32 [b, sum t/s]).
-    Returns dict(codes, recon, gap, n_flagged)."""
+    level_counts: also return, per level, the rows with an incomplete
+    candidate chunk ("flagged") and the rows that needed any exact distance
+    ("scored"), through ncm_rvq_encode_counts.
+    Returns dict(codes, recon, gap, n_flagged[, flagged, scored])."""
     import torch
 
     W = "rvq_encode"
@@ -86,6 +89,16 @@ def encode(x, codebooks, strides, csq=None, want_recon=True, want_gap=True, forc
     nf = C.c_int64(-1)
     a.done()
     ctx = _ctx(x, ctx)
+    if level_counts:
+        fl = np.zeros(L, dtype=np.int64)
+        sc = np.zeros(L, dtype=np.int64)
+        check(lib().ncm_rvq_encode_counts(ctx.handle, px, B, T, D, L, C.c_void_p(s.ctypes.data),
+                                          pcb, pcs, V, pco, pr, pg, pf,
+                                          C.c_void_p(fl.ctypes.data), C.c_void_p(sc.ctypes.data)),
+              W)
+        return {"codes": codes, "recon": recon if want_recon else None,
+                "gap": gap if want_gap else None, "n_flagged": int(fl.sum()),
+                "flagged": fl.tolist(), "scored": sc.tolist()}
     check(lib().ncm_rvq_encode(ctx.handle, px, B, T, D, L, C.c_void_p(s.ctypes.data), pcb, pcs, V,
                                pco, pr, pg, pf, C.byref(nf) if count_flagged else None), W)
     return {"codes": codes, "recon": recon if want_recon else None,

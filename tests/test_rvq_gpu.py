@@ -140,6 +140,37 @@ def test_teacher_forcing(ncm, oracle, cuda):
     assert np.array_equal(r["recon"], want["recon"])
 
 
+def test_level_counts(ncm, oracle, cuda):
+    """ncm_rvq_encode_counts: the same codes, reconstruction and gaps as the
+    plain encode; per level, the rows with an exact rescore include every
+    row whose gap is finite (two or more exact distances) and never exceed
+    the level's rows; an all-equal codebook makes every row rescored."""
+    import torch
+    from ncmorph_amd import vq
+
+    strides = (8, 2, 1)
+    x, cb = synth.rvq_inputs(11, 2, 64, 256, 3, 96)
+    xd, cbd = _dev(x, cuda), _dev(cb, cuda, bf16=True)
+    plain = vq.encode(xd, cbd, strides, count_flagged=True)
+    cnt = vq.encode(xd, cbd, strides, level_counts=True)
+    torch.cuda.synchronize()
+    for k in ("codes", "recon", "gap"):
+        assert torch.equal(plain[k], cnt[k]), k
+    assert cnt["n_flagged"] == plain["n_flagged"] == sum(cnt["flagged"])
+    gap = cnt["gap"].cpu().numpy()
+    off = 0
+    for l, s in enumerate(strides):
+        n = 2 * (64 // s)
+        finite = int(np.isfinite(gap[:, off:off + 64 // s]).sum())
+        assert finite <= cnt["scored"][l] <= n, (l, finite, cnt["scored"][l])
+        off += 64 // s
+    same = np.repeat(cb[:, :1], cb.shape[1], axis=1)
+    eq = vq.encode(xd, _dev(same, cuda, bf16=True), strides, level_counts=True)
+    torch.cuda.synchronize()
+    assert eq["scored"] == [2 * (64 // s) for s in strides]
+    assert np.array_equal(eq["codes"].cpu().numpy(), oracle.rvq_encode(x, same, strides)["codes"])
+
+
 def test_decode_matches_oracle(ncm, oracle, cuda):
     import torch
     from ncmorph_amd import vq
