@@ -282,6 +282,7 @@ struct PrepArgs {
     const float* cmax;
     uint16_t* ubuf;
     float* rowc;
+    RowStats* stats;
     int level;
     int64_t n_rows;
 };
@@ -300,7 +301,10 @@ __global__ __launch_bounds__(256) void rvq_prep_kernel(PrepArgs a) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
     const RowStats s = write_bf16_row<NCH>(u, a.g.d, lane, a.ubuf + row * a.g.d);
-    if (lane == 0) a.rowc[row] = row_offset(s, a.cmax[a.level]);
+    if (lane == 0) {
+        a.rowc[row] = row_offset(s, a.cmax[a.level]);
+        a.stats[row] = s;
+    }
 }
 
 // ------------------------------------------------------- distance kernel
@@ -479,6 +483,8 @@ struct RowArgs {
     float* gap;                  // nullable
     const uint32_t* cand;
     const float* rowc_in;
+    const RowStats* stats_in;
+    RowStats* stats_out;
     const float* cmax;
     const float* d_in;           // D_l, one row per level l-1 row (level > 0)
     float* d_out;                // D_{l+1}, one row per level-l row (not last level)
@@ -645,10 +651,11 @@ __device__ __forceinline__ void load_residual(const RowArgs& a, int64_t row, int
 // the reconstruction at the last level.
 // best_row holds the elements of b.code when have_row is true. KEEP_D: D_l
 // is still in D (else it is loaded again).
-template <int NCH, bool KEEP_D>
+template <int NCH, bool KEEP_D, bool PAIR>
 __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const Best& b,
                                           const CodeRow<NCH>& best_row, bool have_row,
-                                          double unorm2, int lane, RowVec<NCH>& D) {
+                                          double unorm2, int lane, RowVec<NCH>& D,
+                                          RowVec<NCH> (&ch)[2]) {
     const RvqGeom& g = a.g;
     const int l = a.level;
     const int64_t d = g.d;
@@ -696,17 +703,23 @@ __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const 
                 *(f32x4_t*)(dst + m * 256 + 4 * lane) = o;
             }
     }
-    const int64_t ratio = s / g.L.stride[l + 1];
+    const int64_t ratio = PAIR ? 2 : s / g.L.stride[l + 1];
     for (int64_t c = 0; c < ratio; ++c) {
         const int64_t child = row * ratio + c;
         RowVec<NCH> u;
-        load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l + 1, child), d, lane, u);
+        if constexpr (PAIR)
+            u = ch[c];
+        else
+            load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l + 1, child), d, lane, u);
 #pragma unroll
         for (int m = 0; m < NCH; ++m)
 #pragma unroll
             for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
         const RowStats st = write_bf16_row<NCH>(u, d, lane, a.ubuf + child * d);
-        if (lane == 0) a.rowc_out[child] = row_offset(st, a.cmax[l + 1]);
+        if (lane == 0) {
+            a.rowc_out[child] = row_offset(st, a.cmax[l + 1]);
+            a.stats_out[child] = st;
+        }
     }
 }
 
@@ -716,8 +729,9 @@ __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const 
 // kept in LDS, 1 KB per 256 elements and wavefront (the large levels at d <=
 // 2048: their 32 KB per workgroup fits the three workgroups per CU that the
 // registers allow).
-template <int NCH, int KS, int DMODE>
-__global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
+template <int NCH, int KS, int DMODE, bool PAIR>
+__global__ __launch_bounds__(256)
+void rvq_rescore_kernel(RowArgs a) {
     constexpr int kKeySlots = KS;
     __shared__ int32_t cand_list[4][kKeySlots * 64];
     __shared__ int32_t inc_list[4][kKeySlots * 16];
@@ -731,7 +745,13 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     const int64_t d = g.d;
 
     RowVec<NCH> u, D;
-    load_residual<NCH>(a, row, lane, u, D);
+    RowVec<NCH> ch[2];
+    if constexpr (PAIR) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l + 1, 2 * row + c), d, lane, ch[c]);
+    }
+    load_coarse<NCH>(a, row, lane, D);
     if constexpr (DMODE == 2) {
         // Each lane stashes, and later reads back, its own elements.
 #pragma unroll
@@ -749,7 +769,7 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
         const int idx = lane + 64 * s;
         key[s] = idx < nk ? ck[idx] : 0xFFFFFFFFu;
     }
-    const RowStats st = write_bf16_row<NCH>(u, d, lane, nullptr);
+    const RowStats st = a.stats_in[row];
 
     // Rigorous bound E on |key distance - (offset + exact dist)|:
     //   bf16 rounding of u:     2 cmax ||u - bf16(u)||
@@ -821,6 +841,28 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
         b.code = list[0];
     } else {
         if (a.score_count && lane == 0) atomicAdd(a.score_count, 1);
+        // The exact residual, only for rows that need exact distances.
+        if constexpr (PAIR) {
+#pragma unroll
+            for (int m = 0; m < NCH; ++m)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) u.v[m][e] = (ch[0].v[m][e] + ch[1].v[m][e]) * 0.5f;
+        } else {
+            load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l, row), d, lane, u);
+        }
+        if constexpr (DMODE == 2) {
+#pragma unroll
+            for (int m = 0; m < NCH; ++m) {
+                const f32x4_t v = d_stash[wave][m * 64 + lane];
+                D.v[m][0] = v[0]; D.v[m][1] = v[1]; D.v[m][2] = v[2]; D.v[m][3] = v[3];
+            }
+        } else if constexpr (DMODE == 0) {
+            load_coarse<NCH>(a, row, lane, D);
+        }
+#pragma unroll
+        for (int m = 0; m < NCH; ++m)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
         score_list<NCH>(u, cbl, csql, list, nsel, d, lane, b, best_row);
         have_row = nsel > 0;
     }
@@ -860,7 +902,7 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
             D.v[m][0] = v[0]; D.v[m][1] = v[1]; D.v[m][2] = v[2]; D.v[m][3] = v[3];
         }
     }
-    finish_row<NCH, DMODE != 0>(a, row, b, best_row, have_row, st.unorm2, lane, D);
+    finish_row<NCH, DMODE != 0, PAIR>(a, row, b, best_row, have_row, st.unorm2, lane, D, ch);
 }
 
 // ------------------------------------------------------------ host side
@@ -902,20 +944,34 @@ static int nch_for(int64_t d) {
     return 16;
 }
 
+template <int NCH, bool PAIR>
+static void launch_rescore_p(const RowArgs* ra, int64_t rows, dim3 grid, hipStream_t st) {
+    if (ra->cg.nchunk > kMaxChunks)
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlotsWide, 1, PAIR>), grid, dim3(256), 0,
+                           st, *ra);
+    else if (rows <= kSmallLevelRows)
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, 1, PAIR>), grid, dim3(256), 0, st,
+                           *ra);
+    else
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, PAIR ? 1 : (NCH <= 8 ? 2 : 0), PAIR>), grid,
+                           dim3(256), 0, st, *ra);
+}
+
 template <int NCH>
 static hipError_t launch_row_kernels(const PrepArgs* pa, const RowArgs* ra, int64_t rows,
                                      hipStream_t st) {
     const dim3 grid((unsigned)((rows + 3) / 4));
-    if (pa)
+    if (pa) {
         hipLaunchKernelGGL(rvq_prep_kernel<NCH>, grid, dim3(256), 0, st, *pa);
-    else if (ra->cg.nchunk > kMaxChunks)
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlotsWide, 1>), grid, dim3(256), 0, st,
-                           *ra);
-    else if (rows <= kSmallLevelRows)
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, 1>), grid, dim3(256), 0, st, *ra);
+        return hipGetLastError();
+    }
+    const int l = ra->level;
+    const bool pair = NCH <= 8 && l + 1 < ra->g.L.levels &&
+                      ra->g.L.stride[l] == 2 * ra->g.L.stride[l + 1];
+    if (pair)
+        launch_rescore_p<NCH, NCH <= 8>(ra, rows, grid, st);
     else
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, NCH <= 8 ? 2 : 0>), grid, dim3(256),
-                           0, st, *ra);
+        launch_rescore_p<NCH, false>(ra, rows, grid, st);
     return hipGetLastError();
 }
 
@@ -1010,7 +1066,7 @@ static size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
 
 // Workspace layout of one encode (byte offsets from a 256-byte aligned base).
 struct RvqLayout {
-    size_t pyr, u, d0, d1, rc0, rc1, cand, cmax, fc, total;
+    size_t pyr, u, d0, d1, rc0, rc1, st0, st1, cand, cmax, fc, total;
 };
 
 // Fills the geometry and the workspace layout; NCM_E_SHAPE if the strides
@@ -1045,6 +1101,8 @@ static int rvq_layout(int64_t b, int64_t t, int64_t d, int64_t levels, const int
     lay.d1 = carve(levels > 1 ? (size_t)max_rows * d * 4 : 0);
     lay.rc0 = carve((size_t)max_rows * 4);
     lay.rc1 = carve((size_t)max_rows * 4);
+    lay.st0 = carve((size_t)max_rows * sizeof(RowStats));
+    lay.st1 = carve((size_t)max_rows * sizeof(RowStats));
     lay.cand = carve((size_t)max_cand * 4);
     lay.cmax = carve((size_t)levels * 4);
     // Per level: rows with an incomplete chunk, then rows with any exact
@@ -1095,6 +1153,7 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
     float* pyr = (float*)(W + lay.pyr);
     uint16_t* ubuf = (uint16_t*)(W + lay.u);
     float* rowc[2] = {(float*)(W + lay.rc0), (float*)(W + lay.rc1)};
+    RowStats* stats[2] = {(RowStats*)(W + lay.st0), (RowStats*)(W + lay.st1)};
     uint32_t* cand = (uint32_t*)(W + lay.cand);
     float* cmax = (float*)(W + lay.cmax);
     int32_t* fcount = (int32_t*)(W + lay.fc);  // [levels] flagged, [levels] scored
@@ -1135,7 +1194,7 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
     {
         PrepArgs pa{};
         pa.g = g; pa.x = x; pa.pyr = pyr; pa.cb = codebooks; pa.resid_codes = codes;
-        pa.cmax = cmax; pa.ubuf = ubuf; pa.rowc = rowc[0]; pa.level = 0;
+        pa.cmax = cmax; pa.ubuf = ubuf; pa.rowc = rowc[0]; pa.stats = stats[0]; pa.level = 0;
         pa.n_rows = b * (t / strides[0]);
         e = launch_rows(nch, &pa, nullptr, pa.n_rows, st);
         if (e != hipSuccess) return NCM_E_HIP;
@@ -1168,6 +1227,7 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
         ra.g = g; ra.x = x; ra.pyr = pyr; ra.cb = codebooks; ra.csq = csq;
         ra.force_codes = force_codes; ra.codes = codes; ra.gap = gap;
         ra.cand = cand; ra.rowc_in = rowc[l & 1]; ra.cmax = cmax;
+        ra.stats_in = stats[l & 1]; ra.stats_out = stats[(l + 1) & 1];
         ra.d_in = l > 0 ? dbuf[l & 1] : nullptr;
         ra.d_out = l + 1 < levels ? dbuf[(l + 1) & 1] : nullptr;
         ra.d_div = l > 0 ? strides[l - 1] / strides[l] : 1;
