@@ -18,12 +18,14 @@
 //      bf16-rounded residual rows (B, N = rows); the epilogue forms
 //      offset + csq_k - 2 S and keeps, per row and per lane chunk of codes,
 //      the four smallest as 32-bit keys (distance bits | local code index).
-//   2. rvq_rescore_kernel (one wavefront per row): rebuilds u in fp32, bounds
-//      the MFMA pass's error rigorously, rescores every candidate that could
-//      be the exact argmin in the fixed fp32 order (bit-identical to the
-//      oracle), and writes code, gap and the next level's bf16 rows. A lane
-//      chunk whose kept keys cannot be proven to cover every code under the
-//      threshold has all of its codes rescored.
+//   2. rvq_rescore_kernel (one wavefront per row): bounds the MFMA pass's
+//      error rigorously from the row statistics stored with the bf16 row,
+//      rescores every candidate that could be the exact argmin in the fixed
+//      fp32 order (bit-identical to the oracle; u in fp32 is formed only for
+//      rows with more than one candidate), and writes code, gap, D_{l+1} and
+//      the next level's bf16 rows with their statistics (or the
+//      reconstruction). A lane chunk whose kept keys cannot be proven to
+//      cover every code under the threshold has all of its codes rescored.
 #include <algorithm>
 
 #include "gemm_core.h"
@@ -635,18 +637,6 @@ __device__ __forceinline__ void load_coarse(const RowArgs& a, int64_t row, int l
     }
 }
 
-// u = P_l - D_l for one row (D_l left in D).
-template <int NCH>
-__device__ __forceinline__ void load_residual(const RowArgs& a, int64_t row, int lane,
-                                              RowVec<NCH>& u, RowVec<NCH>& D) {
-    load_coarse<NCH>(a, row, lane, D);
-    load_f32_row<NCH>(pooled_row_ptr(a.g, a.x, a.pyr, a.level, row), a.g.d, lane, u);
-#pragma unroll
-    for (int m = 0; m < NCH; ++m)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) u.v[m][e] = u.v[m][e] - D.v[m][e];
-}
-
 // Code and gap of a finished row; D_{l+1} and the next level's bf16 rows, or
 // the reconstruction at the last level.
 // best_row holds the elements of b.code when have_row is true. KEEP_D: D_l
@@ -723,19 +713,20 @@ __device__ __forceinline__ void finish_row(const RowArgs& a, int64_t row, const 
     }
 }
 
-// Where D_l waits between the residual and the finish (DMODE): 0 reloaded
-// from global memory; 1 kept in registers (one memory round trip less, more
-// registers: the small levels, whose few rows leave occupancy to spare); 2
-// kept in LDS, 1 KB per 256 elements and wavefront (the large levels at d <=
-// 2048: their 32 KB per workgroup fits the three workgroups per CU that the
-// registers allow).
-template <int NCH, int KS, int DMODE, bool PAIR>
-__global__ __launch_bounds__(256)
-void rvq_rescore_kernel(RowArgs a) {
+// One wavefront per row. The row's offset and statistics come from the
+// kernel that built its bf16 row, so the exact residual u = P_s - D_l is
+// formed only when some candidate needs an exact distance.
+// KEEP_D: D_l stays in registers from the start to the finish (else it is
+// loaded again for each use: d above 2048 at the large levels).
+// PAIR: the next level pools by half this level's stride; its two child rows
+// are loaded at the start, give P_s = (c0 + c1) * 0.5 (the pyramid's own
+// operation, so the pyramid's bits) when u is needed, and the next level's
+// rows at the finish.
+template <int NCH, int KS, bool KEEP_D, bool PAIR>
+__global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     constexpr int kKeySlots = KS;
     __shared__ int32_t cand_list[4][kKeySlots * 64];
     __shared__ int32_t inc_list[4][kKeySlots * 16];
-    __shared__ f32x4_t d_stash[4][DMODE == 2 ? NCH * 64 : 1];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int64_t row = (int64_t)blockIdx.x * 4 + wave;
@@ -751,16 +742,7 @@ void rvq_rescore_kernel(RowArgs a) {
         for (int c = 0; c < 2; ++c)
             load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l + 1, 2 * row + c), d, lane, ch[c]);
     }
-    load_coarse<NCH>(a, row, lane, D);
-    if constexpr (DMODE == 2) {
-        // Each lane stashes, and later reads back, its own elements.
-#pragma unroll
-        for (int m = 0; m < NCH; ++m) {
-            f32x4_t v;
-            v[0] = D.v[m][0]; v[1] = D.v[m][1]; v[2] = D.v[m][2]; v[3] = D.v[m][3];
-            d_stash[wave][m * 64 + lane] = v;
-        }
-    }
+    if constexpr (KEEP_D) load_coarse<NCH>(a, row, lane, D);
     const int nk = a.cg.nchunk * 4;
     const uint32_t* ck = a.cand + row * (int64_t)nk;
     uint32_t key[kKeySlots];
@@ -850,15 +832,7 @@ void rvq_rescore_kernel(RowArgs a) {
         } else {
             load_f32_row<NCH>(pooled_row_ptr(g, a.x, a.pyr, l, row), d, lane, u);
         }
-        if constexpr (DMODE == 2) {
-#pragma unroll
-            for (int m = 0; m < NCH; ++m) {
-                const f32x4_t v = d_stash[wave][m * 64 + lane];
-                D.v[m][0] = v[0]; D.v[m][1] = v[1]; D.v[m][2] = v[2]; D.v[m][3] = v[3];
-            }
-        } else if constexpr (DMODE == 0) {
-            load_coarse<NCH>(a, row, lane, D);
-        }
+        if constexpr (!KEEP_D) load_coarse<NCH>(a, row, lane, D);
 #pragma unroll
         for (int m = 0; m < NCH; ++m)
 #pragma unroll
@@ -895,14 +869,7 @@ void rvq_rescore_kernel(RowArgs a) {
             }
         }
     }
-    if constexpr (DMODE == 2) {
-#pragma unroll
-        for (int m = 0; m < NCH; ++m) {
-            const f32x4_t v = d_stash[wave][m * 64 + lane];
-            D.v[m][0] = v[0]; D.v[m][1] = v[1]; D.v[m][2] = v[2]; D.v[m][3] = v[3];
-        }
-    }
-    finish_row<NCH, DMODE != 0, PAIR>(a, row, b, best_row, have_row, st.unorm2, lane, D, ch);
+    finish_row<NCH, KEEP_D, PAIR>(a, row, b, best_row, have_row, st.unorm2, lane, D, ch);
 }
 
 // ------------------------------------------------------------ host side
@@ -932,7 +899,7 @@ using DistSmall2 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 2>;
 using DistTiny = GemmShape<64, 64, 64, 2, 2, 2, 8, true, 4>;
 constexpr int64_t kCus = 256;
 // Levels with at most this many rows keep D_l in registers through the
-// rescore.
+// rescore at any d (their few rows leave occupancy to spare).
 constexpr int64_t kSmallLevelRows = 4096;
 
 static int nch_for(int64_t d) {
@@ -947,14 +914,14 @@ static int nch_for(int64_t d) {
 template <int NCH, bool PAIR>
 static void launch_rescore_p(const RowArgs* ra, int64_t rows, dim3 grid, hipStream_t st) {
     if (ra->cg.nchunk > kMaxChunks)
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlotsWide, 1, PAIR>), grid, dim3(256), 0,
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlotsWide, true, PAIR>), grid, dim3(256),
+                           0, st, *ra);
+    else if (NCH <= 8 || rows <= kSmallLevelRows)
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, true, PAIR>), grid, dim3(256), 0,
                            st, *ra);
-    else if (rows <= kSmallLevelRows)
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, 1, PAIR>), grid, dim3(256), 0, st,
-                           *ra);
     else
-        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, PAIR ? 1 : (NCH <= 8 ? 2 : 0), PAIR>), grid,
-                           dim3(256), 0, st, *ra);
+        hipLaunchKernelGGL((rvq_rescore_kernel<NCH, kKeySlots, false, PAIR>), grid, dim3(256), 0,
+                           st, *ra);
 }
 
 template <int NCH>
