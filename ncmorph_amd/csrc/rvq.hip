@@ -313,9 +313,10 @@ __global__ __launch_bounds__(256) void rvq_prep_kernel(PrepArgs a) {
 
 // Candidate key layout: the distance bits (offset + csq - 2S >= 0, so the
 // fp32 pattern orders like the value) with the low `ib` bits replaced by the
-// code's index inside its lane chunk. Lane chunk = (range, wave row wm, lane
-// half h); local index = (tile * MB + mb) * 16 + i for accumulator element i
-// of block mb in tile `tile` of the range.
+// code's index inside its chunk. Chunk = (range, wave row wm): the four
+// smallest keys of the codes that one wavefront row holds for a row, over
+// both lane halves h; local index = ((tile * MB + mb) * 16 + i) * 2 + h for
+// accumulator element i of block mb in tile `tile` of the range.
 struct CandGeom {
     int bm;       // codes per tile
     int wm_codes; // codes per wave along M
@@ -324,7 +325,7 @@ struct CandGeom {
     int ntv;      // tiles per range
     int nranges;
     int ib;       // index bits
-    int nchunk;   // chunks per row = nranges * wgm * 2
+    int nchunk;   // chunks per row = nranges * wgm
     int mb_log2;  // log2(mb), log2(wgm): both are powers of two
     int wgm_log2;
 };
@@ -357,7 +358,7 @@ __device__ __forceinline__ void dist_epilogue(const GemmAcc<S>& acc, const DistA
         }
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const uint32_t local = (uint32_t)((tile * S::MB + mb) * 16 + i);
+            const uint32_t local = (uint32_t)(((tile * S::MB + mb) * 16 + i) * 2 + half);
             const bool ok = FULL || (cbase + 8 * (i >> 2) + (i & 3) < a.v);
 #pragma unroll
             for (int nb = 0; nb < S::NB; ++nb) {
@@ -413,12 +414,23 @@ __attribute__((amdgpu_waves_per_eu(S::OCC, S::OCC))) void rvq_dist_kernel(DistAr
 #pragma unroll
             for (int j = 0; j < 4; ++j) top[nb][j] = 0xFFFFFFFFu;
     };
-    auto store_top = [&](const uint32_t (&top)[S::NB][4]) {
-        const int chunk = (range * S::WGM + wm) * 2 + half;
+    // Lanes l and l + 32 hold the same rows (the two halves of each 8-code
+    // group): lanes 0-31 fold the other half's four keys into their own and
+    // store one chunk per (range, wave row).
+    auto store_top = [&](uint32_t (&top)[S::NB][4]) {
+        const int chunk = range * S::WGM + wm;
+#pragma unroll
+        for (int nb = 0; nb < S::NB; ++nb) {
+            uint32_t other[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) other[j] = swap32(top[nb][j])[1];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) top4_insert(top[nb], other[j]);
+        }
 #pragma unroll
         for (int nb = 0; nb < S::NB; ++nb) {
             const int64_t r = row0 + wn * S::WN + nb * 32 + (lane & 31);
-            if (r < a.n_rows) {
+            if (half == 0 && r < a.n_rows) {
                 u32x4_t o;
                 o[0] = top[nb][0]; o[1] = top[nb][1]; o[2] = top[nb][2]; o[3] = top[nb][3];
                 *(u32x4_t*)(a.cand + (r * a.cg.nchunk + chunk) * 4) = o;
@@ -505,9 +517,10 @@ struct RowArgs {
 };
 
 __device__ __forceinline__ int64_t decode_code(const CandGeom& cg, int chunk, uint32_t local) {
-    const int half = chunk & 1;
-    const int wm = (chunk >> 1) & (cg.wgm - 1);
-    const int range = (chunk >> 1) >> cg.wgm_log2;
+    const int half = (int)(local & 1u);
+    local >>= 1;
+    const int wm = chunk & (cg.wgm - 1);
+    const int range = chunk >> cg.wgm_log2;
     const int i = (int)(local & 15u);
     const int mb = (int)((local >> 4) & (uint32_t)(cg.mb - 1));
     const int tile = (int)((local >> 4) >> cg.mb_log2);
@@ -843,7 +856,7 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     if (ninc > 0) {
         if (lane == 0) atomicAdd(a.flag_count, 1);
         // Every code of each incomplete chunk, listed in LDS then rescored.
-        const int nloc = a.cg.ntv * a.cg.mb * 16;
+        const int nloc = a.cg.ntv * a.cg.mb * 32;
         for (int c = 0; c < ninc; ++c) {
             const int chunk = inc[c];
             for (int base = 0; base < nloc; base += kKeySlots * 64) {
@@ -969,11 +982,11 @@ static CandGeom cand_geom_t(int64_t n_rows, int64_t v, int max_chunks = kMaxChun
     while (nr > 8 && rt * nr > 2048) nr /= 2;
     cg.ntv = (int)((tiles_v + nr - 1) / nr);
     cg.nranges = (int)((tiles_v + cg.ntv - 1) / cg.ntv);
-    const int locals = cg.ntv * S::MB * 16;
+    const int locals = cg.ntv * S::MB * 32;
     int ib = 0;
     while ((1 << ib) < locals) ++ib;
     cg.ib = ib;
-    cg.nchunk = cg.nranges * S::WGM * 2;
+    cg.nchunk = cg.nranges * S::WGM;
     static_assert((S::MB & (S::MB - 1)) == 0 && (S::WGM & (S::WGM - 1)) == 0,
                   "candidate decoding shifts by log2(MB) and log2(WGM)");
     cg.mb_log2 = __builtin_ctz(S::MB);
