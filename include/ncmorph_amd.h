@@ -93,6 +93,23 @@ int ncm_matmul_bf16_bias(const float* input, size_t input_len, const float* weig
                          float* output, size_t output_len, size_t token_count,
                          size_t input_width, size_t output_width);
 
+/* `kernels.matmul_bf16` and `matmul_bf16_bias` (packages/kernels/root.zig:
+ * 96-142) with the reference's own arithmetic, bit for bit: per output, fp32
+ * fma chains over bf16 operand pairs (x[i+1] w[i+1] first, then x[i] w[i]),
+ * operands and every partial flushed (root.zig:144-148), blocks of 512
+ * (1024 above K = 1024) summed in order, the bias added, one bf16 rounding.
+ * Same arguments and errors as the two drop-ins above; VALU arithmetic, for
+ * callers whose acceptance gates compare bf16 logits with the reference's
+ * (its B9 and C2-C5 checks, src/loader.zig:778-783, :1385-1400), not for
+ * speed. */
+int ncm_matmul_bf16_exact(const float* input, size_t input_len, const float* weights,
+                          size_t weights_len, float* output, size_t output_len,
+                          size_t token_count, size_t input_width, size_t output_width);
+int ncm_matmul_bf16_bias_exact(const float* input, size_t input_len, const float* weights,
+                               size_t weights_len, const float* bias, size_t bias_len,
+                               float* output, size_t output_len, size_t token_count,
+                               size_t input_width, size_t output_width);
+
 /* Replaces `kernels.matmul` (packages/kernels/root.zig:25-65): fp32
  * output[t, o] = sum_k input[t, k] * weights[o, k] on the fp32 MFMA. The
  * reference accumulates in increasing k (root.zig:55-58); the MFMA order
@@ -135,6 +152,16 @@ int ncm_silu_bf16(const float* input, size_t input_len, float* output, size_t ou
 int ncm_linear_bf16(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
                     const uint16_t* bias, void* y, int64_t m, int64_t k, int64_t n,
                     int out_mode);
+
+/* ncm_linear_bf16 in the reference's arithmetic bit for bit (the pair-order
+ * fma chains of ncm_matmul_bf16_exact; bf16 operand subnormals are flushed
+ * in the kernel): out_mode BF16_F32 gives matmul_bf16_impl's output
+ * (packages/kernels/root.zig:106-142), F32 its fp32 sum before the output
+ * rounding (bias included). Any k >= 0 with row stride k; no alignment
+ * requirement. VALU arithmetic, not the benchmarked path. */
+int ncm_linear_bf16_exact(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                          const uint16_t* bias, void* y, int64_t m, int64_t k, int64_t n,
+                          int out_mode);
 
 /* y = residual + ncm_linear_bf16(x, w, bias): the projection and the
  * residual add that follows it in the decoder layer (add_rows,

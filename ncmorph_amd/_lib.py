@@ -41,10 +41,13 @@ SIGNATURES = [
     ("ncm_matmul_f32", i32, [vp, sz, vp, sz, vp, sz, sz, sz, sz]),
     ("ncm_matmul_bf16", i32, [vp, sz, vp, sz, vp, sz, sz, sz, sz]),
     ("ncm_matmul_bf16_bias", i32, [vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz]),
+    ("ncm_matmul_bf16_exact", i32, [vp, sz, vp, sz, vp, sz, sz, sz, sz]),
+    ("ncm_matmul_bf16_bias_exact", i32, [vp, sz, vp, sz, vp, sz, vp, sz, sz, sz, sz]),
     ("ncm_round_bf16", i32, [vp, vp, sz]),
     ("ncm_rms_norm_bf16", i32, [vp, sz, vp, sz, vp, sz, C.c_float]),
     ("ncm_silu_bf16", i32, [vp, sz, vp, sz]),
     ("ncm_linear_bf16", i32, [vp, vp, vp, vp, vp, i64, i64, i64, i32]),
+    ("ncm_linear_bf16_exact", i32, [vp, vp, vp, vp, vp, i64, i64, i64, i32]),
     ("ncm_linear_bf16_residual", i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i32]),
     ("ncm_linear_bf16_swiglu", i32, [vp, vp, vp, vp, vp, i64, i64, i64]),
     ("ncm_linear_bf16_rope64", i32, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp]),

@@ -338,6 +338,24 @@ int ncm_linear_bf16(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w, const 
     return NCM_OK;
 }
 
+int ncm_linear_bf16_exact(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
+                          const uint16_t* bias, void* y, int64_t m, int64_t k, int64_t n,
+                          int out_mode) {
+    if (!ctx) return NCM_E_NULL;
+    if (m < 0 || n < 0 || k < 0) return NCM_E_SHAPE;
+    if (out_mode < NCM_OUT_F32 || out_mode > NCM_OUT_BF16) return NCM_E_ARG;
+    if (m == 0 || n == 0) return NCM_OK;
+    if (!y || (k > 0 && (!x || !w))) return NCM_E_NULL;
+    if (m > (int64_t(1) << 31) || n > (int64_t(1) << 31) || k > (int64_t(1) << 31) ||
+        ((m + 63) / 64) * ((n + 63) / 64) > 0x7FFFFFFF)
+        return NCM_E_SHAPE;
+    int rc = ctx_bind(ctx);
+    if (rc) return rc;
+    hipError_t e = ncm::launch_linear_exact(x, w, bias, y, m, k, n, out_mode, ctx->stream);
+    if (e != hipSuccess) return fail_hip(e, "exact linear kernel launch");
+    return NCM_OK;
+}
+
 int ncm_linear_bf16_residual(ncm_ctx_t* ctx, const uint16_t* x, const uint16_t* w,
                              const uint16_t* bias, const float* residual, void* y, int64_t m,
                              int64_t k, int64_t n, int out_mode) {
@@ -893,9 +911,11 @@ ncm_ctx_t* default_ctx(int* rc) {
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
+// exact: the reference's own pair-order arithmetic (launch_linear_exact)
+// instead of the MFMA linear.
 int host_linear(const float* input, size_t input_len, const float* weights, size_t weights_len,
                 const float* bias, size_t bias_len, float* output, size_t output_len, size_t T,
-                size_t K, size_t N) {
+                size_t K, size_t N, bool exact = false) {
     // root.zig:107-110: the slice lengths must match the dimensions.
     if (input_len != T * K || weights_len != N * K || output_len != T * N) return NCM_E_LENGTH;
     if (bias && bias_len != N) return NCM_E_LENGTH;
@@ -908,7 +928,9 @@ int host_linear(const float* input, size_t input_len, const float* weights, size
     if (rc) return rc;
     rc = ctx_bind(ctx);
     if (rc) return rc;
-    const size_t K8 = align_up(K, 8);
+    // The MFMA path reads rows padded to a multiple of 8 elements; the exact
+    // path reads them with stride K.
+    const size_t K8 = exact ? K : align_up(K, 8);
     size_t off = 0;
     auto carve = [&](size_t bytes) {
         size_t o = off;
@@ -942,8 +964,12 @@ int host_linear(const float* input, size_t input_len, const float* weights, size
         NCM_HIP(hipMemcpyAsync(bf, bias, N * 4, hipMemcpyHostToDevice, st));
         NCM_HIP(ncm::launch_bf16_from_f32(bf, bb, N, 0, st));  // root.zig:138: no flush
     }
-    NCM_HIP(ncm::launch_linear(xb, wb, bias ? bb : nullptr, y, T, K8, N, NCM_OUT_BF16_F32, -1,
-                               st));
+    if (exact)
+        NCM_HIP(ncm::launch_linear_exact(xb, wb, bias ? bb : nullptr, y, T, K, N,
+                                         NCM_OUT_BF16_F32, st));
+    else
+        NCM_HIP(ncm::launch_linear(xb, wb, bias ? bb : nullptr, y, T, K8, N, NCM_OUT_BF16_F32, -1,
+                                   st));
     NCM_HIP(hipMemcpyAsync(output, y, T * N * 4, hipMemcpyDeviceToHost, st));
     NCM_HIP(hipStreamSynchronize(st));
     return NCM_OK;
@@ -1005,6 +1031,22 @@ int ncm_matmul_bf16_bias(const float* input, size_t input_len, const float* weig
     if (!bias) return NCM_E_NULL;
     return host_linear(input, input_len, weights, weights_len, bias, bias_len, output,
                        output_len, token_count, input_width, output_width);
+}
+
+int ncm_matmul_bf16_exact(const float* input, size_t input_len, const float* weights,
+                          size_t weights_len, float* output, size_t output_len,
+                          size_t token_count, size_t input_width, size_t output_width) {
+    return host_linear(input, input_len, weights, weights_len, nullptr, 0, output, output_len,
+                       token_count, input_width, output_width, true);
+}
+
+int ncm_matmul_bf16_bias_exact(const float* input, size_t input_len, const float* weights,
+                               size_t weights_len, const float* bias, size_t bias_len,
+                               float* output, size_t output_len, size_t token_count,
+                               size_t input_width, size_t output_width) {
+    if (!bias) return NCM_E_NULL;
+    return host_linear(input, input_len, weights, weights_len, bias, bias_len, output,
+                       output_len, token_count, input_width, output_width, true);
 }
 
 int ncm_rms_norm_bf16(const float* input, size_t input_len, const float* weight,

@@ -13,6 +13,12 @@ int linear_tile_config(int64_t M, int64_t N, int64_t K, int forced);
 hipError_t launch_linear(const uint16_t* x, const uint16_t* w, const uint16_t* bias, void* y,
                          int64_t M, int64_t K, int64_t N, int out_mode, int config,
                          hipStream_t stream);
+// The reference's matmul_bf16 arithmetic bit for bit (VALU pair-order fma
+// chains, 512 / 1024 K blocks, operand and partial flush): x [M, K], w
+// [N, K] bf16 with row stride K, bias bf16 [N] or null, y [M, N].
+hipError_t launch_linear_exact(const uint16_t* x, const uint16_t* w, const uint16_t* bias,
+                               void* y, int64_t M, int64_t K, int64_t N, int out_mode,
+                               hipStream_t stream);
 
 // y = residual + linear (bf16 modes: round_bf16(residual + round_bf16(linear)));
 // residual fp32 [M, N], may equal y for the fp32 output mode.

@@ -66,6 +66,32 @@ def matmul_bf16_bias(input, weights, bias, output, token_count, input_width, out
           "matmul_bf16_bias")
 
 
+def matmul_bf16_exact(input, weights, output, token_count, input_width, output_width):
+    """kernels.matmul_bf16 (root.zig:96-98, :106-142) in the reference's own
+    arithmetic bit for bit (pair-order fma chains, 512 / 1024 K blocks,
+    operand and partial flush) on the GPU's VALU: for callers that compare
+    bf16 outputs with the reference's exactly."""
+    for a, n in ((input, "input"), (weights, "weights"), (output, "output")):
+        _host_f32(a, n)
+    check(lib().ncm_matmul_bf16_exact(_p(input), input.size, _p(weights), weights.size,
+                                      _p(output), output.size, token_count, input_width,
+                                      output_width),
+          "matmul_bf16_exact")
+
+
+def matmul_bf16_bias_exact(input, weights, bias, output, token_count, input_width,
+                           output_width):
+    """kernels.matmul_bf16_bias (root.zig:102-104) bit for bit, as
+    matmul_bf16_exact."""
+    for a, n in ((input, "input"), (weights, "weights"), (bias, "bias"), (output, "output")):
+        _host_f32(a, n)
+    check(lib().ncm_matmul_bf16_bias_exact(_p(input), input.size, _p(weights), weights.size,
+                                           C.c_void_p(bias.ctypes.data), bias.size,
+                                           _p(output), output.size, token_count, input_width,
+                                           output_width),
+          "matmul_bf16_bias_exact")
+
+
 def rms_norm_bf16(input, weight, output, epsilon):
     """kernels.rms_norm_bf16 (root.zig:246-254) of one vector, on the GPU,
     bit-identical to the reference."""
@@ -141,6 +167,31 @@ def linear_bf16(x, w, bias=None, out=None, out_mode: str = "f32", ctx=None):
     a.done()
     ctx = _ctx_for(x, ctx)
     check(lib().ncm_linear_bf16(ctx.handle, px, pw, pb, po, m, k, n, mode), W)
+    return out
+
+
+def linear_bf16_exact(x, w, bias=None, out=None, out_mode: str = "bf16_f32", ctx=None):
+    """linear_bf16 in the reference's arithmetic bit for bit (the VALU
+    pair-order fma chains of matmul_bf16_impl, root.zig:106-142): "bf16_f32"
+    gives its output, "f32" its fp32 sum before the output rounding. Any k;
+    not the fast path."""
+    import torch
+
+    W = "linear_bf16_exact"
+    a = _ck.Args(W)
+    m, k = _ck.dims(x, "x", W, 2)
+    n, _ = _ck.dims(w, "w", W, 2)
+    mode = _mode(out_mode, W)
+    dv = x.device
+    px = a.dev(x, "x", _ck.BF16, (m, k))
+    pw = a.dev(w, "w", _ck.BF16, (n, k))
+    pb = a.dev(bias, "bias", _ck.BF16, (n,), optional=True)
+    if out is None:
+        out = _new_out(torch, mode, (m, n), dv, torch.int16)
+    po = a.dev(out, "out", _out_dtypes(mode), (m, n))
+    a.done()
+    ctx = _ctx_for(x, ctx)
+    check(lib().ncm_linear_bf16_exact(ctx.handle, px, pw, pb, po, m, k, n, mode), W)
     return out
 
 
