@@ -372,12 +372,18 @@ typedef struct ncm_decoder_layer {
  * live in the context's workspace. A layer with q_norm / k_norm applies the
  * QK-norm (Qwen3 layouts). Linear outputs, scores and P V are summed in MFMA
  * order, so logits agree with the reference within bf16 tolerance, not bit
- * for bit. */
+ * for bit. trace: NULL or the stages of forward_with_trace to keep
+ * (decoder_trace_t, src/decoder.zig:30-47; ncm_decoder_trace_t below), as
+ * float holding the bf16 values; the projections the fused kernels never
+ * store (attention_output, gate_projection, up_projection, mlp_output) are
+ * computed again for the trace with the same sums. */
+typedef struct ncm_decoder_trace ncm_decoder_trace_t;
 int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
                             const ncm_decoder_layer_t* layers, const uint16_t* embed,
                             const float* final_norm, const uint16_t* lm_head,
                             const float* cosine, const float* sine, const int64_t* token_ids,
-                            int64_t batch, int64_t seq_len, float* logits);
+                            int64_t batch, int64_t seq_len, float* logits,
+                            const ncm_decoder_trace_t* trace);
 
 /* One layer's device weights in the f32 mode (decoder.zig:10-20,
  * attention_weights_t of root.zig:351-362), all float: qkv_weight holds the
@@ -412,7 +418,7 @@ typedef struct ncm_decoder_layer_f32 {
  * [layers, batch * seq_len, width] layer-major (block_input: [batch *
  * seq_len, hidden]); width is hidden, q_heads * head_dim (attention_context)
  * or intermediate (gate_projection, up_projection, gate_up_product). */
-typedef struct ncm_decoder_trace {
+struct ncm_decoder_trace {
     float* block_input;
     float* input_norm;
     float* attention_context;
@@ -424,7 +430,7 @@ typedef struct ncm_decoder_trace {
     float* gate_up_product;
     float* mlp_output;
     float* block_output;
-} ncm_decoder_trace_t;
+};
 
 /* The prefill forward in the reference's f32 mode (forward_with_trace with
  * bf16_compute false, decoder.zig:62-228: rms_norm, kernels.matmul + bias,
@@ -496,8 +502,8 @@ typedef struct ncm_ncm_weights {
     const float* const* conv_bias;
 } ncm_ncm_weights_t;
 
-/* The NCM body forward (forward_with_trace without the trace,
- * src/ncm_model.zig:89-250) for one prefix and one target sequence, in the
+/* The NCM body forward (forward_with_trace, src/ncm_model.zig:89-250) for
+ * one prefix and one target sequence, in the
  * bf16 mode of the source decoder: bf16 projections with fp32 accumulation
  * (operands rounded and flushed as matmul_bf16 does), rms_norm_bf16,
  * silu_bf16, bf16 attention, every add rounded to bf16; the convolutions
@@ -511,13 +517,16 @@ typedef struct ncm_ncm_weights {
  * prefix_length + sum level_lengths, the RoPE tables gathered at the
  * positions of fill_level_positions (src/ncm_position.zig:11-118).
  * output: float [S, hidden] (bf16 values), the final-normalized hidden
- * states in [prefix | levels] order. Intermediates live in the context's
+ * states in [prefix | levels] order. hidden_states: NULL or float
+ * [layers + 1, S, hidden], the reference's trace (ncm_model.zig:169-171,
+ * :243-249): the input stage, the output of layers 0 .. layers - 2, then the
+ * final-normalized states. Intermediates live in the context's
  * workspace. */
 int ncm_ncm_forward_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
                         const ncm_decoder_layer_t* layers, const ncm_ncm_weights_t* weights,
                         const int64_t* prefix_ids, const uint8_t* prefix_pad_mask,
                         int64_t pad_len, const float* target_inputs, const float* cosine,
-                        const float* sine, float* output);
+                        const float* sine, float* output, float* hidden_states);
 
 /* weights_t (src/ncm_model.zig:61-72) for the f32 body: every tensor float.
  * conv_weight / conv_bias as in ncm_ncm_weights_t. */
@@ -549,7 +558,7 @@ int ncm_ncm_forward_f32_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
                             const ncm_ncm_weights_f32_t* weights, const int64_t* prefix_ids,
                             const uint8_t* prefix_pad_mask, int64_t pad_len,
                             const float* target_inputs, const float* cosine, const float* sine,
-                            float* output);
+                            float* output, float* hidden_states);
 
 /* ---- multiscale residual vector quantization ---- */
 

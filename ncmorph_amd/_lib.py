@@ -64,10 +64,10 @@ SIGNATURES = [
     ("ncm_block_diagonal_segments", i32, [i64, vp, i64, vp, i64, i64, vp, vp, vp]),
     ("ncm_tied_head_logits", i32, [vp, vp, vp, vp, vp, C.c_float, vp, i64, i64, i64]),
     ("ncm_tied_head_logits_levels", i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, vp]),
-    ("ncm_decoder_forward_dev", i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp]),
+    ("ncm_decoder_forward_dev", i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp, vp]),
     ("ncm_decoder_forward_f32_dev", i32, [vp, vp, vp, vp, vp, vp, vp, vp, vp, i64, i64, vp, vp]),
-    ("ncm_ncm_forward_dev", i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp]),
-    ("ncm_ncm_forward_f32_dev", i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp]),
+    ("ncm_ncm_forward_dev", i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
+    ("ncm_ncm_forward_f32_dev", i32, [vp, vp, vp, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
     ("ncm_rvq_prepare", i32, [vp, vp, i64, i64, i64, vp]),
     ("ncm_rvq_encode", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp]),
     ("ncm_rvq_encode_counts", i32, [vp, vp, i64, i64, i64, i64, vp, vp, vp, i64, vp, vp, vp, vp,

@@ -677,7 +677,8 @@ int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
                             const ncm_decoder_layer_t* layers, const uint16_t* embed,
                             const float* final_norm, const uint16_t* lm_head,
                             const float* cosine, const float* sine, const int64_t* token_ids,
-                            int64_t batch, int64_t seq_len, float* logits) {
+                            int64_t batch, int64_t seq_len, float* logits,
+                            const ncm_decoder_trace_t* trace) {
     if (!ctx || !shape) return NCM_E_NULL;
     const ncm_decoder_shape_t& s = *shape;
     if (batch < 0 || seq_len < 0) return NCM_E_SHAPE;
@@ -701,10 +702,11 @@ int ncm_decoder_forward_dev(ncm_ctx_t* ctx, const ncm_decoder_shape_t* shape,
     rc = ctx_bind(ctx);
     if (rc) return rc;
     void* ws = nullptr;
-    rc = ncm_ctx_workspace(ctx, ncm::decoder_workspace_bytes(s, batch, seq_len), &ws);
+    rc = ncm_ctx_workspace(ctx, ncm::decoder_workspace_bytes(s, batch, seq_len, trace), &ws);
     if (rc) return rc;
     hipError_t e = ncm::decoder_forward(s, layers, embed, final_norm, lm_head, cosine, sine,
-                                        token_ids, batch, seq_len, logits, ws, ctx->stream);
+                                        token_ids, batch, seq_len, logits, trace, ws,
+                                        ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "decoder forward");
     return NCM_OK;
 }
@@ -764,7 +766,7 @@ int ncm_ncm_forward_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
                         const ncm_decoder_layer_t* layers, const ncm_ncm_weights_t* weights,
                         const int64_t* prefix_ids, const uint8_t* prefix_pad_mask,
                         int64_t pad_len, const float* target_inputs, const float* cosine,
-                        const float* sine, float* output) {
+                        const float* sine, float* output, float* hidden_states) {
     if (!ctx || !shape || !weights) return NCM_E_NULL;
     const ncm_ncm_shape_t& s = *shape;
     if (s.prefix_length < 0 || s.n_levels < 0 || s.n_levels > NCM_MAX_LEVELS) return NCM_E_SHAPE;
@@ -804,6 +806,10 @@ int ncm_ncm_forward_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
     if (pad_len > 0 && !prefix_pad_mask) return NCM_E_NULL;
     if (s.prefix_length > 0 && !prefix_ids) return NCM_E_NULL;
     if ((uintptr_t)weights->input_projection % 16) return NCM_E_ARG;
+    // The convolutions run on the fp32 MFMA's 16-byte loads.
+    if (convs)
+        for (int l = 0; l < s.n_levels; ++l)
+            if ((uintptr_t)weights->conv_weight[l] % 16) return NCM_E_ARG;
     int rc = check_layers(layers, s.layers);
     if (rc) return rc;
     for (int64_t i = 0; i < s.prefix_length; ++i)
@@ -815,7 +821,8 @@ int ncm_ncm_forward_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
     rc = ncm_ctx_workspace(ctx, ncm::ncm_workspace_bytes(s, convs), &ws);
     if (rc) return rc;
     hipError_t e = ncm::ncm_forward(s, layers, *weights, prefix_ids, prefix_pad_mask, pad_len,
-                                    target_inputs, cosine, sine, output, ws, ctx->stream);
+                                    target_inputs, cosine, sine, output, hidden_states, ws,
+                                    ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "ncm forward");
     return NCM_OK;
 }
@@ -827,7 +834,7 @@ int ncm_ncm_forward_f32_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
                             const ncm_ncm_weights_f32_t* weights, const int64_t* prefix_ids,
                             const uint8_t* prefix_pad_mask, int64_t pad_len,
                             const float* target_inputs, const float* cosine, const float* sine,
-                            float* output) {
+                            float* output, float* hidden_states) {
     if (!ctx || !shape || !weights) return NCM_E_NULL;
     const ncm_ncm_shape_t& s = *shape;
     if (s.prefix_length < 0 || s.n_levels < 0 || s.n_levels > NCM_MAX_LEVELS) return NCM_E_SHAPE;
@@ -891,7 +898,8 @@ int ncm_ncm_forward_f32_dev(ncm_ctx_t* ctx, const ncm_ncm_shape_t* shape,
     rc = ncm_ctx_workspace(ctx, ncm::ncm_f32_workspace_bytes(s, convs), &ws);
     if (rc) return rc;
     hipError_t e = ncm::ncm_forward_f32(s, layers, *weights, prefix_ids, prefix_pad_mask, pad_len,
-                                        target_inputs, cosine, sine, output, ws, ctx->stream);
+                                        target_inputs, cosine, sine, output, hidden_states, ws,
+                                        ctx->stream);
     if (e != hipSuccess) return fail_hip(e, "ncm forward (f32)");
     return NCM_OK;
 }

@@ -8,7 +8,8 @@
 
 namespace ncm {
 
-size_t decoder_workspace_bytes(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq);
+size_t decoder_workspace_bytes(const ncm_decoder_shape_t& s, int64_t batch, int64_t seq,
+                               const ncm_decoder_trace_t* trace = nullptr);
 
 // The layer stack of the bf16 forward over `batch` sequences of `seq` rows:
 // hidden [batch * seq, hidden] fp32 (bf16 values) is updated in place.
@@ -33,15 +34,23 @@ struct LayerStack {
     uint16_t* ctx;
     uint16_t* act;
     uint16_t* vt;  // attention_workspace_bytes(batch, seq, kv_heads, head_dim)
+    // Nullable: the stages of decoder_trace_t to keep, each [layers, T,
+    // width] (block_input is not written here). trace_gu: bf16 [T, 2 I]
+    // scratch for the unfused gate|up projection, needed when the gate or
+    // up projection is traced.
+    const ncm_decoder_trace_t* trace;
+    uint16_t* trace_gu;
 };
 hipError_t run_layers(const LayerStack& a, hipStream_t st);
+// Bytes of trace_gu for T rows (0 when the trace keeps neither projection).
+size_t trace_gu_bytes(const ncm_decoder_shape_t& s, int64_t T, const ncm_decoder_trace_t* trace);
 
 // All pointers device memory except `layers` (host array) and `host_ids`.
 hipError_t decoder_forward(const ncm_decoder_shape_t& s, const ncm_decoder_layer_t* layers,
                            const uint16_t* embed, const float* final_norm,
                            const uint16_t* lm_head, const float* cosine, const float* sine,
                            const int64_t* host_ids, int64_t batch, int64_t seq, float* logits,
-                           void* ws, hipStream_t st);
+                           const ncm_decoder_trace_t* trace, void* ws, hipStream_t st);
 
 // f32 mode (decoder_f32.hip): workspace bytes and the forward. All pointers
 // device memory except `layers` (host array) and `host_ids`; trace may be

@@ -256,8 +256,8 @@ size_t ncm_workspace_bytes(const ncm_ncm_shape_t& s, bool convs) {
 hipError_t ncm_forward(const ncm_ncm_shape_t& s, const ncm_decoder_layer_t* layers,
                        const ncm_ncm_weights_t& w, const int64_t* host_ids,
                        const uint8_t* host_pad, int64_t pad_len, const float* target,
-                       const float* cosine, const float* sine, float* output, void* ws,
-                       hipStream_t st) {
+                       const float* cosine, const float* sine, float* output,
+                       float* hidden_states, void* ws, hipStream_t st) {
     const bool convs = w.conv_weight != nullptr;
     const NcmPlan p = ncm_plan(s, convs);
     char* base = (char*)ws;
@@ -320,10 +320,23 @@ hipError_t ncm_forward(const ncm_ncm_shape_t& s, const ncm_decoder_layer_t* laye
                            w.level_embedding, lt, H);
         NCM_TRY(hipGetLastError());
     }
+    // hidden_states [layers + 1, S, H] (src/ncm_model.zig:169-171, :243-249):
+    // the input stage, each layer's output (the last one's place then takes
+    // the final-normalized output).
+    ncm_decoder_trace_t tr{};
+    if (hidden_states) {
+        NCM_TRY(hipMemcpyAsync(hidden_states, a.hidden, (size_t)S * H * 4,
+                               hipMemcpyDeviceToDevice, st));
+        tr.block_output = hidden_states + S * H;
+        a.trace = &tr;
+    }
     NCM_TRY(run_layers(a, st));
     NCM_TRY(launch_rms_norm_rows(a.hidden, w.final_norm, output, S, H, s.rms_eps,
                                  NCM_OUT_BF16_F32, st));
     if (w.final_norm_bias) NCM_TRY(launch_bias_round(output, w.final_norm_bias, S, H, false, st));
+    if (hidden_states)
+        NCM_TRY(hipMemcpyAsync(hidden_states + (int64_t)s.layers * S * H, output,
+                               (size_t)S * H * 4, hipMemcpyDeviceToDevice, st));
     return hipSuccess;
 }
 
@@ -385,8 +398,8 @@ size_t ncm_f32_workspace_bytes(const ncm_ncm_shape_t& s, bool convs) {
 hipError_t ncm_forward_f32(const ncm_ncm_shape_t& s, const ncm_decoder_layer_f32_t* layers,
                            const ncm_ncm_weights_f32_t& w, const int64_t* host_ids,
                            const uint8_t* host_pad, int64_t pad_len, const float* target,
-                           const float* cosine, const float* sine, float* output, void* ws,
-                           hipStream_t st) {
+                           const float* cosine, const float* sine, float* output,
+                           float* hidden_states, void* ws, hipStream_t st) {
     const bool convs = w.conv_weight != nullptr;
     const NcmPlanF32 p = ncm_plan_f32(s, convs);
     char* base = (char*)ws;
@@ -445,10 +458,21 @@ hipError_t ncm_forward_f32(const ncm_ncm_shape_t& s, const ncm_decoder_layer_f32
                            w.level_embedding, hin.lt, H);
         NCM_TRY(hipGetLastError());
     }
+    // hidden_states as in ncm_forward.
+    ncm_decoder_trace_t tr{};
+    if (hidden_states) {
+        NCM_TRY(hipMemcpyAsync(hidden_states, a.hidden, (size_t)S * H * 4,
+                               hipMemcpyDeviceToDevice, st));
+        tr.block_output = hidden_states + S * H;
+        a.trace = &tr;
+    }
     NCM_TRY(run_layers_f32(a, st));
     NCM_TRY(launch_rms_norm_rows(a.hidden, w.final_norm, output, S, H, s.rms_eps, NCM_OUT_F32,
                                  st));
     if (w.final_norm_bias) NCM_TRY(launch_add_f32(output, w.final_norm_bias, S, H, 1, st));
+    if (hidden_states)
+        NCM_TRY(hipMemcpyAsync(hidden_states + (int64_t)s.layers * S * H, output,
+                               (size_t)S * H * 4, hipMemcpyDeviceToDevice, st));
     return hipSuccess;
 }
 

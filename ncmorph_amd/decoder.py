@@ -207,11 +207,14 @@ def _ptr(t):
 
 
 def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine, logits=None,
-            ctx=None):
+            ctx=None, trace: bool = False):
     """Logits [batch * seq, vocab] (float32 holding bf16 values) of the bf16
     prefill forward of every row of token_ids (int [batch, seq]); cosine and
     sine: float32 device tensors [seq, head_dim]. Runs on torch's current
-    stream."""
+    stream. trace=True also returns the stages of decoder_trace_t
+    (decoder.zig:30-47) as a dict of float32 tensors [layers, batch * seq,
+    width] (block_input [batch * seq, hidden]) holding bf16 values:
+    (logits, trace)."""
     import torch
 
     ids = np.ascontiguousarray(token_ids, dtype=np.int64)
@@ -238,6 +241,7 @@ def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine,
     arr = (_Layer * max(1, spec.layers))()
     for i, layer in enumerate(weights.layers):
         arr[i] = _Layer(*[_ptr(layer.get(n)) for n in _LAYER_FIELDS])
+    tr = _trace_buffers(torch, spec, batch * seq, dev) if trace else None
     a.done()
     ctx = ctx or default_context(dev.index or 0)
     ctx.bind_stream()
@@ -245,9 +249,23 @@ def forward(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, sine,
                                         _ptr(weights.final_norm), _ptr(weights.lm_head),
                                         _ptr(cosine), _ptr(sine),
                                         ids.ctypes.data_as(C.c_void_p), batch, seq,
-                                        _ptr(logits)),
+                                        _ptr(logits),
+                                        C.byref(_Trace(*[_ptr(tr[f]) for f in TRACE_FIELDS]))
+                                        if tr else None),
           "decoder_forward")
-    return logits
+    return (logits, tr) if trace else logits
+
+
+def _trace_buffers(torch, spec, T, dev):
+    """float32 [layers, T, width] per stage of decoder_trace_t (block_input
+    [T, hidden])."""
+    widths = {"attention_context": spec.q_heads * spec.head_dim,
+              "gate_projection": spec.intermediate, "up_projection": spec.intermediate,
+              "gate_up_product": spec.intermediate}
+    return {f: torch.empty((T, spec.hidden) if f == "block_input" else
+                           (spec.layers, T, widths.get(f, spec.hidden)),
+                           dtype=torch.float32, device=dev)
+            for f in TRACE_FIELDS}
 
 
 _LAYER_F32_FIELDS = ("input_norm", "qkv_weight", "qkv_bias", "o_weight", "o_bias",
@@ -308,14 +326,7 @@ def forward_f32(spec: DecoderSpec, weights: DecoderWeights, token_ids, cosine, s
     for i, layer in enumerate(weights.layers):
         for f in _LAYER_F32_FIELDS:
             a.dev(layer.get(f), f"layers[{i}].{f}", _ck.F32, shapes[f], optional=f in optional)
-    tr = None
-    if trace:
-        T = batch * seq
-        widths = {"attention_context": qw, "gate_projection": I, "up_projection": I,
-                  "gate_up_product": I}
-        tr = {f: torch.empty((T, H) if f == "block_input" else
-                             (spec.layers, T, widths.get(f, H)), dtype=torch.float32, device=dev)
-              for f in TRACE_FIELDS}
+    tr = _trace_buffers(torch, spec, batch * seq, dev) if trace else None
     a.done()
     shape = _Shape(H, I, spec.vocab, spec.q_heads, spec.kv_heads, hd, spec.layers, spec.window,
                    spec.rms_eps)

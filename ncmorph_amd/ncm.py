@@ -205,12 +205,14 @@ def rope_tables(spec: NcmSpec):
 
 
 def forward(spec: NcmSpec, weights: NcmWeights, prefix_ids, target_inputs, cosine, sine,
-            prefix_pad_mask=None, out=None, ctx=None):
+            prefix_pad_mask=None, out=None, ctx=None, hidden_states: bool = False):
     """Final-normalized hidden states float32 [S, hidden] (bf16 values) of
     the NCM body for one prefix (host ints [prefix_length]) and the target
     inputs (float32 device [sum level_lengths, vq_width]); cosine / sine:
     float32 device [S, head_dim] (rope_tables). Runs on torch's current
-    stream."""
+    stream. hidden_states=True also returns forward_with_trace's states
+    (src/ncm_model.zig:89-250) float32 [layers + 1, S, hidden]: (out,
+    states)."""
     import torch
 
     W = "ncm_forward"
@@ -247,6 +249,8 @@ def forward(spec: NcmSpec, weights: NcmWeights, prefix_ids, target_inputs, cosin
     if out is None:
         out = torch.empty((S, spec.hidden), dtype=torch.float32, device=target_inputs.device)
     po = a.dev(out, "out", _ck.F32, (S, spec.hidden))
+    states = (torch.empty((spec.layers + 1, S, spec.hidden), dtype=torch.float32,
+                          device=target_inputs.device) if hidden_states else None)
     a.done()
 
     ptr = lambda t: None if t is None else t.data_ptr()
@@ -274,8 +278,9 @@ def forward(spec: NcmSpec, weights: NcmWeights, prefix_ids, target_inputs, cosin
         ctx.handle, C.byref(shape), arr, C.byref(wts), ids.ctypes.data_as(C.c_void_p),
         None if pad is None else pad.ctypes.data_as(C.c_void_p), 0 if pad is None else pad.size,
         C.c_void_p(target_inputs.data_ptr()), C.c_void_p(cosine.data_ptr()),
-        C.c_void_p(sine.data_ptr()), po), W)
-    return out
+        C.c_void_p(sine.data_ptr()), po,
+        None if states is None else C.c_void_p(states.data_ptr())), W)
+    return (out, states) if hidden_states else out
 
 
 def code_head_logits(spec: NcmSpec, hidden, z_weights, codebooks, csq, log_inv_t=None,
@@ -354,11 +359,12 @@ def device_weights_f32(spec: NcmSpec, ref: dict, device) -> NcmWeights:
 
 
 def forward_f32(spec: NcmSpec, weights: NcmWeights, prefix_ids, target_inputs, cosine, sine,
-                prefix_pad_mask=None, out=None, ctx=None):
+                prefix_pad_mask=None, out=None, ctx=None, hidden_states: bool = False):
     """The NCM body in the reference's f32 arithmetic (forward_with_trace,
     src/ncm_model.zig:89-250): final-normalized hidden states float32 [S,
     hidden]. Arguments as forward, with float32 weights (device_weights_f32;
-    layers[i] maps the names of decoder._LAYER_F32_FIELDS)."""
+    layers[i] maps the names of decoder._LAYER_F32_FIELDS); hidden_states as
+    forward."""
     import torch
 
     W = "ncm_forward_f32"
@@ -406,6 +412,8 @@ def forward_f32(spec: NcmSpec, weights: NcmWeights, prefix_ids, target_inputs, c
     if out is None:
         out = torch.empty((S, H), dtype=torch.float32, device=target_inputs.device)
     po = a.dev(out, "out", _ck.F32, (S, H))
+    states = (torch.empty((spec.layers + 1, S, H), dtype=torch.float32,
+                          device=target_inputs.device) if hidden_states else None)
     a.done()
 
     ptr = lambda t: None if t is None else t.data_ptr()
@@ -432,5 +440,6 @@ def forward_f32(spec: NcmSpec, weights: NcmWeights, prefix_ids, target_inputs, c
         ctx.handle, C.byref(shape), arr, C.byref(wts), ids.ctypes.data_as(C.c_void_p),
         None if pad is None else pad.ctypes.data_as(C.c_void_p), 0 if pad is None else pad.size,
         C.c_void_p(target_inputs.data_ptr()), C.c_void_p(cosine.data_ptr()),
-        C.c_void_p(sine.data_ptr()), po), W)
-    return out
+        C.c_void_p(sine.data_ptr()), po,
+        None if states is None else C.c_void_p(states.data_ptr())), W)
+    return (out, states) if hidden_states else out

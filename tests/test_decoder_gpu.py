@@ -83,6 +83,68 @@ def test_decoder_forward_against_oracle(ncm, oracle, cuda, hd, window, biases, b
         assert np.max(np.abs(got[b] - f64)) <= 0.02 * scale
 
 
+@pytest.mark.parametrize("hd,biases,qk_norm", [(64, True, False), (128, False, True)])
+def test_decoder_trace_against_oracle(ncm, oracle, cuda, hd, biases, qk_norm):
+    """The bf16 forward's trace (decoder_trace_t, src/decoder.zig:30-47): the
+    traced run gives the untraced logits bit for bit; on the device's own
+    stages the layer's arithmetic holds exactly (block input = embedding
+    rows, attention_residual = round(h + attention_output), block_output =
+    round(attention_residual + mlp_output), gate_up_product =
+    round(silu_bf16(gate) * up) by the device's SiLU kernel, every stage
+    bf16-valued); and every stage agrees with the oracle's trace within 1% of
+    the stage's largest magnitude (the logits' bound: the MFMA order moves
+    an intermediate bf16 rounding now and then)."""
+    import torch
+    from ncmorph_amd import decoder, kernels
+
+    rng = np.random.default_rng(17 + hd)
+    hidden, inter, vocab, hq, hkv, nl, seq = 256, 512, 300, 4, 2, 2, 48
+    embed, layers, fnorm = random_model(rng, oracle.round_bf16, hidden, inter, vocab, hq, hkv,
+                                        hd, nl, biases=biases, qk_norm=qk_norm)
+    spec = decoder.DecoderSpec(hidden=hidden, intermediate=inter, vocab=vocab, q_heads=hq,
+                               kv_heads=hkv, head_dim=hd, layers=nl)
+    cos, sin = decoder.rope_tables(spec, seq)
+    dl = []
+    for L in layers:
+        d = {k: (_dev_f32(v, cuda) if k.endswith("norm") else _dev_bf16(v, cuda))
+             for k, v in L.items()}
+        for name in ("gate_up_weight", "gate_up_bias"):
+            if L.get(name) is not None:
+                d[name] = _dev_bf16(kernels.interleave_gate_up(L[name][:inter], L[name][inter:]),
+                                    cuda)
+        dl.append(d)
+    w = decoder.DecoderWeights(embed=_dev_bf16(embed, cuda), final_norm=_dev_f32(fnorm, cuda),
+                               layers=dl)
+    ids = rng.integers(0, vocab, (1, seq))
+    cd, sd = _dev_f32(cos, cuda), _dev_f32(sin, cuda)
+    plain = decoder.forward(spec, w, ids, cd, sd)
+    logits, tr = decoder.forward(spec, w, ids, cd, sd, trace=True)
+    torch.cuda.synchronize()
+    assert torch.equal(plain, logits)
+    t = {k: v.cpu().numpy() for k, v in tr.items()}
+    for k, v in t.items():
+        assert np.array_equal(v, oracle.round_bf16(v)), k
+    assert np.array_equal(t["block_input"], embed[ids[0]])
+    for l in range(nl):
+        prev = t["block_input"] if l == 0 else t["block_output"][l - 1]
+        assert np.array_equal(t["attention_residual"][l],
+                              oracle.round_bf16(prev + t["attention_output"][l])), l
+        assert np.array_equal(t["block_output"][l],
+                              oracle.round_bf16(t["attention_residual"][l] + t["mlp_output"][l])), l
+        act = kernels.silu_mul(tr["gate_projection"][l].contiguous(),
+                               tr["up_projection"][l].contiguous())
+        torch.cuda.synchronize()
+        assert np.array_equal(act.cpu().numpy(), t["gate_up_product"][l]), l
+    ref_trace = {}
+    oracle.decoder_forward(ids[0], embed, layers, fnorm, None, cos, sin, hq, hkv, hd, 1e-5,
+                           trace=ref_trace)
+    for k in decoder.TRACE_FIELDS:
+        r = ref_trace[k]
+        scale = max(float(np.max(np.abs(r))), 1e-30)
+        err = float(np.max(np.abs(t[k] - r)))
+        assert err <= 0.01 * scale, (k, err / scale)
+
+
 def test_decoder_rejects_out_of_range_token(ncm, cuda):
     import torch
     from ncmorph_amd import decoder

@@ -88,6 +88,41 @@ def test_ncm_f32_body_matches_oracle(cuda, ncm, oracle, mask, hd, extras, window
     assert err.max() <= TOL * scale, err.max() / scale
 
 
+def test_ncm_f32_hidden_states_match_oracle(cuda, ncm, oracle):
+    """hidden_states in the reference's own arithmetic (forward_with_trace,
+    src/ncm_model.zig:169-171, :243-249): [layers + 1, S, hidden], the
+    input stage, every layer but the last, then the final-normalized output
+    (equal to the body's output bit for bit); each state within TOL of the
+    largest magnitude of the oracle's."""
+    import torch
+    from ncmorph_amd import ncm as N
+
+    rng = np.random.default_rng(29)
+    levels, P = [8, 16, 32], 10
+    hidden, vq, hq, hkv, hd, inter, nl, vocab = 192, 96, 4, 2, 64, 384, 3, 40
+    spec = _spec(N, levels, P, hidden, vq, hq, hkv, hd, inter, nl, "block_diagonal", vocab)
+    w = random_ncm(rng, _ident, hidden, vq, inter, hq, hkv, hd, nl, levels, P, vocab,
+                   biases=True)
+    ids = rng.integers(0, vocab, P)
+    tgt = rng.standard_normal((sum(levels), vq)).astype(np.float32)
+    dw = N.device_weights_f32(spec, w, cuda)
+    cos, sin = N.rope_tables(spec)
+    args = (spec, dw, ids, torch.from_numpy(tgt).to(cuda), torch.from_numpy(cos).to(cuda),
+            torch.from_numpy(sin).to(cuda))
+    plain = N.forward_f32(*args)
+    out, states = N.forward_f32(*args, hidden_states=True)
+    torch.cuda.synchronize()
+    assert states.shape == (nl + 1, spec.seq_len, hidden)
+    assert torch.equal(plain, out)
+    assert torch.equal(states[nl], out)
+    _, ref_states = oracle.ncm_forward(_cfg(spec), w, ids, None, tgt, bf16=False,
+                                       mask="block_diagonal", trace=True)
+    got = states.cpu().numpy()
+    for i, r in enumerate(ref_states):
+        scale = np.max(np.abs(r))
+        assert np.max(np.abs(got[i] - r)) <= TOL * scale, i
+
+
 def test_ncm_f32_reference_invariants(cuda, ncm, oracle):
     """src/ncm_model.zig:332-429 in the reference's arithmetic on the device:
     level-0 inputs do not reach the output when query_level0 (bit for bit);

@@ -82,6 +82,75 @@ def test_ncm_body_matches_oracle(cuda, ncm, oracle, mask, hd, extras, window, ql
     print("max / mean error relative to max|ref|:", err.max() / scale, err.mean() / scale)
 
 
+@pytest.mark.parametrize("mask", ["block_causal", "block_diagonal"])
+def test_ncm_hidden_states_match_oracle(cuda, ncm, oracle, mask):
+    """hidden_states (forward_with_trace, src/ncm_model.zig:169-171, :243-249):
+    [layers + 1, S, hidden] = the input stage, the output of every layer but
+    the last, then the final-normalized output (equal to the body's output
+    bit for bit); with the states the output is the same bits as without;
+    every state agrees with the oracle's within the body's bound."""
+    import torch
+    from ncmorph_amd import ncm as N
+
+    rng = np.random.default_rng(23)
+    levels, P = [8, 16, 32], 10
+    hidden, vq, hq, hkv, hd, inter, nl, vocab = 256, 128, 4, 2, 64, 512, 3, 40
+    spec = _spec(N, levels, P, hidden, vq, hq, hkv, hd, inter, nl, mask, vocab)
+    w = random_ncm(rng, oracle.round_bf16, hidden, vq, inter, hq, hkv, hd, nl, levels, P, vocab,
+                   biases=True)
+    ids = rng.integers(0, vocab, P)
+    tgt = oracle.round_bf16(rng.standard_normal((sum(levels), vq)).astype(np.float32))
+    dw = N.device_weights(spec, w, cuda)
+    cos, sin = N.rope_tables(spec)
+    args = (spec, dw, ids, torch.from_numpy(tgt).to(cuda), torch.from_numpy(cos).to(cuda),
+            torch.from_numpy(sin).to(cuda))
+    plain = N.forward(*args)
+    out, states = N.forward(*args, hidden_states=True)
+    torch.cuda.synchronize()
+    assert states.shape == (nl + 1, spec.seq_len, hidden)
+    assert torch.equal(plain, out)
+    assert torch.equal(states[nl], out)
+    ref, ref_states = oracle.ncm_forward(_oracle_cfg(spec), w, ids, None, tgt, bf16=True,
+                                         mask=mask, trace=True)
+    got = states.cpu().numpy()
+    for i, r in enumerate(ref_states):
+        scale = np.max(np.abs(r))
+        err = np.abs(got[i] - r)
+        assert err.max() <= 0.03 * scale, (i, err.max() / scale)
+        assert err.mean() <= 0.003 * scale, (i, err.mean() / scale)
+    # The input stage has no summation-order freedom beyond the input
+    # projection: it is bf16-valued.
+    assert np.array_equal(got[0], oracle.round_bf16(got[0]))
+
+
+def test_ncm_rejects_misaligned_conv_weight(cuda, ncm, oracle):
+    """The convolutions read their weights with 16-byte loads: a conv weight
+    that is not 16-byte aligned is refused (NCM_E_ARG) before any launch, as
+    the f32 body does."""
+    import torch
+    from ncmorph_amd import ncm as N
+    from ncmorph_amd._lib import NCM_E_ARG, NcmError
+
+    rng = np.random.default_rng(31)
+    levels, P = [8, 16], 4
+    hidden, vq, hq, hkv, hd, inter, nl, vocab = 128, 64, 2, 1, 64, 256, 1, 20
+    spec = _spec(N, levels, P, hidden, vq, hq, hkv, hd, inter, nl, "block_causal", vocab)
+    w = random_ncm(rng, oracle.round_bf16, hidden, vq, inter, hq, hkv, hd, nl, levels, P, vocab,
+                   convs=True)
+    dw = N.device_weights(spec, w, cuda)
+    buf = torch.empty(vq * vq * 3 + 1, dtype=torch.float32, device=cuda)
+    odd = buf[1:].view(vq, vq, 3)
+    odd.copy_(dw.convs[0]["weight"])
+    assert odd.data_ptr() % 16 != 0
+    dw.convs[0]["weight"] = odd
+    cos, sin = N.rope_tables(spec)
+    tgt = torch.zeros((sum(levels), vq), dtype=torch.float32, device=cuda)
+    with pytest.raises(NcmError) as e:
+        N.forward(spec, dw, rng.integers(0, vocab, P), tgt, torch.from_numpy(cos).to(cuda),
+                  torch.from_numpy(sin).to(cuda))
+    assert e.value.status == NCM_E_ARG
+
+
 def test_ncm_body_reference_invariants(cuda, ncm, oracle):
     """src/ncm_model.zig:332-429 on the device: level-0 inputs do not reach
     the output when query_level0 (bit for bit), the queries, the level

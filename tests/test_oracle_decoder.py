@@ -72,7 +72,7 @@ def test_decoder_struct_layout(ncm):
 def test_decoder_entry_rejects_before_device_use(ncm):
     L = ncm.lib()
     assert L.ncm_decoder_forward_dev(None, None, None, None, None, None, None, None, None, 1, 1,
-                                     None) == -1
+                                     None, None) == -1
 
 
 def test_tiny_decoder_kat(oracle):
