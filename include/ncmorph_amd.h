@@ -605,8 +605,11 @@ int ncm_rvq_encode_counts(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, 
  * n_flagged. Its workspace is a fixed device array of NCM_RVQ_SCRATCH_BYTES
  * per GPU, held until the process ends; a shape that needs more returns
  * NCM_E_SCRATCH (ncm_last_error() gives both sizes) before any device work.
- * It calls no hipMalloc / hipFree. Calls on one GPU share that array: calls
- * that overlap on one GPU (other streams or host threads) race. */
+ * It calls no hipMalloc / hipFree. Calls on one GPU share that array and are
+ * ordered through one event per device (created by ncm_init): a call on any
+ * stream or host thread runs after the previous call's kernels. On a stream
+ * under graph capture that event is left out, and the caller orders captured
+ * calls that share a GPU. */
 #define NCM_RVQ_SCRATCH_BYTES (64u << 20)
 int ncm_rvq_encode_noalloc(ncm_ctx_t* ctx, const float* x, int64_t b, int64_t t, int64_t d,
                            int64_t levels, const int32_t* strides, const uint16_t* codebooks,
@@ -760,7 +763,11 @@ int ncm_vq_tok_quantize_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const float
                             int64_t batch, int32_t* codes, float* zhat);
 
 /* zhat = sum_l Phi_l(Up_l(e_l[codes_l])) (the decoder's input in eval mode);
- * codes as ncm_vq_tok_encode_dev writes them, each clamped to [0, V_l). */
+ * codes as ncm_vq_tok_encode_dev writes them. A code outside [0, V_l) is
+ * clamped into it (the lookup stays in bounds; this stream-ordered entry
+ * cannot report it), so a caller validates caller-made codes first, as
+ * upstream's embedding lookup would raise (the Python mirror refuses them
+ * with NCM_E_ARG before the call). */
 int ncm_vq_tok_reconstruct_dev(ncm_ctx_t* ctx, const ncm_vq_tok_t* tok, const int32_t* codes,
                                int64_t batch, float* zhat);
 

@@ -12,8 +12,14 @@
 // Every encode on one GPU shares that GPU's array, and the array keeps the
 // previous call's contents. Each encode writes every workspace byte it reads
 // (its set-up kernel zeroes the per-level counters), so stale contents never
-// reach a result; two calls that overlap on one GPU (different streams, or
-// different host threads) race on the array.
+// reach a result. Calls on one GPU are ordered through one event per device
+// (created with the address lookup): a call's stream waits for the event,
+// then the call's kernels are queued and the event recorded after them, all
+// under one host lock, so a call on another stream (or from another host
+// thread) runs after the previous one. On a stream under graph capture the
+// event is left out (a captured wait on an event recorded outside the
+// capture is not portable): there the caller orders calls that share the
+// array.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -30,6 +36,7 @@ namespace {
 constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices];
+hipEvent_t g_scratch_done[kMaxDevices];  // the last call's kernels on that device
 
 }  // namespace
 
@@ -43,13 +50,21 @@ int noalloc_setup(int device) {
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (g_scratch_ptr[device]) return NCM_OK;
     void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p) {
         (void)hipGetLastError();
         ncm_set_error_detail(std::string("hipGetSymbolAddress(scratch): ") +
                              hipGetErrorString(e));
         return NCM_E_HIP;
     }
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) {
+        (void)hipGetLastError();
+        ncm_set_error_detail(std::string("hipEventCreateWithFlags: ") + hipGetErrorString(e));
+        return NCM_E_HIP;
+    }
+    g_scratch_done[device] = ev;
     g_scratch_ptr[device] = p;
     return NCM_OK;
 }
@@ -80,16 +95,33 @@ extern "C" int ncm_rvq_encode_noalloc(ncm_ctx_t* ctx, const float* x, int64_t b,
         ncm_set_error_detail(std::string("hipSetDevice: ") + hipGetErrorString(e));
         return NCM_E_HIP;
     }
-    void* ws = nullptr;
-    {
-        std::lock_guard<std::mutex> lock(g_scratch_mu);
-        if (device >= 0 && device < kMaxDevices) ws = g_scratch_ptr[device];
-    }
+    // The lock covers the wait, the queued kernels and the record, so two
+    // host threads cannot both queue work behind the same previous call.
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    void* ws = device >= 0 && device < kMaxDevices ? g_scratch_ptr[device] : nullptr;
     if (!ws) {
         ncm_set_error_detail("scratch address of this device was not looked up");
         return NCM_E_HIP;
     }
-    return ncm::rvq_encode_ws(ncm_ctx_stream(ctx), ws, (size_t)NCM_RVQ_SCRATCH_BYTES, x, b, t, d,
-                              levels, strides, codebooks, csq, v, codes, recon, gap, force_codes,
-                              nullptr);
+    const hipStream_t st = ncm_ctx_stream(ctx);
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    hipError_t he = hipStreamIsCapturing(st, &cap);
+    if (he != hipSuccess) {
+        ncm_set_error_detail(std::string("hipStreamIsCapturing: ") + hipGetErrorString(he));
+        return NCM_E_HIP;
+    }
+    const bool order = cap == hipStreamCaptureStatusNone;
+    if (order && (he = hipStreamWaitEvent(st, g_scratch_done[device], 0)) != hipSuccess) {
+        ncm_set_error_detail(std::string("hipStreamWaitEvent: ") + hipGetErrorString(he));
+        return NCM_E_HIP;
+    }
+    rc = ncm::rvq_encode_ws(st, ws, (size_t)NCM_RVQ_SCRATCH_BYTES, x, b, t, d, levels, strides,
+                            codebooks, csq, v, codes, recon, gap, force_codes, nullptr);
+    // Recorded even after a failed call: whatever it queued is then ordered
+    // before the next call.
+    if (order && (he = hipEventRecord(g_scratch_done[device], st)) != hipSuccess) {
+        ncm_set_error_detail(std::string("hipEventRecord: ") + hipGetErrorString(he));
+        return rc ? rc : NCM_E_HIP;
+    }
+    return rc;
 }

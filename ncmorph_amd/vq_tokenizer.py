@@ -326,7 +326,11 @@ class Tokenizer:
         return {"codes": codes, "zhat": zhat}
 
     def reconstruct(self, codes, zhat=None):
-        """zhat = sum_l Phi_l(Up_l(e_l[codes_l])): codes int32 [B, sum levels]."""
+        """zhat = sum_l Phi_l(Up_l(e_l[codes_l])): codes int32 [B, sum levels].
+        A code outside [0, V_l) of its level raises NcmError (NCM_E_ARG), as
+        upstream's embedding lookup does; the check reads the codes on the
+        device and synchronizes the stream (the C entry point itself only
+        clamps, to stay in bounds)."""
         import torch
 
         W = "vq_tok_reconstruct"
@@ -339,10 +343,24 @@ class Tokenizer:
         pc = a.dev(codes, "codes", _ck.I32, (B, cfg.codes_per_sequence))
         pz = a.dev(zhat, "zhat", _ck.F32, (B, cfg.seq_len, cfg.embed_dim))
         a.done()
+        limit = self._code_limits()
+        if bool(((codes < 0) | (codes >= limit[None, :])).any()):
+            raise NcmError(NCM_E_ARG, W, "a code is outside [0, V) of its level")
         self.ctx.bind_stream()
         check(lib().ncm_vq_tok_reconstruct_dev(self.ctx.handle, C.byref(self.desc), pc, B, pz), W)
         return zhat
 
+
+    def _code_limits(self):
+        """int32 [codes_per_sequence]: V_l of each code position's level."""
+        import numpy as np
+        import torch
+
+        if getattr(self, "_limits", None) is None:
+            v = np.concatenate([np.full(n, vs, np.int32)
+                                for n, vs in zip(self.cfg.levels, self.cfg.vocab_sizes)])
+            self._limits = torch.from_numpy(v).to(self.device)
+        return self._limits
 
     def decode(self, zhat, logits=None):
         """logits float32 [B, L, C] of the decoder block, ln_f and the output

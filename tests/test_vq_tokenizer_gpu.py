@@ -162,17 +162,25 @@ def test_ties_take_the_lowest_index():
     assert out["codes"].cpu().numpy().tolist() == [[7, 20] * 4]
 
 
-def test_reconstruct_clamps_codes():
+def test_reconstruct_rejects_out_of_range_codes():
+    """A caller code outside [0, V) of its level is refused (NCM_E_ARG), as
+    upstream's embedding lookup raises; codes at both ends of the range are
+    accepted."""
     torch = _torch()
+    from ncmorph_amd._lib import NCM_E_ARG, NcmError
+
     ocfg, enc, qw, dec, tok = _model(SMALL_WMT, seed=4)
     codes = torch.randint(0, 512, (2, sum(SMALL_WMT.levels)), dtype=torch.int32, device="cuda")
-    bad = codes.clone()
-    bad[:, 0] = -5
-    bad[:, 7] = 10 ** 6
-    fixed = codes.clone()
-    fixed[:, 0] = 0
-    fixed[:, 7] = 511
-    assert torch.equal(tok.reconstruct(bad), tok.reconstruct(fixed))
+    edge = codes.clone()
+    edge[:, 0] = 0
+    edge[:, 7] = 511
+    tok.reconstruct(edge)
+    for pos, val in ((0, -5), (7, 512), (7, 10 ** 6)):
+        bad = codes.clone()
+        bad[1, pos] = val
+        with pytest.raises(NcmError) as e:
+            tok.reconstruct(bad)
+        assert e.value.status == NCM_E_ARG
 
 
 def test_encode_rejects_out_of_range_ids():

@@ -1,7 +1,10 @@
 """The allocation-free RVQ encode (ncm_rvq_encode_noalloc) against the
 allocating one (ncm_rvq_encode), through the C ABI: identical codes,
 reconstruction and gaps on two calls in a row, the second on a smaller
-input, and a clear error for a shape beyond the fixed scratch."""
+input; two calls queued on two streams of two contexts without a host
+synchronization between them (they share the device's scratch array, so
+the second must run after the first); and a clear error for a shape beyond
+the fixed scratch."""
 import ctypes as C
 
 import numpy as np
@@ -108,3 +111,50 @@ def test_noalloc_rejects_shape_beyond_scratch(cuda, ncm):
                                     _p(tiny), None, None, None)
     assert rc == _lib.NCM_E_SCRATCH
     assert b"scratch" in lib.ncm_last_error()
+
+
+def test_noalloc_calls_on_two_streams_are_ordered(cuda, ncm):
+    """Two contexts on two streams queue an encode each, back to back with no
+    host synchronization: both results equal the allocating encode's."""
+    import torch
+    from ncmorph_amd import _lib
+    from ncmorph_amd.context import Context
+
+    lib = _lib.lib()
+    cases = [(11, 2, 256, 512, (16, 4, 2, 1), 700), (12, 1, 128, 256, (8, 2, 1), 200)]
+    ins, refs = [], []
+    c0 = Context(0)
+    c0.bind_stream()
+    for seed, b, t, d, strides, v in cases:
+        x, cb, xd, cbd, csq = _inputs(torch, cuda, seed, b, t, d, len(strides), v)
+        rc, codes, recon, gap = _encode(lib, "ncm_rvq_encode", c0, xd, cbd, csq, strides)
+        assert rc == 0
+        ins.append((xd, cbd, csq, strides))
+        refs.append((codes, recon, gap))
+    streams = [torch.cuda.Stream(), torch.cuda.Stream()]
+    ctxs = [Context(0), Context(0)]
+    outs = []
+    torch.cuda.synchronize()
+    for i in range(2):
+        xd, cbd, csq, strides = ins[i]
+        b, t, d = xd.shape
+        levels, v, _ = cbd.shape
+        total = sum(t // s for s in strides)
+        with torch.cuda.stream(streams[i]):
+            ctxs[i].bind_stream(streams[i])
+            codes = torch.full((b, total), -7, dtype=torch.int32, device=cuda)
+            recon = torch.full((b, t, d), float("nan"), dtype=torch.float32, device=cuda)
+            gap = torch.full((b, total), -1.0, dtype=torch.float32, device=cuda)
+            s = np.ascontiguousarray(strides, dtype=np.int32)
+            rc = lib.ncm_rvq_encode_noalloc(ctxs[i].handle, _p(xd), b, t, d, levels,
+                                            C.c_void_p(s.ctypes.data), _p(cbd), _p(csq), v,
+                                            _p(codes), _p(recon), _p(gap), None)
+            assert rc == 0
+            outs.append((codes, recon, gap))
+    torch.cuda.synchronize()
+    for (codes, recon, gap), (rc_, rr, rg) in zip(outs, refs):
+        assert np.array_equal(codes.cpu().numpy(), rc_)
+        assert np.array_equal(recon.cpu().numpy().view(np.uint32), rr.view(np.uint32))
+        assert np.array_equal(gap.cpu().numpy().view(np.uint32), rg.view(np.uint32))
+    for c in ctxs + [c0]:
+        c.close()
