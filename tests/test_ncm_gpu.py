@@ -237,6 +237,49 @@ def test_ncm_code_heads_match_oracle(cuda, ncm, oracle):
         off += n
 
 
+def test_ncm_body_8b_layer_shape_against_oracle(cuda, ncm, oracle):
+    """Two layers at the Llama-3-8B layer shape (hidden 4096, 32 / 8 heads of
+    128, FFN 14336, vq width 4096) over an 8-token prefix and levels of 1, 2,
+    4 and 8 positions, block-causal, against the oracle's bf16 body (its
+    matmuls threaded over the host's cores, bit-identical to one thread):
+    the body's bar of 3% (max) and 0.3% (mean) of max|ref|, on the output and
+    on every hidden state."""
+    import os
+
+    import torch
+    from ncmorph_amd import ncm as N
+
+    rng = np.random.default_rng(84)
+    levels, P = [1, 2, 4, 8], 8
+    hidden, vq, hq, hkv, hd, inter, nl, vocab = 4096, 4096, 32, 8, 128, 14336, 2, 64
+    spec = _spec(N, levels, P, hidden, vq, hq, hkv, hd, inter, nl, "block_causal", vocab)
+    w = random_ncm(rng, oracle.round_bf16, hidden, vq, inter, hq, hkv, hd, nl, levels, P, vocab,
+                   std=0.02, biases=True)
+    ids = rng.integers(0, vocab, P)
+    tgt = oracle.round_bf16(rng.standard_normal((sum(levels), vq)).astype(np.float32))
+    dw = N.device_weights(spec, w, cuda)
+    cos, sin = N.rope_tables(spec)
+    out, states = N.forward(spec, dw, ids, torch.from_numpy(tgt).to(cuda),
+                            torch.from_numpy(cos).to(cuda), torch.from_numpy(sin).to(cuda),
+                            hidden_states=True)
+    torch.cuda.synchronize()
+    got_states = states.cpu().numpy()
+    del dw, states
+    threads = max(1, min(16, len(os.sched_getaffinity(0))))
+    prev = oracle.set_threads(threads)
+    try:
+        ref, ref_states = oracle.ncm_forward(_oracle_cfg(spec), w, ids, None, tgt, bf16=True,
+                                             mask="block_causal", trace=True)
+    finally:
+        oracle.set_threads(prev)
+    for i, (g, r) in enumerate(list(zip(got_states, ref_states)) + [(out.cpu().numpy(), ref)]):
+        scale = np.max(np.abs(r))
+        err = np.abs(g - r)
+        assert np.all(np.isfinite(g)), i
+        assert err.max() <= 0.03 * scale, (i, err.max() / scale)
+        assert err.mean() <= 0.003 * scale, (i, err.mean() / scale)
+
+
 def test_ncm_body_8b_shape_properties(cuda, ncm):
     """The Llama-3-8B-shaped body (32 layers, hidden 4096, 32/8 heads of 128,
     FFN 14336) over a 64-token prefix and the 8 levels of a 4096-position

@@ -154,3 +154,53 @@ def test_tied_head_levels_split_launch(ncm, oracle, cuda):
         clear = r["gap"].cpu().numpy()[0] > 1e-4
         assert np.array_equal(np.argmax(got[off:off + n], axis=1)[clear], codes[clear]), l
         off += n
+
+
+def test_tied_head_levels_full_8b_layout(ncm, oracle, cuda):
+    """The NCM step's whole head launch: 8 levels of 32 ... 4096 rows (8160),
+    z and codebooks of width 4096, 8192 codes per level, a scale and a bias
+    per level. 16 sampled rows of every level against the oracle's f64 head
+    within the bound above, and the argmax of every row of the level with a
+    clear top-2 gap against the exact nearest code."""
+    import torch
+    from ncmorph_amd import kernels, vq
+
+    rng = np.random.default_rng(8192)
+    d, v = 4096, 8192
+    level_rows = [32, 64, 128, 256, 512, 1024, 2048, 4096]
+    lit = [0.05 * l - 0.1 for l in range(len(level_rows))]
+    L = len(level_rows)
+    zb = synth.bf16_bits(rng.standard_normal((sum(level_rows), d), dtype=np.float32))
+    eb = synth.bf16_bits((rng.standard_normal((L, v, d), dtype=np.float32) /
+                          np.float32(np.sqrt(d))))
+    bf = (rng.standard_normal((L, v), dtype=np.float32) * np.float32(0.1))
+    zd, ed = _bf16_dev(zb, cuda), _bf16_dev(eb, cuda)
+    csq = vq.prepare(ed)
+    got = kernels.tied_head_logits_levels(zd, ed, csq, level_rows, lit,
+                                          bias=torch.from_numpy(bf).to(cuda))
+    torch.cuda.synchronize()
+    off = 0
+    for l, n in enumerate(level_rows):
+        print(f"level {l}: {n} rows", flush=True)
+        sel = off + np.sort(rng.choice(n, size=min(n, 16), replace=False))
+        z = synth.bf16_to_f32(zb[sel])
+        E = synth.bf16_to_f32(eb[l])
+        ref, mag = oracle.tied_head_logits_f64(z, E, lit[l], bf[l])
+        esq = np.sum(E.astype(np.float64) ** 2, axis=1)
+        scale = np.exp(lit[l]) / esq.mean()
+        t = np.abs(ref - bf[l]) / scale
+        bound = (scale * ((d + 4) * 2.0**-24 * mag + d * 2.0**-24 * esq[None, :] + 2.0**-22 * t)
+                 + 2.0**-21 * (np.abs(ref) + np.abs(bf[l])) + 1e-30)
+        gl = got[off:off + n]
+        err = np.abs(gl[torch.from_numpy(sel - off).to(cuda)].cpu().numpy().astype(np.float64)
+                     - ref)
+        assert np.all(err <= bound), (l, float(np.max(err / bound)))
+        # Without the bias the argmax is the exact nearest code; with it, the
+        # argmax of (logit - bias) is.
+        r = vq.encode(zd[off:off + n].float().view(1, n, d), ed[l].view(1, v, d), (1,),
+                      csq=csq[l].view(1, v), want_gap=True)
+        codes = r["codes"].cpu().numpy()[0]
+        clear = r["gap"].cpu().numpy()[0] > 1e-4
+        unb = (gl - torch.from_numpy(bf[l]).to(cuda)[None, :]).argmax(dim=1).cpu().numpy()
+        assert np.array_equal(unb[clear], codes[clear]), l
+        off += n
