@@ -126,6 +126,43 @@ def test_attention_against_oracle(ncm, oracle, cuda, batch, seq, hq, hkv, hd, wi
         assert np.array_equal(got, np.repeat(v, hq // hkv, axis=1))
 
 
+@pytest.mark.parametrize("seq,hq,hkv,hd", [(64, 4, 2, 64), (128, 4, 1, 128), (100, 2, 2, 128)])
+def test_attention_probabilities_bits(ncm, oracle, cuda, seq, hq, hkv, hd):
+    """The probabilities themselves against the reference's rounding path,
+    p = round_bf16(exp(s - m) / l) (packages/kernels/root.zig:272-284,
+    :563-567): with one-hot value rows (v[k] = e_k, seq <= head_dim) every
+    context element is one probability times 1 added to zeros, so the
+    context holds the p matrix exactly, on the device and in the oracle.
+    Bar: at least 99.95% of the allowed (causal) entries bit-identical
+    (measured: 99.99-100%; a score whose fp32 sum, in MFMA order, lies next
+    to a bf16 boundary rounds the other way, and exp is the device's), the
+    masked ones exactly 0, and every entry within 2^-7 |p| + 2^-16."""
+    import torch
+    from ncmorph_amd import kernels
+
+    rng = np.random.default_rng(seq + hd)
+    rb = oracle.round_bf16
+    q = rb(rng.standard_normal((seq, hq * hd)).astype(np.float32) * 1.2)
+    k = rb(rng.standard_normal((seq, hkv * hd)).astype(np.float32) * 1.2)
+    v = np.zeros((seq, hkv * hd), np.float32)
+    for h in range(hkv):
+        v[np.arange(seq), h * hd + np.arange(seq)] = 1.0
+    out = kernels.attention_bf16(_bf16_dev(q, cuda), _bf16_dev(k, cuda), _bf16_dev(v, cuda),
+                                 1, seq, hq, hkv, hd)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy().reshape(seq, hq, hd)[:, :, :seq]
+    ref = oracle.attention_core(q, k, v, oracle.causal_mask(seq, 0), hq, hkv,
+                                hd).reshape(seq, hq, hd)[:, :, :seq]
+    allowed = np.broadcast_to(oracle.causal_mask(seq, 0).astype(bool)[:, None, :], got.shape)
+    assert np.all(got[~allowed] == 0)
+    same = float(np.mean(got[allowed].view(np.uint32) == ref[allowed].view(np.uint32)))
+    print(f"p bit-identical: {same:.6f} of {int(allowed.sum())}", flush=True)
+    assert np.all(np.abs(got - ref) <= 2.0**-7 * np.abs(ref) + 2.0**-16)
+    assert same >= 0.9995, same
+    # Each query's probabilities sum to 1 within the bf16 roundings.
+    assert np.all(np.abs(got.sum(axis=2) - 1.0) <= 2.0**-7 * (1 + np.arange(seq))[:, None])
+
+
 def test_attention_decoder_shape_fused_qkv(ncm, oracle, cuda):
     """The Llama-3.2-1B prefill shape (4 sequences x 1024 tokens, 32 query /
     8 key-value heads of 64) read from one q|k|v buffer, after the device
@@ -209,3 +246,42 @@ def test_attention_level_mask_against_oracle(ncm, oracle, cuda, batch, prefix, l
         _check(got[rows], ref, v[rows])
     if pad is not None and np.all(pad):
         assert np.all(got.reshape(batch, seq, -1)[:, :prefix] == 0)
+
+
+@pytest.mark.parametrize("prefix,levels,pad", [(16, [8, 16, 32, 48], "rand"),
+                                               (4, [4, 8, 16, 32, 64], None)])
+def test_attention_level_mask_probabilities_bits(ncm, oracle, cuda, prefix, levels, pad):
+    """The NCM level mask (block-diagonal: prefix keys without their pad bit,
+    then the query's own level), head_dim 128: with one-hot value rows the
+    context is the p matrix; at least 99.95% of the allowed entries
+    bit-identical to the oracle's round_bf16(exp(s - m) / l), the others
+    within 2^-7 |p| + 2^-16, masked entries exactly 0."""
+    import torch
+    from ncmorph_amd import kernels
+
+    if pad == "rand":
+        pad = (np.random.default_rng(prefix).random(prefix) < 0.3).astype(np.uint8)
+    hq, hkv, hd = 4, 1, 128
+    seq = prefix + sum(levels)
+    assert seq <= hd
+    rng = np.random.default_rng(seq)
+    rb = oracle.round_bf16
+    q = rb(rng.standard_normal((seq, hq * hd)).astype(np.float32) * 1.2)
+    k = rb(rng.standard_normal((seq, hkv * hd)).astype(np.float32) * 1.2)
+    v = np.zeros((seq, hkv * hd), np.float32)
+    v[np.arange(seq), np.arange(seq)] = 1.0
+    lo, hi, bits = kernels.block_diagonal_segments(prefix, levels, pad)
+    dl, dh = torch.from_numpy(lo).to(cuda), torch.from_numpy(hi).to(cuda)
+    db = torch.from_numpy(bits.view(np.int64)).to(cuda) if pad is not None else None
+    out = kernels.attention_bf16_seg(_bf16_dev(q, cuda), _bf16_dev(k, cuda), _bf16_dev(v, cuda),
+                                     1, seq, hq, hkv, hd, prefix, dl, dh, db)
+    torch.cuda.synchronize()
+    mask = oracle.block_diagonal_mask(prefix, levels, pad)
+    got = out.cpu().numpy().reshape(seq, hq, hd)[:, :, :seq]
+    ref = oracle.attention_core(q, k, v, mask, hq, hkv, hd).reshape(seq, hq, hd)[:, :, :seq]
+    allowed = np.broadcast_to(mask.astype(bool)[:, None, :], got.shape)
+    assert np.all(got[~allowed] == 0)
+    same = float(np.mean(got[allowed].view(np.uint32) == ref[allowed].view(np.uint32)))
+    print(f"p bit-identical: {same:.6f} of {int(allowed.sum())}", flush=True)
+    assert np.all(np.abs(got - ref) <= 2.0**-7 * np.abs(ref) + 2.0**-16)
+    assert same >= 0.9995, same
