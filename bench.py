@@ -35,11 +35,12 @@ LINEAR_M = 2048
 LINEAR_NK = [(2048, 2048), (8192, 2048), (2048, 8192)]
 # HBM-side bytes measured with rocprofv3 FETCH_SIZE / WRITE_SIZE (each in its
 # own run, fetch scaled by the factor a plain copy shows): the linear figure is
-# the mean over the step's three launches (466.0 MB per step), the RVQ figure
-# one whole encode; the summaries and commands are in
-# profiles/linear_bf16_1b_shapes.md and profiles/rvq_encode_b16_t2048_d2048_l8_v4096.md.
-LINEAR_TRAFFIC_BYTES_PER_LAUNCH = 155.3e6
-RVQ_TRAFFIC_BYTES_PER_ENCODE = 5099e6
+# the mean over the step's three launches (466.1 MB per step), the RVQ figure
+# one whole encode (3521 MB fetched, 1049 MB written); the summaries and
+# commands are in profiles/linear_bf16_1b_shapes.md and
+# profiles/rvq_encode_b16_t2048_d2048_l8_v4096.md.
+LINEAR_TRAFFIC_BYTES_PER_LAUNCH = 155.4e6
+RVQ_TRAFFIC_BYTES_PER_ENCODE = 4570e6
 NEAR_TIE_REL = 1e-5  # relative top-2 distance gap under which a code is a near-tie
 
 
@@ -90,6 +91,22 @@ def _ramp(torch, fn, ms=RAMP_MS):
         n *= 2
 
 
+def _queued_launch_time(torch, run, reps=20):
+    """Seconds per launch of `run` with its launches queued behind a GPU
+    spin: a 2048^3 launch takes less time than one host-side launch call,
+    so an unqueued loop would time the host. Used for ours and hipBLASLt's
+    per-shape figures alike."""
+    e0, e1 = _events(torch)
+    if hasattr(torch.cuda, "_sleep"):
+        torch.cuda._sleep(2_000_000)  # about 1 ms of GPU cycles
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps * 1e-3
+
+
 def run_linear(torch, steps, warmup):
     from ncmorph_amd import kernels
 
@@ -106,14 +123,7 @@ def run_linear(torch, steps, warmup):
     for (n, k) in LINEAR_NK:
         run = lambda: kernels.linear_bf16(xs[k], ws[(n, k)], out=ys[(n, k)])  # noqa: E731
         _ramp(torch, run, ms=SHAPE_RAMP_MS)
-        e0, e1 = _events(torch)
-        reps = 20
-        e0.record()
-        for _ in range(reps):
-            run()
-        e1.record()
-        torch.cuda.synchronize()
-        per_shape[(n, k)] = e0.elapsed_time(e1) / reps * 1e-3
+        per_shape[(n, k)] = _queued_launch_time(torch, run)
     # Clock ramp, then `warmup` untimed steps, then the timed region:
     # exactly `steps` steps, synchronized on both sides.
     _ramp(torch, step)
@@ -143,13 +153,7 @@ def run_linear(torch, steps, warmup):
         for (n, k) in LINEAR_NK:
             run = lambda: fn(xs[k], ws[(n, k)])  # noqa: E731
             _ramp(torch, run, ms=SHAPE_RAMP_MS)
-            e0, e1 = _events(torch)
-            e0.record()
-            for _ in range(20):
-                run()
-            e1.record()
-            torch.cuda.synchronize()
-            out[(n, k)] = e0.elapsed_time(e1) / 20 * 1e-3
+            out[(n, k)] = _queued_launch_time(torch, run)
         return out
 
     vendor = vendor_times(torch.nn.functional.linear)
