@@ -519,35 +519,29 @@ def rms_norm_rows_with_bias(x, weight, bias, epsilon: float, bf16: bool) -> np.n
     return y
 
 
-def ncm_forward(cfg, weights, prefix_ids, prefix_pad_mask, target_inputs, bf16: bool = False,
-                mask: str = "block_diagonal", trace: bool = False):
-    """forward_with_trace of the NCM level-parallel body (src/ncm_model.zig:
-    89-250). bf16=False restates the reference exactly (f32 matmul,
-    attention, RMSNorm and SiLU); bf16=True is the same body in the bf16
-    mode of the source decoder (src/decoder.zig:62-228 with bf16_compute):
-    every projection is matmul_bf16(_bias), norms are rms_norm_bf16, SiLU is
-    silu_bf16 with a rounded product, attention is attention_bf16, and every
-    add (level embedding, norm bias, residual) is rounded to bf16.
-    mask: "block_diagonal" (the reference, src/ncm_mask.zig:10-42) or
-    "block_causal". Returns the final-normalized hidden states [S, hidden]
-    (and the states after the input stage and each layer when trace)."""
-    H = cfg["hidden_size"]
-    vq = cfg["vq_width"]
-    hq, hkv, hd = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"]
-    inter = cfg["intermediate_size"]
-    eps = cfg["rms_norm_epsilon"]
-    levels = [int(n) for n in cfg["level_lengths"]]
-    P = cfg["prefix_length"]
+def _ncm_dims(cfg):
+    return (cfg["hidden_size"], cfg["vq_width"], cfg["num_attention_heads"],
+            cfg["num_key_value_heads"], cfg["head_dim"], cfg["intermediate_size"],
+            cfg["rms_norm_epsilon"], [int(n) for n in cfg["level_lengths"]],
+            cfg["prefix_length"])
+
+
+def _ncm_project(bf16):
+    def project(x, w, b):
+        if bf16:
+            return matmul_bf16(x, w, b)
+        y = matmul_reference(x, w)
+        return y if b is None else (y + np.asarray(b, np.float32)[None, :]).astype(np.float32)
+    return project
+
+
+def ncm_input_stage(cfg, weights, prefix_ids, target_inputs, bf16: bool = False):
+    """The NCM body's input stage (src/ncm_model.zig:99-168): prefix table
+    rows, the target inputs (level 0 replaced by l0_queries when
+    query_level0), each level's post-upsample conv, the input projection
+    (+ bias) and the level embeddings. Returns hidden [S, hidden]."""
+    H, vq, hq, hkv, hd, inter, eps, levels, P = _ncm_dims(cfg)
     ids = [int(i) for i in prefix_ids]
-    pad = [] if prefix_pad_mask is None else list(prefix_pad_mask)
-    if len(ids) != P:
-        raise ValueError("InvalidPrefixLength")
-    if len(pad) not in (0, P):
-        raise ValueError("InvalidPrefixMask")
-    if not levels:
-        raise ValueError("InvalidNcmMode")
-    if min(H, vq, hd, inter) == 0 or hd % 2 or hq == 0 or hkv == 0 or hq % hkv:
-        raise ValueError("InvalidNcmDimensions")
     T = sum(levels)
     S = P + T
     tgt = np.asarray(target_inputs, np.float32).reshape(-1)
@@ -561,18 +555,8 @@ def ncm_forward(cfg, weights, prefix_ids, prefix_pad_mask, target_inputs, bf16: 
     convs = weights.get("post_upsample_convs") or []
     if convs and len(convs) != len(levels):
         raise ValueError("InvalidNcmTensorSize")
-    layers = weights["layers"]
-    if not layers:
-        raise ValueError("InvalidNcmTensorSize")
-
     rb = round_bf16 if bf16 else (lambda a: np.asarray(a, np.float32))
-
-    def project(x, w, b):
-        if bf16:
-            return matmul_bf16(x, w, b)
-        y = matmul_reference(x, w)
-        return y if b is None else (y + np.asarray(b, np.float32)[None, :]).astype(np.float32)
-
+    project = _ncm_project(bf16)
     projected = np.empty((S, vq), np.float32)
     for i, t in enumerate(ids):
         if t >= table.shape[0] or t < 0:
@@ -593,8 +577,16 @@ def ncm_forward(cfg, weights, prefix_ids, prefix_pad_mask, target_inputs, bf16: 
         for l, n in enumerate(levels):
             hidden[off:off + n] = rb(hidden[off:off + n] + emb[l][None, :])
             off += n
-    states = [hidden.copy()] if trace else None
+    return hidden
 
+
+def ncm_tables_and_mask(cfg, prefix_pad_mask=None, mask: str = "block_diagonal"):
+    """The RoPE tables at the restarting level positions
+    (src/ncm_position.zig:11-118) and the attention mask of the NCM body:
+    (cos, sin, mask [S, S] bool)."""
+    H, vq, hq, hkv, hd, inter, eps, levels, P = _ncm_dims(cfg)
+    pad = [] if prefix_pad_mask is None else list(prefix_pad_mask)
+    S = P + sum(levels)
     positions = fill_level_positions(P, levels)
     if cfg.get("rope", "default") == "llama3":
         inv = rope_llama3(hd, cfg["rope_theta"], cfg.get("rope_factor", 1.0),
@@ -610,37 +602,83 @@ def ncm_forward(cfg, weights, prefix_ids, prefix_pad_mask, target_inputs, bf16: 
         m = block_causal_mask(P, levels, pad if pad else None)
     else:
         m = block_diagonal_mask(P, levels, pad if pad else None)
+    return cos, sin, m
 
+
+def ncm_layer(cfg, layer, hidden, cos, sin, mask, bf16: bool = False):
+    """One layer of the NCM body (src/ncm_model.zig:172-242): normalized
+    input (+ norm bias), fused q|k|v projection, optional QK-norm, rotation
+    at the level positions, masked attention, output projection and
+    residual, post-attention norm, SiLU MLP and residual."""
+    H, vq, hq, hkv, hd, inter, eps, levels, P = _ncm_dims(cfg)
+    S = hidden.shape[0]
+    rb = round_bf16 if bf16 else (lambda a: np.asarray(a, np.float32))
+    project = _ncm_project(bf16)
     qw, kvw = hq * hd, hkv * hd
+    n = rms_norm_rows_with_bias(hidden, layer["ln_1_weight"], layer.get("ln_1_bias"), eps, bf16)
+    wq, bq = np.asarray(layer["fused_qkv_weight"], np.float32), layer.get("fused_qkv_bias")
+    sl = lambda lo, hi: (wq[lo:hi], None if bq is None else np.asarray(bq)[lo:hi])
+    q = project(n, *sl(0, qw))
+    k = project(n, *sl(qw, qw + kvw))
+    v = project(n, *sl(qw + kvw, qw + 2 * kvw))
+    if layer.get("query_norm_weight") is not None:
+        q = rms_norm(q.reshape(S * hq, hd), layer["query_norm_weight"], eps,
+                     bf16=bf16).reshape(S, qw)
+        k = rms_norm(k.reshape(S * hkv, hd), layer["key_norm_weight"], eps,
+                     bf16=bf16).reshape(S, kvw)
+    q = rotate_heads(q, cos, sin, hq, hd, bf16=bf16)
+    k = rotate_heads(k, cos, sin, hkv, hd, bf16=bf16)
+    ctx = attention_core(q, k, v, mask, hq, hkv, hd, bf16=bf16)
+    attn = project(ctx, layer["output_weight"], layer.get("output_bias"))
+    hidden = rb(hidden + attn)
+    n = rms_norm_rows_with_bias(hidden, layer["ln_2_weight"], layer.get("ln_2_bias"), eps, bf16)
+    gate = project(n, layer["gate_weight"], layer.get("gate_bias"))
+    up = project(n, layer["up_weight"], layer.get("up_bias"))
+    act = silu_mul_bf16(gate, up) if bf16 else (silu(gate) * up).astype(np.float32)
+    mlp = project(act, layer["down_weight"], layer.get("down_bias"))
+    return rb(hidden + mlp)
+
+
+def ncm_final_norm(cfg, weights, hidden, bf16: bool = False):
+    """The body's final norm (+ bias)."""
+    return rms_norm_rows_with_bias(hidden, weights["final_norm_weight"],
+                                   weights.get("final_norm_bias"), cfg["rms_norm_epsilon"], bf16)
+
+
+def ncm_forward(cfg, weights, prefix_ids, prefix_pad_mask, target_inputs, bf16: bool = False,
+                mask: str = "block_diagonal", trace: bool = False):
+    """forward_with_trace of the NCM level-parallel body (src/ncm_model.zig:
+    89-250). bf16=False restates the reference exactly (f32 matmul,
+    attention, RMSNorm and SiLU); bf16=True is the same body in the bf16
+    mode of the source decoder (src/decoder.zig:62-228 with bf16_compute):
+    every projection is matmul_bf16(_bias), norms are rms_norm_bf16, SiLU is
+    silu_bf16 with a rounded product, attention is attention_bf16, and every
+    add (level embedding, norm bias, residual) is rounded to bf16.
+    mask: "block_diagonal" (the reference, src/ncm_mask.zig:10-42) or
+    "block_causal". Returns the final-normalized hidden states [S, hidden]
+    (and the states after the input stage and each layer when trace)."""
+    H, vq, hq, hkv, hd, inter, eps, levels, P = _ncm_dims(cfg)
+    ids = [int(i) for i in prefix_ids]
+    pad = [] if prefix_pad_mask is None else list(prefix_pad_mask)
+    if len(ids) != P:
+        raise ValueError("InvalidPrefixLength")
+    if len(pad) not in (0, P):
+        raise ValueError("InvalidPrefixMask")
+    if not levels:
+        raise ValueError("InvalidNcmMode")
+    if min(H, vq, hd, inter) == 0 or hd % 2 or hq == 0 or hkv == 0 or hq % hkv:
+        raise ValueError("InvalidNcmDimensions")
+    layers = weights["layers"]
+    if not layers:
+        raise ValueError("InvalidNcmTensorSize")
+    hidden = ncm_input_stage(cfg, weights, ids, target_inputs, bf16)
+    states = [hidden.copy()] if trace else None
+    cos, sin, m = ncm_tables_and_mask(cfg, pad if pad else None, mask)
     for layer in layers:
-        n = rms_norm_rows_with_bias(hidden, layer["ln_1_weight"], layer.get("ln_1_bias"), eps,
-                                    bf16)
-        wq, bq = np.asarray(layer["fused_qkv_weight"], np.float32), layer.get("fused_qkv_bias")
-        sl = lambda lo, hi: (wq[lo:hi], None if bq is None else np.asarray(bq)[lo:hi])
-        q = project(n, *sl(0, qw))
-        k = project(n, *sl(qw, qw + kvw))
-        v = project(n, *sl(qw + kvw, qw + 2 * kvw))
-        if layer.get("query_norm_weight") is not None:
-            q = rms_norm(q.reshape(S * hq, hd), layer["query_norm_weight"], eps,
-                         bf16=bf16).reshape(S, qw)
-            k = rms_norm(k.reshape(S * hkv, hd), layer["key_norm_weight"], eps,
-                         bf16=bf16).reshape(S, kvw)
-        q = rotate_heads(q, cos, sin, hq, hd, bf16=bf16)
-        k = rotate_heads(k, cos, sin, hkv, hd, bf16=bf16)
-        ctx = attention_core(q, k, v, m, hq, hkv, hd, bf16=bf16)
-        attn = project(ctx, layer["output_weight"], layer.get("output_bias"))
-        hidden = rb(hidden + attn)
-        n = rms_norm_rows_with_bias(hidden, layer["ln_2_weight"], layer.get("ln_2_bias"), eps,
-                                    bf16)
-        gate = project(n, layer["gate_weight"], layer.get("gate_bias"))
-        up = project(n, layer["up_weight"], layer.get("up_bias"))
-        act = silu_mul_bf16(gate, up) if bf16 else (silu(gate) * up).astype(np.float32)
-        mlp = project(act, layer["down_weight"], layer.get("down_bias"))
-        hidden = rb(hidden + mlp)
+        hidden = ncm_layer(cfg, layer, hidden, cos, sin, m, bf16)
         if trace:
             states.append(hidden.copy())
-    out = rms_norm_rows_with_bias(hidden, weights["final_norm_weight"],
-                                  weights.get("final_norm_bias"), eps, bf16)
+    out = ncm_final_norm(cfg, weights, hidden, bf16)
     if trace:
         states[-1] = out
         return out, states

@@ -145,6 +145,154 @@ def test_decoder_trace_against_oracle(ncm, oracle, cuda, hd, biases, qk_norm):
         assert err <= 0.01 * scale, (k, err / scale)
 
 
+def _replay_attention(oracle, n, L, cos, sin, hq, hkv, hd, window):
+    """attention_context of one sequence from its normalized input n: the
+    oracle's q / k / v projections, QK-norm, rotation and attention."""
+    qw, kvw = hq * hd, hkv * hd
+    w, b = L["qkv_weight"], L.get("qkv_bias")
+
+    def proj(lo, hi):
+        return oracle.matmul_bf16(n, w[lo:hi], None if b is None else b[lo:hi])
+
+    q, k, v = proj(0, qw), proj(qw, qw + kvw), proj(qw + kvw, qw + 2 * kvw)
+    t = n.shape[0]
+    if L.get("q_norm") is not None:
+        q = oracle.rms_norm(q.reshape(t * hq, hd), L["q_norm"], 1e-5).reshape(t, qw)
+        k = oracle.rms_norm(k.reshape(t * hkv, hd), L["k_norm"], 1e-5).reshape(t, kvw)
+    q = oracle.rotate_heads(q, cos[:t], sin[:t], hq, hd)
+    k = oracle.rotate_heads(k, cos[:t], sin[:t], hkv, hd)
+    return oracle.attention_core(q, k, v, oracle.causal_mask(t, window), hq, hkv, hd)
+
+
+# Stage-replay bars. A projection: every output within the fp32 error bound
+# of both sums (the MFMA's order and matmul_bf16's pair order) plus half a
+# bf16 step of each rounding, i.e. one bf16 step apart unless the sum
+# cancels to near zero, and at least 99% identical (measured 99.97-100%).
+# SiLU * up (the device's expf): within two bf16 steps, 99.9% identical. The
+# attention context (with the oracle's own q / k / v projections, which
+# differ from the device's by such steps): |d| <= 2^-7 |ref| + 2^-7 max|v|,
+# 95% identical (measured 99.8-100%).
+PROJ_SAME = 0.99
+SILU_SAME, SILU_STEPS = 0.999, 2
+ATTN_SAME = 0.95
+
+
+def _attn_close(dev, ref, vmax):
+    same = float(np.mean(dev == ref))
+    ok = bool(np.all(np.abs(dev - ref) <= 2.0 ** -7 * np.abs(ref) + 2.0 ** -7 * vmax))
+    return ok and same >= ATTN_SAME, same
+
+
+@pytest.mark.parametrize("hd,biases,qk_norm,window", [(64, True, False, 0),
+                                                       (128, False, True, 0),
+                                                       (64, False, True, 12)])
+def test_decoder_stages_replayed_against_oracle(ncm, oracle, cuda, hd, biases, qk_norm, window):
+    """Each traced stage of the bf16 forward (decoder_trace_t,
+    src/decoder.zig:30-47) against the oracle's op applied to the device's
+    own inputs of that stage, so that no difference is carried from an
+    earlier stage: the RMSNorms bit for bit; every projection (attention
+    output, gate, up, MLP output, logits) within the fp32 bound of both
+    summation orders plus half a bf16 step of each rounding and identical
+    for at least 99% of its elements; SiLU * up within two steps and 99.9%
+    identical; the attention context (with the oracle's own q / k / v
+    projections of the device's normalized input) within the attention bar
+    and 95% identical. Planted mistakes in the replay (the rotation one
+    position off, two output-projection input columns swapped, gate and up
+    exchanged) fail these bars."""
+    import torch
+    from ncmorph_amd import decoder, kernels
+
+    from .replay import projection_close, stage_report
+
+    print(f"decoder replay hd={hd} biases={biases} qk_norm={qk_norm} window={window}",
+          flush=True)
+    rng = np.random.default_rng(31 + hd + window)
+    hidden, inter, vocab, hq, hkv, nl, batch, seq = 256, 512, 300, 4, 2, 2, 2, 48
+    embed, layers, fnorm = random_model(rng, oracle.round_bf16, hidden, inter, vocab, hq, hkv,
+                                        hd, nl, biases=biases, qk_norm=qk_norm)
+    spec = decoder.DecoderSpec(hidden=hidden, intermediate=inter, vocab=vocab, q_heads=hq,
+                               kv_heads=hkv, head_dim=hd, layers=nl, window=window)
+    cos, sin = decoder.rope_tables(spec, seq + 1)
+    dl = []
+    for L in layers:
+        d = {k: (_dev_f32(v, cuda) if k.endswith("norm") else _dev_bf16(v, cuda))
+             for k, v in L.items()}
+        for name in ("gate_up_weight", "gate_up_bias"):
+            if L.get(name) is not None:
+                d[name] = _dev_bf16(kernels.interleave_gate_up(L[name][:inter], L[name][inter:]),
+                                    cuda)
+        dl.append(d)
+    w = decoder.DecoderWeights(embed=_dev_bf16(embed, cuda), final_norm=_dev_f32(fnorm, cuda),
+                               layers=dl)
+    ids = rng.integers(0, vocab, (batch, seq))
+    logits, tr = decoder.forward(spec, w, ids, _dev_f32(cos[:seq], cuda),
+                                 _dev_f32(sin[:seq], cuda), trace=True)
+    torch.cuda.synchronize()
+    t = {k: v.cpu().numpy() for k, v in tr.items()}
+    report = {}
+
+    def exact(name, dev, ref):
+        report[name] = float(np.mean(dev == ref))
+        assert np.array_equal(dev, ref), (name, report[name])
+
+    def proj(name, dev, x, wt, b, lo=None, hi=None):
+        if lo is not None:
+            wt = wt[lo:hi]
+            b = None if b is None else b[lo:hi]
+        ok, same, worst = projection_close(dev, oracle.matmul_bf16(x, wt, b), x, wt, b,
+                                           PROJ_SAME)
+        report[name] = (round(same, 4), round(worst, 3))
+        assert ok, (name, report[name])
+
+    def attn_ref(l, cs, sn):
+        return np.concatenate([
+            _replay_attention(oracle, t["input_norm"][l][b * seq:(b + 1) * seq], layers[l], cs,
+                              sn, hq, hkv, hd, window) for b in range(batch)])
+
+    vmax = [float(np.max(np.abs(oracle.matmul_bf16(
+        t["input_norm"][l], layers[l]["qkv_weight"][(hq + hkv) * hd:])))) + 1.0
+        for l in range(nl)]
+    for l, L in enumerate(layers):
+        prev = t["block_input"] if l == 0 else t["block_output"][l - 1]
+        exact(f"input_norm{l}", t["input_norm"][l], oracle.rms_norm(prev, L["input_norm"], 1e-5))
+        ok, same = _attn_close(t["attention_context"][l], attn_ref(l, cos, sin), vmax[l])
+        report[f"attention_context{l}"] = round(same, 4)
+        assert ok, (l, report)
+        proj(f"attention_output{l}", t["attention_output"][l], t["attention_context"][l],
+             L["o_weight"], L.get("o_bias"))
+        exact(f"post_attention_norm{l}", t["post_attention_norm"][l],
+              oracle.rms_norm(t["attention_residual"][l], L["post_attention_norm"], 1e-5))
+        gw, gb = L["gate_up_weight"], L.get("gate_up_bias")
+        n2 = t["post_attention_norm"][l]
+        proj(f"gate_projection{l}", t["gate_projection"][l], n2, gw, gb, 0, inter)
+        proj(f"up_projection{l}", t["up_projection"][l], n2, gw, gb, inter, 2 * inter)
+        same, steps = stage_report(t["gate_up_product"][l],
+                                   oracle.silu_mul_bf16(t["gate_projection"][l],
+                                                        t["up_projection"][l]))
+        report[f"gate_up_product{l}"] = (round(same, 5), steps)
+        assert same >= SILU_SAME and steps <= SILU_STEPS, (l, report)
+        proj(f"mlp_output{l}", t["mlp_output"][l], t["gate_up_product"][l], L["down_weight"],
+             L.get("down_bias"))
+    final = oracle.rms_norm(t["block_output"][nl - 1], fnorm, 1e-5)
+    proj("logits", logits.cpu().numpy(), final, embed, None)
+    print("stage (identical fraction[, worst error / allowed]):", report, flush=True)
+
+    # Planted mistakes, in the oracle's replay only.
+    assert not _attn_close(t["attention_context"][0], attn_ref(0, cos[1:], sin[1:]), vmax[0])[0]
+    L0 = layers[0]
+    wo = L0["o_weight"].copy()
+    wo[:, [0, hd]] = wo[:, [hd, 0]]
+    x0 = t["attention_context"][0]
+    assert not projection_close(t["attention_output"][0],
+                                oracle.matmul_bf16(x0, wo, L0.get("o_bias")), x0, wo,
+                                L0.get("o_bias"), PROJ_SAME)[0]
+    n2 = t["post_attention_norm"][0]
+    gu = L0["gate_up_weight"][inter:]
+    gub = None if L0.get("gate_up_bias") is None else L0["gate_up_bias"][inter:]
+    assert not projection_close(t["gate_projection"][0], oracle.matmul_bf16(n2, gu, gub), n2, gu,
+                                gub, PROJ_SAME)[0]
+
+
 def test_decoder_rejects_out_of_range_token(ncm, cuda):
     import torch
     from ncmorph_amd import decoder

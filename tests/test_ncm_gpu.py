@@ -123,6 +123,88 @@ def test_ncm_hidden_states_match_oracle(cuda, ncm, oracle, mask):
     assert np.array_equal(got[0], oracle.round_bf16(got[0]))
 
 
+# Layer-replay bars: one layer of the body from the device's own input state
+# (the oracle's ncm_layer) against the device's next state. Inside a layer
+# the MFMA's summation order moves a projection's bf16 output by one step
+# for a few percent of the elements, and such steps pass through the
+# attention, the MLP and both residual adds of that layer only.
+# A flip of the largest element is one bf16 step, up to 2^-7 of it.
+LAYER_SAME, LAYER_ERR = 0.85, 2.0 ** -6
+INPUT_SAME = 0.95
+
+
+def _layer_close(dev, ref, min_same=LAYER_SAME):
+    same = float(np.mean(dev == ref))
+    err = float(np.max(np.abs(dev - ref))) / max(float(np.max(np.abs(ref))), 1e-30)
+    return same >= min_same and err <= LAYER_ERR, (round(same, 4), round(err, 5))
+
+
+@pytest.mark.parametrize("mask,hd,extras", [("block_diagonal", 64, dict(biases=True)),
+                                             ("block_causal", 128, dict(qk_norm=True,
+                                                                        convs=True))])
+def test_ncm_layers_replayed_against_oracle(cuda, ncm, oracle, mask, hd, extras):
+    """Every stage of the bf16 body against the oracle applied to the
+    device's own input of that stage (hidden_states): the input stage
+    (prefix rows, queries, convs, input projection, level embeddings) at
+    least 95% identical and within 2^-6 of its largest magnitude (two bf16
+    steps of the largest element); each layer (oracle.ncm_layer on the
+    device's state before it) at least 85% identical and within 2^-6; the
+    last layer with the final norm likewise (measured 91-100% identical,
+    errors up to 0.55%). The whole-body comparison allows 3%, because it
+    carries differences through every layer. Planted mistakes in the
+    replay (the other level mask; positions that do not restart at each
+    level; two heads' output-projection columns exchanged) fail them."""
+    import torch
+    from ncmorph_amd import ncm as N
+
+    print(f"ncm replay mask={mask} hd={hd} extras={extras}", flush=True)
+    rng = np.random.default_rng(41 + hd)
+    levels, P = [8, 16, 32, 64], 12
+    hidden, vq, hq, hkv, inter, nl, vocab = 256, 128, 4, 2, 512, 3, 50
+    spec = _spec(N, levels, P, hidden, vq, hq, hkv, hd, inter, nl, mask, vocab)
+    w = random_ncm(rng, oracle.round_bf16, hidden, vq, inter, hq, hkv, hd, nl, levels, P, vocab,
+                   **extras)
+    ids = rng.integers(0, vocab, P)
+    pad = rng.random(P) < 0.3
+    tgt = oracle.round_bf16(rng.standard_normal((sum(levels), vq)).astype(np.float32))
+    dw = N.device_weights(spec, w, cuda)
+    cos, sin = N.rope_tables(spec)
+    out, states = N.forward(spec, dw, ids, torch.from_numpy(tgt).to(cuda),
+                            torch.from_numpy(cos).to(cuda), torch.from_numpy(sin).to(cuda),
+                            prefix_pad_mask=pad, hidden_states=True)
+    torch.cuda.synchronize()
+    st = states.cpu().numpy()
+    cfg = _oracle_cfg(spec)
+    report = {}
+    inp = oracle.ncm_input_stage(cfg, w, ids, tgt, bf16=True)
+    ok, report["input"] = _layer_close(st[0], inp, INPUT_SAME)
+    assert ok, report
+    ocos, osin, m = oracle.ncm_tables_and_mask(cfg, pad, mask)
+    for l in range(nl):
+        ref = oracle.ncm_layer(cfg, w["layers"][l], st[l], ocos, osin, m, bf16=True)
+        if l == nl - 1:
+            ref = oracle.ncm_final_norm(cfg, w, ref, bf16=True)
+        ok, report[f"layer{l}"] = _layer_close(st[l + 1], ref)
+        assert ok, (l, report)
+    print("stage (identical fraction, max error / max|ref|):", report, flush=True)
+
+    # Planted mistakes, in the oracle's replay of layer 0 only.
+    other = "block_causal" if mask == "block_diagonal" else "block_diagonal"
+    _, _, m_other = oracle.ncm_tables_and_mask(cfg, pad, other)
+    bad = oracle.ncm_layer(cfg, w["layers"][0], st[0], ocos, osin, m_other, bf16=True)
+    assert not _layer_close(st[1], bad)[0]
+    inv = oracle.rope_default_frequencies(hd, spec.rope_theta)
+    lin_cos, lin_sin = oracle.rope_tables(inv, spec.seq_len)
+    bad = oracle.ncm_layer(cfg, w["layers"][0], st[0], lin_cos, lin_sin, m, bf16=True)
+    assert not _layer_close(st[1], bad)[0]
+    L0 = dict(w["layers"][0])
+    wo = np.array(L0["output_weight"], np.float32)
+    wo[:, :hd], wo[:, hd:2 * hd] = wo[:, hd:2 * hd].copy(), wo[:, :hd].copy()
+    L0["output_weight"] = wo
+    bad = oracle.ncm_layer(cfg, L0, st[0], ocos, osin, m, bf16=True)
+    assert not _layer_close(st[1], bad)[0]
+
+
 def test_ncm_rejects_misaligned_conv_weight(cuda, ncm, oracle):
     """The convolutions read their weights with 16-byte loads: a conv weight
     that is not 16-byte aligned is refused (NCM_E_ARG) before any launch, as

@@ -220,3 +220,29 @@ def test_oracle_ncm_trace_layout(oracle):
     # the final-normalized output (src/ncm_model.zig:169-172, 242-249).
     assert len(states) == 3 and np.array_equal(states[-1], out)
     assert not np.array_equal(states[0], states[1])
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_oracle_ncm_stages_compose_to_the_body(oracle, bf16):
+    """ncm_input_stage, ncm_layer on each state and ncm_final_norm (the
+    stages the device replay tests call one at a time) reproduce
+    ncm_forward's traced states bit for bit, in both arithmetic modes."""
+    rng = np.random.default_rng(7 + bf16)
+    levels, P = [4, 8, 16], 5
+    hidden, vq, hq, hkv, hd, inter = 128, 64, 4, 2, 32, 256
+    cfg = _cfg(levels, P, hidden, vq, hq, hkv, hd, inter)
+    w = random_ncm(rng, oracle.round_bf16, hidden, vq, inter, hq, hkv, hd, 3, levels, P, 11,
+                   biases=True, qk_norm=True, convs=True)
+    ids = rng.integers(0, 11, P)
+    pad = [False, True, False, False, True]
+    tgt = oracle.round_bf16(rng.standard_normal((sum(levels), vq)).astype(np.float32))
+    out, states = oracle.ncm_forward(cfg, w, ids, pad, tgt, bf16=bf16, mask="block_causal",
+                                     trace=True)
+    assert np.array_equal(oracle.ncm_input_stage(cfg, w, ids, tgt, bf16=bf16), states[0])
+    cos, sin, m = oracle.ncm_tables_and_mask(cfg, pad, "block_causal")
+    h = states[0]
+    for l, layer in enumerate(w["layers"]):
+        h = oracle.ncm_layer(cfg, layer, h, cos, sin, m, bf16=bf16)
+        if l + 1 < len(w["layers"]):
+            assert np.array_equal(h, states[l + 1]), l
+    assert np.array_equal(oracle.ncm_final_norm(cfg, w, h, bf16=bf16), out)
