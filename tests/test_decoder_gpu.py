@@ -389,3 +389,98 @@ def test_decoder_llama_1b_full_size_against_oracle(ncm, oracle, cuda):
 
 
 BAR_1B = 0.03  # measured 0.0153 (mean 0.0024) on the MI355X
+
+
+def test_decoder_llama_1b_stages_replayed(ncm, oracle, cuda):
+    """The benchmark's own forward (Llama-3.2-1B, 4 x 1024 tokens, 16 layers,
+    the tile choices of M = 4096) with the trace, replayed stage by stage
+    by the oracle from the device's own inputs of each stage, for the first
+    and the last layer: the RMSNorms of sampled rows bit for bit; the
+    sampled rows of every projection (attention output, gate, up, MLP
+    output) and of the logits (tied 128256-row head) within the fp32 bound
+    of both summation orders plus half a bf16 step of each rounding, at
+    least 99% identical; SiLU * up within two steps; the whole attention
+    context of the second sequence (1024 queries, 32 heads, with the
+    oracle's own q / k / v projections) at least 95% identical and within
+    the attention bar."""
+    import os
+
+    import torch
+    from ncmorph_amd import decoder
+
+    from .replay import projection_close, stage_report
+
+    spec = decoder.LLAMA_3_2_1B
+    H, I, hq, hkv, hd = spec.hidden, spec.intermediate, spec.q_heads, spec.kv_heads, 64
+    batch, seq = 4, 1024
+    wd = decoder.random_weights(spec, cuda, seed=5, norm_std=0.1)
+    cos, sin = decoder.rope_tables(spec, seq)
+    ids = np.random.default_rng(6).integers(0, spec.vocab, (batch, seq))
+    print("decoder 1B 4 x 1024 traced", flush=True)
+    logits, tr = decoder.forward(spec, wd, ids, _dev_f32(cos, cuda), _dev_f32(sin, cuda),
+                                 trace=True)
+    torch.cuda.synchronize()
+    rows = np.array([0, 1, 517, 1023, 1024, 1800, 3071, 4095])
+    ri = torch.from_numpy(rows).to(cuda)
+
+    def host(t):
+        return t.float().cpu().numpy()
+
+    def stage(name, l, sel=True):
+        t = tr[name] if name == "block_input" else tr[name][l]
+        return host(t.index_select(0, ri) if sel else t)
+
+    prev_threads = oracle.set_threads(max(1, min(16, len(os.sched_getaffinity(0)))))
+    report = {}
+    try:
+        for l in (0, spec.layers - 1):
+            L = wd.layers[l]
+            qkv, wo, down = host(L["qkv_weight"]), host(L["o_weight"]), host(L["down_weight"])
+            gu = host(L["gate_up_weight"]).reshape(I // 32, 2, 32, H)
+            gate_w, up_w = gu[:, 0].reshape(I, H), gu[:, 1].reshape(I, H)
+            prev = stage("block_input", l) if l == 0 else stage("block_output", l - 1)
+            n1 = stage("input_norm", l)
+            assert np.array_equal(n1, oracle.rms_norm(prev, host(L["input_norm"]), 1e-5)), l
+            # Attention of sequence 1 from the device's normalized input.
+            xs = host(tr["input_norm"][l][seq:2 * seq])
+            q = oracle.matmul_bf16(xs, qkv[:hq * hd])
+            k = oracle.matmul_bf16(xs, qkv[hq * hd:(hq + hkv) * hd])
+            v = oracle.matmul_bf16(xs, qkv[(hq + hkv) * hd:])
+            q = oracle.rotate_heads(q, cos, sin, hq, hd)
+            k = oracle.rotate_heads(k, cos, sin, hkv, hd)
+            ctx = oracle.attention_core(q, k, v, oracle.causal_mask(seq), hq, hkv, hd)
+            dev_ctx = host(tr["attention_context"][l][seq:2 * seq])
+            ok, same = _attn_close(dev_ctx, ctx, float(np.max(np.abs(v))))
+            report[f"attention_context{l}"] = round(same, 5)
+            assert ok, (l, report)
+            c_rows = stage("attention_context", l)
+            for name, dev, x, wt in (
+                    ("attention_output", stage("attention_output", l), c_rows, wo),
+                    ("gate_projection", stage("gate_projection", l),
+                     stage("post_attention_norm", l), gate_w),
+                    ("up_projection", stage("up_projection", l), stage("post_attention_norm", l),
+                     up_w),
+                    ("mlp_output", stage("mlp_output", l), stage("gate_up_product", l), down)):
+                ok, same, worst = projection_close(dev, oracle.matmul_bf16(x, wt), x, wt,
+                                                   None, PROJ_SAME)
+                report[f"{name}{l}"] = (round(same, 5), round(worst, 3))
+                assert ok, (l, name, report)
+            assert np.array_equal(stage("post_attention_norm", l),
+                                  oracle.rms_norm(stage("attention_residual", l),
+                                                  host(L["post_attention_norm"]), 1e-5)), l
+            same, steps = stage_report(stage("gate_up_product", l),
+                                       oracle.silu_mul_bf16(stage("gate_projection", l),
+                                                            stage("up_projection", l)))
+            report[f"gate_up_product{l}"] = (round(same, 5), steps)
+            assert same >= SILU_SAME and steps <= SILU_STEPS, (l, report)
+        final = oracle.rms_norm(stage("block_output", spec.layers - 1), host(wd.final_norm),
+                                1e-5)
+        embed = host(wd.embed)
+        dev_logits = host(logits.index_select(0, ri))
+        ok, same, worst = projection_close(dev_logits, oracle.matmul_bf16(final, embed), final,
+                                           embed, None, PROJ_SAME)
+        report["logits"] = (round(same, 5), round(worst, 3))
+        assert ok, report
+    finally:
+        oracle.set_threads(prev_threads)
+    print("stage (identical fraction[, worst error / allowed]):", report, flush=True)
