@@ -24,11 +24,6 @@ def stage_report(dev, ref):
     return float(np.mean(s == 0)), int(s.max()) if s.size else 0
 
 
-def within(dev, ref, min_identical: float, max_steps: int) -> bool:
-    same, worst = stage_report(dev, ref)
-    return same >= min_identical and worst <= max_steps
-
-
 def bf16_spacing(values) -> np.ndarray:
     """The distance from each bf16 value to the next one away from zero
     (2^(e - 7) for a normal value of exponent e; 2^-133 below the normal
