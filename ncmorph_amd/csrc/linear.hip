@@ -197,7 +197,8 @@ static hipError_t launch_linear_s(const uint16_t* x, const uint16_t* w, const ui
 //     2 LDS stages; SCHED 8: loads and fragment reads interleaved between
 //     the MFMAs of the first two k-steps, barrier in the middle of the last
 //     k-step
-//  1: 128x128x64, 4 waves (64x64), DMA, SCHED 8, 4 LDS stages
+//  1: 128x128x64, 8 waves (32x64, 2 per SIMD), DMA, SCHED 8, 4 LDS stages,
+//     16x16x32 MFMAs
 //  2: 128x128x64, 4 waves, DMA, fences (SCHED 4), 2 stages: two workgroups
 //     per CU
 //  3: 256x256x32, 8 waves, DMA, ping-pong (SCHED 6), 4 LDS stages
@@ -212,7 +213,7 @@ static hipError_t launch_linear_s(const uint16_t* x, const uint16_t* w, const ui
 // 11, 12, 13: as 0, 1 and 5 with SCHED 5 (all loads of a tile issued
 //     together at its start, fragment reads of a k-step as one group)
 using Lin0 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, -1, true>;
-using Lin1 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
+using Lin1 = GemmShape<128, 128, 64, 4, 2, 2, 8, true, 4, false, 1, -1, -1, true>;
 using Lin2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
 using Lin3 = GemmShape<256, 256, 32, 4, 2, 2, 6, true, 4>;
 using Lin4 = GemmShape<256, 256, 64, 2, 2, 1, 5, true>;

@@ -218,7 +218,7 @@ static hipError_t launch_pair(const uint16_t* x, const uint16_t* w, const uint16
                               uint16_t* y, int64_t M, int64_t K, int64_t N, PairArgs pa,
                               hipStream_t st) {
     using L0 = GemmShape<256, 256, 64, 4, 2, 2, 8, true, 2, false, 1, -1, -1, true>;
-    using L1 = GemmShape<128, 128, 64, 2, 2, 2, 8, true, 4>;
+    using L1 = GemmShape<128, 128, 64, 4, 2, 2, 8, true, 4, false, 1, -1, -1, true>;
     using L2 = GemmShape<128, 128, 64, 2, 2, 2, 4, true>;
     using L5 = GemmShape<256, 128, 64, 4, 2, 2, 8, true, 3, false, 1, -1, -1, true>;
     const bool hb = bias != nullptr;
