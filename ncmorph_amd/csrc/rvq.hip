@@ -786,9 +786,12 @@ __global__ __launch_bounds__(256) void rvq_rescore_kernel(RowArgs a) {
     mn = wave_min_u32(mn);
     const float m_f = __uint_as_float(mn & ~imask);
     const float eps_q = __uint_as_float((uint32_t)(127 + a.cg.ib - 23) << 23);  // 2^(ib-23)
-    // Codes whose exact relative gap to the best is below ~2e-5 are always
-    // rescored, so the reported gap is exact for near-ties.
-    const float tau = 2e-5f * (st.unorm * st.unorm + fabsf(m_f - rowc) + 2.0f * E);
+    // When gaps are reported, codes whose exact relative gap to the best is
+    // below ~2e-5 are always rescored, so the reported gap is exact for
+    // near-ties. The argmin itself needs only the 2E window: the true
+    // nearest code's key is at most 2E above the smallest key.
+    const float tau = a.gap ? 2e-5f * (st.unorm * st.unorm + fabsf(m_f - rowc) + 2.0f * E)
+                            : 0.0f;
     const float thr = (m_f * (1.0f + eps_q) + 2.0f * E + tau) * (1.0f + 0x1p-20f);
 
     // Candidates: keys under the threshold. A chunk whose fourth (largest

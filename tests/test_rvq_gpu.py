@@ -100,6 +100,50 @@ def test_multiscale_matches_oracle(ncm, oracle, cuda, case):
     print("flagged rows:", r["n_flagged"])
 
 
+@pytest.mark.parametrize("case", [
+    dict(b=2, t=256, d=256, v=512, strides=(128, 64, 32, 16, 8, 4, 2, 1), seed=21),
+    dict(b=2, t=4096, d=64, v=4000, strides=(2, 1), seed=29),
+    dict(b=3, t=4096, d=128, v=4096, strides=(4, 1), seed=30),
+])
+def test_encode_without_gaps_matches_oracle(ncm, oracle, cuda, case):
+    """An encode that reports no gaps has no near-tie margin in its candidate
+    window (only the rigorous error bound): codes and reconstruction are the
+    oracle's and the gap-reporting encode's, bit for bit."""
+    import torch
+    from ncmorph_amd import vq
+
+    L = len(case["strides"])
+    x, cb = synth.rvq_inputs(case["seed"], case["b"], case["t"], case["d"], L, case["v"])
+    xd, cbd = _dev(x, cuda), _dev(cb, cuda, bf16=True)
+    with_gap = vq.encode(xd, cbd, case["strides"], want_gap=True)
+    no_gap = vq.encode(xd, cbd, case["strides"], want_gap=False)
+    torch.cuda.synchronize()
+    ref = oracle.rvq_encode(x, cb, case["strides"], threads=8)
+    assert "gap" not in no_gap or no_gap["gap"] is None
+    assert np.array_equal(no_gap["codes"].cpu().numpy(), ref["codes"])
+    assert np.array_equal(no_gap["recon"].cpu().numpy(), ref["recon"])
+    assert torch.equal(no_gap["codes"], with_gap["codes"])
+    assert torch.equal(no_gap["recon"].view(torch.int32), with_gap["recon"].view(torch.int32))
+
+
+def test_duplicate_codewords_without_gaps(ncm, oracle, cuda):
+    """Exact ties (identical codewords) with no near-tie margin: still the
+    lowest index."""
+    import torch
+    from ncmorph_amd import vq
+
+    d, V = 256, 300
+    x, cb = synth.rvq_inputs(31, 1, 64, d, 2, V)
+    for l in range(2):
+        for k in range(5, V, 7):
+            cb[l, k] = cb[l, 3]
+    x[0, :8] = synth.bf16_to_f32(cb[0, 3])
+    r = vq.encode(_dev(x, cuda), _dev(cb, cuda, bf16=True), (4, 1), want_gap=False)
+    torch.cuda.synchronize()
+    ref = oracle.rvq_encode(x, cb, (4, 1))
+    assert np.array_equal(r["codes"].cpu().numpy(), ref["codes"])
+
+
 def test_duplicate_codewords_take_lowest_index(ncm, oracle, cuda):
     # Identical codewords tie exactly; the flagged path (every code of an
     # incomplete group rescored) must still return the lowest index, as the
