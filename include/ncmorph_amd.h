@@ -639,7 +639,10 @@ int ncm_rvq_decode(ncm_ctx_t* ctx, const int32_t* codes, int64_t b, int64_t t, i
 typedef struct ncm_st_file ncm_st_file_t;
 typedef struct ncm_st_index ncm_st_index_t;
 typedef struct ncm_st_tensor {
-    const char* name;        /* owned by the file handle */
+    const char* name;        /* owned by the file handle; a name that holds
+                                U+0000 reads as cut there, and ncm_st_find
+                                does not match it (ncm_st_tensor still
+                                lists it) */
     int32_t dtype;           /* index in the reference's Dtype order: BOOL 0, U8, I8,
                                 U16, I16, U32, I32, U64, I64, F4, F6_E2M3, F6_E3M2,
                                 F8_E5M2, F8_E4M3, F8_E8M0, F8_E4M3FNUZ, F8_E5M2FNUZ,

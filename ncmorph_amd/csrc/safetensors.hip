@@ -38,8 +38,10 @@ struct JValue {
     std::vector<JValue> items;                              // Array
     std::vector<std::pair<std::string, JValue>> members;    // Object, in document order
     // A repeated key keeps its first position and its last value (the
-    // behaviour of an insertion-ordered map that is assigned to).
-    const JValue* get(const char* key) const {
+    // behaviour of an insertion-ordered map that is assigned to). Keys are
+    // compared as whole strings: a key may hold U+0000 (a "\u0000" escape),
+    // so it must never be looked up through its c_str().
+    const JValue* get(const std::string& key) const {
         for (size_t k = members.size(); k-- > 0;)
             if (members[k].first == key) return &members[k].second;
         return nullptr;
@@ -338,7 +340,7 @@ int parse_header(const unsigned char* bytes, size_t len, uint64_t file_size, ncm
         bool seen = false;
         for (size_t k = 0; k < mi; ++k) seen = seen || root.members[k].first == m.first;
         if (seen) continue;  // handled at its first position, with its last value
-        const JValue& v = *root.get(m.first.c_str());
+        const JValue& v = *root.get(m.first);
         if (m.first == "__metadata__") {
             if (v.kind != JValue::Object) return format_error("InvalidHeader");
             for (const auto& mm : v.members)
@@ -514,7 +516,7 @@ int ncm_st_parse_index(const char* json, size_t len, ncm_st_index_t** out) {
         bool seen = false;
         for (size_t k = 0; k < mi; ++k) seen = seen || wm->members[k].first == key;
         if (seen) continue;
-        const JValue& val = *wm->get(key.c_str());
+        const JValue& val = *wm->get(key);
         if (val.kind != JValue::String) { delete ix; return format_error("InvalidIndex"); }
         if (!plain_file_name(val.s)) { delete ix; return format_error("UnsafeShardName"); }
         ix->weight_map.emplace_back(key, val.s);

@@ -118,6 +118,43 @@ def test_sharded_index(ncm, oracle):
     assert st.parse_index('{"weight_map":{}}') == ([], None)
 
 
+def _cut_at_nul(r):
+    """A C string ends at U+0000: the C ABI's names read as cut there."""
+    if r[0] != "ok":
+        return r
+    return r[:3] + ([(t[0].split("\0")[0],) + tuple(t[1:]) for t in r[3]],)
+
+
+def test_names_holding_nul(ncm, oracle):
+    """A "\\u0000" escape in a tensor name or index key is a character of the
+    key (the reference's JSON strings are byte slices). Repeated keys are
+    matched whole, so "a\\u0000b" and "a" are two tensors, and a repeated
+    "a\\u0000" keeps its last value (these inputs once made the reader
+    dereference a failed lookup)."""
+    js = ('{"a\\u0000b":{"dtype":"U8","shape":[1],"data_offsets":[0,1]},'
+          '"a":{"dtype":"U8","shape":[2],"data_offsets":[1,3]}}')
+    data = make_file(js, 3)
+    c = c_parse(data)
+    assert c == _cut_at_nul(o_parse(oracle, data))
+    assert [t[2] for t in c[3]] == [[1], [2]]
+    f = st.SafetensorsFile(data=data)
+    assert f.find("a").shape == (2,)  # the whole-name match, not "a\0b"
+    f.close()
+    js2 = ('{"a\\u0000":{"dtype":"U8","shape":[9],"data_offsets":[0,9]},'
+           '"a\\u0000":{"dtype":"U8","shape":[1],"data_offsets":[0,1]}}')
+    data2 = make_file(js2, 1)
+    c2 = c_parse(data2)
+    assert c2 == _cut_at_nul(o_parse(oracle, data2)) and c2[3][0][2] == [1]
+
+    ix = '{"weight_map":{"a\\u0000b":"s1.safetensors","a":"s2.safetensors"}}'
+    entries, _ = st.parse_index(ix)
+    want, _ = oracle.st_parse_index(ix)
+    assert entries == [(k.split("\0")[0], v) for k, v in want] and len(entries) == 2
+    ix2 = '{"weight_map":{"a\\u0000":"s1.safetensors","a\\u0000":"s2.safetensors"}}'
+    assert st.parse_index(ix2)[0] == [("a", "s2.safetensors")]
+    assert oracle.st_parse_index(ix2)[0] == [("a\0", "s2.safetensors")]
+
+
 # ---- generated headers: the C parser and the oracle agree on every outcome
 
 def _random_header(rng):
