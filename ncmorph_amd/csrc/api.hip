@@ -546,7 +546,9 @@ int ncm_rope_rotate_dev(ncm_ctx_t* ctx, uint16_t* x, int64_t rows, int64_t row_s
     if (row_stride < (int64_t)heads * head_dim) return NCM_E_SHAPE;
     if (rows == 0 || heads == 0) return NCM_OK;
     if (!x || !cosine || !sine) return NCM_E_NULL;
-    if (rows * heads * (int64_t)(head_dim / 2) > (int64_t(1) << 40)) return NCM_E_SHAPE;
+    if (rows > (int64_t(1) << 40) || (int64_t)heads * head_dim > (int64_t(1) << 31) ||
+        rows * heads * (int64_t)(head_dim / 2) > (int64_t(1) << 40))
+        return NCM_E_SHAPE;
     int rc = ctx_bind(ctx);
     if (rc) return rc;
     hipError_t e = ncm::launch_rope_rotate(x, rows, row_stride, heads, head_dim, seq_len, cosine,

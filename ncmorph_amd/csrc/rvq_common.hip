@@ -17,7 +17,8 @@ int rvq_check_shape(int64_t b, int64_t t, int64_t d, int64_t levels, const int32
         if (l > 0 && strides[l] > strides[l - 1]) return NCM_E_SHAPE;
     }
     if (t % strides[0] != 0) return NCM_E_SHAPE;
-    if (b * t > (int64_t(1) << 31)) return NCM_E_SHAPE;
+    if (b > (int64_t(1) << 31) || t > (int64_t(1) << 31) || b * t > (int64_t(1) << 31))
+        return NCM_E_SHAPE;
     return NCM_OK;
 }
 

@@ -44,3 +44,24 @@ def test_two_streams_share_the_workspace(ncm, cuda):
             assert torch.equal(a.view(torch.int32) if a.dtype == torch.float32 else a, 
                                b_.view(torch.int32) if b_.dtype == torch.float32 else b_)
     assert default_context(0)._bound == s2.cuda_stream
+
+
+def test_shape_products_that_would_wrap_are_refused(ncm, cuda):
+    """Shape checks bound each factor before multiplying, so sizes whose
+    products wrap int64 are refused (NCM_E_SHAPE) before any device work."""
+    import ctypes as C
+
+    import torch
+    from ncmorph_amd._lib import NCM_E_SHAPE, lib
+    from ncmorph_amd.context import default_context
+
+    h = default_context().handle
+    buf = torch.zeros(64, dtype=torch.float32, device=cuda)
+    p = C.c_void_p(buf.data_ptr())
+    strides = (C.c_int32 * 1)(1)
+    # b * t = 2^62 * 4 wraps to 0.
+    assert lib().ncm_rvq_encode(h, p, 1 << 62, 4, 64, 1, strides, p, p, 1, p, p, None, None,
+                                None) == NCM_E_SHAPE
+    # rows * heads * head_dim / 2 = 2^62 * 2 * 1 wraps to 0.
+    assert lib().ncm_rope_rotate_dev(h, p, 1 << 62, 4, 2, 2, 1, p, p) == NCM_E_SHAPE
+    torch.cuda.synchronize()
