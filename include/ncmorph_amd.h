@@ -577,7 +577,8 @@ int ncm_rvq_prepare(ncm_ctx_t* ctx, const uint16_t* codebooks, int64_t levels, i
  * candidate needed rescoring). force_codes (device, codes layout) or NULL:
  * teacher forcing; when given, later levels' residuals are built from these
  * codes while `codes` still receives this library's own argmin.
- * Requires d % 64 == 0, v <= 65536. n_flagged (host, nullable) receives the
+ * Requires d % 64 == 0, d <= 4096 (NCM_E_SHAPE above: the row kernels hold
+ * a row in registers), v <= 65536. n_flagged (host, nullable) receives the
  * number of rows for which some group of codes had more near-best members
  * than the approximate pass kept, so that every code of the group was
  * rescored exactly (a synchronizing read). */

@@ -18,6 +18,8 @@ int noalloc_setup(int device);
 
 constexpr int kMaxLevels = 32;
 constexpr int kMaxPyr = 24;  // pyramid strides 2^1 .. 2^23
+// Widest row the encode's row kernels hold: 16 chunks of 256 elements.
+constexpr int64_t kMaxEncodeWidth = 4096;
 
 struct LevelTable {
     int32_t stride[kMaxLevels];

@@ -1052,10 +1052,12 @@ struct RvqLayout {
     size_t pyr, u, d0, d1, rc0, rc1, st0, st1, cand, cmax, fc, total;
 };
 
-// Fills the geometry and the workspace layout; NCM_E_SHAPE if the strides
-// need more pyramid levels than the geometry holds.
+// Fills the geometry and the workspace layout; NCM_E_SHAPE if the rows are
+// wider than the row kernels hold or the strides need more pyramid levels
+// than the geometry holds.
 static int rvq_layout(int64_t b, int64_t t, int64_t d, int64_t levels, const int32_t* strides,
                       int64_t v, RvqGeom& g, RvqLayout& lay) {
+    if (d > kMaxEncodeWidth) return NCM_E_SHAPE;
     g = RvqGeom{};
     g.b = b; g.t = t; g.d = d; g.v = v;
     g.L = make_level_table(t, levels, strides);

@@ -89,6 +89,15 @@ def test_small_config_golden(ncm, oracle, cuda):
     # 756 tiles (not a multiple of the 8 XCDs, so the tile order is not
     # remapped), ragged last row tile, 12 code tiles with the last one ragged
     dict(b=1, t=16000, d=64, v=3000, strides=(1,), seed=36),
+    # the widest rows (16 register chunks): 4096 rows keep D in registers,
+    # then 8192 rows load it again for each use
+    dict(b=1, t=8192, d=4096, v=300, strides=(2, 1), seed=37),
+    # 16 chunks, the last ones partly or wholly past the row (2112 = 8.25 x 256)
+    dict(b=1, t=8192, d=2112, v=64, strides=(1,), seed=38),
+    # a single code per level: every code is 0
+    dict(b=2, t=64, d=128, v=1, strides=(4, 1), seed=39),
+    # the most levels (32)
+    dict(b=1, t=64, d=64, v=16, strides=(32, 16, 8, 4, 2) + (1,) * 27, seed=40),
 ])
 def test_multiscale_matches_oracle(ncm, oracle, cuda, case):
     L = len(case["strides"])
@@ -281,3 +290,17 @@ def test_large_config_properties(ncm, oracle, cuda):
     assert np.array_equal(ref["codes"][0], codes[0]), int(np.sum(ref["codes"][0] != codes[0]))
     assert np.array_equal(ref["recon"][0].view(np.uint32),
                           r["recon"][0].cpu().numpy().view(np.uint32))
+
+
+def test_rows_wider_than_the_row_kernels_are_refused(ncm, cuda):
+    """The row kernels hold a row of up to 4096 elements in registers: a
+    wider encode is NCM_E_SHAPE, not a partial row."""
+    import torch
+    from ncmorph_amd import vq
+    from ncmorph_amd._lib import NCM_E_SHAPE, NcmError
+
+    x = torch.zeros((1, 4, 4160), dtype=torch.float32, device=cuda)
+    cb = torch.zeros((1, 8, 4160), dtype=torch.bfloat16, device=cuda)
+    with pytest.raises(NcmError) as e:
+        vq.encode(x, cb, (1,))
+    assert e.value.status == NCM_E_SHAPE
