@@ -14,8 +14,11 @@ namespace ncm {
 // vector sum, lanes into the scalar sum) run in the reference's order on
 // values gathered by shuffles. Every product and sum is a separate fp32 op
 // (built with -ffp-contract=off), as in the reference.
-// Both passes read the row from global memory (the second mostly from the
-// L2): staging it in LDS first measured slower at widths 2048-8192, since the
+// Widths 1024, 2048 and 4096 (the decoder and NCM hidden sizes) hold the
+// row in registers for both passes (rms_norm_rows_reg_kernel: 8224 x 4096
+// rows measured 53.5 -> 39.0 us, 4096 x 2048 11.95 -> 10.7 us). Other widths
+// read the row from global memory twice (the second pass mostly from the
+// caches): staging it in LDS measured slower at widths 2048-8192, since the
 // 16 KB-per-row stages held the kernel to two workgroups per CU.
 
 // The pinned sum of squares of one row (root.zig:152-227) by one
@@ -170,6 +173,126 @@ __device__ __forceinline__ void rms_write_row(const float* __restrict__ x,
         }
     } else {
         for (int64_t i = lane; i < n; i += 64) out1(i, xr[i], weight[i]);
+    }
+}
+
+// Widths 64 NR (NR = 16, 32, 64: 1024 to 4096 elements): one row per
+// wavefront, read once and held in registers (lane j holds x[64 i + j] in
+// v[i]) for both passes, instead of the second pass reading the row again.
+// The pinned cascade above, on the same chains: chain c = lane c < 32 takes
+// x[32 q + c] as its q-th element, which is v[q / 2] of lane c for even q
+// and of lane c + 32 for odd q (a permlane32 swap), in the same order with
+// the same operations, so the sum has the same bits.
+constexpr int rms_ilog2_ceil(int v) {
+    int lg = 0;
+    while ((1 << lg) < v) ++lg;
+    return lg;
+}
+
+template <int NR>
+__device__ __forceinline__ float rms_sum_squares_reg(const float (&v)[NR], int lane) {
+    constexpr int groups = 2 * NR;
+    constexpr int lg = rms_ilog2_ceil(groups);
+    constexpr int power = lg / 4 > 4 ? lg / 4 : 4;
+    constexpr int step = 1 << power, mask = step - 1;
+    const int l = lane & 7;
+    auto elem = [&](int q) {
+        return (q & 1) ? __uint_as_float(swap32(__float_as_uint(v[q >> 1]))[1]) : v[q >> 1];
+    };
+    float a0 = 0.0f, a1 = 0.0f, a2 = 0.0f, a3 = 0.0f;
+    int g = 0;
+#pragma unroll
+    for (int run = 0; run < groups / step; ++run) {
+        // One run's swaps at a time (all of them at once would double the
+        // registers).
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < step; ++s) {
+            const float e = elem(run * step + s);
+            a0 = a0 + e * e;
+        }
+        g += step;
+        a1 = a1 + a0;
+        a0 = 0.0f;
+        if ((g & (mask << power)) == 0) {
+            a2 = a2 + a1;
+            a1 = 0.0f;
+            if ((g & (mask << (2 * power))) == 0) {
+                a3 = a3 + a2;
+                a2 = 0.0f;
+            }
+        }
+    }
+#pragma unroll
+    for (int q = (groups / step) * step; q < groups; ++q) {
+        const float e = elem(q);
+        a0 = a0 + e * e;
+    }
+    a0 = a0 + a1;
+    a0 = a0 + a2;
+    a0 = a0 + a3;
+    // The merges of rms_sum_squares (no vector or scalar tail at these widths).
+    const float r1 = __shfl(a0, l + 8, 64), r2 = __shfl(a0, l + 16, 64),
+                r3 = __shfl(a0, l + 24, 64);
+    float vs = a0;
+    vs = vs + r1;
+    vs = vs + r2;
+    vs = vs + r3;
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sum = sum + __shfl(vs, k, 64);
+    return sum;
+}
+
+template <int OUT_MODE, int NR>
+__global__ __launch_bounds__(256) void rms_norm_rows_reg_kernel(const float* __restrict__ x,
+                                                                const float* __restrict__ weight,
+                                                                void* __restrict__ y,
+                                                                int64_t rows, float epsilon) {
+    static_assert(NR % 2 == 0, "element pairs");
+    constexpr int64_t n = 64 * NR;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    // Buffer loads: the row's base in the resource, the lane's offset in one
+    // VGPR, each 256-byte step in the scalar offset.
+    const __amdgpu_buffer_rsrc_t rx = make_rsrc(x + row * n, (uint32_t)(n * 4));
+    const __amdgpu_buffer_rsrc_t rw = make_rsrc(weight, (uint32_t)(n * 4));
+    const uint32_t lo = 4u * (uint32_t)lane;
+    float v[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i)
+        v[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rx, lo, 256 * i, 0));
+    const float sum = rms_sum_squares_reg<NR>(v, lane);
+    const float mean = sum / (float)n;
+    const float inv = 1.0f / sqrtf(mean + epsilon);
+    // The output pass of rms_write_row: the same operations, two elements
+    // (v[i], v[i + 1]) per rounding instruction.
+#pragma unroll
+    for (int i = 0; i < NR; i += 2) {
+        if (i % 8 == 0) __builtin_amdgcn_sched_barrier(0);
+        const float w0 = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, lo, 256 * i, 0));
+        const float w1 =
+            __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rw, lo, 256 * (i + 1), 0));
+        const int64_t e0 = row * n + 64 * i + lane, e1 = e0 + 64;
+        if (OUT_MODE == NCM_OUT_F32) {
+            const float n0 = v[i] * inv, n1 = v[i + 1] * inv;
+            ((float*)y)[e0] = n0 * w0;
+            ((float*)y)[e1] = n1 * w1;
+            continue;
+        }
+        const uint32_t nb = bf16x2_rne(v[i] * inv, v[i + 1] * inv);
+        const uint32_t wb = bf16x2_rne(w0, w1);
+        const uint32_t r = bf16x2_bits_rne(
+            __uint_as_float(nb << 16) * __uint_as_float(wb << 16),
+            __uint_as_float(nb & 0xFFFF0000u) * __uint_as_float(wb & 0xFFFF0000u));
+        if (OUT_MODE == NCM_OUT_BF16) {
+            ((uint16_t*)y)[e0] = (uint16_t)(r & 0xFFFFu);
+            ((uint16_t*)y)[e1] = (uint16_t)(r >> 16);
+        } else {
+            ((float*)y)[e0] = __uint_as_float(r << 16);
+            ((float*)y)[e1] = __uint_as_float(r & 0xFFFF0000u);
+        }
     }
 }
 
@@ -450,6 +573,23 @@ hipError_t launch_bias_round(void* y, const float* bias, int64_t rows, int64_t n
 template <int OUT_MODE>
 static hipError_t launch_rms_t(const float* x, const float* weight, void* y, int64_t rows,
                                int64_t n, float epsilon, hipStream_t stream) {
+    const dim3 grid1((unsigned)((rows + 3) / 4));
+    switch (n) {
+        case 1024:
+            hipLaunchKernelGGL((rms_norm_rows_reg_kernel<OUT_MODE, 16>), grid1, dim3(256), 0,
+                               stream, x, weight, y, rows, epsilon);
+            return hipGetLastError();
+        case 2048:
+            hipLaunchKernelGGL((rms_norm_rows_reg_kernel<OUT_MODE, 32>), grid1, dim3(256), 0,
+                               stream, x, weight, y, rows, epsilon);
+            return hipGetLastError();
+        case 4096:
+            hipLaunchKernelGGL((rms_norm_rows_reg_kernel<OUT_MODE, 64>), grid1, dim3(256), 0,
+                               stream, x, weight, y, rows, epsilon);
+            return hipGetLastError();
+        default:
+            break;
+    }
     // Wavefronts resident at once: 8 per SIMD on 256 CUs.
     constexpr int64_t kResidentWaves = 256 * 4 * 8;
     if (rows > kResidentWaves)

@@ -47,10 +47,13 @@ def test_rms_norm_dropin_kats_and_random(ncm, oracle, cuda):
 
 @pytest.mark.parametrize("rows,width", [(64, 2048), (5, 11), (3, 2050), (4096, 2048),
                                         (3, 6144), (3, 8192), (2, 16384), (2, 8204),
-                                        (8193, 2048), (8224, 4096), (8194, 11)])
+                                        (8193, 2048), (8224, 4096), (8194, 11), (9, 1024),
+                                        (8195, 1024)])
 def test_rms_norm_rows_device(ncm, oracle, cuda, rows, width):
-    """Every row bit-identical to the oracle; above 8192 rows the kernel runs
-    two rows per wavefront (8193: the last wavefront's second row absent)."""
+    """Every row bit-identical to the oracle, in both modes. Widths 1024,
+    2048 and 4096 run one row per wavefront held in registers; the others
+    read the row twice, and above 8192 rows run two rows per wavefront
+    (8193: the last wavefront's second row absent)."""
     import torch
     from ncmorph_amd import kernels
 
@@ -69,6 +72,13 @@ def test_rms_norm_rows_device(ncm, oracle, cuda, rows, width):
         assert np.array_equal(y32n[r].view(np.uint32), ref.view(np.uint32)), r
     bits = y16.cpu().view(torch.int16).numpy().view(np.uint16).astype(np.uint32) << 16
     assert np.array_equal(bits, y32n.view(np.uint32))
+    # The f32 mode (rms_norm, root.zig:226-239) on unrounded inputs.
+    xf = (rng.standard_normal((rows, width)) * 3).astype(np.float32)
+    yf = kernels.rms_norm_rows(torch.from_numpy(xf).to(cuda), wd, 1e-5, out_mode="f32")
+    yfn = yf.cpu().numpy()
+    for r in sample:
+        ref = oracle.rms_norm(xf[r], w, 1e-5, bf16=False)
+        assert np.array_equal(yfn[r].view(np.uint32), ref.view(np.uint32)), r
 
 
 def test_silu_dropin(ncm, oracle, cuda):
