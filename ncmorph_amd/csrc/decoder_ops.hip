@@ -437,63 +437,92 @@ __global__ __launch_bounds__(256) void rope_rotate_kernel(uint16_t* __restrict__
 }
 
 // The same rotation, four consecutive pairs per thread (8-byte element and
-// 16-byte table loads, 32-bit index arithmetic): hd % 8 == 0, row_stride % 4
-// == 0, x 8-byte and the tables 16-byte aligned, rows * heads * hd / 8 <
+// 16-byte table loads, 32-bit index arithmetic) for a batch of hb heads of
+// one row (hb 8, or 1 when the launch would otherwise have too few threads
+// to fill the chip): the table values of a (row, pair group) are loaded and
+// rounded once per batch and serve its heads. The roundings run two values per v_cvt_pk_bf16_f32 (the
+// bits of rb for every non-NaN value; a NaN stays a NaN up to the final
+// rounding, which maps it to 0x7FC0 as rb does). hd % 8 == 0, row_stride %
+// 4 == 0, x 8-byte and the tables 16-byte aligned, rows * heads * hd / 8 <
 // 2^31.
+constexpr int kRopeHeadBatch = 8;
 __global__ __launch_bounds__(256) void rope_rotate4_kernel(uint16_t* __restrict__ x, int rows,
                                                            int64_t row_stride, int heads, int hd,
                                                            int seq_len,
                                                            const float* __restrict__ cosine,
-                                                           const float* __restrict__ sine) {
+                                                           const float* __restrict__ sine,
+                                                           int hb) {
     const int half = hd >> 1, groups = half >> 2;
+    const int nbatch = (heads + hb - 1) / hb;
     const int64_t idx64 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx64 >= (int64_t)rows * heads * groups) return;
+    if (idx64 >= (int64_t)rows * nbatch * groups) return;
     const int idx = (int)idx64;  // < 2^31 (checked by the launcher)
     const int i = 4 * (idx % groups);
-    const int rh = idx / groups;
-    const int h = rh % heads;
-    const int r = rh / heads;
+    const int rb = idx / groups;
+    const int h0 = hb * (rb % nbatch);
+    const int h1 = h0 + hb < heads ? h0 + hb : heads;  // the batch's end
+    const int r = rb / nbatch;
     const int pos = r % seq_len;
-    auto rb = [](float v) { return __uint_as_float(bf16_bits_rne(v) << 16); };
-    uint16_t* e = x + (int64_t)r * row_stride + (int64_t)h * hd + i;
-    const u32x2_t fa = *(const u32x2_t*)e;
-    const u32x2_t fb = *(const u32x2_t*)(e + half);
     const float* ct = cosine + (int64_t)pos * hd + i;
     const float* st = sine + (int64_t)pos * hd + i;
     const f32x4_t c1 = *(const f32x4_t*)ct, s1 = *(const f32x4_t*)st;
     const f32x4_t c2 = *(const f32x4_t*)(ct + half), s2 = *(const f32x4_t*)(st + half);
-    uint32_t o1[4], o2[4];
+    auto lo = [](uint32_t p) { return __uint_as_float(p << 16); };
+    auto hi = [](uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); };
+    // rb(table) for elements (0, 1) and (2, 3).
+    uint32_t tc1[2], ts1[2], tc2[2], ts2[2];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        const uint32_t wa = fa[j >> 1], wb = fb[j >> 1];
-        const float first = __uint_as_float((j & 1) ? (wa & 0xFFFF0000u) : (wa << 16));
-        const float second = __uint_as_float((j & 1) ? (wb & 0xFFFF0000u) : (wb << 16));
-        const float left = rb(first * rb(c1[j]));
-        const float right = rb(-second * rb(s1[j]));
-        const float right2 = rb(first * rb(s2[j]));
-        const float left2 = rb(second * rb(c2[j]));
-        o1[j] = bf16_bits_rne(left + right);
-        o2[j] = bf16_bits_rne(left2 + right2);
+    for (int k = 0; k < 2; ++k) {
+        tc1[k] = bf16x2_rne(c1[2 * k], c1[2 * k + 1]);
+        ts1[k] = bf16x2_rne(s1[2 * k], s1[2 * k + 1]);
+        tc2[k] = bf16x2_rne(c2[2 * k], c2[2 * k + 1]);
+        ts2[k] = bf16x2_rne(s2[2 * k], s2[2 * k + 1]);
     }
-    u32x2_t w1, w2;
-    w1[0] = o1[0] | (o1[1] << 16);
-    w1[1] = o1[2] | (o1[3] << 16);
-    w2[0] = o2[0] | (o2[1] << 16);
-    w2[1] = o2[2] | (o2[3] << 16);
-    *(u32x2_t*)e = w1;
-    *(u32x2_t*)(e + half) = w2;
+    uint16_t* row = x + (int64_t)r * row_stride + i;
+    // The batch's loads issued together, then its rotations and stores.
+    u32x2_t fa[kRopeHeadBatch], fb[kRopeHeadBatch];
+#pragma unroll
+    for (int b = 0; b < kRopeHeadBatch; ++b) {
+        if (h0 + b < h1) {
+            const uint16_t* e = row + (int64_t)(h0 + b) * hd;
+            fa[b] = *(const u32x2_t*)e;
+            fb[b] = *(const u32x2_t*)(e + half);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < kRopeHeadBatch; ++b) {
+        if (h0 + b >= h1) break;
+        uint16_t* e = row + (int64_t)(h0 + b) * hd;
+        u32x2_t w1, w2;
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const uint32_t wa = fa[b][k], wb = fb[b][k];
+            const float f0 = lo(wa), f1 = hi(wa), s0 = lo(wb), s1v = hi(wb);
+            const uint32_t left = bf16x2_rne(f0 * lo(tc1[k]), f1 * hi(tc1[k]));
+            const uint32_t right = bf16x2_rne(-s0 * lo(ts1[k]), -s1v * hi(ts1[k]));
+            const uint32_t right2 = bf16x2_rne(f0 * lo(ts2[k]), f1 * hi(ts2[k]));
+            const uint32_t left2 = bf16x2_rne(s0 * lo(tc2[k]), s1v * hi(tc2[k]));
+            w1[k] = bf16x2_bits_rne(lo(left) + lo(right), hi(left) + hi(right));
+            w2[k] = bf16x2_bits_rne(lo(left2) + lo(right2), hi(left2) + hi(right2));
+        }
+        *(u32x2_t*)e = w1;
+        *(u32x2_t*)(e + half) = w2;
+    }
 }
 
 hipError_t launch_rope_rotate(uint16_t* x, int64_t rows, int64_t row_stride, int heads, int hd,
                               int64_t seq_len, const float* cosine, const float* sine,
                               hipStream_t stream) {
-    const int64_t n4 = rows * heads * (hd / 8);
+    // Batches of 8 heads when one head per thread would give at least 2^20
+    // threads, else one head per thread.
+    const int hb = rows * heads * (hd / 8) >= ((int64_t)1 << 20) ? kRopeHeadBatch : 1;
+    const int64_t n4 = rows * ((heads + hb - 1) / hb) * (hd / 8);
     if (hd % 8 == 0 && row_stride % 4 == 0 && ((uintptr_t)x & 7) == 0 &&
         ((uintptr_t)cosine & 15) == 0 && ((uintptr_t)sine & 15) == 0 && n4 < ((int64_t)1 << 31) &&
         seq_len < ((int64_t)1 << 31)) {
         hipLaunchKernelGGL(rope_rotate4_kernel, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0,
                            stream, x, (int)rows, row_stride, heads, hd, (int)seq_len, cosine,
-                           sine);
+                           sine, hb);
         return hipGetLastError();
     }
     const int64_t n = rows * heads * (hd / 2);
