@@ -12,9 +12,15 @@
 // whole K; its 8 wavefronts take one eighth of K each, in 128-element steps
 // of v_mfma_f32_16x16x32_bf16 (A = x rows, B = weight rows, operands loaded
 // straight from global memory: MFMA i of a step covers k = 32 i .. 32 i + 31,
-// lane group g holding 32 i + 8 g .. + 7, so each load instruction reads 64
-// contiguous bytes of 16 rows), and the eight partial sums are added in
-// wavefront order through LDS. The epilogue is the tile
+// lane group g holding 32 i + 8 g .. + 7: each weight load instruction
+// reads 64 contiguous bytes of 16 rows), and the eight partial sums are
+// added in wavefront order through LDS. The x rows, which every workgroup
+// reads (from the L2), are loaded 4 rows x 256 contiguous bytes per
+// instruction instead (16 rows x 64 bytes at a stride of K elements all
+// fall on few L2 channels: the q|k|v tail of the NCM step measured 24.8 ->
+// 15.0 us with contiguous x loads alone), written to the wavefront's own
+// LDS region and read back as the same A fragments, so every MFMA sees
+// the operands it saw before. The epilogue is the tile
 // kernels' own: bias, bf16 rounding, residual add (linear_kernel) or
 // swiglu_bits2 (linear_pair_kernel). Every output is the same function of
 // its row of x and its weight row(s) wherever the row sits in the batch, but
@@ -37,8 +43,15 @@ template <int RB, bool SWIGLU>
 struct TailBuf {
     u32x4_t g[4];               // weight rows (SwiGLU: gate rows)
     u32x4_t u[SWIGLU ? 4 : 1];  // SwiGLU: up rows
-    u32x4_t a[RB][4];           // x rows 16 rb + lane % 16
+    u32x4_t a[4 * RB];          // x: load j holds rows 4 j .. 4 j + 3 (16 lanes each)
 };
+
+// LDS bytes of the x staging: per wavefront 16 RB rows of one step (256
+// bytes each; 16-byte chunk c of row r stored at chunk c ^ (r % 16)).
+template <int RB>
+constexpr int tail_lds_bytes() {
+    return kTailWaves * 16 * RB * kTailStepK * 2;
+}
 
 template <int RB, bool SWIGLU, int OUT_MODE, bool HAS_BIAS, bool HAS_RES>
 __global__ __launch_bounds__(64 * kTailWaves) void linear_tail_kernel(
@@ -46,7 +59,10 @@ __global__ __launch_bounds__(64 * kTailWaves) void linear_tail_kernel(
     const uint16_t* __restrict__ bias, const float* residual, void* y, int64_t R, int64_t K,
     int64_t N) {
     constexpr int NACC = SWIGLU ? 2 : 1;
-    __shared__ f32x4_t part[kTailWaves - 1][NACC * RB][64];
+    // x staging during the main loop, then the partial sums (which fit in it).
+    extern __shared__ __attribute__((aligned(16))) char tail_lds[];
+    static_assert((kTailWaves - 1) * NACC * RB * 64 * 16 <= tail_lds_bytes<RB>(), "partials");
+    auto part = reinterpret_cast<f32x4_t(*)[NACC * RB][64]>(tail_lds);
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int r16 = lane & 15, grp = lane >> 4;
@@ -64,9 +80,9 @@ __global__ __launch_bounds__(64 * kTailWaves) void linear_tail_kernel(
     const uint32_t kb0 = (uint32_t)((wave * kq + 8 * grp) * 2);
     const uint32_t goff = (uint32_t)(r16 * K * 2) + kb0;
     const uint32_t uoff = (uint32_t)((32 + r16) * K * 2) + kb0;
-    uint32_t aoff[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; ++rb) aoff[rb] = (uint32_t)((16 * rb + r16) * K * 2) + kb0;
+    // x load j: row 4 j + lane / 16, 16-byte chunk lane % 16 of the step.
+    const uint32_t xoff = (uint32_t)(((lane >> 4) * K + wave * kq + 8 * r16) * 2);
+    char* xs = tail_lds + wave * (16 * RB * kTailStepK * 2);
 
     // A step past the end loads from outside both resources (zeros, no
     // memory traffic), so every iteration issues the same loads and the
@@ -78,9 +94,10 @@ __global__ __launch_bounds__(64 * kTailWaves) void linear_tail_kernel(
         for (int i = 0; i < 4; ++i) {
             b.g[i] = buffer_load_b128(rsw, goff + kb + 64 * i);
             if (SWIGLU) b.u[i] = buffer_load_b128(rsw, uoff + kb + 64 * i);
-#pragma unroll
-            for (int rb = 0; rb < RB; ++rb) b.a[rb][i] = buffer_load_b128(rsx, aoff[rb] + kb + 64 * i);
         }
+#pragma unroll
+        for (int j = 0; j < 4 * RB; ++j)
+            b.a[j] = buffer_load_b128(rsx, xoff + (uint32_t)(4 * j * K * 2) + kb);
     };
     f32x4_t acc[NACC][RB];
 #pragma unroll
@@ -88,16 +105,32 @@ __global__ __launch_bounds__(64 * kTailWaves) void linear_tail_kernel(
 #pragma unroll
         for (int rb = 0; rb < RB; ++rb) acc[a][rb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
     auto compute = [&](const TailBuf<RB, SWIGLU>& b) {
+        // The step's x rows into this wavefront's LDS region, then the A
+        // fragments (row 16 rb + r16, chunk 4 i + grp) back out.
+#pragma unroll
+        for (int j = 0; j < 4 * RB; ++j) {
+            const int row = 4 * j + grp;
+            *(u32x4_t*)(xs + row * 256 + ((r16 ^ (row & 15)) << 4)) = b.a[j];
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        u32x4_t af[RB][4];
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = 16 * rb + r16;
+                af[rb][i] = *(const u32x4_t*)(xs + row * 256 + (((4 * i + grp) ^ r16) << 4));
+            }
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int rb = 0; rb < RB; ++rb) {
                 acc[0][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                    __builtin_bit_cast(bf16x8_t, b.a[rb][i]), __builtin_bit_cast(bf16x8_t, b.g[i]),
+                    __builtin_bit_cast(bf16x8_t, af[rb][i]), __builtin_bit_cast(bf16x8_t, b.g[i]),
                     acc[0][rb], 0, 0, 0);
                 if (SWIGLU)
                     acc[NACC - 1][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                        __builtin_bit_cast(bf16x8_t, b.a[rb][i]),
+                        __builtin_bit_cast(bf16x8_t, af[rb][i]),
                         __builtin_bit_cast(bf16x8_t, b.u[i]), acc[NACC - 1][rb], 0, 0, 0);
             }
     };
@@ -118,8 +151,10 @@ __global__ __launch_bounds__(64 * kTailWaves) void linear_tail_kernel(
         __builtin_amdgcn_sched_barrier(0);
     }
 
-    // Partial sums of wavefronts 1 .. 7 to LDS; wavefront 0 adds them in
+    // Partial sums of wavefronts 1 .. 7 to LDS (over the x staging, once
+    // every wavefront is past its last step); wavefront 0 adds them in
     // order and runs the epilogue.
+    __syncthreads();
     if (wave > 0) {
 #pragma unroll
         for (int a = 0; a < NACC; ++a)
@@ -187,9 +222,13 @@ hipError_t launch_tail_t(const uint16_t* x, const uint16_t* w, const uint16_t* b
                          const float* residual, void* y, int64_t R, int64_t K, int64_t N,
                          hipStream_t st) {
     // Plain: N output columns; SwiGLU: N = features (weight rows 2 N).
-    hipLaunchKernelGGL((linear_tail_kernel<RB, SWIGLU, OUT_MODE, HAS_BIAS, HAS_RES>),
-                       dim3((unsigned)(N / 16)), dim3(64 * kTailWaves), 0, st, x, w, bias,
-                       residual, y, R, K, N);
+    auto kern = linear_tail_kernel<RB, SWIGLU, OUT_MODE, HAS_BIAS, HAS_RES>;
+    constexpr int lds = tail_lds_bytes<RB>();
+    static const hipError_t attr = hipFuncSetAttribute(
+        (const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds);
+    if (attr != hipSuccess) return attr;
+    hipLaunchKernelGGL(kern, dim3((unsigned)(N / 16)), dim3(64 * kTailWaves), lds, st, x, w,
+                       bias, residual, y, R, K, N);
     return hipGetLastError();
 }
 
