@@ -248,6 +248,9 @@ def run_decoder_ops(torch, reps=20):
              2 * t * inter * 4 + t * inter * 2)):
         _ramp(torch, fn)
         e0, e1 = _events(torch)
+        # Kernels of about 10 us: the launches are queued behind a GPU spin so
+        # that the events time the kernels, not the host's launch calls.
+        _queue_ahead(torch)
         e0.record()
         for _ in range(reps):
             fn()
