@@ -440,11 +440,11 @@ __global__ __launch_bounds__(256) void rope_rotate_kernel(uint16_t* __restrict__
 // 16-byte table loads, 32-bit index arithmetic) for a batch of hb heads of
 // one row (hb 8, or 1 when the launch would otherwise have too few threads
 // to fill the chip): the table values of a (row, pair group) are loaded and
-// rounded once per batch and serve its heads. The roundings run two values per v_cvt_pk_bf16_f32 (the
-// bits of rb for every non-NaN value; a NaN stays a NaN up to the final
-// rounding, which maps it to 0x7FC0 as rb does). hd % 8 == 0, row_stride %
-// 4 == 0, x 8-byte and the tables 16-byte aligned, rows * heads * hd / 8 <
-// 2^31.
+// rounded once per batch and serve its heads. The roundings run two values
+// per v_cvt_pk_bf16_f32 (the bits of bf16_bits_rne for every non-NaN value;
+// a NaN stays a NaN up to the final rounding, which maps it to 0x7FC0 as
+// bf16_bits_rne does). hd % 8 == 0, row_stride % 4 == 0, x 8-byte and the
+// tables 16-byte aligned, rows * heads * hd / 8 < 2^31.
 constexpr int kRopeHeadBatch = 8;
 __global__ __launch_bounds__(256) void rope_rotate4_kernel(uint16_t* __restrict__ x, int rows,
                                                            int64_t row_stride, int heads, int hd,

@@ -10,17 +10,17 @@
 // A skinny product: workgroup b takes 16 output columns (SwiGLU: 16
 // features, i.e. their 16 gate and 16 up weight rows) of all R rows over the
 // whole K; its 8 wavefronts take one eighth of K each, in 128-element steps
-// of v_mfma_f32_16x16x32_bf16 (A = x rows, B = weight rows, operands loaded
-// straight from global memory: MFMA i of a step covers k = 32 i .. 32 i + 31,
-// lane group g holding 32 i + 8 g .. + 7: each weight load instruction
-// reads 64 contiguous bytes of 16 rows), and the eight partial sums are
-// added in wavefront order through LDS. The x rows, which every workgroup
-// reads (from the L2), are loaded 4 rows x 256 contiguous bytes per
-// instruction instead (16 rows x 64 bytes at a stride of K elements all
-// fall on few L2 channels: the q|k|v tail of the NCM step measured 24.8 ->
-// 15.0 us with contiguous x loads alone), written to the wavefront's own
-// LDS region and read back as the same A fragments, so every MFMA sees
-// the operands it saw before. The epilogue is the tile
+// of v_mfma_f32_16x16x32_bf16 (A = x rows, B = weight rows; MFMA i of a
+// step covers k = 32 i .. 32 i + 31, lane group g holding 32 i + 8 g .. + 7,
+// so a weight load instruction in that layout reads 64 contiguous bytes of
+// 16 rows, straight into registers), and the eight partial sums are added in
+// wavefront order through LDS. The x rows, which every workgroup reads (from
+// the L2), are loaded 4 rows x 256 contiguous bytes per instruction instead
+// (a 16-row x 64-byte instruction touches 16 cache lines and uses half of
+// each: the q|k|v tail of the NCM step measured 24.8 -> 15.0 us with
+// contiguous x loads alone), written to the wavefront's own LDS region and
+// read back as the same A fragments, so every MFMA sees the operands it saw
+// before. The epilogue is the tile
 // kernels' own: bias, bf16 rounding, residual add (linear_kernel) or
 // swiglu_bits2 (linear_pair_kernel). Every output is the same function of
 // its row of x and its weight row(s) wherever the row sits in the batch, but
