@@ -201,13 +201,65 @@ __device__ __forceinline__ float row_offset(const RowStats& s, float cmax) {
 // the stride-2^(k+1) pool relative to src. A thread owns 4 columns of one
 // group of 2^DEPTH consecutive rows (groups never straddle a batch row,
 // because t is a multiple of the largest stride).
+// The per-encode set-up of one level by one workgroup of NT threads:
+// cmax[l] = sqrt(max_k csq[l, k]) (rounded up); zeroes the level's two
+// counters (counts[l], counts[levels + l]). Each thread issues its (up to)
+// four loads of a pass together, so the workgroup waits for one memory round
+// trip per 4 NT codes. The maximum does not depend on the order, so any NT
+// gives the same bits.
+struct SetupArgs {
+    const float* csq;
+    int64_t v, levels;
+    float* cmax;
+    int32_t* counts;
+};
+
+template <int NT>
+__device__ __forceinline__ void rvq_setup_level(const SetupArgs& sa, int l) {
+    const float* row = sa.csq + (int64_t)l * sa.v;
+    float m = 0.0f;
+    for (int64_t k0 = threadIdx.x; k0 < sa.v; k0 += 4 * NT) {
+        float t[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int64_t k = k0 + (int64_t)j * NT;
+            t[j] = k < sa.v ? row[k] : 0.0f;
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m = fmaxf(m, t[j]);
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    __shared__ float red[NT / 64];
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float r = red[0];
+        for (int w = 1; w < NT / 64; ++w) r = fmaxf(r, red[w]);
+        sa.cmax[l] = sqrtf(r) * 1.00001f;
+        sa.counts[l] = 0;
+        sa.counts[sa.levels + l] = 0;
+    }
+}
+
+// Pooling passes of up to four halvings; the first pass also runs the
+// per-encode set-up in its first setup_blocks workgroups (one per level),
+// which then finish while the pooling streams.
 template <int DEPTH>
-__global__ void rvq_pyramid_kernel(const float* __restrict__ src, int64_t rows, int64_t d,
-                                   float* __restrict__ dst0, float* __restrict__ dst1,
-                                   float* __restrict__ dst2, float* __restrict__ dst3) {
+__global__ __launch_bounds__(256) void rvq_pyramid_kernel(const float* __restrict__ src,
+                                                          int64_t rows, int64_t d,
+                                                          float* __restrict__ dst0,
+                                                          float* __restrict__ dst1,
+                                                          float* __restrict__ dst2,
+                                                          float* __restrict__ dst3,
+                                                          SetupArgs sa, int setup_blocks) {
+    if ((int)blockIdx.x < setup_blocks) {
+        rvq_setup_level<256>(sa, (int)blockIdx.x);
+        return;
+    }
     constexpr int N = 1 << DEPTH;
     const int64_t q = d / 4;
-    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t idx = (int64_t)(blockIdx.x - setup_blocks) * blockDim.x + threadIdx.x;
     const int64_t groups = rows >> DEPTH;
     if (idx >= groups * q) return;
     const int64_t g = idx / q, c = (idx % q) * 4;
@@ -237,40 +289,10 @@ __global__ void rvq_pyramid_kernel(const float* __restrict__ src, int64_t rows, 
 
 // ------------------------------------------------- per-encode set-up kernel
 
-// cmax[l] = sqrt(max_k csq[l, k]) (rounded up); zeroes the level's two
-// counters (counts[l], counts[levels + l]).
-// One 1024-thread block per level; each thread issues its (up to) four loads
-// of a pass together, so the block waits for one memory round trip per
-// 4096 codes.
+// The set-up alone (no pyramid pass to carry it: every stride is 1).
 constexpr int kSetupThreads = 1024;
-__global__ __launch_bounds__(kSetupThreads) void rvq_setup_kernel(const float* __restrict__ csq,
-                                                                 int64_t v, int64_t levels,
-                                                                 float* cmax, int32_t* counts) {
-    const int l = blockIdx.x;
-    const float* row = csq + (int64_t)l * v;
-    float m = 0.0f;
-    for (int64_t k0 = threadIdx.x; k0 < v; k0 += 4 * kSetupThreads) {
-        float t[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int64_t k = k0 + (int64_t)j * kSetupThreads;
-            t[j] = k < v ? row[k] : 0.0f;
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) m = fmaxf(m, t[j]);
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-    __shared__ float red[kSetupThreads / 64];
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float r = red[0];
-        for (int w = 1; w < kSetupThreads / 64; ++w) r = fmaxf(r, red[w]);
-        cmax[l] = sqrtf(r) * 1.00001f;
-        counts[l] = 0;
-        counts[levels + l] = 0;
-    }
+__global__ __launch_bounds__(kSetupThreads) void rvq_setup_kernel(SetupArgs sa) {
+    rvq_setup_level<kSetupThreads>(sa, (int)blockIdx.x);
 }
 
 // ------------------------------------------------------ level-0 prep kernel
@@ -1145,12 +1167,17 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
     // D_{l+1} (coarse reconstruction) is written by level l into dbuf[(l+1)&1].
     float* dbuf[2] = {(float*)(W + lay.d0), (float*)(W + lay.d1)};
 
-    hipLaunchKernelGGL(rvq_setup_kernel, dim3((unsigned)levels), dim3(kSetupThreads), 0, st, csq,
-                       v, levels, cmax, fcount);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return NCM_E_HIP;
+    const SetupArgs sa{csq, v, levels, cmax, fcount};
+    hipError_t e = hipSuccess;
+    if (jmax == 0) {
+        hipLaunchKernelGGL(rvq_setup_kernel, dim3((unsigned)levels), dim3(kSetupThreads), 0, st,
+                           sa);
+        e = hipGetLastError();
+        if (e != hipSuccess) return NCM_E_HIP;
+    }
 
-    // Pyramid, in passes of up to four halvings.
+    // Pyramid, in passes of up to four halvings; the first pass carries the
+    // set-up in its first `levels` workgroups.
     {
         int j0 = 0;
         while (j0 < jmax) {
@@ -1160,12 +1187,13 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
             float* dst[4] = {nullptr, nullptr, nullptr, nullptr};
             for (int k = 0; k < depth; ++k) dst[k] = pyr + g.pyr_off[j0 + k + 1];
             const int64_t work = (rows >> depth) * (d / 4);
-            const dim3 grid((unsigned)((work + 255) / 256));
+            const int sb = j0 == 0 ? (int)levels : 0;
+            const dim3 grid((unsigned)((work + 255) / 256 + sb));
             switch (depth) {
-                case 1: hipLaunchKernelGGL(rvq_pyramid_kernel<1>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3]); break;
-                case 2: hipLaunchKernelGGL(rvq_pyramid_kernel<2>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3]); break;
-                case 3: hipLaunchKernelGGL(rvq_pyramid_kernel<3>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3]); break;
-                default: hipLaunchKernelGGL(rvq_pyramid_kernel<4>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3]); break;
+                case 1: hipLaunchKernelGGL(rvq_pyramid_kernel<1>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3], sa, sb); break;
+                case 2: hipLaunchKernelGGL(rvq_pyramid_kernel<2>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3], sa, sb); break;
+                case 3: hipLaunchKernelGGL(rvq_pyramid_kernel<3>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3], sa, sb); break;
+                default: hipLaunchKernelGGL(rvq_pyramid_kernel<4>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3], sa, sb); break;
             }
             e = hipGetLastError();
             if (e != hipSuccess) return NCM_E_HIP;
