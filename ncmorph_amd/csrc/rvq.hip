@@ -242,9 +242,10 @@ __device__ __forceinline__ void rvq_setup_level(const SetupArgs& sa, int l) {
     }
 }
 
-// Pooling passes of up to four halvings; the first pass also runs the
+// Pooling passes of up to seven halvings; the first pass also runs the
 // per-encode set-up in its first setup_blocks workgroups (one per level),
 // which then finish while the pooling streams.
+constexpr int kMaxPyrPass = 7;  // halvings per pyramid pass
 template <int DEPTH>
 __global__ __launch_bounds__(256) void rvq_pyramid_kernel(const float* __restrict__ src,
                                                           int64_t rows, int64_t d,
@@ -252,6 +253,9 @@ __global__ __launch_bounds__(256) void rvq_pyramid_kernel(const float* __restric
                                                           float* __restrict__ dst1,
                                                           float* __restrict__ dst2,
                                                           float* __restrict__ dst3,
+                                                          float* __restrict__ dst4,
+                                                          float* __restrict__ dst5,
+                                                          float* __restrict__ dst6,
                                                           SetupArgs sa, int setup_blocks) {
     if ((int)blockIdx.x < setup_blocks) {
         rvq_setup_level<256>(sa, (int)blockIdx.x);
@@ -263,25 +267,33 @@ __global__ __launch_bounds__(256) void rvq_pyramid_kernel(const float* __restric
     const int64_t groups = rows >> DEPTH;
     if (idx >= groups * q) return;
     const int64_t g = idx / q, c = (idx % q) * 4;
-    float* dst[4] = {dst0, dst1, dst2, dst3};
+    float* dst[kMaxPyrPass] = {dst0, dst1, dst2, dst3, dst4, dst5, dst6};
+    // Rows are loaded RB at a time; every loop is unrolled, so the stack
+    // level each row reaches is known at compile time.
+    constexpr int RB = N < 16 ? N : 16;
     f32x4_t stk[DEPTH];
-    f32x4_t in[N];
 #pragma unroll
-    for (int r = 0; r < N; ++r) in[r] = *(const f32x4_t*)(src + ((g << DEPTH) + r) * d + c);
+    for (int r0 = 0; r0 < N; r0 += RB) {
+        f32x4_t in[RB];
 #pragma unroll
-    for (int r = 0; r < N; ++r) {
-        f32x4_t v = in[r];
+        for (int i = 0; i < RB; ++i)
+            in[i] = *(const f32x4_t*)(src + ((g << DEPTH) + r0 + i) * d + c);
 #pragma unroll
-        for (int k = 0; k < DEPTH; ++k) {
-            if ((r >> k) & 1) {
-                f32x4_t s;
+        for (int i = 0; i < RB; ++i) {
+            const int r = r0 + i;
+            f32x4_t v = in[i];
 #pragma unroll
-                for (int e = 0; e < 4; ++e) s[e] = (stk[k][e] + v[e]) * 0.5f;
-                v = s;
-                *(f32x4_t*)(dst[k] + (((g << DEPTH) + r) >> (k + 1)) * d + c) = v;
-            } else {
-                stk[k] = v;
-                break;
+            for (int k = 0; k < DEPTH; ++k) {
+                if ((r >> k) & 1) {
+                    f32x4_t s;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) s[e] = (stk[k][e] + v[e]) * 0.5f;
+                    v = s;
+                    *(f32x4_t*)(dst[k] + (((g << DEPTH) + r) >> (k + 1)) * d + c) = v;
+                } else {
+                    stk[k] = v;
+                    break;
+                }
             }
         }
     }
@@ -1176,25 +1188,32 @@ int rvq_encode_ws(hipStream_t st, void* ws, size_t ws_bytes, const float* x, int
         if (e != hipSuccess) return NCM_E_HIP;
     }
 
-    // Pyramid, in passes of up to four halvings; the first pass carries the
+    // Pyramid, in passes of up to seven halvings; the first pass carries the
     // set-up in its first `levels` workgroups.
     {
         int j0 = 0;
         while (j0 < jmax) {
-            const int depth = std::min(4, jmax - j0);
+            const int depth = std::min(kMaxPyrPass, jmax - j0);
             const float* src = j0 == 0 ? x : pyr + g.pyr_off[j0];
             const int64_t rows = b * (t >> j0);
-            float* dst[4] = {nullptr, nullptr, nullptr, nullptr};
+            float* dst[kMaxPyrPass] = {};
             for (int k = 0; k < depth; ++k) dst[k] = pyr + g.pyr_off[j0 + k + 1];
             const int64_t work = (rows >> depth) * (d / 4);
             const int sb = j0 == 0 ? (int)levels : 0;
             const dim3 grid((unsigned)((work + 255) / 256 + sb));
+#define NCM_PYR(D)                                                                            \
+    hipLaunchKernelGGL(rvq_pyramid_kernel<D>, grid, dim3(256), 0, st, src, rows, d, dst[0],    \
+                       dst[1], dst[2], dst[3], dst[4], dst[5], dst[6], sa, sb)
             switch (depth) {
-                case 1: hipLaunchKernelGGL(rvq_pyramid_kernel<1>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3], sa, sb); break;
-                case 2: hipLaunchKernelGGL(rvq_pyramid_kernel<2>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3], sa, sb); break;
-                case 3: hipLaunchKernelGGL(rvq_pyramid_kernel<3>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3], sa, sb); break;
-                default: hipLaunchKernelGGL(rvq_pyramid_kernel<4>, grid, dim3(256), 0, st, src, rows, d, dst[0], dst[1], dst[2], dst[3], sa, sb); break;
+                case 1: NCM_PYR(1); break;
+                case 2: NCM_PYR(2); break;
+                case 3: NCM_PYR(3); break;
+                case 4: NCM_PYR(4); break;
+                case 5: NCM_PYR(5); break;
+                case 6: NCM_PYR(6); break;
+                default: NCM_PYR(7); break;
             }
+#undef NCM_PYR
             e = hipGetLastError();
             if (e != hipSuccess) return NCM_E_HIP;
             j0 += depth;
